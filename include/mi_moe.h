@@ -1,0 +1,183 @@
+/*
+ * mi_moe.h - C ABI of the MI355X-native routed mixture-of-experts FFN layer.
+ *
+ * Plain C types only (device pointers, sizes, ggml-style tensor descriptors);
+ * no C++ or torch types cross this boundary.  Every entry point returns an
+ * mi_moe_status (0 = success, negative = error) and never synchronizes the
+ * stream it is given unless documented.  Device pointers are owned by the
+ * caller; the library never frees them.  A context is not thread-safe: use
+ * one context per host thread / stream (the same rule as the reference's
+ * vqa::Model, src/core/vqa.hpp:121-122).
+ *
+ * Each entry point names the reference interface it replaces (file:line in
+ * SkyVision.cpp).  Type ids follow ggml_type numbering (GGUF type ids), so a
+ * ggml backend can pass tensor->type through unchanged.
+ */
+#ifndef MI_MOE_H
+#define MI_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI_MOE_ABI_VERSION 1
+
+/* hipStream_t without pulling in HIP headers */
+typedef struct ihipStream_t *mi_stream_t;
+
+typedef enum {
+    MI_MOE_OK               = 0,
+    MI_MOE_ERR_NULL         = -1,  /* a required pointer is NULL                  */
+    MI_MOE_ERR_SHAPE        = -2,  /* shapes / strides inconsistent               */
+    MI_MOE_ERR_TYPE         = -3,  /* tensor type not supported by this op        */
+    MI_MOE_ERR_CAPACITY     = -4,  /* exceeds what mi_moe_ctx_reserve sized       */
+    MI_MOE_ERR_HIP          = -5,  /* a HIP runtime call failed                   */
+    MI_MOE_ERR_UNSUPPORTED  = -6,  /* valid request this build does not handle    */
+    MI_MOE_ERR_DEVICE       = -7,  /* no such device / device not usable          */
+    MI_MOE_ERR_ARG          = -8,  /* other invalid argument (enum out of range)  */
+} mi_moe_status;
+
+typedef enum {                     /* ggml_type ids */
+    MI_TYPE_F32  = 0,
+    MI_TYPE_F16  = 1,
+    MI_TYPE_Q4_K = 12,             /* 144 B / 256 values, convert/q4k.py:9-10  */
+    MI_TYPE_Q6_K = 14,             /* 210 B / 256 values, convert/q6k.py:10-11 */
+    MI_TYPE_I32  = 26,
+} mi_type;
+
+typedef enum {                     /* activation between the two expert products */
+    MI_ACT_SILU          = 0,      /* silu(gate)*up: ggml_swiglu_split, qwen3omni_model.cpp:771     */
+    MI_ACT_GELU_ERF_GP1  = 1,      /* gelu_erf(h)*(g+1): geglu_erf_split(h, g+1), moondream.cpp:534 */
+    MI_ACT_GELU_TANH     = 2,      /* gelu_tanh(gate)*up                                            */
+    MI_ACT_GELU_ERF      = 3,      /* gelu_erf(gate)*up: ggml_mul(ggml_unary(gu, act), up),
+                                      moe_compute.cpp:127-129                                       */
+} mi_act;
+
+typedef enum {
+    MI_GATING_SOFTMAX_TOPK = 0,    /* top_k on logits, softmax over the K selected
+                                      (moondream.cpp:510-516, qwen3omni_model.cpp:759-766) */
+} mi_gating;
+
+/* ggml_tensor stand-in: data on the device, ne fastest-first, nb in bytes. */
+typedef struct {
+    void    *data;
+    int32_t  type;                 /* mi_type */
+    int64_t  ne[4];
+    size_t   nb[4];
+} mi_tensor;
+
+/* One MoE FFN layer as the reference binds it (moondream.cpp:241-251,
+ * qwen3omni_model.cpp:362-364, convert_hf_to_gguf.py:177-183,
+ * convert_qwen3omni.py:188-219). */
+typedef struct {
+    int32_t n_embd;                /* D */
+    int32_t n_expert;              /* E */
+    int32_t n_expert_used;         /* K */
+    int32_t n_ff;                  /* I (expert inner dim) */
+    const float *router_w;         /* F32 ne=[D, E]: E rows of D (ffn_gate_inp.weight) */
+    const float *router_b;         /* F32 [E] or NULL (ffn_gate_inp.bias, moondream only) */
+    mi_tensor gate;                /* fused_gate_up=1: ffn_up_exps ne=[D, 2I, E], rows [0,I)=h, [I,2I)=g
+                                      fused_gate_up=0: ffn_gate_exps ne=[D, I, E] */
+    mi_tensor up;                  /* ffn_up_exps ne=[D, I, E]; ignored when fused */
+    mi_tensor down;                /* ffn_down_exps ne=[I, D, E] */
+    int32_t fused_gate_up;
+    int32_t act;                   /* mi_act */
+    int32_t gating;                /* mi_gating */
+} mi_moe_layer;
+
+/* Optional routing outputs of mi_moe_forward (device pointers, any may be
+ * NULL).  Layouts are row-major with tokens outermost. */
+typedef struct {
+    float   *logits;               /* [T][E]   router logits                      */
+    int32_t *sel;                  /* [T][K]   expert ids, descending logit        */
+    float   *weights;              /* [T][K]   softmax over the K selected logits  */
+    int32_t *counts;               /* [E]      tokens routed to each expert        */
+    int32_t *offsets;              /* [E+1]    exclusive prefix sum of counts      */
+    int32_t *perm;                 /* [T*K]    per-expert lists, value t*K+k,
+                                               token-ascending within an expert    */
+} mi_moe_routing;
+
+typedef struct mi_moe_ctx mi_moe_ctx;
+
+/* ---- context -------------------------------------------------------------
+ * Replaces the backend bring-up + graph allocator pre-grow of the reference
+ * (moondream.cpp:306-353, gallocr pre-grow :340-351).  Workspace is allocated
+ * only by mi_moe_ctx_reserve; forward calls never allocate. */
+int  mi_moe_ctx_create(mi_moe_ctx **out, int device);
+void mi_moe_ctx_destroy(mi_moe_ctx *ctx);
+/* size the workspace for up to max_tokens tokens of layers with these dims */
+int  mi_moe_ctx_reserve(mi_moe_ctx *ctx, int64_t max_tokens, int32_t n_embd, int32_t n_ff,
+                        int32_t n_expert, int32_t n_expert_used);
+
+/* ---- whole MoE block ------------------------------------------------------
+ * out[t] = res[t] + sum_k w[t][k] * down_{sel[t][k]}( act(gate x[t], up x[t]) )
+ * Replaces the inline ggml MoE block: router mul_mat(+bias) -> top_k ->
+ * get_rows -> soft_max -> mul_mat_id (gate/up) -> GLU -> mul_mat_id (down) ->
+ * mul(w) -> permute/cont -> sum_rows (-> add res)
+ *   moondream3: src/models/moondream/moondream.cpp:509-544 (+ residual :547)
+ *   qwen3omni : src/models/qwen3omni/qwen3omni_model.cpp:759-780
+ * x, res, out: F32 [T][D] device; res may be NULL (out = MoE only); out may
+ * alias res.  routing may be NULL. */
+int mi_moe_forward(mi_moe_ctx *ctx, const mi_moe_layer *layer, const float *x, int64_t n_tokens,
+                   const float *res, float *out, const mi_moe_routing *routing,
+                   mi_stream_t stream);
+
+/* ---- routed FFN with caller-supplied routing ------------------------------
+ * Replaces vqa::moe::build_expert_ffn_table_res (src/core/engine/moe_compute.hpp:66-71,
+ * moe_compute.cpp:93-136) and the default graph B of the expert-cache decode
+ * driver (moe_decode_driver.hpp:503-514):
+ *   out = res + sum_k w[k] * down_k(act(gate_k x, up_k x))
+ * gate_up_ids / down_ids: I32 [T][K] device (may be the same pointer);
+ * w: F32 [T][K] device.  The layer's router fields are ignored. */
+int mi_moe_expert_ffn(mi_moe_ctx *ctx, const mi_moe_layer *layer, const float *x, int64_t n_tokens,
+                      const float *res, const int32_t *gate_up_ids, const int32_t *down_ids,
+                      const float *w, float *out, mi_stream_t stream);
+
+/* ---- op-level contracts (ggml op semantics) ------------------------------
+ * ggml_top_k(ctx, a F32 ne=[E,T], k) -> I32 ne=[k,T] (moondream.cpp:511,
+ * qwen3omni_model.cpp:761): indices of the k largest, descending, ties ->
+ * lower index. */
+int mi_top_k(mi_moe_ctx *ctx, const mi_tensor *a, int32_t k, mi_tensor *dst, mi_stream_t stream);
+
+/* ggml_mul_mat_id(ctx, as ne=[Kin,N,E], b F32 ne=[Kin, 1|n_used, T],
+ * ids I32 ne=[n_used, T]) -> F32 ne=[N, n_used, T]
+ * (moondream.cpp:519,537; qwen3omni_model.cpp:769-774; moe_compute.cpp:124-130).
+ * dst[:, k, t] = as[:, :, ids[k,t]] . b[:, k % ne11, t].  as types: Q4_K,
+ * Q6_K, F32.  k-quant products quantize b to Q8_K first, like ggml-cpu. */
+int mi_mul_mat_id(mi_moe_ctx *ctx, const mi_tensor *as, const mi_tensor *b, const mi_tensor *ids,
+                  mi_tensor *dst, mi_stream_t stream);
+
+/* ---- weight preparation ----------------------------------------------------
+ * quantize_row_q4_K_ref / quantize_row_q6_K_ref (ggml; ported in
+ * convert/q4k.py:27-127 and convert/q6k.py:103-193; called through
+ * ggml_quantize_chunk in tools/moe_cpu_bench.cpp:141).  src: F32 [nrows][n_per_row]
+ * device, dst: nrows * row_size bytes device.  Byte-identical to the CPU
+ * restatement of ggml's reference quantizers. */
+int mi_quantize(mi_moe_ctx *ctx, int32_t type, const float *src, void *dst, int64_t nrows,
+                int64_t n_per_row, mi_stream_t stream);
+
+/* Seeded synthetic N(mean, std^2) fill: value i of (seed, stream_id) does not
+ * depend on n or the launch shape.  Counterpart of the reference's seeded
+ * test RNG (src/core/test/seg_test.hpp:57-68). */
+int mi_fill_normal(mi_moe_ctx *ctx, float *dst, int64_t n, uint64_t seed, uint64_t stream_id,
+                   float mean, float stddev, mi_stream_t stream);
+
+/* ---- introspection ---------------------------------------------------------
+ * Per-stage timing (HIP events on the call's stream) for the last forward
+ * when profiling is on.  Stage names are static strings. */
+int mi_moe_ctx_set_profiling(mi_moe_ctx *ctx, int on);
+int mi_moe_ctx_stage_times(mi_moe_ctx *ctx, int max_stages, const char **names, float *ms,
+                           int *n_stages);
+/* path choice for a token count: 0 = grouped GEMV (decode), 1 = grouped MFMA GEMM */
+int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *ctx, int64_t min_tokens_for_gemm);
+size_t      mi_row_size(int32_t type, int64_t n_per_row);
+const char *mi_moe_status_string(int status);
+int         mi_moe_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MI_MOE_H */

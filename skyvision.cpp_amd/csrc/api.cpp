@@ -1,0 +1,691 @@
+// api.cpp - the C ABI (include/mi_moe.h, include/mi_moe_util.h).
+//
+// Validates arguments the way the reference's graph builders do
+// (moe_compute.cpp:102-120: bad shapes / types -> error, nothing enqueued),
+// then enqueues the kernel chain on the caller's stream:
+//   router -> top-k/softmax -> dispatch -> Q8_K(x) -> gate/up (+GLU, +Q8_K)
+//   -> down -> weighted combine (+residual)
+// Decode-sized calls (fewer than gemm_threshold tokens) use the grouped
+// integer-dot GEMV kernels; larger calls use the grouped MFMA GEMM kernels.
+// All workspace comes from mi_moe_ctx_reserve; forward calls never allocate.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/mi_moe.h"
+#include "../../include/mi_moe_util.h"
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace mimoe {
+int launch_mm_id_f32(const GemvArgs &g, const float *b, int64_t ldb, hipStream_t st);
+int launch_glu_rows(const float *h, int64_t ldh, const float *gg, int64_t ldg, float *out, int64_t ldo,
+                    int64_t rows, int64_t I, int act, hipStream_t st);
+
+static thread_local std::string g_last_error;
+
+int record_hip_error(hipError_t e) {
+    g_last_error = hipGetErrorString(e);
+    return MI_MOE_ERR_HIP;
+}
+int hip_check_launch() {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : record_hip_error(e);
+}
+}  // namespace mimoe
+
+using namespace mimoe;
+
+#define HIP_TRY(x)                                         \
+    do {                                                   \
+        const hipError_t e_ = (x);                         \
+        if (e_ != hipSuccess) return record_hip_error(e_); \
+    } while (0)
+#define TRY(x)                \
+    do {                      \
+        const int r_ = (x);   \
+        if (r_) return r_;    \
+    } while (0)
+
+namespace {
+
+constexpr int kMaxStages = 16;
+
+struct ActBuf {                // one Q8_K activation set
+    int8_t *q8 = nullptr;
+    float *d8 = nullptr;
+    int16_t *bs = nullptr;
+    _Float16 *h = nullptr;
+};
+
+struct DispBuf {
+    int32_t *counts, *offsets, *perm, *tile_e, *tile_r0, *n_tiles, *active_e, *n_active, *bad;
+    Dispatch view() const {
+        Dispatch d;
+        d.counts = counts; d.offsets = offsets; d.perm = perm; d.tile_e = tile_e; d.tile_r0 = tile_r0;
+        d.n_tiles = n_tiles; d.active_e = active_e; d.n_active = n_active; d.bad_ids = bad;
+        return d;
+    }
+};
+
+}  // namespace
+
+struct mi_moe_ctx {
+    int device = 0;
+    bool reserved = false;
+    int64_t cap_T = 0;
+    int32_t cap_D = 0, cap_I = 0, cap_E = 0, cap_K = 0;
+    int64_t cap_rows = 0, cap_kmax = 0, cap_tiles = 0;
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+
+    float *logits = nullptr;
+    int32_t *sel = nullptr;
+    float *w = nullptr;
+    DispBuf disp[2];
+    ActBuf ax, aact;
+    float *f1 = nullptr;      // [rows][max(2I, kmax)]  GLU / F32 scratch
+    float *f2 = nullptr;      // [rows][I]
+    float *z = nullptr;       // [rows][max(D, 2I)]
+    int64_t gemm_threshold = 16;
+
+    bool profiling = false;
+    hipEvent_t ev[kMaxStages + 1] = {};
+    const char *stage_name[kMaxStages] = {};
+    int n_stages = 0;
+    hipStream_t prof_stream = nullptr;
+};
+
+namespace {
+
+void stage_begin(mi_moe_ctx *c, hipStream_t st) {
+    if (!c->profiling) return;
+    c->n_stages = 0;
+    c->prof_stream = st;
+    (void)hipEventRecord(c->ev[0], st);
+}
+void stage_end(mi_moe_ctx *c, const char *name, hipStream_t st) {
+    if (!c->profiling || c->n_stages >= kMaxStages) return;
+    c->stage_name[c->n_stages] = name;
+    c->n_stages++;
+    (void)hipEventRecord(c->ev[c->n_stages], st);
+}
+
+bool is_kquant(int t) { return t == MI_TYPE_Q4_K || t == MI_TYPE_Q6_K; }
+
+size_t type_row_size(int32_t type, int64_t n) {
+    switch (type) {
+    case MI_TYPE_F32: return (size_t)n * 4;
+    case MI_TYPE_F16: return (size_t)n * 2;
+    case MI_TYPE_Q4_K: return n % QK ? 0 : (size_t)(n / QK) * Q4K_BYTES;
+    case MI_TYPE_Q6_K: return n % QK ? 0 : (size_t)(n / QK) * Q6K_BYTES;
+    default: return 0;
+    }
+}
+
+// an expert table ne=[K, N, E] with ggml strides
+int check_table(const mi_tensor &t, int64_t K, int64_t N, int64_t E) {
+    if (!t.data) return MI_MOE_ERR_NULL;
+    if (t.type != MI_TYPE_Q4_K && t.type != MI_TYPE_Q6_K && t.type != MI_TYPE_F32) return MI_MOE_ERR_TYPE;
+    if (t.ne[0] != K || t.ne[1] != N || t.ne[2] < E || t.ne[3] != 1) return MI_MOE_ERR_SHAPE;
+    const size_t rs = type_row_size(t.type, K);
+    if (rs == 0) return MI_MOE_ERR_SHAPE;
+    if (t.nb[1] < rs || t.nb[2] < t.nb[1] * (size_t)N) return MI_MOE_ERR_SHAPE;
+    if (t.type == MI_TYPE_Q4_K && ((uintptr_t)t.data % 16 || t.nb[1] % 16 || t.nb[2] % 16))
+        return MI_MOE_ERR_UNSUPPORTED;   // Q4_K rows are read with 16-byte loads
+    if (t.type == MI_TYPE_Q6_K && ((uintptr_t)t.data % 4 || t.nb[1] % 2 || t.nb[2] % 2))
+        return MI_MOE_ERR_UNSUPPORTED;
+    if (t.type == MI_TYPE_F32 && ((uintptr_t)t.data % 4 || t.nb[1] % 4)) return MI_MOE_ERR_UNSUPPORTED;
+    return MI_MOE_OK;
+}
+
+ExpertMat as_mat(const mi_tensor &t) {
+    ExpertMat m;
+    m.data = (const uint8_t *)t.data;
+    m.type = t.type;
+    m.row_bytes = (int64_t)t.nb[1];
+    m.mat_bytes = (int64_t)t.nb[2];
+    m.K = t.ne[0];
+    m.N = t.ne[1];
+    return m;
+}
+
+int validate_layer(const mi_moe_ctx *c, const mi_moe_layer *L, bool need_router) {
+    if (!L) return MI_MOE_ERR_NULL;
+    const int64_t D = L->n_embd, E = L->n_expert, K = L->n_expert_used, I = L->n_ff;
+    if (D <= 0 || E <= 0 || K <= 0 || I <= 0 || K > E) return MI_MOE_ERR_SHAPE;
+    if (E > 256 || K > 64) return MI_MOE_ERR_UNSUPPORTED;
+    if (L->act < MI_ACT_SILU || L->act > MI_ACT_GELU_ERF) return MI_MOE_ERR_ARG;
+    if (L->gating != MI_GATING_SOFTMAX_TOPK) return MI_MOE_ERR_ARG;
+    if (need_router && !L->router_w) return MI_MOE_ERR_NULL;
+    const int64_t Ng = L->fused_gate_up ? 2 * I : I;
+    TRY(check_table(L->gate, D, Ng, E));
+    if (!L->fused_gate_up) {
+        TRY(check_table(L->up, D, I, E));
+        if (L->up.type != L->gate.type) return MI_MOE_ERR_TYPE;   // gate/up interchangeable (moe_compute.cpp:114-116)
+    }
+    TRY(check_table(L->down, I, D, E));
+    const bool kq = is_kquant(L->gate.type);
+    if (kq != is_kquant(L->down.type)) return MI_MOE_ERR_UNSUPPORTED;   // mixed F32 / k-quant layers
+    if (!c->reserved) return MI_MOE_ERR_CAPACITY;
+    if (D > c->cap_D || I > c->cap_I || E > c->cap_E || K > c->cap_K) return MI_MOE_ERR_CAPACITY;
+    return MI_MOE_OK;
+}
+
+// routed FFN body: needs c->sel-like ids (device [T][K]) and weights w [T][K]
+int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const int32_t *ids_gu,
+                const int32_t *ids_dn, const float *w, const float *res, float *out, hipStream_t st) {
+    const int D = L->n_embd, E = L->n_expert, K = L->n_expert_used, I = L->n_ff;
+    const int64_t rows = T * K;
+    const int max_active = (int)std::min<int64_t>(E, rows);
+    const int max_tiles = (int)((rows + GEMM_BM - 1) / GEMM_BM + max_active);
+    const bool same_ids = ids_gu == ids_dn;
+
+    TRY(launch_dispatch(ids_gu, T, K, E, GEMM_BM, c->disp[0].view(), st));
+    if (!same_ids) TRY(launch_dispatch(ids_dn, T, K, E, GEMM_BM, c->disp[1].view(), st));
+    const DispBuf &dg = c->disp[0];
+    const DispBuf &dd = same_ids ? c->disp[0] : c->disp[1];
+    stage_end(c, "dispatch", st);
+
+    const ExpertMat gate = as_mat(L->gate), down = as_mat(L->down);
+    ExpertMat up = {};
+    if (!L->fused_gate_up) up = as_mat(L->up);
+
+    if (!is_kquant(L->gate.type)) {
+        // fp32 expert tables: reference semantics without activation quantization
+        const int64_t Ng = L->fused_gate_up ? 2LL * I : I;
+        GemvArgs a = {};
+        a.a = gate; a.ne11 = 1; a.K = K;
+        a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.active_e = dg.active_e;
+        a.n_active = dg.n_active; a.max_active = max_active;
+        a.y = c->f1; a.ldy = Ng; a.ncols = Ng;
+        TRY(launch_mm_id_f32(a, x, D, st));
+        const float *hbuf = c->f1, *gbuf = c->f1 + I;
+        int64_t ldh = Ng, ldg = Ng;
+        if (!L->fused_gate_up) {
+            a.a = up; a.y = c->f2; a.ldy = I; a.ncols = I;
+            TRY(launch_mm_id_f32(a, x, D, st));
+            gbuf = c->f2;
+            ldg = I;
+        }
+        // act into z scratch rows [rows][I]
+        float *act = c->z;
+        TRY(launch_glu_rows(hbuf, ldh, gbuf, ldg, act, I, rows, I, L->act, st));
+        stage_end(c, "gate_up", st);
+        GemvArgs d = {};
+        d.a = down; d.ne11 = K; d.K = K;
+        d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.active_e = dd.active_e;
+        d.n_active = dd.n_active; d.max_active = max_active;
+        d.y = c->f1; d.ldy = D; d.ncols = D;
+        TRY(launch_mm_id_f32(d, act, I, st));
+        stage_end(c, "down", st);
+        TRY(launch_combine(c->f1, w, res, out, T, K, D, st));
+        stage_end(c, "combine", st);
+        return MI_MOE_OK;
+    }
+
+    const bool gemm = T >= c->gemm_threshold || D > 8 * QK || I > 8 * QK;
+    if (!gemm) {
+        Q8Out qx;
+        qx.q8 = c->ax.q8; qx.d8 = c->ax.d8; qx.bsums = c->ax.bs;
+        TRY(launch_q8k_rows(x, D, T, D, qx, st));
+        stage_end(c, "q8k_x", st);
+        GemvArgs a = {};
+        a.a = gate; a.b = up; a.epi = EPI_GLU; a.act = L->act; a.I = I; a.fused = L->fused_gate_up;
+        a.q8 = c->ax.q8; a.d8 = c->ax.d8; a.bsums = c->ax.bs; a.ne11 = 1; a.K = K;
+        a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.active_e = dg.active_e;
+        a.n_active = dg.n_active; a.max_active = max_active;
+        a.y = c->f1; a.ldy = I; a.ncols = I;
+        TRY(launch_gemv(a, st));
+        stage_end(c, "gate_up", st);
+        Q8Out qa;
+        qa.q8 = c->aact.q8; qa.d8 = c->aact.d8; qa.bsums = c->aact.bs;
+        TRY(launch_q8k_rows(c->f1, I, rows, I, qa, st));
+        stage_end(c, "q8k_act", st);
+        GemvArgs d = {};
+        d.a = down; d.epi = EPI_STORE;
+        d.q8 = c->aact.q8; d.d8 = c->aact.d8; d.bsums = c->aact.bs; d.ne11 = K; d.K = K;
+        d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.active_e = dd.active_e;
+        d.n_active = dd.n_active; d.max_active = max_active;
+        d.y = c->z; d.ldy = D; d.ncols = D;
+        TRY(launch_gemv(d, st));
+        stage_end(c, "down", st);
+    } else {
+        Q8Out qx;
+        qx.xh = c->ax.h; qx.wtype = gate.type;
+        TRY(launch_q8k_rows(x, D, T, D, qx, st));
+        stage_end(c, "q8k_x", st);
+        GemmArgs a = {};
+        a.a = gate; a.b = up; a.epi = EPI_GLU; a.act = L->act; a.I = I; a.fused = L->fused_gate_up;
+        a.xh = c->ax.h; a.ne11 = 1; a.K = K;
+        a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.tile_e = dg.tile_e;
+        a.tile_r0 = dg.tile_r0; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
+        a.acth = c->aact.h; a.next_type = down.type; a.ncols = I;
+        TRY(launch_gemm(a, st));
+        stage_end(c, "gate_up", st);
+        GemmArgs d = {};
+        d.a = down; d.epi = EPI_STORE; d.xh = c->aact.h; d.ne11 = K; d.K = K;
+        d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
+        d.tile_r0 = dd.tile_r0; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles;
+        d.y = c->z; d.ldy = D; d.ncols = D;
+        TRY(launch_gemm(d, st));
+        stage_end(c, "down", st);
+    }
+    TRY(launch_combine(c->z, w, res, out, T, K, D, st));
+    stage_end(c, "combine", st);
+    return MI_MOE_OK;
+}
+
+template <typename T>
+T *carve(char *&p, size_t n) {
+    T *r = (T *)p;
+    size_t bytes = (sizeof(T) * n + 255) & ~(size_t)255;
+    p += bytes;
+    return r;
+}
+template <typename T>
+size_t carve_size(size_t n) {
+    return (sizeof(T) * n + 255) & ~(size_t)255;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi_moe_abi_version(void) { return MI_MOE_ABI_VERSION; }
+
+const char *mi_moe_status_string(int s) {
+    switch (s) {
+    case MI_MOE_OK: return "ok";
+    case MI_MOE_ERR_NULL: return "null pointer";
+    case MI_MOE_ERR_SHAPE: return "bad shape";
+    case MI_MOE_ERR_TYPE: return "unsupported type";
+    case MI_MOE_ERR_CAPACITY: return "exceeds reserved capacity";
+    case MI_MOE_ERR_HIP: return "HIP error";
+    case MI_MOE_ERR_UNSUPPORTED: return "unsupported";
+    case MI_MOE_ERR_DEVICE: return "bad device";
+    case MI_MOE_ERR_ARG: return "bad argument";
+    default: return "unknown";
+    }
+}
+
+size_t mi_row_size(int32_t type, int64_t n) { return type_row_size(type, n); }
+
+int mi_moe_ctx_create(mi_moe_ctx **out, int device) {
+    if (!out) return MI_MOE_ERR_NULL;
+    *out = nullptr;
+    int n = 0;
+    HIP_TRY(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return MI_MOE_ERR_DEVICE;
+    HIP_TRY(hipSetDevice(device));
+    mi_moe_ctx *c = new mi_moe_ctx();
+    c->device = device;
+    for (int i = 0; i <= kMaxStages; ++i) {
+        const hipError_t e = hipEventCreate(&c->ev[i]);
+        if (e != hipSuccess) {
+            for (int j = 0; j < i; ++j) (void)hipEventDestroy(c->ev[j]);
+            delete c;
+            return record_hip_error(e);
+        }
+    }
+    *out = c;
+    return MI_MOE_OK;
+}
+
+void mi_moe_ctx_destroy(mi_moe_ctx *c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->ws) (void)hipFree(c->ws);
+    for (int i = 0; i <= kMaxStages; ++i)
+        if (c->ev[i]) (void)hipEventDestroy(c->ev[i]);
+    delete c;
+}
+
+int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, int32_t E, int32_t K) {
+    if (!c) return MI_MOE_ERR_NULL;
+    if (max_tokens <= 0 || D <= 0 || I <= 0 || E <= 0 || K <= 0 || K > E) return MI_MOE_ERR_SHAPE;
+    if (E > 256 || K > 64) return MI_MOE_ERR_UNSUPPORTED;
+    HIP_TRY(hipSetDevice(c->device));
+    const int64_t rows = max_tokens * K;
+    const int64_t kmax = std::max<int64_t>(D, I);
+    const int64_t kmax_q = (kmax + QK - 1) / QK * QK;
+    const int64_t wide = std::max<int64_t>(std::max<int64_t>(D, 2LL * I), kmax);
+    const int64_t tiles = (rows + GEMM_BM - 1) / GEMM_BM + std::min<int64_t>(E, rows);
+    size_t need = 0;
+    need += carve_size<float>(max_tokens * E) + carve_size<int32_t>(rows) + carve_size<float>(rows);
+    for (int s = 0; s < 2; ++s)
+        need += carve_size<int32_t>(E) + carve_size<int32_t>(E + 1) + carve_size<int32_t>(rows) +
+                2 * carve_size<int32_t>(tiles) + carve_size<int32_t>(1) + carve_size<int32_t>(E) +
+                2 * carve_size<int32_t>(1);
+    // activation sets: x/b rows (rows x kmax) and act rows (rows x I)
+    need += carve_size<int8_t>(rows * kmax_q) + carve_size<float>(rows * kmax_q / QK) +
+            carve_size<int16_t>(rows * kmax_q / 16) + carve_size<_Float16>(rows * kmax_q);
+    const int64_t iq = (I + QK - 1) / QK * QK;
+    need += carve_size<int8_t>(rows * iq) + carve_size<float>(rows * iq / QK) +
+            carve_size<int16_t>(rows * iq / 16) + carve_size<_Float16>(rows * iq);
+    need += carve_size<float>(rows * wide) + carve_size<float>(rows * I) + carve_size<float>(rows * wide);
+
+    if (c->ws) {
+        (void)hipFree(c->ws);
+        c->ws = nullptr;
+        c->reserved = false;
+    }
+    void *p = nullptr;
+    HIP_TRY(hipMalloc(&p, need));
+    c->ws = p;
+    c->ws_bytes = need;
+    char *q = (char *)p;
+    c->logits = carve<float>(q, max_tokens * E);
+    c->sel = carve<int32_t>(q, rows);
+    c->w = carve<float>(q, rows);
+    for (int s = 0; s < 2; ++s) {
+        DispBuf &d = c->disp[s];
+        d.counts = carve<int32_t>(q, E);
+        d.offsets = carve<int32_t>(q, E + 1);
+        d.perm = carve<int32_t>(q, rows);
+        d.tile_e = carve<int32_t>(q, tiles);
+        d.tile_r0 = carve<int32_t>(q, tiles);
+        d.n_tiles = carve<int32_t>(q, 1);
+        d.active_e = carve<int32_t>(q, E);
+        d.n_active = carve<int32_t>(q, 1);
+        d.bad = carve<int32_t>(q, 1);
+    }
+    c->ax.q8 = carve<int8_t>(q, rows * kmax_q);
+    c->ax.d8 = carve<float>(q, rows * kmax_q / QK);
+    c->ax.bs = carve<int16_t>(q, rows * kmax_q / 16);
+    c->ax.h = carve<_Float16>(q, rows * kmax_q);
+    c->aact.q8 = carve<int8_t>(q, rows * iq);
+    c->aact.d8 = carve<float>(q, rows * iq / QK);
+    c->aact.bs = carve<int16_t>(q, rows * iq / 16);
+    c->aact.h = carve<_Float16>(q, rows * iq);
+    c->f1 = carve<float>(q, rows * wide);
+    c->f2 = carve<float>(q, rows * I);
+    c->z = carve<float>(q, rows * wide);
+    HIP_TRY(hipMemset(p, 0, need));
+    c->cap_T = max_tokens;
+    c->cap_D = D;
+    c->cap_I = I;
+    c->cap_E = E;
+    c->cap_K = K;
+    c->cap_rows = rows;
+    c->cap_kmax = kmax_q;
+    c->cap_tiles = tiles;
+    c->reserved = true;
+    return MI_MOE_OK;
+}
+
+int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *c, int64_t t) {
+    if (!c) return MI_MOE_ERR_NULL;
+    if (t < 1) return MI_MOE_ERR_ARG;
+    c->gemm_threshold = t;
+    return MI_MOE_OK;
+}
+
+int mi_moe_ctx_set_profiling(mi_moe_ctx *c, int on) {
+    if (!c) return MI_MOE_ERR_NULL;
+    c->profiling = on != 0;
+    c->n_stages = 0;
+    return MI_MOE_OK;
+}
+
+int mi_moe_ctx_stage_times(mi_moe_ctx *c, int max_stages, const char **names, float *ms, int *n_stages) {
+    if (!c || !n_stages) return MI_MOE_ERR_NULL;
+    *n_stages = 0;
+    if (!c->profiling || c->n_stages == 0) return MI_MOE_OK;
+    HIP_TRY(hipEventSynchronize(c->ev[c->n_stages]));
+    const int n = std::min(max_stages, c->n_stages);
+    for (int i = 0; i < n; ++i) {
+        if (names) names[i] = c->stage_name[i];
+        if (ms) HIP_TRY(hipEventElapsedTime(&ms[i], c->ev[i], c->ev[i + 1]));
+    }
+    *n_stages = n;
+    return MI_MOE_OK;
+}
+
+int mi_moe_forward(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const float *res,
+                   float *out, const mi_moe_routing *routing, mi_stream_t stream) {
+    if (!c) return MI_MOE_ERR_NULL;
+    if (T < 0) return MI_MOE_ERR_SHAPE;
+    TRY(validate_layer(c, L, true));
+    if (T == 0) return MI_MOE_OK;
+    if (!x || !out) return MI_MOE_ERR_NULL;
+    if (T > c->cap_T) return MI_MOE_ERR_CAPACITY;
+    HIP_TRY(hipSetDevice(c->device));
+    hipStream_t st = (hipStream_t)stream;
+    const int D = L->n_embd, E = L->n_expert, K = L->n_expert_used;
+    stage_begin(c, st);
+    TRY(launch_router(L->router_w, L->router_b, x, D, T, D, E, c->logits, st));
+    stage_end(c, "router", st);
+    TRY(launch_topk_softmax(c->logits, E, T, E, K, c->sel, K, c->w, st));
+    stage_end(c, "topk_softmax", st);
+    TRY(run_experts(c, L, x, T, c->sel, c->sel, c->w, res, out, st));
+    if (routing) {
+        const DispBuf &d = c->disp[0];
+        if (routing->logits)
+            HIP_TRY(hipMemcpyAsync(routing->logits, c->logits, sizeof(float) * T * E, hipMemcpyDeviceToDevice, st));
+        if (routing->sel)
+            HIP_TRY(hipMemcpyAsync(routing->sel, c->sel, sizeof(int32_t) * T * K, hipMemcpyDeviceToDevice, st));
+        if (routing->weights)
+            HIP_TRY(hipMemcpyAsync(routing->weights, c->w, sizeof(float) * T * K, hipMemcpyDeviceToDevice, st));
+        if (routing->counts)
+            HIP_TRY(hipMemcpyAsync(routing->counts, d.counts, sizeof(int32_t) * E, hipMemcpyDeviceToDevice, st));
+        if (routing->offsets)
+            HIP_TRY(hipMemcpyAsync(routing->offsets, d.offsets, sizeof(int32_t) * (E + 1),
+                                   hipMemcpyDeviceToDevice, st));
+        if (routing->perm)
+            HIP_TRY(hipMemcpyAsync(routing->perm, d.perm, sizeof(int32_t) * T * K, hipMemcpyDeviceToDevice, st));
+    }
+    return MI_MOE_OK;
+}
+
+int mi_moe_expert_ffn(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const float *res,
+                      const int32_t *gate_up_ids, const int32_t *down_ids, const float *w, float *out,
+                      mi_stream_t stream) {
+    if (!c) return MI_MOE_ERR_NULL;
+    if (T < 0) return MI_MOE_ERR_SHAPE;
+    TRY(validate_layer(c, L, false));
+    if (T == 0) return MI_MOE_OK;
+    if (!x || !out || !gate_up_ids || !down_ids || !w) return MI_MOE_ERR_NULL;
+    if (T > c->cap_T) return MI_MOE_ERR_CAPACITY;
+    HIP_TRY(hipSetDevice(c->device));
+    hipStream_t st = (hipStream_t)stream;
+    stage_begin(c, st);
+    return run_experts(c, L, x, T, gate_up_ids, down_ids, w, res, out, st);
+}
+
+int mi_top_k(mi_moe_ctx *c, const mi_tensor *a, int32_t k, mi_tensor *dst, mi_stream_t stream) {
+    if (!c || !a || !dst || !a->data || !dst->data) return MI_MOE_ERR_NULL;
+    if (a->type != MI_TYPE_F32 || dst->type != MI_TYPE_I32) return MI_MOE_ERR_TYPE;
+    const int64_t E = a->ne[0], T = a->ne[1];
+    if (E <= 0 || T < 0 || k <= 0 || k > E || a->ne[2] != 1 || a->ne[3] != 1) return MI_MOE_ERR_SHAPE;
+    if (dst->ne[0] != k || dst->ne[1] != T || dst->ne[2] != 1 || dst->ne[3] != 1) return MI_MOE_ERR_SHAPE;
+    if (a->nb[0] != 4 || dst->nb[0] != 4 || a->nb[1] % 4 || dst->nb[1] % 4) return MI_MOE_ERR_SHAPE;
+    if (a->nb[1] < (size_t)E * 4 || dst->nb[1] < (size_t)k * 4) return MI_MOE_ERR_SHAPE;
+    if (E > 256 || k > 64) return MI_MOE_ERR_UNSUPPORTED;
+    if (T == 0) return MI_MOE_OK;
+    HIP_TRY(hipSetDevice(c->device));
+    return launch_topk_softmax((const float *)a->data, (int64_t)(a->nb[1] / 4), T, (int)E, k, (int32_t *)dst->data,
+                               (int64_t)(dst->nb[1] / 4), nullptr, (hipStream_t)stream);
+}
+
+int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const mi_tensor *ids, mi_tensor *dst,
+                  mi_stream_t stream) {
+    if (!c || !as || !b || !ids || !dst) return MI_MOE_ERR_NULL;
+    if (!b->data || !ids->data || !dst->data) return MI_MOE_ERR_NULL;
+    const int64_t Kin = as->ne[0], N = as->ne[1], E = as->ne[2];
+    TRY(check_table(*as, Kin, N, E));
+    if (as->ne[3] != 1) return MI_MOE_ERR_SHAPE;
+    if (b->type != MI_TYPE_F32 || ids->type != MI_TYPE_I32 || dst->type != MI_TYPE_F32) return MI_MOE_ERR_TYPE;
+    const int64_t n_used = ids->ne[0], T = ids->ne[1], ne11 = b->ne[1];
+    if (b->ne[0] != Kin || b->ne[2] != T || b->ne[3] != 1) return MI_MOE_ERR_SHAPE;
+    if (ne11 != 1 && ne11 != n_used) return MI_MOE_ERR_SHAPE;
+    if (dst->ne[0] != N || dst->ne[1] != n_used || dst->ne[2] != T || dst->ne[3] != 1) return MI_MOE_ERR_SHAPE;
+    if (n_used <= 0 || T < 0) return MI_MOE_ERR_SHAPE;
+    // contiguous layouts (ggml's default strides)
+    if (b->nb[0] != 4 || b->nb[1] != (size_t)Kin * 4 || b->nb[2] != (size_t)ne11 * Kin * 4) return MI_MOE_ERR_UNSUPPORTED;
+    if (ids->nb[0] != 4 || ids->nb[1] != (size_t)n_used * 4) return MI_MOE_ERR_UNSUPPORTED;
+    if (dst->nb[0] != 4 || dst->nb[1] != (size_t)N * 4 || dst->nb[2] != (size_t)n_used * N * 4)
+        return MI_MOE_ERR_UNSUPPORTED;
+    if (!c->reserved) return MI_MOE_ERR_CAPACITY;
+    if (E > c->cap_E || E > 256) return MI_MOE_ERR_CAPACITY;
+    if (T * n_used > c->cap_rows || T * ne11 > c->cap_rows || Kin > c->cap_kmax) return MI_MOE_ERR_CAPACITY;
+    if (T == 0) return MI_MOE_OK;
+    HIP_TRY(hipSetDevice(c->device));
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t rows = T * n_used;
+    const int max_active = (int)std::min<int64_t>(E, rows);
+    const int max_tiles = (int)((rows + GEMM_BM - 1) / GEMM_BM + max_active);
+    const DispBuf &dsp = c->disp[0];
+    TRY(launch_dispatch((const int32_t *)ids->data, T, (int)n_used, (int)E, GEMM_BM, dsp.view(), st));
+    const ExpertMat M = as_mat(*as);
+    const float *bp = (const float *)b->data;
+    if (as->type == MI_TYPE_F32) {
+        GemvArgs a = {};
+        a.a = M; a.ne11 = (int)ne11; a.K = (int)n_used;
+        a.counts = dsp.counts; a.offsets = dsp.offsets; a.perm = dsp.perm; a.active_e = dsp.active_e;
+        a.n_active = dsp.n_active; a.max_active = max_active;
+        a.y = (float *)dst->data; a.ldy = N; a.ncols = N;
+        return launch_mm_id_f32(a, bp, Kin, st);
+    }
+    const bool gemm = T >= c->gemm_threshold || Kin > 8 * QK;
+    if (!gemm) {
+        Q8Out qx;
+        qx.q8 = c->ax.q8; qx.d8 = c->ax.d8; qx.bsums = c->ax.bs;
+        TRY(launch_q8k_rows(bp, Kin, T * ne11, Kin, qx, st));
+        GemvArgs a = {};
+        a.a = M; a.epi = EPI_STORE; a.q8 = c->ax.q8; a.d8 = c->ax.d8; a.bsums = c->ax.bs;
+        a.ne11 = (int)ne11; a.K = (int)n_used;
+        a.counts = dsp.counts; a.offsets = dsp.offsets; a.perm = dsp.perm; a.active_e = dsp.active_e;
+        a.n_active = dsp.n_active; a.max_active = max_active;
+        a.y = (float *)dst->data; a.ldy = N; a.ncols = N;
+        return launch_gemv(a, st);
+    }
+    Q8Out qx;
+    qx.xh = c->ax.h; qx.wtype = as->type;
+    TRY(launch_q8k_rows(bp, Kin, T * ne11, Kin, qx, st));
+    GemmArgs a = {};
+    a.a = M; a.epi = EPI_STORE; a.xh = c->ax.h; a.ne11 = (int)ne11; a.K = (int)n_used;
+    a.counts = dsp.counts; a.offsets = dsp.offsets; a.perm = dsp.perm; a.tile_e = dsp.tile_e;
+    a.tile_r0 = dsp.tile_r0; a.n_tiles = dsp.n_tiles; a.max_tiles = max_tiles;
+    a.y = (float *)dst->data; a.ldy = N; a.ncols = N;
+    return launch_gemm(a, st);
+}
+
+int mi_quantize(mi_moe_ctx *c, int32_t type, const float *src, void *dst, int64_t nrows, int64_t n_per_row,
+                mi_stream_t stream) {
+    if (!c || !src || !dst) return MI_MOE_ERR_NULL;
+    if (type != MI_TYPE_Q4_K && type != MI_TYPE_Q6_K) return MI_MOE_ERR_TYPE;
+    if (nrows < 0 || n_per_row <= 0 || n_per_row % QK) return MI_MOE_ERR_SHAPE;
+    if (type == MI_TYPE_Q4_K && ((uintptr_t)dst % 4)) return MI_MOE_ERR_UNSUPPORTED;
+    if ((uintptr_t)src % 4) return MI_MOE_ERR_UNSUPPORTED;
+    HIP_TRY(hipSetDevice(c->device));
+    return launch_quantize(type, src, dst, nrows * (n_per_row / QK), (hipStream_t)stream);
+}
+
+int mi_fill_normal(mi_moe_ctx *c, float *dst, int64_t n, uint64_t seed, uint64_t stream_id, float mean,
+                   float stddev, mi_stream_t stream) {
+    if (!c || !dst) return MI_MOE_ERR_NULL;
+    if (n < 0) return MI_MOE_ERR_SHAPE;
+    HIP_TRY(hipSetDevice(c->device));
+    return launch_fill_normal(dst, n, seed, stream_id, mean, stddev, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------ util ABI
+int mi_device_count(int *count) {
+    if (!count) return MI_MOE_ERR_NULL;
+    HIP_TRY(hipGetDeviceCount(count));
+    return MI_MOE_OK;
+}
+int mi_set_device(int device) {
+    HIP_TRY(hipSetDevice(device));
+    return MI_MOE_OK;
+}
+int mi_device_info(int device, char *name, int name_len, int *cu_count, int *clock_khz, char *arch, int arch_len) {
+    hipDeviceProp_t p;
+    HIP_TRY(hipGetDeviceProperties(&p, device));
+    if (name && name_len > 0) {
+        std::strncpy(name, p.name, (size_t)name_len - 1);
+        name[name_len - 1] = 0;
+    }
+    if (arch && arch_len > 0) {
+        std::strncpy(arch, p.gcnArchName, (size_t)arch_len - 1);
+        arch[arch_len - 1] = 0;
+    }
+    if (cu_count) *cu_count = p.multiProcessorCount;
+    if (clock_khz) *clock_khz = p.clockRate;
+    return MI_MOE_OK;
+}
+int mi_dev_malloc(void **ptr, size_t bytes) {
+    if (!ptr) return MI_MOE_ERR_NULL;
+    HIP_TRY(hipMalloc(ptr, bytes));
+    return MI_MOE_OK;
+}
+int mi_dev_free(void *ptr) {
+    HIP_TRY(hipFree(ptr));
+    return MI_MOE_OK;
+}
+int mi_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+    HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return MI_MOE_OK;
+}
+int mi_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+    HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return MI_MOE_OK;
+}
+int mi_memcpy_d2d(void *dst, const void *src, size_t bytes) {
+    HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+    return MI_MOE_OK;
+}
+int mi_memset_d(void *dst, int value, size_t bytes) {
+    HIP_TRY(hipMemset(dst, value, bytes));
+    return MI_MOE_OK;
+}
+int mi_device_synchronize(void) {
+    HIP_TRY(hipDeviceSynchronize());
+    return MI_MOE_OK;
+}
+int mi_stream_create(mi_stream_t *s) {
+    if (!s) return MI_MOE_ERR_NULL;
+    hipStream_t h;
+    HIP_TRY(hipStreamCreate(&h));
+    *s = (mi_stream_t)h;
+    return MI_MOE_OK;
+}
+int mi_stream_destroy(mi_stream_t s) {
+    HIP_TRY(hipStreamDestroy((hipStream_t)s));
+    return MI_MOE_OK;
+}
+int mi_stream_synchronize(mi_stream_t s) {
+    HIP_TRY(hipStreamSynchronize((hipStream_t)s));
+    return MI_MOE_OK;
+}
+int mi_event_create(mi_event_t *e) {
+    if (!e) return MI_MOE_ERR_NULL;
+    hipEvent_t h;
+    HIP_TRY(hipEventCreate(&h));
+    *e = (mi_event_t)h;
+    return MI_MOE_OK;
+}
+int mi_event_destroy(mi_event_t e) {
+    HIP_TRY(hipEventDestroy((hipEvent_t)e));
+    return MI_MOE_OK;
+}
+int mi_event_record(mi_event_t e, mi_stream_t s) {
+    HIP_TRY(hipEventRecord((hipEvent_t)e, (hipStream_t)s));
+    return MI_MOE_OK;
+}
+int mi_event_synchronize(mi_event_t e) {
+    HIP_TRY(hipEventSynchronize((hipEvent_t)e));
+    return MI_MOE_OK;
+}
+int mi_event_elapsed_ms(float *ms, mi_event_t a, mi_event_t b) {
+    if (!ms) return MI_MOE_ERR_NULL;
+    HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+    return MI_MOE_OK;
+}
+const char *mi_last_hip_error(void) { return g_last_error.c_str(); }
+
+}  // extern "C"

@@ -1,0 +1,116 @@
+// launch.hpp - host-side launchers of the MoE kernels (one per kernel family)
+// and the shared HIP error bookkeeping.  Every launcher returns 0 or a
+// negative mi_moe_status.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mimoe {
+
+// records the HIP error string for mi_last_hip_error(); returns MI_MOE_ERR_HIP (-5)
+int record_hip_error(hipError_t e);
+// check hipGetLastError() after a launch
+int hip_check_launch();
+
+// ---- data preparation (k_data.hip)
+int launch_fill_normal(float *out, int64_t n, uint64_t seed, uint64_t stream, float mean, float sd,
+                       hipStream_t st);
+int launch_quantize(int type, const float *src, void *dst, int64_t nblocks, hipStream_t st);
+
+// ---- routing (k_route.hip)
+struct Q8Out {
+    int8_t *q8 = nullptr;        // [rows][K] natural order (GEMV path)
+    float *d8 = nullptr;         // [rows][K/256]
+    int16_t *bsums = nullptr;    // [rows][K/16]
+    _Float16 *xh = nullptr;      // [rows][K] fp16(d*q) in MFMA K order of wtype (GEMM path)
+    int wtype = 12;              // consumer weight type for xh order
+};
+// quantize rows of src (row r at src + r*ld floats) to Q8_K
+int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, const Q8Out &o, hipStream_t st);
+// router logits, fixed fp64 order; W: [E][D], x rows at x + t*ldx
+int launch_router(const float *W, const float *b, const float *x, int64_t ldx, int64_t T, int D, int E,
+                  float *logits, hipStream_t st);
+// top-k (descending, ties -> lower id) and softmax over the selected logits;
+// w may be NULL (op-level top_k)
+int launch_topk_softmax(const float *logits, int64_t ld_logits, int64_t T, int E, int K, int32_t *sel,
+                        int64_t ld_sel, float *w, hipStream_t st);
+
+struct Dispatch {
+    int32_t *counts;     // [E]
+    int32_t *offsets;    // [E+1]
+    int32_t *perm;       // [T*K] value t*K+k, per expert token-ascending
+    int32_t *tile_e;     // [max_tiles] expert of each GEMM M-tile
+    int32_t *tile_r0;    // [max_tiles] first list row of each tile
+    int32_t *n_tiles;    // [1]
+    int32_t *active_e;   // [E] experts with count > 0, ascending
+    int32_t *n_active;   // [1]
+    int32_t *bad_ids;    // [1] number of ids outside [0, E) (skipped)
+};
+int launch_dispatch(const int32_t *ids, int64_t T, int K, int E, int BM, const Dispatch &d, hipStream_t st);
+
+// out[t][n] = res[t][n] + sum_k (double)(z[t*K+k][n] * w[t][k])   (res may be NULL)
+int launch_combine(const float *z, const float *w, const float *res, float *out, int64_t T, int K, int D,
+                   hipStream_t st);
+
+// ---- expert products
+struct ExpertMat {
+    const uint8_t *data;  // E matrices
+    int type;             // 12 Q4_K, 14 Q6_K, 0 F32
+    int64_t row_bytes;    // nb[1]
+    int64_t mat_bytes;    // nb[2]
+    int64_t K;            // ne[0]
+    int64_t N;            // ne[1]
+};
+
+// epilogue modes of the grouped products
+enum { EPI_STORE = 0, EPI_GLU = 1 };
+
+struct GemvArgs {
+    ExpertMat a;          // gate (or fused gate|up) / down / generic
+    ExpertMat b;          // up (separate gate/up GLU); data == nullptr when fused
+    int epi;              // EPI_STORE: y[p][n]; EPI_GLU: act[p][i]
+    int act;              // mi_act for EPI_GLU
+    int64_t I;            // GLU width (output columns)
+    int fused;            // gate holds [h | g] rows
+    // activations (Q8_K rows)
+    const int8_t *q8;
+    const float *d8;
+    const int16_t *bsums;
+    int ne11;             // 1: row = t; else row = t*K + k
+    int K;                // slots per token
+    // dispatch
+    const int32_t *counts, *offsets, *perm, *active_e, *n_active;
+    int max_active;
+    // output rows p = t*K + k, row stride ldy floats
+    float *y;
+    int64_t ldy;
+    int64_t ncols;        // N (EPI_STORE) or I (EPI_GLU)
+};
+int launch_gemv(const GemvArgs &g, hipStream_t st);
+
+struct GemmArgs {
+    ExpertMat a;          // gate (or fused gate|up) / down / generic
+    ExpertMat b;          // up (separate gate/up); data == nullptr when fused
+    int epi;
+    int act;
+    int64_t I;
+    int fused;
+    const _Float16 *xh;   // activations fp16 in MFMA K order of a.type
+    int ne11;
+    int K;
+    const int32_t *counts, *offsets, *perm, *tile_e, *tile_r0, *n_tiles;
+    int max_tiles;
+    // EPI_STORE output: fp32 rows p, stride ldy
+    float *y;
+    int64_t ldy;
+    // EPI_GLU output: Q8_K-quantized activations as fp16 in the MFMA K order
+    // of `next_type`, rows p, stride I
+    _Float16 *acth;
+    int next_type;
+    int64_t ncols;
+};
+constexpr int GEMM_BM = 64;
+int launch_gemm(const GemmArgs &g, hipStream_t st);
+
+}  // namespace mimoe

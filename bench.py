@@ -1,0 +1,219 @@
+"""bench.py - MoE layer throughput on one MI355X (BASELINE.json metric).
+
+Default workload: config 1, the moondream3-shape MoE layer on a 1024-token
+prefill (gate/up Q4_K, down Q6_K, E=64, top-8), seeded synthetic data.  One
+step = one full layer forward (router -> top-k -> dispatch -> gate/up GEMM +
+GeGLU + Q8_K -> down GEMM -> weighted combine) over the 1024 tokens, with
+the inputs resident in HBM.  Steps rotate over --copies distinct layer copies
+so the 256 MB Infinity Cache cannot hold the weights between steps.
+
+Printed JSON line (rank 0):
+  value          tokens/s of the whole layer (T * steps / time)
+  roofline       the dominant kernel (gate/up grouped GEMM): algorithmic flops
+                 per launch / its average duration (HIP events on its stream)
+                 vs the 2.5 PFLOP/s dense fp16/bf16 MFMA peak
+  decode         config 0 (1 token) on the same box: tokens/s and the HBM
+                 roofline of its dominant kernel (selected experts' bytes /
+                 duration vs 8 TB/s)
+  cpu_baseline   the CPU oracle (ggml-semantics restatement, C, OpenMP) on a
+                 bounded sample of the same workload, physical cores
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "skyvision.cpp_amd"))
+
+import numpy as np  # noqa: E402
+
+import mimoe as M  # noqa: E402
+import workloads as W  # noqa: E402
+
+PEAK_MFMA_TFLOPS = 2500.0      # MI355X dense fp16 / bf16 MFMA
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_layer(ctx, layers, xs, T, out, steps, warmup, profile=False):
+    """Run `steps` forwards rotating over layer copies; returns (ms/step,
+    per-stage mean ms or None)."""
+    n = len(layers)
+    for i in range(warmup):
+        M.check("forward", ctx.forward(layers[i % n].layer, xs[i % n], T, None, out))
+    M.synchronize()
+    if profile:
+        ctx.set_profiling(True)
+        acc = {}
+        for i in range(steps):
+            M.check("forward", ctx.forward(layers[i % n].layer, xs[i % n], T, None, out))
+            for name, ms in ctx.stage_times():
+                acc.setdefault(name, []).append(ms)
+        ctx.set_profiling(False)
+        M.synchronize()
+        return None, {k: float(np.mean(v)) for k, v in acc.items()}
+    e0, e1 = M.Event(), M.Event()
+    M.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(steps):
+        M.check("forward", ctx.forward(layers[i % n].layer, xs[i % n], T, None, out))
+    e1.record()
+    e1.synchronize()
+    M.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    dev = e0.elapsed_ms(e1)
+    return max(dev, 0.0) / steps, {"wall_ms_per_step": wall / steps}
+
+
+def touched_experts(ctx, layer, x, T):
+    counts = M.DeviceBuffer(4 * layer.spec.E)
+    r = M.Routing()
+    r.counts = counts.addr
+    out = M.DeviceBuffer(4 * T * layer.spec.D)
+    M.check("forward", ctx.forward(layer.layer, x, T, None, out, r))
+    M.synchronize()
+    c = counts.download(np.int32, (layer.spec.E,))
+    return int((c > 0).sum()), c
+
+
+def cpu_baseline(spec, layer0: W.GpuLayer, T_sample: int, budget_s: float = 20.0):
+    """CPU oracle (ggml-semantics restatement) on T_sample tokens of the same
+    layer; weights copied from the GPU tables (bit-identical to the oracle's
+    own quantizer output)."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import pyoracle as O
+    cores = O.physical_cores()
+    tables = layer0.download_tables()
+    rw = layer0.download_router()
+    L = dict(D=spec.D, E=spec.E, K=spec.K, I=spec.I, router_w=rw, router_b=layer0.bias_host,
+             gate_type=spec.gate_type, down_type=spec.down_type, fused=spec.fused, act=spec.act,
+             gate=tables["gate"], down=tables["down"])
+    if "up" in tables:
+        L["up"] = tables["up"]
+    x = O.fill_normal(T_sample * spec.D, spec.seed, W.S_X, 0.0, 1.0, cores).reshape(T_sample, spec.D)
+    O.moe_forward(L, x, nthreads=cores, debug=False)          # warm
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 10 and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        O.moe_forward(L, x, nthreads=cores, debug=False)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": T_sample / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{spec.name}: {T_sample} tokens x {len(times)} runs (median {med * 1e3:.1f} ms), "
+                      f"ggml-semantics CPU restatement (Q8_K activations x k-quant integer dots), "
+                      f"{cores} threads"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--copies", type=int, default=16)
+    ap.add_argument("--config", type=int, default=1, choices=[1, 2])
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=64)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the MoE layer is sharded by replicating experts per GPU; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+
+    M.load()
+    info = M.device_info(0)
+    log(f"device: {info}")
+    cfg = W.CONFIGS[args.config]
+    spec = cfg["spec"]
+    T = cfg["tokens"][0]
+    ctx = M.Context(0)
+    ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
+    t0 = time.perf_counter()
+    layers = [W.GpuLayer(ctx, spec, copy=c) for c in range(args.copies)]
+    xs = [W.gen_x(ctx, spec, T, copy=c) for c in range(args.copies)]
+    out = M.DeviceBuffer(4 * T * spec.D)
+    M.synchronize()
+    log(f"built {args.copies} layer copies of {spec.name} in {time.perf_counter() - t0:.1f}s "
+        f"({sum(l.expert_bytes() * spec.E for l in layers) / 1e9:.2f} GB of expert tables)")
+
+    ms, extra = time_layer(ctx, layers, xs, T, out, args.steps, args.warmup)
+    log(f"config {args.config}: {ms:.4f} ms/step, wall {extra['wall_ms_per_step']:.4f} ms/step")
+    _, stages = time_layer(ctx, layers, xs, T, out, min(args.steps, 20), 2, profile=True)
+    log(f"stages (ms): {json.dumps({k: round(v, 4) for k, v in stages.items()})}")
+    gu_ms = stages.get("gate_up", float("nan"))
+    gu_flops = 2.0 * T * spec.K * spec.D * (2 * spec.I)
+    achieved = gu_flops / (gu_ms * 1e-3) / 1e12
+    touched, _ = touched_experts(ctx, layers[0], xs[0], T)
+
+    result = {
+        "metric": "MoE layer tokens/s + % HBM roofline (decode) / % MFMA peak (prefill), 1 GPU",
+        "value": T / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": f"config {args.config}: moondream3 MoE layer prefill",
+                   "tokens": T, "n_embd": spec.D, "n_expert": spec.E, "n_expert_used": spec.K,
+                   "n_ff": spec.I, "gate_up": "Q4_K", "down": "Q6_K" if spec.down_type == M.TYPE_Q6_K else "Q4_K",
+                   "act": "gelu_erf(h)*(g+1)", "layer_copies": args.copies,
+                   "touched_experts": touched, "layer_flops": W.flops(spec, T)},
+        "roofline": {"bound": "mfma", "kernel": "gate_up grouped GEMM (k_gemm GLU)",
+                     "achieved": achieved, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": None,
+                     "kernel_ms": gu_ms, "flops_per_launch": gu_flops},
+        "stages_ms": stages,
+    }
+
+    if not args.no_decode:
+        dspec = W.CONFIGS[0]["spec"]
+        dctx = M.Context(0)
+        dctx.reserve(64, dspec.D, dspec.I, dspec.E, dspec.K)
+        dl = [W.GpuLayer(dctx, dspec, copy=c) for c in range(args.copies)]
+        dx = [W.gen_x(dctx, dspec, 1, copy=c) for c in range(args.copies)]
+        dout = M.DeviceBuffer(4 * dspec.D)
+        dms, _ = time_layer(dctx, dl, dx, 1, dout, 200, 20)
+        _, dst = time_layer(dctx, dl, dx, 1, dout, 50, 5, profile=True)
+        dtouched, _ = touched_experts(dctx, dl[0], dx[0], 1)
+        gu_bytes = dtouched * 2 * dspec.I * M.row_size(dspec.gate_type, dspec.D)
+        dgu = dst.get("gate_up", float("nan"))
+        layer_bytes = W.algorithmic_bytes(dspec, dtouched)
+        result["decode"] = {
+            "workload": "config 0: moondream3 MoE layer, 1-token decode, Q4_K",
+            "tokens_per_s": 1.0 / (dms * 1e-3), "ms_per_token": dms,
+            "layer_bytes": layer_bytes, "layer_GBs": layer_bytes / (dms * 1e-3) / 1e9,
+            "layer_frac_hbm": layer_bytes / (dms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+            "roofline": {"bound": "hbm", "kernel": "gate_up grouped GEMV (k_gemv GLU)",
+                         "achieved": gu_bytes / (dgu * 1e-3) / 1e9, "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": gu_bytes / (dgu * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                         "kernel_ms": dgu, "bytes_per_launch": gu_bytes},
+            "stages_ms": dst,
+        }
+        del dl, dx
+        dctx.close()
+
+    if not args.no_cpu:
+        cb = cpu_baseline(spec, layers[0], args.cpu_tokens)
+        result["cpu_baseline"] = cb
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -696,9 +696,13 @@ void orc_router_logits(const float *W, const float *b, const float *x,
             const float *we = W + (int64_t)e * D;
             double acc = 0.0;
             for (int c0 = 0; c0 < D; c0 += 64) {
-                const int c1 = MIN(D, c0 + 64);
+                /* inside a 64-wide chunk: d = c0 + 16*g + s, s outer, g inner */
                 double part = 0.0;
-                for (int d = c0; d < c1; d++) part += (double)we[d] * (double)xt[d];
+                for (int s = 0; s < 16; s++)
+                    for (int g = 0; g < 4; g++) {
+                        const int d = c0 + 16 * g + s;
+                        if (d < D) part += (double)we[d] * (double)xt[d];
+                    }
                 acc += part;
             }
             float v = (float)acc;

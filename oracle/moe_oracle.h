@@ -119,9 +119,12 @@ double orc_poly_log(double x);
 void   orc_poly_sincos_2pi(double u, double *s, double *c);
 
 /* ---- router, gating, dispatch ------------------------------------------ */
-/* logits[t][e] = fl32( fl32(dot(W[e], x[t])) + b[e] ), dot in fp64 with the
- * fixed order: 64-element chunks summed left to right inside the chunk, chunk
- * partials summed left to right.  W is ggml ne=[D, E] (E rows of D). */
+/* logits[t][e] = fl32( fl32(dot(W[e], x[t])) + b[e] ), dot in fp64 with one
+ * fixed order: the 64-element chunk c contributes part_c = sum over s = 0..15
+ * (outer), g = 0..3 (inner) of W[e][64c+16g+s] * x[t][64c+16g+s], each added
+ * left to right; the chunk partials are then summed left to right.  fp32 x
+ * fp32 products are exact in fp64, so only this order matters.  W is ggml
+ * ne=[D, E] (E rows of D). */
 void orc_router_logits(const float *W, const float *b, const float *x,
                        int64_t T, int D, int E, float *logits, int nthreads);
 /* ggml_top_k: K largest, descending, ties -> lower id */

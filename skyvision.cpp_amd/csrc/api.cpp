@@ -59,6 +59,7 @@ struct ActBuf {                // one Q8_K activation set
     float *d8 = nullptr;
     int16_t *bs = nullptr;
     _Float16 *h = nullptr;
+    _Float16 *bsh = nullptr;   // block sums as fp16 (exact MFMA path)
 };
 
 struct DispBuf {
@@ -253,7 +254,30 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         d.y = c->z; d.ldy = D; d.ncols = D;
         TRY(launch_gemv(d, st));
         stage_end(c, "down", st);
+    } else if (gate.type == MI_TYPE_Q4_K) {
+        // exact Q4_K x Q8_K gate/up on 32x32x16 MFMA, fp16 down
+        Q8Out qx;
+        qx.xh = c->ax.h; qx.d8 = c->ax.d8; qx.xbs = c->ax.bsh;
+        qx.wtype = MI_TYPE_Q4_K; qx.order = 1; qx.exact = 1;
+        TRY(launch_q8k_rows(x, D, T, D, qx, st));
+        stage_end(c, "q8k_x", st);
+        G2Args a = {};
+        a.a = gate; a.b = up; a.glu = 1; a.fused = L->fused_gate_up; a.act = L->act; a.I = I;
+        a.xh = c->ax.h; a.xd = c->ax.d8; a.xbs = c->ax.bsh; a.ne11 = 1; a.K = K;
+        a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.tile_e = dg.tile_e;
+        a.tile_r0 = dg.tile_r0; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
+        a.acth = c->aact.h; a.next_type = down.type; a.ncols = I;
+        TRY(launch_gemm2(a, st));
+        stage_end(c, "gate_up", st);
+        G2Args d = {};
+        d.a = down; d.glu = 0; d.xh = c->aact.h; d.ne11 = K; d.K = K;
+        d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
+        d.tile_r0 = dd.tile_r0; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles;
+        d.y = c->z; d.ldy = D; d.ncols = D;
+        TRY(launch_gemm2(d, st));
+        stage_end(c, "down", st);
     } else {
+        // Q6_K gate/up: fp16 dequant on 16x16x32 MFMA
         Q8Out qx;
         qx.xh = c->ax.h; qx.wtype = gate.type;
         TRY(launch_q8k_rows(x, D, T, D, qx, st));
@@ -362,7 +386,8 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
                 2 * carve_size<int32_t>(1);
     // activation sets: x/b rows (rows x kmax) and act rows (rows x I)
     need += carve_size<int8_t>(rows * kmax_q) + carve_size<float>(rows * kmax_q / QK) +
-            carve_size<int16_t>(rows * kmax_q / 16) + carve_size<_Float16>(rows * kmax_q);
+            carve_size<int16_t>(rows * kmax_q / 16) + carve_size<_Float16>(rows * kmax_q) +
+            carve_size<_Float16>(rows * kmax_q / 16);
     const int64_t iq = (I + QK - 1) / QK * QK;
     need += carve_size<int8_t>(rows * iq) + carve_size<float>(rows * iq / QK) +
             carve_size<int16_t>(rows * iq / 16) + carve_size<_Float16>(rows * iq);
@@ -397,6 +422,7 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
     c->ax.d8 = carve<float>(q, rows * kmax_q / QK);
     c->ax.bs = carve<int16_t>(q, rows * kmax_q / 16);
     c->ax.h = carve<_Float16>(q, rows * kmax_q);
+    c->ax.bsh = carve<_Float16>(q, rows * kmax_q / 16);
     c->aact.q8 = carve<int8_t>(q, rows * iq);
     c->aact.d8 = carve<float>(q, rows * iq / QK);
     c->aact.bs = carve<int16_t>(q, rows * iq / 16);
@@ -564,14 +590,14 @@ int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const 
         return launch_gemv(a, st);
     }
     Q8Out qx;
-    qx.xh = c->ax.h; qx.wtype = as->type;
+    qx.xh = c->ax.h; qx.wtype = as->type; qx.order = 1;
     TRY(launch_q8k_rows(bp, Kin, T * ne11, Kin, qx, st));
-    GemmArgs a = {};
-    a.a = M; a.epi = EPI_STORE; a.xh = c->ax.h; a.ne11 = (int)ne11; a.K = (int)n_used;
+    G2Args a = {};
+    a.a = M; a.glu = 0; a.xh = c->ax.h; a.ne11 = (int)ne11; a.K = (int)n_used;
     a.counts = dsp.counts; a.offsets = dsp.offsets; a.perm = dsp.perm; a.tile_e = dsp.tile_e;
     a.tile_r0 = dsp.tile_r0; a.n_tiles = dsp.n_tiles; a.max_tiles = max_tiles;
     a.y = (float *)dst->data; a.ldy = N; a.ncols = N;
-    return launch_gemm(a, st);
+    return launch_gemm2(a, st);
 }
 
 int mi_quantize(mi_moe_ctx *c, int32_t type, const float *src, void *dst, int64_t nrows, int64_t n_per_row,

@@ -103,6 +103,18 @@ __device__ __host__ inline void scale_min_k4(int j, const uint8_t *q, int &d, in
     }
 }
 
+// the same unpack from the three packed dwords w0..w2 = scales[0..12) held in
+// registers (j may vary per lane; no local-memory array, no branch)
+__device__ inline void scale_min_k4_reg(int j, uint32_t w0, uint32_t w1, uint32_t w2, int &d, int &m) {
+    const uint32_t sh = 8u * (uint32_t)(j & 3);
+    const int b0 = (int)((w0 >> sh) & 0xffu), b1 = (int)((w1 >> sh) & 0xffu), b2 = (int)((w2 >> sh) & 0xffu);
+    const int d_lo = b0 & 63, m_lo = b1 & 63;
+    const int d_hi = (b2 & 0xF) | ((b0 >> 6) << 4), m_hi = (b2 >> 4) | ((b1 >> 6) << 4);
+    const bool lo = j < 4;
+    d = lo ? d_lo : d_hi;
+    m = lo ? m_lo : m_hi;
+}
+
 // ---------------------------------------------------------------- MFMA K order
 // The prefill GEMM feeds v_mfma_f32_16x16x32_f16 with 8 fp16 values per lane.
 // Inside a 256-value super-block, MFMA step s (0..7), lane group g (lane/16,
@@ -129,6 +141,41 @@ __device__ __host__ inline int q6k_elem(int pos) {
 }
 __device__ __host__ inline int mfma_elem(int wtype, int pos) {
     return wtype == 14 ? q6k_elem(pos) : q4k_elem(pos);
+}
+
+// v_mfma_f32_32x32x16_f16 order: step s (0..15), lane group g (lane/32, 0..1),
+// slot p (0..7), pos = 16*s + 8*g + p.
+// Q4_K: lane group g owns qs[64g .. 64g+64) = chunks 2g, 2g+1; step s uses
+// dword s&7 of chunk 2g + (s>>3): elements 64c + 4(s&7) + {0..3} (low
+// nibbles, sub-block 2c) and 64c + 32 + 4(s&7) + {0..3} (high, 2c+1), in
+// the operand order of q4k_elem.
+__device__ __host__ inline int q4k_elem32(int pos) {
+    const int s = pos >> 4, g = (pos >> 3) & 1, p = pos & 7;
+    const int off[8] = {0, 2, 32, 34, 1, 3, 33, 35};
+    return 64 * (2 * g + (s >> 3)) + 4 * (s & 7) + off[p];
+}
+// Q6_K: lane group g owns half g (ql[64g..64g+64), qh[32g..32g+32)); step s =
+// 2*jj + w covers l = 4jj..4jj+3 of quarters (q1, q2) for w = 0 or (q3, q4)
+// for w = 1; slots 0..3 the first quarter, 4..7 the second.
+__device__ __host__ inline int q6k_elem32(int pos) {
+    const int s = pos >> 4, g = (pos >> 3) & 1, p = pos & 7;
+    return 128 * g + 4 * (s >> 1) + 64 * (s & 1) + 32 * (p >> 2) + (p & 3);
+}
+__device__ __host__ inline int q4k_pos32(int e) {
+    const int c = e >> 6, r = e & 63, hi = r >> 5, r2 = r & 31, j = r2 >> 2, lo = r2 & 3;
+    const int g = c >> 1, s = 8 * (c & 1) + j, p = (lo & 1) * 4 + hi * 2 + (lo >> 1);
+    return 16 * s + 8 * g + p;
+}
+__device__ __host__ inline int q6k_pos32(int e) {
+    const int g = e >> 7, r = e & 127, qq = r >> 5, l = r & 31, jj = l >> 2, i = l & 3;
+    const int s = 2 * jj + (qq >> 1), p = 4 * (qq & 1) + i;
+    return 16 * s + 8 * g + p;
+}
+__device__ __host__ inline int mfma32_elem(int wtype, int pos) {
+    return wtype == 14 ? q6k_elem32(pos) : q4k_elem32(pos);
+}
+__device__ __host__ inline int mfma32_pos(int wtype, int e) {
+    return wtype == 14 ? q6k_pos32(e) : q4k_pos32(e);
 }
 
 // ---------------------------------------------------------------- wave helpers

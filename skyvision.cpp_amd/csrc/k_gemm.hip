@@ -193,12 +193,9 @@ __global__ void __launch_bounds__(GM_THREADS) k_gemm(GemmArgs g) {
                 w4[nt].qs[0] = q0.x; w4[nt].qs[1] = q0.y; w4[nt].qs[2] = q0.z; w4[nt].qs[3] = q0.w;
                 w4[nt].qs[4] = q1.x; w4[nt].qs[5] = q1.y; w4[nt].qs[6] = q1.z; w4[nt].qs[7] = q1.w;
                 const float d = h2f((uint16_t)(h.x & 0xffff)), dmin = h2f((uint16_t)(h.x >> 16));
-                uint8_t sc[12];
-                const uint32_t hw[3] = {h.y, h.z, h.w};
-                for (int i = 0; i < 12; ++i) sc[i] = (uint8_t)(hw[i >> 2] >> (8 * (i & 3)));
                 int scA, mA, scB, mB;
-                scale_min_k4(2 * g4, sc, scA, mA);
-                scale_min_k4(2 * g4 + 1, sc, scB, mB);
+                scale_min_k4_reg(2 * g4, h.y, h.z, h.w, scA, mA);
+                scale_min_k4_reg(2 * g4 + 1, h.y, h.z, h.w, scB, mB);
                 w4[nt].sA = splat(d * (float)scA);
                 w4[nt].nmA = splat(-(dmin * (float)mA));
                 w4[nt].sB = splat(d * (float)scB);

@@ -1,0 +1,610 @@
+// k_gemm2.hip - grouped k-quant GEMM on v_mfma_f32_32x32x16_f16 (prefill).
+//
+// A work-group owns a 64-row tile of one expert's dispatched rows (tokens
+// gathered through the permutation) and 8 waves; each wave owns 64 rows x 64
+// weight rows as 2 x 2 MFMA tiles of 32 x 32.  Activation tiles are staged in
+// LDS, double buffered; weights stream straight from the GGUF blocks into
+// registers (the next super-block's bytes are fetched while the current one
+// is consumed) and are expanded in-register with packed fp16 math.
+//
+// Gate/up (GLU) on Q4_K is computed exactly like ggml-cpu's Q4_K x Q8_K dot
+// (ggml_vec_dot_q4_K_q8_K): the MFMA operands are exact small integers - the
+// activation codes q8 and sc_j * q4 (<= 63 * 15) - so the fp32 accumulator holds
+// the integer sum  P = sum_j sc_j sum_i q4 q8  of each 256-value super-block,
+// and a second MFMA gives the min term  Q = sum_j m_j bsum_j  from the Q8_K
+// block sums.  Per super-block the fp32 epilogue adds
+//     d_x * (d_w * P - dmin_w * Q)
+// which is the ggml formula up to fp32 summation order.  The GLU output is then
+// quantized to Q8_K per 256 columns (ggml: the down mul_mat_id quantizes its
+// F32 input) and stored as fp16(d * q) in the down weight's K order.
+//
+// Down (STORE) dequantizes Q4_K / Q6_K to fp16 in-register and multiplies the
+// fp16 Q8_K activations, accumulating in fp32.
+#include "act.hpp"
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace mimoe {
+
+constexpr int G2_BM = 64;
+constexpr int G2_WAVES = 8;
+constexpr int G2_THREADS = G2_WAVES * 64;
+constexpr int G2_LDA = QK + 8;          // halfs per LDS row: 528 B rows spread the LDS banks
+
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+__device__ inline half2_t u2h2_(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ inline uint32_t h22u_(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+__device__ inline half2_t splat_(float f) {
+    const _Float16 h = (_Float16)f;
+    half2_t r = {h, h};
+    return r;
+}
+__device__ inline uint32_t dword_of(const uint4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+
+__device__ inline uint4 load16_a2_(const uint8_t *p) {
+    const uintptr_t a = (uintptr_t)p;
+    const uint32_t mis = (uint32_t)(a & 3u);
+    const uint32_t *w = (const uint32_t *)(a - mis);
+    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3];
+    const uint32_t w4 = mis ? w[4] : 0u;
+    uint4 r;
+    r.x = __builtin_amdgcn_alignbyte(w1, w0, mis);
+    r.y = __builtin_amdgcn_alignbyte(w2, w1, mis);
+    r.z = __builtin_amdgcn_alignbyte(w3, w2, mis);
+    r.w = __builtin_amdgcn_alignbyte(w4, w3, mis);
+    return r;
+}
+
+// exact integer operand: nibbles of dword v -> (a0,a2,b0,b2,a1,a3,b1,b3) * sc,
+// a = low nibbles (sub-block lo), b = high nibbles (sub-block hi).
+// fma((1024 + a), sc, -1024 sc) = a * sc exactly (<= 945 is an fp16 integer).
+__device__ inline half8_t dq4_exact(uint32_t v, half2_t sc_lo, half2_t nc_lo, half2_t sc_hi, half2_t nc_hi) {
+    const uint32_t v8 = v >> 8;
+    const half2_t t0 = u2h2_((v & 0x000F000Fu) | 0x64006400u);
+    const half2_t t1 = u2h2_((v & 0x00F000F0u) | 0x54005400u);
+    const half2_t t2 = u2h2_((v8 & 0x000F000Fu) | 0x64006400u);
+    const half2_t t3 = u2h2_((v8 & 0x00F000F0u) | 0x54005400u);
+    const u32x4 r = {h22u_(__builtin_elementwise_fma(t0, sc_lo, nc_lo)), h22u_(__builtin_elementwise_fma(t1, sc_hi, nc_hi)),
+                     h22u_(__builtin_elementwise_fma(t2, sc_lo, nc_lo)), h22u_(__builtin_elementwise_fma(t3, sc_hi, nc_hi))};
+    return __builtin_bit_cast(half8_t, r);
+}
+
+// fp16 weights: q exact, then one packed fma with s = d*sc, nm = -dmin*m
+__device__ inline half8_t dq4_f16(uint32_t v, half2_t s_lo, half2_t nm_lo, half2_t s_hi, half2_t nm_hi) {
+    const half2_t c1024 = {(_Float16)1024.f, (_Float16)1024.f};
+    const half2_t c64 = {(_Float16)64.f, (_Float16)64.f};
+    const uint32_t v8 = v >> 8;
+    const half2_t t0 = u2h2_((v & 0x000F000Fu) | 0x64006400u) - c1024;
+    const half2_t t1 = u2h2_((v & 0x00F000F0u) | 0x54005400u) - c64;
+    const half2_t t2 = u2h2_((v8 & 0x000F000Fu) | 0x64006400u) - c1024;
+    const half2_t t3 = u2h2_((v8 & 0x00F000F0u) | 0x54005400u) - c64;
+    const u32x4 r = {h22u_(__builtin_elementwise_fma(t0, s_lo, nm_lo)), h22u_(__builtin_elementwise_fma(t1, s_hi, nm_hi)),
+                     h22u_(__builtin_elementwise_fma(t2, s_lo, nm_lo)), h22u_(__builtin_elementwise_fma(t3, s_hi, nm_hi))};
+    return __builtin_bit_cast(half8_t, r);
+}
+
+__device__ inline void q6b_to_h2(uint32_t x, half2_t s, half2_t &lo, half2_t &hi) {
+    const half2_t c1056 = {(_Float16)1056.f, (_Float16)1056.f};
+    const uint32_t p01 = (x & 0x000000FFu) | ((x << 8) & 0x00FF0000u) | 0x64006400u;
+    const uint32_t p23 = ((x >> 16) & 0x000000FFu) | ((x >> 8) & 0x00FF0000u) | 0x64006400u;
+    lo = (u2h2_(p01) - c1056) * s;
+    hi = (u2h2_(p23) - c1056) * s;
+}
+__device__ inline half8_t dq6_f16(uint32_t qla, uint32_t qlb, uint32_t qh, int w, half2_t s_first, half2_t s_second) {
+    uint32_t qa, qb;
+    if (w == 0) {
+        qa = (qla & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u);
+        qb = (qlb & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u);
+    } else {
+        qa = ((qla >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u);
+        qb = ((qlb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u);
+    }
+    half2_t a01, a23, b01, b23;
+    q6b_to_h2(qa, s_first, a01, a23);
+    q6b_to_h2(qb, s_second, b01, b23);
+    const u32x4 r = {h22u_(a01), h22u_(a23), h22u_(b01), h22u_(b23)};
+    return __builtin_bit_cast(half8_t, r);
+}
+
+// XCD-aware tile order.  Work-groups are dealt to the 8 XCDs round robin, so
+// the linear id is remapped XCD-major: each XCD walks a contiguous range of
+// v = nt * max_tiles + mt, i.e. the M tiles of one expert's weight slab (same
+// weights, consecutive in the tile list) run back to back on one XCD and
+// re-read the slab from that XCD's L2.  The grid is a multiple of 8; padding
+// blocks and tiles past n_tiles exit.
+__device__ inline void tile_coords(int max_tiles, int &mt, int &nt) {
+    const int lin = blockIdx.x;
+    const int per = gridDim.x >> 3;
+    const int v = (lin & 7) * per + (lin >> 3);   // a bijection on [0, gridDim.x)
+    nt = v / max_tiles;
+    mt = v - nt * max_tiles;
+}
+
+// ------------------------------------------------------------------ GLU
+// 8 waves (2 per SIMD).  Wave w owns act columns 32w .. 32w+31 of the
+// 256-column tile: col tile 0 holds their h (gate) rows, col tile 1 their g
+// (up) rows; each wave covers all 64 token rows (row tiles 0, 1).
+//
+// Operands reach LDS by direct global -> LDS loads (no staging registers):
+// one load instruction writes 1 KB of LDS, lane i the 16 bytes at +16i.
+//  * activation codes: rows of 256 fp16 padded to 264 (528 B), so an MFMA
+//    operand read of 32 rows at one K chunk touches 32 distinct bank groups
+//    and its address is the lane's row base plus a constant.  The 64 padded
+//    rows are 33 KB = 33 load instructions; slot q = 64*k + lane of load k
+//    holds row q / 33, chunk q % 33 (chunk 32 is the pad: it reloads chunk 0).
+//  * block sums (64 rows x 32 B, 2 loads), row scales (64 x 4 B, 1 load) and
+//    each wave's 64 weight-row headers (64 x 16 B, 1 load per wave).
+// Weight nibbles stay in registers (rolling prefetch of the next block).
+constexpr int G2G_WAVES = 8;
+constexpr int G2G_THREADS = G2G_WAVES * 64;
+constexpr int G2G_LDA = QK + 8;                       // padded row (halfs)
+constexpr int G2G_ALOADS = G2_BM * (QK / 8 + 1) / 64; // 33
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// one stage of the double buffer; the two stages are separate LDS variables
+// so the compiler can tell the loads into one from the reads of the other
+struct G2GBuf {
+    _Float16 As[G2_BM * G2G_LDA];        // 33 KB activation codes
+    uint4 Hs[G2G_WAVES][64];             // 8 KB weight block headers
+    _Float16 Bs[G2_BM * 16];             // 2 KB block sums of 16 codes
+    float Dx[G2_BM];                     // row scales
+};
+
+struct G2GLane {
+    int wave, lane, l32, g2;
+    uint32_t aoff[5], bsoff, dxoff;
+    const uint8_t *rowp[2];
+    const uint8_t *hrow;
+};
+
+// issue the direct loads of block b into stage st
+__device__ __forceinline__ void g2g_issue(const G2Args &g, const G2GLane &L, int b, G2GBuf &st) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        __builtin_amdgcn_global_load_lds(g.xh + (uint32_t)(b * QK) + L.aoff[j],
+                                         (lds_void_t *)&st.As[(L.wave + 8 * j) * 512], 16, 0, 0);
+    if (L.wave == 0)
+        __builtin_amdgcn_global_load_lds(g.xh + (uint32_t)(b * QK) + L.aoff[4], (lds_void_t *)&st.As[32 * 512], 16,
+                                         0, 0);
+    __builtin_amdgcn_global_load_lds(L.hrow + (int64_t)b * Q4K_BYTES, (lds_void_t *)&st.Hs[L.wave][0], 16, 0, 0);
+    if (L.wave < 2)
+        __builtin_amdgcn_global_load_lds(g.xbs + (uint32_t)(b * 16) + L.bsoff, (lds_void_t *)&st.Bs[L.wave * 512],
+                                         16, 0, 0);
+    else if (L.wave == 2)
+        __builtin_amdgcn_global_load_lds(g.xd + (uint32_t)b + L.dxoff, (lds_void_t *)&st.Dx[0], 4, 0, 0);
+}
+
+// one K block: wait for stage cur, start the loads of block b+1 into nxt,
+// accumulate block b.  vmc: the vmcnt that guarantees this wave's loads of
+// block b landed (0 for the first block; afterwards 8 = the weight loads
+// issued after them).
+template <int VMC>
+__device__ __forceinline__ void g2g_block(const G2Args &g, const G2GLane &L, int b, int nb, G2GBuf &cur,
+                                          G2GBuf &nxt, uint4 (&qv)[2][4], float16_t (&acc)[2][2]) {
+    const bool more = b + 1 < nb;
+    const int bn = more ? b + 1 : b;
+    const int l32 = L.l32, g2 = L.g2, wave = L.wave;
+    __builtin_amdgcn_s_waitcnt(0x0F70 | VMC);
+    __syncthreads();
+    if (more) g2g_issue(g, L, b + 1, nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- per-block constants from the headers
+    half2_t sc_lo[2][2], nc_lo[2][2], sc_hi[2][2], nc_hi[2][2];
+    float dw[2], dmw[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+        const uint4 hv = cur.Hs[wave][32 * ct + l32];
+        dw[ct] = h2f((uint16_t)(hv.x & 0xffff));
+        dmw[ct] = h2f((uint16_t)(hv.x >> 16));
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {   // steps 0-7: sub-blocks (4g2, 4g2+1); 8-15: (4g2+2, 4g2+3)
+            int sc0, sc1, m_;
+            scale_min_k4_reg(4 * g2 + 2 * hf, hv.y, hv.z, hv.w, sc0, m_);
+            scale_min_k4_reg(4 * g2 + 2 * hf + 1, hv.y, hv.z, hv.w, sc1, m_);
+            sc_lo[ct][hf] = splat_((float)sc0);
+            nc_lo[ct][hf] = splat_(-1024.f * (float)sc0);
+            sc_hi[ct][hf] = splat_((float)sc1);
+            nc_hi[ct][hf] = splat_(-64.f * (float)sc1);
+        }
+    }
+    // ---- main term: P = sum_j sc_j sum_i q4 q8, 16 MFMA steps of K = 16
+    float16_t P[2][2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) P[rt][ct][i] = 0.f;
+    const _Float16 *Ab = &cur.As[l32 * G2G_LDA + 8 * g2];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        const half8_t A0 = *(const half8_t *)(Ab + 16 * s);
+        const half8_t A1 = *(const half8_t *)(Ab + 32 * G2G_LDA + 16 * s);
+        const int hf = s >> 3;
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            const half8_t B = dq4_exact(dword_of(qv[ct][s >> 2], s & 3), sc_lo[ct][hf], nc_lo[ct][hf],
+                                        sc_hi[ct][hf], nc_hi[ct][hf]);
+            P[0][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B, P[0][ct], 0, 0, 0);
+            P[1][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B, P[1][ct], 0, 0, 0);
+        }
+        if ((s & 3) == 3) {   // refill this chunk with the next block's (the last block reloads itself)
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+                qv[ct][s >> 2] = *(const uint4 *)(L.rowp[ct] + (int64_t)bn * Q4K_BYTES + 16 + 64 * g2 + 16 * (s >> 2));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // ---- min term Q = sum_j m_j * bsum16_j (one MFMA per tile), then
+    // acc += dx * (dw * P - dmin * Q); row scales of rows 32rt + 8a + 4g2 + {0..3}
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+        const uint4 hv = cur.Hs[wave][32 * ct + l32];
+        half8_t mins;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int sc_, m_;
+            scale_min_k4_reg(4 * g2 + j, hv.y, hv.z, hv.w, sc_, m_);
+            mins[2 * j] = (_Float16)(float)m_;
+            mins[2 * j + 1] = (_Float16)(float)m_;
+        }
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            const half8_t Abs = *(const half8_t *)(&cur.Bs[(32 * rt + l32) * 16 + 8 * g2]);
+            float16_t q = {};
+            q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Abs, mins, q, 0, 0, 0);
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const float4 dx4 = *(const float4 *)(&cur.Dx[32 * rt + 8 * a + 4 * g2]);
+                const float dxv[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float t = fmaf(-dmw[ct], q[4 * a + i], dw[ct] * P[rt][ct][4 * a + i]);
+                    acc[rt][ct][4 * a + i] = fmaf(dxv[i], t, acc[rt][ct][4 * a + i]);
+                }
+            }
+        }
+    }
+}
+
+template <int NEXT>
+__global__ void __launch_bounds__(G2G_THREADS) k_g2_glu(G2Args g) {
+    __shared__ __attribute__((aligned(1024))) G2GBuf st0;
+    __shared__ __attribute__((aligned(1024))) G2GBuf st1;
+    __shared__ int s_p[G2_BM], s_arow[G2_BM];
+    __shared__ AmaxIdx s_red[G2_BM][G2G_WAVES];
+    __shared__ float s_is[G2_BM], s_d[G2_BM];
+    const int nx = (int)(g.I / QK);
+    int tile, ctile;
+    tile_coords(g.max_tiles, tile, ctile);
+    if (tile >= *g.n_tiles || ctile >= nx) return;
+    G2GLane L;
+    const int tid = threadIdx.x;
+    L.wave = tid >> 6;
+    L.lane = tid & 63;
+    L.l32 = L.lane & 31;
+    L.g2 = L.lane >> 5;
+    const int wave = L.wave, lane = L.lane, l32 = L.l32, g2 = L.g2;
+    const int e = g.tile_e[tile], r0 = g.tile_r0[tile];
+    const int cnt = g.counts[e], off = g.offsets[e];
+    const int mrows = imin(G2_BM, cnt - r0);
+    const uint32_t Kin = (uint32_t)g.a.K;
+    const int nb = (int)(Kin / QK);
+
+    if (tid < G2_BM) {
+        const int p = tid < mrows ? g.perm[off + r0 + tid] : -1;
+        s_p[tid] = p;
+        s_arow[tid] = p < 0 ? 0 : p / g.K;
+    }
+    // weight rows of this lane: col tile 0 = h row n, col tile 1 = g row
+    const int64_t n = (int64_t)ctile * QK + 32 * wave + l32;
+    L.rowp[0] = g.a.data + (int64_t)e * g.a.mat_bytes + n * g.a.row_bytes;
+    if (g.fused) L.rowp[1] = g.a.data + (int64_t)e * g.a.mat_bytes + (g.I + n) * g.a.row_bytes;
+    else L.rowp[1] = g.b.data + (int64_t)e * g.b.mat_bytes + n * g.b.row_bytes;
+    L.hrow = L.rowp[g2];   // the wave's header load: lane = 32*ct + l32
+    __syncthreads();
+    // per-lane source offsets (halfs, block 0) of this wave's activation
+    // loads k = wave + 8j (j < 4; wave 0 also k = 32)
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+        const int k = wave + 8 * j;
+        const int q = 64 * imin(k, G2G_ALOADS - 1) + lane;
+        const int row = q / 33, ch = q % 33;
+        L.aoff[j] = (uint32_t)s_arow[row] * Kin + 8u * (uint32_t)(ch == 32 ? 0 : ch);
+    }
+    L.bsoff = (uint32_t)s_arow[32 * (wave & 1) + (lane >> 1)] * (uint32_t)(nb * 16) + 8u * (lane & 1);
+    L.dxoff = (uint32_t)s_arow[lane] * (uint32_t)nb;
+
+    // weight nibbles: this lane's 64 bytes (chunks 2*g2, 2*g2+1) of each col tile
+    uint4 qv[2][4];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) qv[ct][q] = *(const uint4 *)(L.rowp[ct] + 16 + 64 * g2 + 16 * q);
+    g2g_issue(g, L, 0, st0);
+
+    float16_t acc[2][2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[rt][ct][i] = 0.f;
+
+    g2g_block<0>(g, L, 0, nb, st0, st1, qv, acc);
+    for (int b = 1; b < nb; b += 2) {
+        g2g_block<8>(g, L, b, nb, st1, st0, qv, acc);
+        if (b + 1 < nb) g2g_block<8>(g, L, b + 1, nb, st0, st1, qv, acc);
+    }
+
+    // ---- GLU + Q8_K of each row's 256 columns (first column with the largest |v|)
+    float v[2][16];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[rt][i] = act_pair(g.act, acc[rt][0][i], acc[rt][1][i]);
+    const int col = 32 * wave + l32;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            AmaxIdx a{fabsf(v[rt][i]), col, v[rt][i]};
+            a = wave_amax_idx(a, 32);
+            if (l32 == 0) s_red[32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3)][wave] = a;
+        }
+    __syncthreads();
+    if (tid < G2_BM) {
+        AmaxIdx a = s_red[tid][0];
+#pragma unroll
+        for (int w = 1; w < G2G_WAVES; ++w) a = amax_better(a, s_red[tid][w]);
+        if (a.ax != 0.f) {
+            const float iscale = -127.f / a.val;
+            s_is[tid] = iscale;
+            s_d[tid] = 1 / iscale;
+        } else {
+            s_is[tid] = 0.f;
+            s_d[tid] = 0.f;
+        }
+    }
+    __syncthreads();
+    // quantized act tile (rows of 256 in the down weight's K order) into As[0]
+    const int pos = mfma32_pos(NEXT, col);
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
+            const float is = s_is[m], d = s_d[m];
+            const int q = d != 0.f ? imin(127, nearest_int(is * v[rt][i])) : 0;
+            st0.As[m * G2G_LDA + pos] = (_Float16)(d * (float)q);
+        }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int idx = tid + G2G_THREADS * it;
+        const int r = idx >> 5, c16 = idx & 31;
+        if (r < mrows)
+            *(uint4 *)(g.acth + (int64_t)s_p[r] * g.I + (int64_t)ctile * QK + c16 * 8) =
+                *(const uint4 *)(&st0.As[r * G2G_LDA + c16 * 8]);
+    }
+}
+
+// ------------------------------------------------------------------ STORE
+// Q4_K: qs of chunks 2g2, 2g2+1 (4 x 16 B) + header.  Q6_K: half g2 of ql
+// (2 x 32 B), qh (32 B), scales[8g2 .. 8g2+8) and d packed into h.
+template <int WT>
+__device__ __forceinline__ void g2_load_w(const uint8_t *rowp, int b, int g2, uint4 *q, uint4 &h) {
+    if constexpr (WT == 12) {
+        const uint8_t *blk = rowp + (int64_t)b * Q4K_BYTES;
+        h = *(const uint4 *)blk;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q[k] = *(const uint4 *)(blk + 16 + 64 * g2 + 16 * k);
+    } else {
+        const uint8_t *blk = rowp + (int64_t)b * Q6K_BYTES;
+        q[0] = load16_a2_(blk + 64 * g2);
+        q[1] = load16_a2_(blk + 64 * g2 + 16);
+        q[2] = load16_a2_(blk + 64 * g2 + 32);
+        q[3] = load16_a2_(blk + 64 * g2 + 48);
+        q[4] = load16_a2_(blk + 128 + 32 * g2);
+        q[5] = load16_a2_(blk + 128 + 32 * g2 + 16);
+        const uint4 s16 = load16_a2_(blk + 192);
+        const uint8_t *pd = blk + 208;
+        h.x = g2 ? s16.z : s16.x;
+        h.y = g2 ? s16.w : s16.y;
+        h.z = (uint32_t)pd[0] | ((uint32_t)pd[1] << 8);
+        h.w = 0u;
+    }
+}
+
+template <int WT>
+__global__ void __launch_bounds__(G2_THREADS) k_g2_store(G2Args g) {
+    __shared__ __attribute__((aligned(16))) _Float16 As[2][G2_BM * G2_LDA];
+    __shared__ int s_p[G2_BM];
+    __shared__ int64_t s_arow[G2_BM];
+    const int nx = (int)((g.ncols + 511) / 512);
+    int tile, ctile;
+    tile_coords(g.max_tiles, tile, ctile);
+    if (tile >= *g.n_tiles || ctile >= nx) return;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, g2 = lane >> 5;
+    const int e = g.tile_e[tile], r0 = g.tile_r0[tile];
+    const int cnt = g.counts[e], off = g.offsets[e];
+    const int mrows = imin(G2_BM, cnt - r0);
+    const bool two = mrows > 32;
+    const int64_t Kin = g.a.K;
+    const int nb = (int)(Kin / QK);
+    if (tid < G2_BM) {
+        const int p = tid < mrows ? g.perm[off + r0 + tid] : -1;
+        s_p[tid] = p;
+        s_arow[tid] = p < 0 ? 0 : (g.ne11 == 1 ? (int64_t)(p / g.K) : (int64_t)p);
+    }
+    int64_t ncol[2];
+    bool nok[2];
+    const uint8_t *rowp[2];
+    #pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+        ncol[ct] = (int64_t)ctile * 512 + 64 * wave + 32 * ct + l32;
+        nok[ct] = ncol[ct] < g.ncols;
+        rowp[ct] = g.a.data + (int64_t)e * g.a.mat_bytes + (nok[ct] ? ncol[ct] : 0) * g.a.row_bytes;
+    }
+    __syncthreads();
+
+    uint4 av0, av1, av2, av3;
+#define G2S_ACT_SRC(it) (g.xh + s_arow[(tid + G2_THREADS * (it)) >> 5] * Kin + (int64_t)b_ * QK + \
+                         ((tid + G2_THREADS * (it)) & 31) * 8)
+#define G2S_ACT_DST(buf, it) (&As[buf][((tid + G2_THREADS * (it)) >> 5) * G2_LDA + ((tid + G2_THREADS * (it)) & 31) * 8])
+#define G2S_LOAD_ACT(bb)                          \
+    do {                                          \
+        const int b_ = (bb);                      \
+        av0 = *(const uint4 *)G2S_ACT_SRC(0);     \
+        av1 = *(const uint4 *)G2S_ACT_SRC(1);     \
+        av2 = *(const uint4 *)G2S_ACT_SRC(2);     \
+        av3 = *(const uint4 *)G2S_ACT_SRC(3);     \
+    } while (0)
+#define G2S_STORE_ACT(buf)                        \
+    do {                                          \
+        *(uint4 *)G2S_ACT_DST(buf, 0) = av0;      \
+        *(uint4 *)G2S_ACT_DST(buf, 1) = av1;      \
+        *(uint4 *)G2S_ACT_DST(buf, 2) = av2;      \
+        *(uint4 *)G2S_ACT_DST(buf, 3) = av3;      \
+    } while (0)
+
+    // Q4_K: qs chunks 2g2, 2g2+1 (4 x 16 B) + header; Q6_K: half g2: ql a/b,
+    // qh (3 x 32 B), scales[8h..8h+8), d
+    uint4 qv[2][WT == 12 ? 4 : 6];
+    uint4 hv[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) g2_load_w<WT>(rowp[ct], 0, g2, qv[ct], hv[ct]);
+    G2S_LOAD_ACT(0);
+    G2S_STORE_ACT(0);
+
+    float16_t acc[2][2];
+    #pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+        #pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+            #pragma unroll
+            for (int i = 0; i < 16; ++i) acc[rt][ct][i] = 0.f;
+
+    for (int b = 0; b < nb; ++b) {
+        const int buf = b & 1;
+        const bool more = b + 1 < nb;
+        __syncthreads();
+        if (more) G2S_LOAD_ACT(b + 1);
+        const _Float16 *Ab0 = &As[buf][(l32)*G2_LDA + 8 * g2];
+        const _Float16 *Ab1 = &As[buf][(32 + l32) * G2_LDA + 8 * g2];
+        if constexpr (WT == 12) {
+            half2_t s_lo[2][2], nm_lo[2][2], s_hi[2][2], nm_hi[2][2];
+            #pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const float d = h2f((uint16_t)(hv[ct].x & 0xffff)), dmin = h2f((uint16_t)(hv[ct].x >> 16));
+                #pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    int sc, m;
+                    scale_min_k4_reg(4 * g2 + 2 * hf, hv[ct].y, hv[ct].z, hv[ct].w, sc, m);
+                    s_lo[ct][hf] = splat_(d * (float)sc);
+                    nm_lo[ct][hf] = splat_(-(dmin * (float)m));
+                    scale_min_k4_reg(4 * g2 + 2 * hf + 1, hv[ct].y, hv[ct].z, hv[ct].w, sc, m);
+                    s_hi[ct][hf] = splat_(d * (float)sc);
+                    nm_hi[ct][hf] = splat_(-(dmin * (float)m));
+                }
+                if (more) hv[ct] = *(const uint4 *)(rowp[ct] + (int64_t)(b + 1) * Q4K_BYTES);
+            }
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const half8_t A0 = *(const half8_t *)(Ab0 + 16 * s);
+                const half8_t A1 = *(const half8_t *)(Ab1 + 16 * s);
+                const int hf = s >> 3;
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    const half8_t B =
+                        dq4_f16(dword_of(qv[ct][s >> 2], s & 3), s_lo[ct][hf], nm_lo[ct][hf], s_hi[ct][hf], nm_hi[ct][hf]);
+                    acc[0][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B, acc[0][ct], 0, 0, 0);
+                    if (two) acc[1][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B, acc[1][ct], 0, 0, 0);
+                }
+                if ((s & 3) == 3 && more) {
+                    #pragma unroll
+                    for (int ct = 0; ct < 2; ++ct)
+                        qv[ct][s >> 2] = *(const uint4 *)(rowp[ct] + (int64_t)(b + 1) * Q4K_BYTES + 16 + 64 * g2 +
+                                                          16 * (s >> 2));
+                }
+            }
+        } else {
+            // scales for step (jj, w): first quarter sub 8h + 4w + jj/4, second +2
+            half2_t sq[2][8];
+            uint4 nq[2][6], nh[2];
+            #pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const float d = h2f((uint16_t)(hv[ct].z & 0xffff));
+                #pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const uint32_t word = k < 4 ? hv[ct].x : hv[ct].y;
+                    const int sc = (int)(int8_t)(word >> (8 * (k & 3)));
+                    sq[ct][k] = splat_(d * (float)sc);
+                }
+                if (more) g2_load_w<WT>(rowp[ct], b + 1, g2, nq[ct], nh[ct]);
+            }
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const half8_t A0 = *(const half8_t *)(Ab0 + 16 * s);
+                const half8_t A1 = *(const half8_t *)(Ab1 + 16 * s);
+                const int jj = s >> 1, w = s & 1;
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    const uint32_t qla = dword_of(qv[ct][jj >> 2], jj & 3);
+                    const uint32_t qlb = dword_of(qv[ct][2 + (jj >> 2)], jj & 3);
+                    const uint32_t qhh = dword_of(qv[ct][4 + (jj >> 2)], jj & 3);
+                    const int k0 = 4 * w + (jj >> 2);
+                    const half8_t B = dq6_f16(qla, qlb, qhh, w, sq[ct][k0], sq[ct][k0 + 2]);
+                    acc[0][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B, acc[0][ct], 0, 0, 0);
+                    if (two) acc[1][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B, acc[1][ct], 0, 0, 0);
+                }
+            }
+            if (more)
+                #pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    #pragma unroll
+                    for (int k = 0; k < 6; ++k) qv[ct][k] = nq[ct][k];
+                    hv[ct] = nh[ct];
+                }
+        }
+        if (more) G2S_STORE_ACT(buf ^ 1);
+    }
+#undef G2S_LOAD_ACT
+#undef G2S_STORE_ACT
+    // rows 32rt + 8(i/4) + 4g2 + i%4, column ncol[ct]
+    #pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+        #pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
+            if (m >= mrows) continue;
+            float *yrow = g.y + (int64_t)s_p[m] * g.ldy;
+            #pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+                if (nok[ct]) yrow[ncol[ct]] = acc[rt][ct][i];
+        }
+}
+
+int launch_gemm2(const G2Args &g, hipStream_t st) {
+    if (g.max_tiles <= 0) return 0;
+    if (g.a.K % QK) return -6;
+    if (g.glu) {
+        if (g.a.type != 12 || (g.I % QK)) return -6;
+        const int nx = (int)(g.I / QK);
+        const dim3 grid((unsigned)((nx * g.max_tiles + 7) / 8 * 8));
+        if (g.next_type == 14) hipLaunchKernelGGL(k_g2_glu<14>, grid, dim3(G2G_THREADS), 0, st, g);
+        else hipLaunchKernelGGL(k_g2_glu<12>, grid, dim3(G2G_THREADS), 0, st, g);
+    } else {
+        const int nx = (int)((g.ncols + 511) / 512);
+        const dim3 grid((unsigned)((nx * g.max_tiles + 7) / 8 * 8));
+        if (g.a.type == 12) hipLaunchKernelGGL(k_g2_store<12>, grid, dim3(G2_THREADS), 0, st, g);
+        else if (g.a.type == 14) hipLaunchKernelGGL(k_g2_store<14>, grid, dim3(G2_THREADS), 0, st, g);
+        else return -3;
+    }
+    return hip_check_launch();
+}
+
+}  // namespace mimoe

@@ -45,12 +45,9 @@ __device__ inline void load_q4_piece(const uint8_t *blk, int sl, Q4Piece &w) {
     w.qs[0] = q.x; w.qs[1] = q.y; w.qs[2] = q.z; w.qs[3] = q.w;
     w.d = h2f((uint16_t)(h.x & 0xffff));
     w.dmin = h2f((uint16_t)(h.x >> 16));
-    uint8_t sc[12];
-    const uint32_t hw[3] = {h.y, h.z, h.w};
-    for (int i = 0; i < 12; ++i) sc[i] = (uint8_t)(hw[i >> 2] >> (8 * (i & 3)));
     const int c = sl >> 1;
-    scale_min_k4(2 * c, sc, w.scA, w.mA);
-    scale_min_k4(2 * c + 1, sc, w.scB, w.mB);
+    scale_min_k4_reg(2 * c, h.y, h.z, h.w, w.scA, w.mA);
+    scale_min_k4_reg(2 * c + 1, h.y, h.z, h.w, w.scB, w.mB);
 }
 
 // lane piece: chunk c = sl/2, l0 = 16*(sl%2); low nibbles = elements 64c+l0+i
@@ -89,10 +86,10 @@ __device__ inline void load_q6_piece(const uint8_t *blk, int sl, Q6Piece &w) {
     w.qh = load8_a2(blk + 128 + 32 * h + l0);
     const uint2 s8 = load8_a2(blk + 192 + 8 * h);
     const int is = l0 >> 4;
-    const uint32_t sv[2] = {s8.x, s8.y};
     for (int qq = 0; qq < 4; ++qq) {
         const int idx = is + 2 * qq;
-        w.sc[qq] = (int)(int8_t)(sv[idx >> 2] >> (8 * (idx & 3)));
+        const uint32_t word = (idx >> 2) ? s8.y : s8.x;
+        w.sc[qq] = (int)(int8_t)(word >> (8 * (idx & 3)));
     }
     const uint8_t *pd = blk + 208;
     w.d = h2f((uint16_t)((uint32_t)pd[0] | ((uint32_t)pd[1] << 8)));

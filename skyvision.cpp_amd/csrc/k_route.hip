@@ -20,7 +20,7 @@ namespace mimoe {
 __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ src, int64_t ld, int64_t nrows,
                                                   int nb, int8_t *__restrict__ q8, float *__restrict__ d8,
                                                   int16_t *__restrict__ bsums, _Float16 *__restrict__ xh,
-                                                  int wtype) {
+                                                  int wtype, int order, int exact, _Float16 *__restrict__ xbs) {
     __shared__ int8_t sq[4][QK];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t item = (int64_t)blockIdx.x * 4 + wave;
@@ -57,11 +57,15 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ src,
         }
         if (d8 && lane == 0) d8[row * nb + b] = d;
     }
-    if (bsums) {
+    if (bsums || xbs) {
         int s = q[0] + q[1] + q[2] + q[3];
         s += __shfl_xor(s, 1, 64);
         s += __shfl_xor(s, 2, 64);
-        if (valid && (lane & 3) == 0) bsums[row * (K / 16) + (int64_t)b * 16 + (lane >> 2)] = (int16_t)s;
+        const int64_t bi = row * (K / 16) + (int64_t)b * 16 + (lane >> 2);
+        if (valid && (lane & 3) == 0) {
+            if (bsums) bsums[bi] = (int16_t)s;
+            if (xbs) xbs[bi] = (_Float16)(float)s;        // |s| <= 2032: exact in fp16
+        }
     }
     if (xh) {
         for (int j = 0; j < 4; ++j) sq[wave][4 * lane + j] = (int8_t)q[j];
@@ -69,10 +73,16 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ src,
         if (valid) {
             half2_t h01, h23;
             const int p0 = 4 * lane;
-            h01[0] = (_Float16)(d * (float)sq[wave][mfma_elem(wtype, p0 + 0)]);
-            h01[1] = (_Float16)(d * (float)sq[wave][mfma_elem(wtype, p0 + 1)]);
-            h23[0] = (_Float16)(d * (float)sq[wave][mfma_elem(wtype, p0 + 2)]);
-            h23[1] = (_Float16)(d * (float)sq[wave][mfma_elem(wtype, p0 + 3)]);
+            float qv[4];
+            for (int j = 0; j < 4; ++j) {
+                const int el = order ? mfma32_elem(wtype, p0 + j) : mfma_elem(wtype, p0 + j);
+                const float qf = (float)sq[wave][el];
+                qv[j] = exact ? qf : d * qf;
+            }
+            h01[0] = (_Float16)qv[0];
+            h01[1] = (_Float16)qv[1];
+            h23[0] = (_Float16)qv[2];
+            h23[1] = (_Float16)qv[3];
             uint2 pk;
             pk.x = __builtin_bit_cast(uint32_t, h01);
             pk.y = __builtin_bit_cast(uint32_t, h23);
@@ -86,16 +96,84 @@ int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, cons
     const int nb = (int)(K / QK);
     const int64_t items = nrows * nb;
     hipLaunchKernelGGL(k_q8k_rows, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, st, src, ld, nrows, nb, o.q8,
-                       o.d8, o.bsums, o.xh, o.wtype);
+                       o.d8, o.bsums, o.xh, o.wtype, o.order, o.exact, o.xbs);
     return hip_check_launch();
 }
 
 // ---------------------------------------------------------------- router
-// logit = fl32( fl32(sum_c part_c) + b ), part_c = sequential fp64 sum over the
-// 64-wide chunk c, chunk partials summed left to right.  fp32 x fp32 products
-// are exact in fp64, so fma and mul+add agree and only the order matters.
+// logit = fl32( fl32(sum_c part_c) + b ) in fp64, one fixed order: the 64-wide
+// chunk c gives part_c = sum over s = 0..15 (outer), g = 0..3 (inner) of
+// W[e][64c+16g+s] * x[t][64c+16g+s] added left to right; chunk partials are
+// added left to right.  fp32 x fp32 products are exact in fp64, so fma and
+// mul+add agree and only this order matters.
+//
+// MFMA form: v_mfma_f64_16x16x4_f64 adds its four k-products to the
+// accumulator one after another in k order (c + p0 + p1 + p2 + p3), so one
+// instruction per s with k = g reproduces the chunk order exactly.  A wave owns
+// a 16 token x 16 expert tile and whole chunks; the chunk partials meet in LDS
+// and are summed in chunk order.
+typedef double double4_t __attribute__((ext_vector_type(4)));
+constexpr int RM_MAX_CHUNKS = 32;   // D <= 2048 (64 KB of LDS partials)
 
-// split form (small T): thread (expert, chunk) computes one partial
+template <bool VEC>
+__global__ void __launch_bounds__(1024) k_router_mfma(const float *__restrict__ W, const float *__restrict__ bias,
+                                                      const float *__restrict__ x, int64_t ldx, int64_t T, int D,
+                                                      int E, float *__restrict__ logits) {
+    extern __shared__ double rparts[];   // [nch][256]
+    const int nw = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nch = (D + 63) / 64;
+    const int e0 = blockIdx.x * 16;
+    const int64_t t0 = (int64_t)blockIdx.y * 16;
+    const int row = lane & 15, g = lane >> 4;
+    const int64_t tok = t0 + row;
+    const int ex = e0 + row;
+    const bool tok_ok = tok < T, ex_ok = ex < E;
+    const float *xr = x + (tok_ok ? tok : 0) * ldx;
+    const float *wr = W + (int64_t)(ex_ok ? ex : 0) * D;
+    for (int c = wave; c < nch; c += nw) {
+        const int base = 64 * c + 16 * g;
+        float xv[16], wv[16];
+        if (VEC) {
+            for (int q = 0; q < 4; ++q) {
+                const float4 a = *(const float4 *)(xr + base + 4 * q);
+                const float4 b = *(const float4 *)(wr + base + 4 * q);
+                xv[4 * q] = a.x; xv[4 * q + 1] = a.y; xv[4 * q + 2] = a.z; xv[4 * q + 3] = a.w;
+                wv[4 * q] = b.x; wv[4 * q + 1] = b.y; wv[4 * q + 2] = b.z; wv[4 * q + 3] = b.w;
+            }
+        } else {
+            for (int s = 0; s < 16; ++s) {
+                const int d = base + s;
+                xv[s] = d < D ? xr[d] : 0.f;
+                wv[s] = d < D ? wr[d] : 0.f;
+            }
+        }
+        double4_t part = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const double a = tok_ok ? (double)xv[s] : 0.0;
+            const double b = ex_ok ? (double)wv[s] : 0.0;
+            part = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, part, 0, 0, 0);
+        }
+        for (int r = 0; r < 4; ++r) rparts[c * 256 + lane * 4 + r] = part[r];
+    }
+    __syncthreads();
+    if (threadIdx.x < 256) {
+        // output slot (lane l, r) holds token row 4r + l/16, expert col l%16
+        const int l = threadIdx.x >> 2, r = threadIdx.x & 3;
+        const int64_t tt = t0 + 4 * r + (l >> 4);
+        const int ee = e0 + (l & 15);
+        double acc = 0.0;
+        for (int c = 0; c < nch; ++c) acc = acc + rparts[c * 256 + threadIdx.x];
+        if (tt < T && ee < E) {
+            float v = (float)acc;
+            if (bias) v = v + bias[ee];
+            logits[tt * E + ee] = v;
+        }
+    }
+}
+
+// generic form (any D): thread (expert, chunk) computes one partial
 __global__ void __launch_bounds__(256) k_router_split(const float *__restrict__ W, const float *__restrict__ bias,
                                                       const float *__restrict__ x, int64_t ldx, int D, int E,
                                                       int nch, int epb, float *__restrict__ logits) {
@@ -109,8 +187,11 @@ __global__ void __launch_bounds__(256) k_router_split(const float *__restrict__ 
     if (act) {
         const float *w = W + (int64_t)e * D;
         const float *xt = x + t * ldx;
-        const int d0 = c * 64, d1 = imin(D, d0 + 64);
-        for (int dd = d0; dd < d1; dd++) part = fma((double)w[dd], (double)xt[dd], part);
+        for (int s = 0; s < 16; ++s)
+            for (int g = 0; g < 4; ++g) {
+                const int dd = 64 * c + 16 * g + s;
+                if (dd < D) part = fma((double)w[dd], (double)xt[dd], part);
+            }
     }
     parts[tid] = part;
     __syncthreads();
@@ -123,71 +204,20 @@ __global__ void __launch_bounds__(256) k_router_split(const float *__restrict__ 
     }
 }
 
-// tile form (large T): a block holds TT = (256/E)*4 tokens and every expert;
-// thread (expert e, group gi) accumulates 4 tokens.  W and x are staged in LDS
-// one 64-wide chunk at a time.
-constexpr int RT_TPT = 4;
-__global__ void __launch_bounds__(256) k_router_tile(const float *__restrict__ W, const float *__restrict__ bias,
-                                                     const float *__restrict__ x, int64_t ldx, int64_t T, int D,
-                                                     int E, float *__restrict__ logits) {
-    extern __shared__ float rsm[];
-    const int G = 256 / E;
-    const int TT = G * RT_TPT;
-    float *Ws = rsm;               // [E][65]
-    float *xs = rsm + E * 65;      // [TT][64]
-    const int tid = threadIdx.x;
-    const int e = tid % E, gi = tid / E;
-    const bool act = gi < G;
-    const int64_t t0 = (int64_t)blockIdx.x * TT;
-    double acc[RT_TPT];
-    for (int j = 0; j < RT_TPT; ++j) acc[j] = 0.0;
-    for (int c0 = 0; c0 < D; c0 += 64) {
-        const int cl = imin(64, D - c0);
-        for (int i = tid; i < E * 64; i += 256) {
-            const int r = i >> 6, cc = i & 63;
-            Ws[r * 65 + cc] = cc < cl ? W[(int64_t)r * D + c0 + cc] : 0.f;
-        }
-        for (int i = tid; i < TT * 64; i += 256) {
-            const int r = i >> 6, cc = i & 63;
-            const int64_t tok = t0 + r;
-            xs[r * 64 + cc] = (tok < T && cc < cl) ? x[tok * ldx + c0 + cc] : 0.f;
-        }
-        __syncthreads();
-        if (act) {
-            for (int j = 0; j < RT_TPT; ++j) {
-                const int tl = gi + G * j;
-                double part = 0.0;
-                for (int dd = 0; dd < cl; ++dd)
-                    part = fma((double)Ws[e * 65 + dd], (double)xs[tl * 64 + dd], part);
-                acc[j] = acc[j] + part;
-            }
-        }
-        __syncthreads();
-    }
-    if (act) {
-        for (int j = 0; j < RT_TPT; ++j) {
-            const int64_t tok = t0 + gi + G * j;
-            if (tok < T) {
-                float v = (float)acc[j];
-                if (bias) v = v + bias[e];
-                logits[tok * E + e] = v;
-            }
-        }
-    }
-}
-
 int launch_router(const float *W, const float *b, const float *x, int64_t ldx, int64_t T, int D, int E,
                   float *logits, hipStream_t st) {
     if (T <= 0) return 0;
     const int nch = (D + 63) / 64;
-    if (T >= 32 && E >= 16 && E <= 256) {   // LDS: E*65 + (256/E)*4*64 floats <= 64 KB
-        const int G = 256 / E;
-        const int TT = G * RT_TPT;
-        const size_t smem = sizeof(float) * ((size_t)E * 65 + (size_t)TT * 64);
-        hipLaunchKernelGGL(k_router_tile, dim3((unsigned)((T + TT - 1) / TT)), dim3(256), smem, st, W, b, x, ldx,
-                           T, D, E, logits);
+    if (nch <= RM_MAX_CHUNKS && T <= 65535 * 16) {
+        const bool vec = (D % 64 == 0) && (ldx % 4 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)W % 16 == 0);
+        const int64_t blocks = (int64_t)((E + 15) / 16) * ((T + 15) / 16);
+        const int nw = blocks >= 256 ? imin(4, nch) : imin(16, nch);
+        const dim3 grid((unsigned)((E + 15) / 16), (unsigned)((T + 15) / 16));
+        const size_t smem = sizeof(double) * 256 * (size_t)nch;
+        if (vec) hipLaunchKernelGGL(k_router_mfma<true>, grid, dim3(64 * nw), smem, st, W, b, x, ldx, T, D, E, logits);
+        else hipLaunchKernelGGL(k_router_mfma<false>, grid, dim3(64 * nw), smem, st, W, b, x, ldx, T, D, E, logits);
     } else {
-        if (nch > 256) return -6;
+        if (nch > 256 || T > 65535) return -6;
         const int epb = 256 / nch;
         hipLaunchKernelGGL(k_router_split, dim3((unsigned)((E + epb - 1) / epb), (unsigned)T), dim3(256), 0, st, W,
                            b, x, ldx, D, E, nch, epb, logits);
@@ -270,73 +300,124 @@ int launch_topk_softmax(const float *logits, int64_t ld_logits, int64_t T, int E
 // ---------------------------------------------------------------- dispatch
 // Single work-group of 1024 threads.  Stable: within an expert the list is in
 // flat (t*K + k) order, i.e. token-ascending then slot-ascending.
+//   1. counts (LDS atomics) -> exclusive scans: offsets, GEMM M-tiles, active list
+//   2. ranks: per chunk of tokens, a bitset bits[e][word] of the tokens that
+//      chose expert e; rank(t, e) = tokens before t in e's bitset + the
+//      expert's running base.  Ids repeated inside one token (legal for
+//      mul_mat_id, never produced by top-k) take the ballot path instead.
 constexpr int DISPATCH_THREADS = 1024;
 constexpr int DISPATCH_WAVES = DISPATCH_THREADS / 64;
+constexpr int DISPATCH_LDS_BYTES = 48 * 1024;
 
-__device__ inline void block_exclusive_scan(int *buf, int n, int tid) {
-    // Hillis-Steele inclusive scan over buf[0..n) (n <= blockDim), then shift
-    for (int off = 1; off < n; off <<= 1) {
-        int add = 0;
-        if (tid < n && tid >= off) add = buf[tid - off];
-        __syncthreads();
-        if (tid < n) buf[tid] += add;
-        __syncthreads();
-    }
-}
-
-__global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__restrict__ ids, int64_t n, int E,
-                                                               int BM, Dispatch d) {
-    extern __shared__ int dsm[];
-    int *cnt = dsm;                                // [E]
-    int *run = cnt + E;                            // [E]
-    int *scan = run + E;                           // [E]  inclusive scan of counts
-    int *tscan = scan + E;                         // [E]  inclusive scan of tiles
-    int *ascan = tscan + E;                        // [E]  inclusive scan of active flags
-    int *wcnt = ascan + E;                         // [16][E]
-    int *wbase = wcnt + DISPATCH_WAVES * E;        // [16][E]
-    __shared__ int bad;
+__global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__restrict__ ids, int64_t T, int K,
+                                                               int E, int BM, int wpc, Dispatch d) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char dsm_raw[];
+    int *cnt = (int *)dsm_raw;                     // [E]
+    int *scn = cnt + E;                            // [E] inclusive scan of counts
+    int *tsc = scn + E;                            // [E] inclusive scan of tiles
+    int *asc = tsc + E;                            // [E] inclusive scan of active flags
+    int *run = asc + E;                            // [E] running list position
+    unsigned char *rest = dsm_raw + (((size_t)5 * E * sizeof(int) + 15) & ~(size_t)15);
+    __shared__ int bad, dup;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int64_t n = T * K;
 
     for (int e = tid; e < E; e += DISPATCH_THREADS) cnt[e] = 0;
-    if (tid == 0) bad = 0;
+    if (tid == 0) { bad = 0; dup = 0; }
     __syncthreads();
-    for (int64_t i = tid; i < n; i += DISPATCH_THREADS) {
-        const int e = ids[i];
-        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-        else atomicAdd(&bad, 1);
+    for (int64_t t = tid; t < T; t += DISPATCH_THREADS) {
+        const int32_t *it = ids + t * K;
+        for (int k = 0; k < K; ++k) {
+            const int e = it[k];
+            if (e >= 0 && e < E) {
+                atomicAdd(&cnt[e], 1);
+                for (int k2 = 0; k2 < k; ++k2)
+                    if (it[k2] == e) dup = 1;
+            } else {
+                atomicAdd(&bad, 1);
+            }
+        }
     }
     __syncthreads();
     if (tid < E) {
-        scan[tid] = cnt[tid];
-        tscan[tid] = (cnt[tid] + BM - 1) / BM;
-        ascan[tid] = cnt[tid] > 0 ? 1 : 0;
+        scn[tid] = cnt[tid];
+        tsc[tid] = (cnt[tid] + BM - 1) / BM;
+        asc[tid] = cnt[tid] > 0 ? 1 : 0;
     }
     __syncthreads();
-    block_exclusive_scan(scan, E, tid);
-    block_exclusive_scan(tscan, E, tid);
-    block_exclusive_scan(ascan, E, tid);
+    for (int off = 1; off < E; off <<= 1) {        // three inclusive scans at once
+        int a0 = 0, a1 = 0, a2 = 0;
+        if (tid < E && tid >= off) { a0 = scn[tid - off]; a1 = tsc[tid - off]; a2 = asc[tid - off]; }
+        __syncthreads();
+        if (tid < E) { scn[tid] += a0; tsc[tid] += a1; asc[tid] += a2; }
+        __syncthreads();
+    }
     if (tid < E) {
         const int c = cnt[tid];
-        const int off = scan[tid] - c;
+        const int off = scn[tid] - c;
         d.counts[tid] = c;
         d.offsets[tid] = off;
         run[tid] = off;
         const int nt = (c + BM - 1) / BM;
-        const int tb = tscan[tid] - nt;
+        const int tb = tsc[tid] - nt;
         for (int j = 0; j < nt; ++j) {
             d.tile_e[tb + j] = tid;
             d.tile_r0[tb + j] = j * BM;
         }
-        if (c > 0) d.active_e[ascan[tid] - 1] = tid;
+        if (c > 0) d.active_e[asc[tid] - 1] = tid;
         if (tid == E - 1) {
-            d.offsets[E] = scan[tid];
-            *d.n_tiles = tscan[tid];
-            *d.n_active = ascan[tid];
+            d.offsets[E] = scn[tid];
+            *d.n_tiles = tsc[tid];
+            *d.n_active = asc[tid];
             *d.bad_ids = bad;
         }
     }
     __syncthreads();
 
+    if (!dup) {
+        unsigned long long *bits = (unsigned long long *)rest;       // [E][wpc]
+        int *pref = (int *)(bits + (size_t)E * wpc);                  // [E][wpc]
+        const int64_t tc = (int64_t)wpc * 64;
+        for (int64_t c0 = 0; c0 < T; c0 += tc) {
+            for (int j = tid; j < E * wpc; j += DISPATCH_THREADS) bits[j] = 0ull;
+            __syncthreads();
+            const int64_t c1 = c0 + tc < T ? c0 + tc : T;
+            for (int64_t t = c0 + tid; t < c1; t += DISPATCH_THREADS) {
+                const int tl = (int)(t - c0);
+                for (int k = 0; k < K; ++k) {
+                    const int e = ids[t * K + k];
+                    if (e >= 0 && e < E) atomicOr(&bits[(size_t)e * wpc + (tl >> 6)], 1ull << (tl & 63));
+                }
+            }
+            __syncthreads();
+            for (int e = tid; e < E; e += DISPATCH_THREADS) {
+                int r = run[e];
+                for (int w = 0; w < wpc; ++w) {
+                    pref[e * wpc + w] = r;
+                    r += __popcll(bits[(size_t)e * wpc + w]);
+                }
+                run[e] = r;
+            }
+            __syncthreads();
+            for (int64_t t = c0 + tid; t < c1; t += DISPATCH_THREADS) {
+                const int tl = (int)(t - c0);
+                const unsigned long long below = (1ull << (tl & 63)) - 1ull;
+                for (int k = 0; k < K; ++k) {
+                    const int e = ids[t * K + k];
+                    if (e >= 0 && e < E) {
+                        const size_t wi = (size_t)e * wpc + (tl >> 6);
+                        d.perm[pref[wi] + __popcll(bits[wi] & below)] = (int32_t)(t * K + k);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        return;
+    }
+
+    // repeated ids inside a token: wave-level ranking by ballot over flat indices
+    int *wcnt = (int *)rest;                       // [16][E]
+    int *wbase = wcnt + DISPATCH_WAVES * E;        // [16][E]
     for (int64_t base = 0; base < n; base += DISPATCH_THREADS) {
         const int64_t i = base + tid;
         const int e = i < n ? ids[i] : -1;
@@ -370,8 +451,16 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
 
 int launch_dispatch(const int32_t *ids, int64_t T, int K, int E, int BM, const Dispatch &d, hipStream_t st) {
     if (E <= 0 || E > 256) return -6;
-    const size_t smem = sizeof(int) * ((size_t)E * 5 + 2 * (size_t)DISPATCH_WAVES * E);
-    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(DISPATCH_THREADS), smem, st, ids, T * K, E, BM, d);
+    const size_t head = ((size_t)5 * E * sizeof(int) + 15) & ~(size_t)15;
+    // bitset chunk: wpc 64-token words per expert, E * wpc * (8 + 4) bytes
+    int64_t wpc = (T + 63) / 64;
+    const int64_t wpc_max = (int64_t)((DISPATCH_LDS_BYTES - head) / ((size_t)E * 12));
+    if (wpc > wpc_max) wpc = wpc_max;
+    if (wpc < 1) wpc = 1;
+    const size_t bitset_bytes = (size_t)E * (size_t)wpc * 12;
+    const size_t ballot_bytes = (size_t)2 * DISPATCH_WAVES * E * sizeof(int);
+    const size_t smem = head + (bitset_bytes > ballot_bytes ? bitset_bytes : ballot_bytes);
+    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(DISPATCH_THREADS), smem, st, ids, T, K, E, BM, (int)wpc, d);
     return hip_check_launch();
 }
 

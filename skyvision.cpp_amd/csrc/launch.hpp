@@ -25,6 +25,9 @@ struct Q8Out {
     int16_t *bsums = nullptr;    // [rows][K/16]
     _Float16 *xh = nullptr;      // [rows][K] fp16(d*q) in MFMA K order of wtype (GEMM path)
     int wtype = 12;              // consumer weight type for xh order
+    int order = 0;               // 0: 16x16x32 K order, 1: 32x32x16 K order
+    int exact = 0;               // 1: xh holds the codes q (exact), d8 and xbs the scales / block sums
+    _Float16 *xbs = nullptr;     // [rows][K/16] block sums of 16 codes, as fp16 (exact)
 };
 // quantize rows of src (row r at src + r*ld floats) to Q8_K
 int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, const Q8Out &o, hipStream_t st);
@@ -112,5 +115,27 @@ struct GemmArgs {
 };
 constexpr int GEMM_BM = 64;
 int launch_gemm(const GemmArgs &g, hipStream_t st);
+
+// 32x32x16 MFMA grouped GEMM (k_gemm2.hip).  glu = 1: exact Q4_K x Q8_K
+// gate/up with GLU + Q8_K epilogue (xh = codes, xd = scales, xbs = block sums);
+// glu = 0: fp16 dequant x fp16(d*q) activations, fp32 rows out.
+struct G2Args {
+    ExpertMat a;
+    ExpertMat b;
+    int glu, fused, act;
+    int64_t I;
+    const _Float16 *xh;
+    const float *xd;
+    const _Float16 *xbs;
+    int ne11, K;
+    const int32_t *counts, *offsets, *perm, *tile_e, *tile_r0, *n_tiles;
+    int max_tiles;
+    float *y;
+    int64_t ldy;
+    _Float16 *acth;
+    int next_type;
+    int64_t ncols;
+};
+int launch_gemm2(const G2Args &g, hipStream_t st);
 
 }  // namespace mimoe

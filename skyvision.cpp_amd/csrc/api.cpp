@@ -266,7 +266,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         a.xh = c->ax.h; a.xd = c->ax.d8; a.xbs = c->ax.bsh; a.ne11 = 1; a.K = K;
         a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.tile_e = dg.tile_e;
         a.tile_r0 = dg.tile_r0; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
-        a.acth = c->aact.h; a.next_type = down.type; a.ncols = I;
+        a.acth = c->aact.h; a.next_type = down.type; a.ncols = I; a.xrows = T;
         TRY(launch_gemm2(a, st));
         stage_end(c, "gate_up", st);
         G2Args d = {};

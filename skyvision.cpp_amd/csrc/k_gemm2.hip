@@ -59,12 +59,25 @@ __device__ inline uint4 load16_a2_(const uint8_t *p) {
 // exact integer operand: nibbles of dword v -> (a0,a2,b0,b2,a1,a3,b1,b3) * sc,
 // a = low nibbles (sub-block lo), b = high nibbles (sub-block hi).
 // fma((1024 + a), sc, -1024 sc) = a * sc exactly (<= 945 is an fp16 integer).
-__device__ inline half8_t dq4_exact(uint32_t v, half2_t sc_lo, half2_t nc_lo, half2_t sc_hi, half2_t nc_hi) {
+// v_and_or_b32 (src0 & src1) | src2 in one instruction; the compiler splits
+// it in two when both constants are literals (gfx9 VOP3 takes no literal)
+__device__ __forceinline__ uint32_t and_or_(uint32_t v, uint32_t mask, uint32_t orv) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask), "v"(orv));
+    return r;
+}
+// 8 nibbles of one qs dword -> 8 exact fp16 values sc * q (pairs (n0,n4)
+// (n1,n5) (n2,n6) (n3,n7); low nibbles scaled by sc_lo, high by sc_hi):
+// 1024 + q via the 0x6400 exponent (64 + q via 0x5400 for bits 4-7), then
+// fma(1024 + q, sc, -1024 sc) = q * sc exactly (|q sc| < 2048).
+// m64 / m54 hold 0x64006400 / 0x54005400 in VGPRs.
+__device__ inline half8_t dq4_exact(uint32_t v, half2_t sc_lo, half2_t nc_lo, half2_t sc_hi, half2_t nc_hi,
+                                    uint32_t m64, uint32_t m54) {
     const uint32_t v8 = v >> 8;
-    const half2_t t0 = u2h2_((v & 0x000F000Fu) | 0x64006400u);
-    const half2_t t1 = u2h2_((v & 0x00F000F0u) | 0x54005400u);
-    const half2_t t2 = u2h2_((v8 & 0x000F000Fu) | 0x64006400u);
-    const half2_t t3 = u2h2_((v8 & 0x00F000F0u) | 0x54005400u);
+    const half2_t t0 = u2h2_(and_or_(v, 0x000F000Fu, m64));
+    const half2_t t1 = u2h2_(and_or_(v, 0x00F000F0u, m54));
+    const half2_t t2 = u2h2_(and_or_(v8, 0x000F000Fu, m64));
+    const half2_t t3 = u2h2_(and_or_(v8, 0x00F000F0u, m54));
     const u32x4 r = {h22u_(__builtin_elementwise_fma(t0, sc_lo, nc_lo)), h22u_(__builtin_elementwise_fma(t1, sc_hi, nc_hi)),
                      h22u_(__builtin_elementwise_fma(t2, sc_lo, nc_lo)), h22u_(__builtin_elementwise_fma(t3, sc_hi, nc_hi))};
     return __builtin_bit_cast(half8_t, r);
@@ -126,75 +139,135 @@ __device__ inline void tile_coords(int max_tiles, int &mt, int &nt) {
 // 256-column tile: col tile 0 holds their h (gate) rows, col tile 1 their g
 // (up) rows; each wave covers all 64 token rows (row tiles 0, 1).
 //
-// Operands reach LDS by direct global -> LDS loads (no staging registers):
-// one load instruction writes 1 KB of LDS, lane i the 16 bytes at +16i.
-//  * activation codes: rows of 256 fp16 padded to 264 (528 B), so an MFMA
-//    operand read of 32 rows at one K chunk touches 32 distinct bank groups
-//    and its address is the lane's row base plus a constant.  The 64 padded
-//    rows are 33 KB = 33 load instructions; slot q = 64*k + lane of load k
-//    holds row q / 33, chunk q % 33 (chunk 32 is the pad: it reloads chunk 0).
-//  * block sums (64 rows x 32 B, 2 loads), row scales (64 x 4 B, 1 load) and
-//    each wave's 64 weight-row headers (64 x 16 B, 1 load per wave).
-// Weight nibbles stay in registers (rolling prefetch of the next block).
+// Every operand reaches LDS by MUBUF loads that write LDS directly (lane i
+// of a load writes the 16 bytes at +16i of a 1 KB span); no global load
+// targets a register inside the K loop.
+//  * activation codes (two stages): rows of 256 fp16 padded to 264 (528 B),
+//    so an MFMA operand read of 32 rows at one K chunk touches 32 distinct
+//    bank groups at the lane's row base plus a constant.  The 64 padded rows
+//    are 33 KB = 33 loads; slot q = 64*k + lane of load k holds row q / 33,
+//    chunk q % 33 (chunk 32 is the pad: it reloads chunk 0).  Block sums
+//    (64 rows x 32 B) and row scales (64 x 4 B) ride in the same stage.
+//  * weights (one stage per wave): the wave's 32 h rows and 32 g rows, each
+//    row's whole 144-byte block (header + qs) at a 144-byte stride (a read
+//    of 32 rows at one chunk is bank-conflict free), 32 rows = 4.5 KB padded
+//    to 5 loads.  Rows are whole lines in global memory, so the loads are
+//    coalesced.  The wave reads its block into registers right after the
+//    block's barrier and only then loads the next block over it.
 constexpr int G2G_WAVES = 8;
 constexpr int G2G_THREADS = G2G_WAVES * 64;
 constexpr int G2G_LDA = QK + 8;                       // padded row (halfs)
 constexpr int G2G_ALOADS = G2_BM * (QK / 8 + 1) / 64; // 33
+constexpr int G2G_LDV = QK + 4;                       // fp32 GLU row in the epilogue
+constexpr int G2G_WGRP = 5 * 1024;                    // 32 rows x 144 B, padded
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// one stage of the double buffer; the two stages are separate LDS variables
-// so the compiler can tell the loads into one from the reads of the other
+// one stage of the activation double buffer; the two stages are separate
+// LDS variables so the compiler can tell the loads into one from the reads
+// of the other
 struct G2GBuf {
     _Float16 As[G2_BM * G2G_LDA];        // 33 KB activation codes
-    uint4 Hs[G2G_WAVES][64];             // 8 KB weight block headers
     _Float16 Bs[G2_BM * 16];             // 2 KB block sums of 16 codes
     float Dx[G2_BM];                     // row scales
 };
 
 struct G2GLane {
     int wave, lane, l32, g2;
-    uint32_t aoff[5], bsoff, dxoff;
-    const uint8_t *rowp[2];
-    const uint8_t *hrow;
+    __amdgpu_buffer_rsrc_t rx, rbs, rd, rw[2];   // xh, xbs, xd, weight matrices of col tiles 0 / 1
+    uint32_t kin2;                               // activation row bytes
+    uint32_t nb;                                 // K blocks
+    uint32_t w0;                                 // byte offset of the wave's first weight row
+    uint32_t rowb;                               // weight row bytes
+    uint32_t wct;                                // col tile 1 offset when it shares col tile 0's matrix
+    const int *arow;                             // LDS: activation row of each tile row
 };
 
-// issue the direct loads of block b into stage st
-__device__ __forceinline__ void g2g_issue(const G2Args &g, const G2GLane &L, int b, G2GBuf &st) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        __builtin_amdgcn_global_load_lds(g.xh + (uint32_t)(b * QK) + L.aoff[j],
-                                         (lds_void_t *)&st.As[(L.wave + 8 * j) * 512], 16, 0, 0);
-    if (L.wave == 0)
-        __builtin_amdgcn_global_load_lds(g.xh + (uint32_t)(b * QK) + L.aoff[4], (lds_void_t *)&st.As[32 * 512], 16,
-                                         0, 0);
-    __builtin_amdgcn_global_load_lds(L.hrow + (int64_t)b * Q4K_BYTES, (lds_void_t *)&st.Hs[L.wave][0], 16, 0, 0);
-    if (L.wave < 2)
-        __builtin_amdgcn_global_load_lds(g.xbs + (uint32_t)(b * 16) + L.bsoff, (lds_void_t *)&st.Bs[L.wave * 512],
-                                         16, 0, 0);
-    else if (L.wave == 2)
-        __builtin_amdgcn_global_load_lds(g.xd + (uint32_t)b + L.dxoff, (lds_void_t *)&st.Dx[0], 4, 0, 0);
+// buffer resource of a raw byte range (bounds-checked: reads past nbytes return 0)
+__device__ inline __amdgpu_buffer_rsrc_t g2_rsrc(const void *p, int64_t nbytes) {
+    const int n = nbytes > 0x7fffffff ? 0x7fffffff : (int)nbytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, n, 0x00020000);
 }
 
-// one K block: wait for stage cur, start the loads of block b+1 into nxt,
-// accumulate block b.  vmc: the vmcnt that guarantees this wave's loads of
-// block b landed (0 for the first block; afterwards 8 = the weight loads
-// issued after them).
-template <int VMC>
+// loads of block b: activation stage st (5 loads per wave, the 33rd issued
+// by every wave with identical bytes; waves 0-1 block sums, wave 2 row
+// scales) and the wave's weight region W (10 loads).  The per-lane offsets
+// are recomputed here each block from the lane index and the tile's row
+// table (a dozen registers less across the K loop); the opaque copy of the
+// lane index keeps the compiler from hoisting them back out of the loop.
+__device__ __forceinline__ void g2g_issue(const G2GLane &L, int b, G2GBuf &st, uint8_t *W) {
+    int lane;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(lane) : "v"(L.lane));
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+        // slot q = 64k + lane of the padded activation tile: row q / 33, chunk q % 33
+        const int k = j < 4 ? L.wave + 8 * j : G2G_ALOADS - 1;
+        const int q = 64 * k + lane;
+        const int row = q / 33, ch = q % 33;
+        const uint32_t aoff = (uint32_t)L.arow[row] * L.kin2 + 16u * (uint32_t)(ch == 32 ? 0 : ch);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rx, (lds_void_t *)&st.As[k * 512], 16, aoff, b * (QK * 2), 0, 0);
+    }
+    if (L.wave < 2) {
+        const uint32_t bsoff = (uint32_t)L.arow[32 * L.wave + (lane >> 1)] * (L.nb * 32u) + 16u * (lane & 1);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rbs, (lds_void_t *)&st.Bs[L.wave * 512], 16, bsoff, b * 32, 0, 0);
+    } else if (L.wave == 2) {
+        const uint32_t dxoff = (uint32_t)L.arow[lane] * (L.nb * 4u);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rd, (lds_void_t *)&st.Dx[0], 4, dxoff, b * 4, 0, 0);
+    }
+    // weight load j of col tile ct: slot 64j + lane of the 32-row group =
+    // row slot / 9, 16-byte chunk slot % 9 (slots past 32 rows x 9 chunks
+    // reload the last chunk: identical bytes into the padding)
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+        const int slot = imin(64 * j + lane, 32 * 9 - 1);
+        const int r = slot / 9, c = slot - 9 * r;
+        const uint32_t woff = L.w0 + (uint32_t)r * L.rowb + 16u * (uint32_t)c;
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rw[ct], (lds_void_t *)(W + ct * G2G_WGRP + j * 1024), 16,
+                                                     woff + ct * L.wct, b * Q4K_BYTES, 0, 0);
+    }
+}
+
+// one K block: wait for every load of block b, read this wave's weights
+// into registers, start the loads of block b+1 (weights over the region just
+// read, activations into stage nxt), accumulate block b
 __device__ __forceinline__ void g2g_block(const G2Args &g, const G2GLane &L, int b, int nb, G2GBuf &cur,
-                                          G2GBuf &nxt, uint4 (&qv)[2][4], float16_t (&acc)[2][2]) {
-    const bool more = b + 1 < nb;
-    const int bn = more ? b + 1 : b;
-    const int l32 = L.l32, g2 = L.g2, wave = L.wave;
-    __builtin_amdgcn_s_waitcnt(0x0F70 | VMC);
-    __syncthreads();
-    if (more) g2g_issue(g, L, b + 1, nxt);
+                                          G2GBuf &nxt, uint8_t *W, float16_t (&acc)[2][2]) {
+    const int l32 = L.l32, g2 = L.g2;
+    // all of this wave's loads have landed (vmcnt(0)); after the barrier,
+    // every wave's have.  A raw barrier: the asm memory clobber keeps the
+    // compiler from moving LDS accesses across it.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    asm volatile("s_barrier" ::: "memory");
+    // weights of block b: header (chunk 0) and the lane's 64 qs bytes
+    // (chunks 1 + 4*g2 .. 4 + 4*g2) of row (ct, l32)
+    u32x4 hvs[2], qv[2][4];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+        const u32x4 *rw = (const u32x4 *)(W + ct * G2G_WGRP + l32 * Q4K_BYTES);
+        hvs[ct] = rw[0];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) qv[ct][q] = rw[1 + 4 * g2 + q];
+    }
+    // the weight loads of block b+1 overwrite the region: wait for the reads
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    __builtin_amdgcn_sched_barrier(0);
+    if (b + 1 < nb) g2g_issue(L, b + 1, nxt, W);
     __builtin_amdgcn_sched_barrier(0);
     // ---- per-block constants from the headers
     half2_t sc_lo[2][2], nc_lo[2][2], sc_hi[2][2], nc_hi[2][2];
+    half8_t mins[2];
     float dw[2], dmw[2];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
-        const uint4 hv = cur.Hs[wave][32 * ct + l32];
+        const u32x4 hv = hvs[ct];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int sc_, m_;
+            scale_min_k4_reg(4 * g2 + j, hv.y, hv.z, hv.w, sc_, m_);
+            mins[ct][2 * j] = (_Float16)(float)m_;
+            mins[ct][2 * j + 1] = (_Float16)(float)m_;
+        }
         dw[ct] = h2f((uint16_t)(hv.x & 0xffff));
         dmw[ct] = h2f((uint16_t)(hv.x >> 16));
 #pragma unroll
@@ -217,6 +290,7 @@ __device__ __forceinline__ void g2g_block(const G2Args &g, const G2GLane &L, int
 #pragma unroll
             for (int i = 0; i < 16; ++i) P[rt][ct][i] = 0.f;
     const _Float16 *Ab = &cur.As[l32 * G2G_LDA + 8 * g2];
+    const uint32_t m64 = 0x64006400u, m54 = 0x54005400u;
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
         const half8_t A0 = *(const half8_t *)(Ab + 16 * s);
@@ -224,41 +298,24 @@ __device__ __forceinline__ void g2g_block(const G2Args &g, const G2GLane &L, int
         const int hf = s >> 3;
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
-            const half8_t B = dq4_exact(dword_of(qv[ct][s >> 2], s & 3), sc_lo[ct][hf], nc_lo[ct][hf],
-                                        sc_hi[ct][hf], nc_hi[ct][hf]);
+            const half8_t B = dq4_exact(qv[ct][s >> 2][s & 3], sc_lo[ct][hf], nc_lo[ct][hf], sc_hi[ct][hf],
+                                        nc_hi[ct][hf], m64, m54);
             P[0][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B, P[0][ct], 0, 0, 0);
             P[1][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B, P[1][ct], 0, 0, 0);
-        }
-        if ((s & 3) == 3) {   // refill this chunk with the next block's (the last block reloads itself)
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct)
-                qv[ct][s >> 2] = *(const uint4 *)(L.rowp[ct] + (int64_t)bn * Q4K_BYTES + 16 + 64 * g2 + 16 * (s >> 2));
-            __builtin_amdgcn_sched_barrier(0);
         }
     }
     // ---- min term Q = sum_j m_j * bsum16_j (one MFMA per tile), then
     // acc += dx * (dw * P - dmin * Q); row scales of rows 32rt + 8a + 4g2 + {0..3}
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
-        const uint4 hv = cur.Hs[wave][32 * ct + l32];
-        half8_t mins;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            int sc_, m_;
-            scale_min_k4_reg(4 * g2 + j, hv.y, hv.z, hv.w, sc_, m_);
-            mins[2 * j] = (_Float16)(float)m_;
-            mins[2 * j + 1] = (_Float16)(float)m_;
-        }
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
             const half8_t Abs = *(const half8_t *)(&cur.Bs[(32 * rt + l32) * 16 + 8 * g2]);
             float16_t q = {};
-            q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Abs, mins, q, 0, 0, 0);
+            q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Abs, mins[ct], q, 0, 0, 0);
 #pragma unroll
             for (int a = 0; a < 4; ++a) {
-                const float4 dx4 = *(const float4 *)(&cur.Dx[32 * rt + 8 * a + 4 * g2]);
-                const float dxv[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+                const float4_t dxv = *(const float4_t *)(&cur.Dx[32 * rt + 8 * a + 4 * g2]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float t = fmaf(-dmw[ct], q[4 * a + i], dw[ct] * P[rt][ct][4 * a + i]);
@@ -269,20 +326,29 @@ __device__ __forceinline__ void g2g_block(const G2Args &g, const G2GLane &L, int
     }
 }
 
+template <int ACT>
+__device__ __forceinline__ void g2g_glu_rows(const float16_t (&acc)[2][2], float *V0, float *V1, int col, int g2) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = (8 * (i >> 2) + 4 * g2 + (i & 3)) * G2G_LDV + col;
+        V0[r] = act_pair_fast<ACT>(acc[0][0][i], acc[0][1][i]);
+        V1[r] = act_pair_fast<ACT>(acc[1][0][i], acc[1][1][i]);
+    }
+}
+
 template <int NEXT>
 __global__ void __launch_bounds__(G2G_THREADS) k_g2_glu(G2Args g) {
     __shared__ __attribute__((aligned(1024))) G2GBuf st0;
     __shared__ __attribute__((aligned(1024))) G2GBuf st1;
+    __shared__ __attribute__((aligned(1024))) uint8_t s_w[G2G_WAVES][2 * G2G_WGRP];
     __shared__ int s_p[G2_BM], s_arow[G2_BM];
-    __shared__ AmaxIdx s_red[G2_BM][G2G_WAVES];
-    __shared__ float s_is[G2_BM], s_d[G2_BM];
     const int nx = (int)(g.I / QK);
     int tile, ctile;
     tile_coords(g.max_tiles, tile, ctile);
     if (tile >= *g.n_tiles || ctile >= nx) return;
     G2GLane L;
     const int tid = threadIdx.x;
-    L.wave = tid >> 6;
+    L.wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar branches
     L.lane = tid & 63;
     L.l32 = L.lane & 31;
     L.g2 = L.lane >> 5;
@@ -298,32 +364,30 @@ __global__ void __launch_bounds__(G2G_THREADS) k_g2_glu(G2Args g) {
         s_p[tid] = p;
         s_arow[tid] = p < 0 ? 0 : p / g.K;
     }
-    // weight rows of this lane: col tile 0 = h row n, col tile 1 = g row
-    const int64_t n = (int64_t)ctile * QK + 32 * wave + l32;
-    L.rowp[0] = g.a.data + (int64_t)e * g.a.mat_bytes + n * g.a.row_bytes;
-    if (g.fused) L.rowp[1] = g.a.data + (int64_t)e * g.a.mat_bytes + (g.I + n) * g.a.row_bytes;
-    else L.rowp[1] = g.b.data + (int64_t)e * g.b.mat_bytes + n * g.b.row_bytes;
-    L.hrow = L.rowp[g2];   // the wave's header load: lane = 32*ct + l32
     __syncthreads();
-    // per-lane source offsets (halfs, block 0) of this wave's activation
-    // loads k = wave + 8j (j < 4; wave 0 also k = 32)
-#pragma unroll
-    for (int j = 0; j < 5; ++j) {
-        const int k = wave + 8 * j;
-        const int q = 64 * imin(k, G2G_ALOADS - 1) + lane;
-        const int row = q / 33, ch = q % 33;
-        L.aoff[j] = (uint32_t)s_arow[row] * Kin + 8u * (uint32_t)(ch == 32 ? 0 : ch);
+    L.kin2 = 2u * Kin;
+    L.nb = (uint32_t)nb;
+    L.arow = s_arow;
+    L.rx = g2_rsrc(g.xh, g.xrows * (int64_t)Kin * 2);
+    L.rbs = g2_rsrc(g.xbs, g.xrows * (int64_t)nb * 32);
+    L.rd = g2_rsrc(g.xd, g.xrows * (int64_t)nb * 4);
+    // weight rows of the wave: h rows n0 + r (col tile 0), g rows I + n0 + r
+    // of the fused matrix or up rows n0 + r (col tile 1), n0 = 256 ctile + 32 wave
+    {
+        const int64_t n0 = (int64_t)ctile * QK + 32 * wave;
+        L.rowb = (uint32_t)g.a.row_bytes;
+        L.w0 = (uint32_t)(n0 * g.a.row_bytes);
+        L.rw[0] = g2_rsrc(g.a.data + (int64_t)e * g.a.mat_bytes, g.a.mat_bytes);
+        if (g.fused) {
+            L.rw[1] = L.rw[0];
+            L.wct = (uint32_t)(g.I * g.a.row_bytes);
+        } else {
+            L.rw[1] = g2_rsrc(g.b.data + (int64_t)e * g.b.mat_bytes, g.b.mat_bytes);
+            L.wct = 0;
+        }
     }
-    L.bsoff = (uint32_t)s_arow[32 * (wave & 1) + (lane >> 1)] * (uint32_t)(nb * 16) + 8u * (lane & 1);
-    L.dxoff = (uint32_t)s_arow[lane] * (uint32_t)nb;
-
-    // weight nibbles: this lane's 64 bytes (chunks 2*g2, 2*g2+1) of each col tile
-    uint4 qv[2][4];
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) qv[ct][q] = *(const uint4 *)(L.rowp[ct] + 16 + 64 * g2 + 16 * q);
-    g2g_issue(g, L, 0, st0);
+    uint8_t *W = &s_w[wave][0];
+    g2g_issue(L, 0, st0, W);
 
     float16_t acc[2][2];
 #pragma unroll
@@ -333,61 +397,71 @@ __global__ void __launch_bounds__(G2G_THREADS) k_g2_glu(G2Args g) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[rt][ct][i] = 0.f;
 
-    g2g_block<0>(g, L, 0, nb, st0, st1, qv, acc);
-    for (int b = 1; b < nb; b += 2) {
-        g2g_block<8>(g, L, b, nb, st1, st0, qv, acc);
-        if (b + 1 < nb) g2g_block<8>(g, L, b + 1, nb, st0, st1, qv, acc);
+    for (int b = 0; b < nb; b += 2) {
+        g2g_block(g, L, b, nb, st0, st1, W, acc);
+        if (b + 1 < nb) g2g_block(g, L, b + 1, nb, st1, st0, W, acc);
     }
 
-    // ---- GLU + Q8_K of each row's 256 columns (first column with the largest |v|)
-    float v[2][16];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) v[rt][i] = act_pair(g.act, acc[rt][0][i], acc[rt][1][i]);
-    const int col = 32 * wave + l32;
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            AmaxIdx a{fabsf(v[rt][i]), col, v[rt][i]};
-            a = wave_amax_idx(a, 32);
-            if (l32 == 0) s_red[32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3)][wave] = a;
-        }
+    // ---- GLU values to LDS as fp32 rows of 256 (+4 pad): rows 0-31 in
+    // stage 0, rows 32-63 in stage 1 (all reads of the stages are done)
     __syncthreads();
-    if (tid < G2_BM) {
-        AmaxIdx a = s_red[tid][0];
-#pragma unroll
-        for (int w = 1; w < G2G_WAVES; ++w) a = amax_better(a, s_red[tid][w]);
-        if (a.ax != 0.f) {
-            const float iscale = -127.f / a.val;
-            s_is[tid] = iscale;
-            s_d[tid] = 1 / iscale;
-        } else {
-            s_is[tid] = 0.f;
-            s_d[tid] = 0.f;
+    {
+        const int col = 32 * wave + l32;
+        float *V0 = (float *)st0.As, *V1 = (float *)st1.As;
+        switch (g.act) {
+        case 0: g2g_glu_rows<0>(acc, V0, V1, col, g2); break;
+        case 1: g2g_glu_rows<1>(acc, V0, V1, col, g2); break;
+        case 2: g2g_glu_rows<2>(acc, V0, V1, col, g2); break;
+        default: g2g_glu_rows<3>(acc, V0, V1, col, g2); break;
         }
     }
     __syncthreads();
-    // quantized act tile (rows of 256 in the down weight's K order) into As[0]
-    const int pos = mfma32_pos(NEXT, col);
+    // ---- Q8_K of each row (first column with the largest |v| sets the
+    // scale), written as fp16(d * q) in the down weight's K order: thread
+    // (row, t) owns K positions 32t .. 32t+31, which hold the row elements
+    // base_t + f(j) (the two orders are affine in t)
+    const int row = tid >> 3, t = tid & 7;
+    const float *Vr = (row < 32 ? (const float *)st0.As : (const float *)st1.As) + (row & 31) * G2G_LDV;
+    const int base = NEXT == 14 ? 4 * t : 64 * (t >> 2) + 8 * (t & 3);
+    float x[32];
+    AmaxIdx best{-1.f, 0, 0.f};
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
-            const float is = s_is[m], d = s_d[m];
-            const int q = d != 0.f ? imin(127, nearest_int(is * v[rt][i])) : 0;
-            st0.As[m * G2G_LDA + pos] = (_Float16)(d * (float)q);
+    for (int j = 0; j < 32; ++j) {
+        int f;
+        if (NEXT == 14) {
+            f = 128 * ((j >> 3) & 1) + 64 * (j >> 4) + 32 * ((j & 7) >> 2) + (j & 3);
+        } else {
+            constexpr int off4[8] = {0, 2, 32, 34, 1, 3, 33, 35};
+            f = 128 * ((j >> 3) & 1) + 4 * (j >> 4) + off4[j & 7];
         }
-    __syncthreads();
+        x[j] = Vr[base + f];
+        best = amax_better(best, AmaxIdx{fabsf(x[j]), base + f, x[j]});
+    }
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int idx = tid + G2G_THREADS * it;
-        const int r = idx >> 5, c16 = idx & 31;
-        if (r < mrows)
-            *(uint4 *)(g.acth + (int64_t)s_p[r] * g.I + (int64_t)ctile * QK + c16 * 8) =
-                *(const uint4 *)(&st0.As[r * G2G_LDA + c16 * 8]);
+    for (int o = 1; o < 8; o <<= 1) {
+        AmaxIdx b;
+        b.ax = __shfl_xor(best.ax, o, 64);
+        b.idx = __shfl_xor(best.idx, o, 64);
+        b.val = __shfl_xor(best.val, o, 64);
+        best = amax_better(best, b);
+    }
+    float is = 0.f, d = 0.f;
+    if (best.ax != 0.f) {
+        is = -127.f / best.val;
+        d = 1 / is;
+    }
+    if (row < mrows) {
+        u32x4 o[4];
+#pragma unroll
+        for (int j = 0; j < 32; j += 2) {
+            const int q0 = d != 0.f ? imin(127, nearest_int(is * x[j])) : 0;
+            const int q1 = d != 0.f ? imin(127, nearest_int(is * x[j + 1])) : 0;
+            const half2_t h = {(_Float16)(d * (float)q0), (_Float16)(d * (float)q1)};
+            o[j >> 3][(j >> 1) & 3] = h22u_(h);
+        }
+        u32x4 *dst = (u32x4 *)(g.acth + (int64_t)s_p[row] * g.I + (int64_t)ctile * QK + 32 * t);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) dst[k] = o[k];
     }
 }
 
@@ -593,6 +667,12 @@ int launch_gemm2(const G2Args &g, hipStream_t st) {
     if (g.a.K % QK) return -6;
     if (g.glu) {
         if (g.a.type != 12 || (g.I % QK)) return -6;
+        // byte offsets of the buffer loads are 32-bit
+        const int64_t lim = 0x7fffffff;
+        if (g.xrows <= 0 || g.xrows * g.a.K * 2 > lim || g.a.mat_bytes > lim || (!g.fused && g.b.mat_bytes > lim))
+            return -6;
+        // the weight loads use one row stride for both col tiles
+        if (!g.fused && g.b.row_bytes != g.a.row_bytes) return -6;
         const int nx = (int)(g.I / QK);
         const dim3 grid((unsigned)((nx * g.max_tiles + 7) / 8 * 8));
         if (g.next_type == 14) hipLaunchKernelGGL(k_g2_glu<14>, grid, dim3(G2G_THREADS), 0, st, g);

@@ -130,6 +130,7 @@ struct G2Args {
     int ne11, K;
     const int32_t *counts, *offsets, *perm, *tile_e, *tile_r0, *n_tiles;
     int max_tiles;
+    int64_t xrows;        // rows of xh / xd / xbs (glu = 1: tokens)
     float *y;
     int64_t ldy;
     _Float16 *acth;

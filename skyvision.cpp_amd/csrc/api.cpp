@@ -272,7 +272,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         G2Args d = {};
         d.a = down; d.glu = 0; d.xh = c->aact.h; d.ne11 = K; d.K = K;
         d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
-        d.tile_r0 = dd.tile_r0; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles;
+        d.tile_r0 = dd.tile_r0; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles; d.xrows = (int64_t)T * K;
         d.y = c->z; d.ldy = D; d.ncols = D;
         TRY(launch_gemm2(d, st));
         stage_end(c, "down", st);
@@ -595,7 +595,7 @@ int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const 
     G2Args a = {};
     a.a = M; a.glu = 0; a.xh = c->ax.h; a.ne11 = (int)ne11; a.K = (int)n_used;
     a.counts = dsp.counts; a.offsets = dsp.offsets; a.perm = dsp.perm; a.tile_e = dsp.tile_e;
-    a.tile_r0 = dsp.tile_r0; a.n_tiles = dsp.n_tiles; a.max_tiles = max_tiles;
+    a.tile_r0 = dsp.tile_r0; a.n_tiles = dsp.n_tiles; a.max_tiles = max_tiles; a.xrows = T * ne11;
     a.y = (float *)dst->data; a.ldy = N; a.ncols = N;
     return launch_gemm2(a, st);
 }

@@ -466,200 +466,244 @@ __global__ void __launch_bounds__(G2G_THREADS) k_g2_glu(G2Args g) {
 }
 
 // ------------------------------------------------------------------ STORE
-// Q4_K: qs of chunks 2g2, 2g2+1 (4 x 16 B) + header.  Q6_K: half g2 of ql
-// (2 x 32 B), qh (32 B), scales[8g2 .. 8g2+8) and d packed into h.
+// fp32 rows out: y[p][n] = sum_k x[p][k] w[n][k] for the dispatched rows p of
+// one expert.  8 waves; the work-group tile is 64 rows x 256 weight rows,
+// wave w owns weight rows 32w .. 32w+31 (one 32-wide col tile) for both
+// 32-row row tiles.  Weights and activations are dequantized to fp16 (the
+// activations arrive as fp16(d * q) in this weight type's K order).
+//
+// Staging as in the GLU kernel: MUBUF loads that write LDS.  Activations:
+// two stages of 64 rows padded to 264 halfs.  Weights: one region per wave,
+// the 32 rows' block b each covered by the 16-byte aligned chunks holding
+// it (Q4_K: 9 chunks, 16-byte aligned; Q6_K: a 210-byte block starts at any
+// even byte of a chunk, 14 chunks cover it, plus one pad chunk so the row
+// stride (240 B) spreads the LDS banks).  Each lane re-aligns its half of
+// the block with v_alignbyte after dword-aligned reads.
+constexpr int G3_NCOL = 256;
+
+template <int WT> struct G3Fmt;
+template <> struct G3Fmt<12> {
+    static constexpr int BB = Q4K_BYTES;   // block bytes
+    static constexpr int NC = 9;           // 16-byte chunks per staged row
+    static constexpr int NLD = 5;          // loads of 1 KB per wave (32 rows x NC chunks)
+};
+template <> struct G3Fmt<14> {
+    static constexpr int BB = Q6K_BYTES;
+    static constexpr int NC = 15;
+    static constexpr int NLD = 8;
+};
+
+struct G3Buf {
+    _Float16 As[G2_BM * G2G_LDA];
+};
+
+struct G3Lane {
+    int wave, lane, l32, g2;
+    __amdgpu_buffer_rsrc_t rx, rw;
+    uint32_t kin2;       // activation row bytes
+    uint32_t mis;        // expert matrix base address & 15
+    int n0, nlast;       // first weight row of the wave, last row of the matrix
+    uint32_t rowb;
+    const int *arow;
+};
+
+// byte offset of block b of the wave's weight row r (rows past the matrix
+// re-read its last row: their outputs are never stored)
+__device__ inline uint32_t g3_wstart(const G3Lane &L, int r, int b, int bb) {
+    return L.mis + (uint32_t)imin(L.n0 + r, L.nlast) * L.rowb + (uint32_t)(b * bb);
+}
+
+// loads of block b: activation stage st (5 per wave, the 33rd issued by every
+// wave with identical bytes) and the wave's weight region W (NLD per wave).
+// Offsets are recomputed per block from an opaque copy of the lane index.
 template <int WT>
-__device__ __forceinline__ void g2_load_w(const uint8_t *rowp, int b, int g2, uint4 *q, uint4 &h) {
-    if constexpr (WT == 12) {
-        const uint8_t *blk = rowp + (int64_t)b * Q4K_BYTES;
-        h = *(const uint4 *)blk;
+__device__ __forceinline__ void g3_issue(const G3Lane &L, int b, G3Buf &st, uint8_t *W) {
+    using F = G3Fmt<WT>;
+    int lane;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(lane) : "v"(L.lane));
 #pragma unroll
-        for (int k = 0; k < 4; ++k) q[k] = *(const uint4 *)(blk + 16 + 64 * g2 + 16 * k);
+    for (int j = 0; j < 5; ++j) {
+        const int k = j < 4 ? L.wave + 8 * j : G2G_ALOADS - 1;
+        const int q = 64 * k + lane;
+        const int row = q / 33, ch = q % 33;
+        const uint32_t aoff = (uint32_t)L.arow[row] * L.kin2 + 16u * (uint32_t)(ch == 32 ? 0 : ch);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rx, (lds_void_t *)&st.As[k * 512], 16, aoff, b * (QK * 2), 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < F::NLD; ++j) {
+        const int slot = imin(64 * j + lane, 32 * F::NC - 1);
+        const int r = slot / F::NC, c = slot - F::NC * r;
+        const uint32_t start = g3_wstart(L, r, b, F::BB);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rw, (lds_void_t *)(W + j * 1024), 16, (start & ~15u) + 16u * c, 0,
+                                                 0, 0);
+    }
+}
+
+// the lane's operand bytes of block b from its staged row (row l32):
+//   Q4_K: q[0..15] = qs chunks 2g2, 2g2+1, hd = header (d, dmin, scales)
+//   Q6_K: q[0..15] = ql half g2, q[16..23] = qh half g2,
+//         hd.x/.y = scales[8g2 .. 8g2+8), hd.z = d (fp16 bits)
+template <int WT>
+__device__ __forceinline__ void g3_read_w(const G3Lane &L, int b, const uint8_t *W, uint32_t (&q)[24], u32x4 &hd) {
+    using F = G3Fmt<WT>;
+    const uint8_t *row = W + L.l32 * (16 * F::NC);
+    if constexpr (WT == 12) {
+        hd = *(const u32x4 *)row;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const u32x4 v = *(const u32x4 *)(row + 16 + 64 * L.g2 + 16 * k);
+            q[4 * k] = v.x; q[4 * k + 1] = v.y; q[4 * k + 2] = v.z; q[4 * k + 3] = v.w;
+        }
     } else {
-        const uint8_t *blk = rowp + (int64_t)b * Q6K_BYTES;
-        q[0] = load16_a2_(blk + 64 * g2);
-        q[1] = load16_a2_(blk + 64 * g2 + 16);
-        q[2] = load16_a2_(blk + 64 * g2 + 32);
-        q[3] = load16_a2_(blk + 64 * g2 + 48);
-        q[4] = load16_a2_(blk + 128 + 32 * g2);
-        q[5] = load16_a2_(blk + 128 + 32 * g2 + 16);
-        const uint4 s16 = load16_a2_(blk + 192);
-        const uint8_t *pd = blk + 208;
-        h.x = g2 ? s16.z : s16.x;
-        h.y = g2 ? s16.w : s16.y;
-        h.z = (uint32_t)pd[0] | ((uint32_t)pd[1] << 8);
-        h.w = 0u;
+        // the block starts at byte s0 (even) of the staged row: dword reads
+        // from s0 & ~3, then a 0- or 2-byte shift
+        const uint32_t s0 = g3_wstart(L, L.l32, b, F::BB) & 15u;
+        const uint32_t sh = s0 & 3u;
+        const uint32_t *rw = (const uint32_t *)(row + (s0 & ~3u));
+        uint32_t t[17];
+#pragma unroll
+        for (int k = 0; k < 17; ++k) t[k] = rw[16 * L.g2 + k];            // ql: bytes 64 g2 ..
+#pragma unroll
+        for (int k = 0; k < 16; ++k) q[k] = __builtin_amdgcn_alignbyte(t[k + 1], t[k], sh);
+#pragma unroll
+        for (int k = 0; k < 9; ++k) t[k] = rw[32 + 8 * L.g2 + k];         // qh: bytes 128 + 32 g2 ..
+#pragma unroll
+        for (int k = 0; k < 8; ++k) q[16 + k] = __builtin_amdgcn_alignbyte(t[k + 1], t[k], sh);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) t[k] = rw[48 + 2 * L.g2 + k];         // scales: bytes 192 + 8 g2 ..
+        hd.x = __builtin_amdgcn_alignbyte(t[1], t[0], sh);
+        hd.y = __builtin_amdgcn_alignbyte(t[2], t[1], sh);
+        hd.z = __builtin_amdgcn_alignbyte(rw[53], rw[52], sh) & 0xffffu;   // d: bytes 208, 209
+        hd.w = 0u;
+    }
+}
+
+// one K block: wait for its loads, read the lane's weights, start the loads
+// of block b+1, accumulate block b
+template <int WT>
+__device__ __forceinline__ void g3_block(const G3Lane &L, int b, int nb, G3Buf &cur, G3Buf &nxt, uint8_t *W,
+                                         float16_t (&acc)[2]) {
+    const int l32 = L.l32, g2 = L.g2;
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    uint32_t q[24];
+    u32x4 hd;
+    g3_read_w<WT>(L, b, W, q, hd);
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the next weight loads overwrite the region
+    __builtin_amdgcn_sched_barrier(0);
+    if (b + 1 < nb) g3_issue<WT>(L, b + 1, nxt, W);
+    __builtin_amdgcn_sched_barrier(0);
+    const _Float16 *Ab = &cur.As[l32 * G2G_LDA + 8 * g2];
+    if constexpr (WT == 12) {
+        half2_t s_lo[2], nm_lo[2], s_hi[2], nm_hi[2];
+        const float d = h2f((uint16_t)(hd.x & 0xffff)), dmin = h2f((uint16_t)(hd.x >> 16));
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            int sc, m;
+            scale_min_k4_reg(4 * g2 + 2 * hf, hd.y, hd.z, hd.w, sc, m);
+            s_lo[hf] = splat_(d * (float)sc);
+            nm_lo[hf] = splat_(-(dmin * (float)m));
+            scale_min_k4_reg(4 * g2 + 2 * hf + 1, hd.y, hd.z, hd.w, sc, m);
+            s_hi[hf] = splat_(d * (float)sc);
+            nm_hi[hf] = splat_(-(dmin * (float)m));
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const half8_t A0 = *(const half8_t *)(Ab + 16 * s);
+            const half8_t A1 = *(const half8_t *)(Ab + 32 * G2G_LDA + 16 * s);
+            const int hf = s >> 3;
+            const half8_t B = dq4_f16(q[s], s_lo[hf], nm_lo[hf], s_hi[hf], nm_hi[hf]);
+            acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B, acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B, acc[1], 0, 0, 0);
+        }
+    } else {
+        // step s = 2 jj + w: first quarter scale 4w + jj/4, second + 2
+        half2_t sq[8];
+        const float d = h2f((uint16_t)hd.z);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t word = k < 4 ? hd.x : hd.y;
+            sq[k] = splat_(d * (float)(int)(int8_t)(word >> (8 * (k & 3))));
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const half8_t A0 = *(const half8_t *)(Ab + 16 * s);
+            const half8_t A1 = *(const half8_t *)(Ab + 32 * G2G_LDA + 16 * s);
+            const int jj = s >> 1, w = s & 1;
+            const int k0 = 4 * w + (jj >> 2);
+            const half8_t B = dq6_f16(q[jj], q[8 + jj], q[16 + jj], w, sq[k0], sq[k0 + 2]);
+            acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B, acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B, acc[1], 0, 0, 0);
+        }
     }
 }
 
 template <int WT>
 __global__ void __launch_bounds__(G2_THREADS) k_g2_store(G2Args g) {
-    __shared__ __attribute__((aligned(16))) _Float16 As[2][G2_BM * G2_LDA];
-    __shared__ int s_p[G2_BM];
-    __shared__ int64_t s_arow[G2_BM];
-    const int nx = (int)((g.ncols + 511) / 512);
+    using F = G3Fmt<WT>;
+    __shared__ __attribute__((aligned(1024))) G3Buf st0;
+    __shared__ __attribute__((aligned(1024))) G3Buf st1;
+    __shared__ __attribute__((aligned(1024))) uint8_t s_w[G2_WAVES][F::NLD * 1024];
+    __shared__ int s_p[G2_BM], s_arow[G2_BM];
+    const int nx = (int)((g.ncols + G3_NCOL - 1) / G3_NCOL);
     int tile, ctile;
     tile_coords(g.max_tiles, tile, ctile);
     if (tile >= *g.n_tiles || ctile >= nx) return;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int l32 = lane & 31, g2 = lane >> 5;
+    G3Lane L;
+    const int tid = threadIdx.x;
+    L.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    L.lane = tid & 63;
+    L.l32 = L.lane & 31;
+    L.g2 = L.lane >> 5;
+    const int wave = L.wave, l32 = L.l32, g2 = L.g2;
     const int e = g.tile_e[tile], r0 = g.tile_r0[tile];
     const int cnt = g.counts[e], off = g.offsets[e];
     const int mrows = imin(G2_BM, cnt - r0);
-    const bool two = mrows > 32;
-    const int64_t Kin = g.a.K;
+    const uint32_t Kin = (uint32_t)g.a.K;
     const int nb = (int)(Kin / QK);
     if (tid < G2_BM) {
         const int p = tid < mrows ? g.perm[off + r0 + tid] : -1;
         s_p[tid] = p;
-        s_arow[tid] = p < 0 ? 0 : (g.ne11 == 1 ? (int64_t)(p / g.K) : (int64_t)p);
-    }
-    int64_t ncol[2];
-    bool nok[2];
-    const uint8_t *rowp[2];
-    #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-        ncol[ct] = (int64_t)ctile * 512 + 64 * wave + 32 * ct + l32;
-        nok[ct] = ncol[ct] < g.ncols;
-        rowp[ct] = g.a.data + (int64_t)e * g.a.mat_bytes + (nok[ct] ? ncol[ct] : 0) * g.a.row_bytes;
+        s_arow[tid] = p < 0 ? 0 : (g.ne11 == 1 ? p / g.K : p);
     }
     __syncthreads();
-
-    uint4 av0, av1, av2, av3;
-#define G2S_ACT_SRC(it) (g.xh + s_arow[(tid + G2_THREADS * (it)) >> 5] * Kin + (int64_t)b_ * QK + \
-                         ((tid + G2_THREADS * (it)) & 31) * 8)
-#define G2S_ACT_DST(buf, it) (&As[buf][((tid + G2_THREADS * (it)) >> 5) * G2_LDA + ((tid + G2_THREADS * (it)) & 31) * 8])
-#define G2S_LOAD_ACT(bb)                          \
-    do {                                          \
-        const int b_ = (bb);                      \
-        av0 = *(const uint4 *)G2S_ACT_SRC(0);     \
-        av1 = *(const uint4 *)G2S_ACT_SRC(1);     \
-        av2 = *(const uint4 *)G2S_ACT_SRC(2);     \
-        av3 = *(const uint4 *)G2S_ACT_SRC(3);     \
-    } while (0)
-#define G2S_STORE_ACT(buf)                        \
-    do {                                          \
-        *(uint4 *)G2S_ACT_DST(buf, 0) = av0;      \
-        *(uint4 *)G2S_ACT_DST(buf, 1) = av1;      \
-        *(uint4 *)G2S_ACT_DST(buf, 2) = av2;      \
-        *(uint4 *)G2S_ACT_DST(buf, 3) = av3;      \
-    } while (0)
-
-    // Q4_K: qs chunks 2g2, 2g2+1 (4 x 16 B) + header; Q6_K: half g2: ql a/b,
-    // qh (3 x 32 B), scales[8h..8h+8), d
-    uint4 qv[2][WT == 12 ? 4 : 6];
-    uint4 hv[2];
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) g2_load_w<WT>(rowp[ct], 0, g2, qv[ct], hv[ct]);
-    G2S_LOAD_ACT(0);
-    G2S_STORE_ACT(0);
-
-    float16_t acc[2][2];
-    #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-        #pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-            #pragma unroll
-            for (int i = 0; i < 16; ++i) acc[rt][ct][i] = 0.f;
-
-    for (int b = 0; b < nb; ++b) {
-        const int buf = b & 1;
-        const bool more = b + 1 < nb;
-        __syncthreads();
-        if (more) G2S_LOAD_ACT(b + 1);
-        const _Float16 *Ab0 = &As[buf][(l32)*G2_LDA + 8 * g2];
-        const _Float16 *Ab1 = &As[buf][(32 + l32) * G2_LDA + 8 * g2];
-        if constexpr (WT == 12) {
-            half2_t s_lo[2][2], nm_lo[2][2], s_hi[2][2], nm_hi[2][2];
-            #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                const float d = h2f((uint16_t)(hv[ct].x & 0xffff)), dmin = h2f((uint16_t)(hv[ct].x >> 16));
-                #pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-                    int sc, m;
-                    scale_min_k4_reg(4 * g2 + 2 * hf, hv[ct].y, hv[ct].z, hv[ct].w, sc, m);
-                    s_lo[ct][hf] = splat_(d * (float)sc);
-                    nm_lo[ct][hf] = splat_(-(dmin * (float)m));
-                    scale_min_k4_reg(4 * g2 + 2 * hf + 1, hv[ct].y, hv[ct].z, hv[ct].w, sc, m);
-                    s_hi[ct][hf] = splat_(d * (float)sc);
-                    nm_hi[ct][hf] = splat_(-(dmin * (float)m));
-                }
-                if (more) hv[ct] = *(const uint4 *)(rowp[ct] + (int64_t)(b + 1) * Q4K_BYTES);
-            }
-#pragma unroll
-            for (int s = 0; s < 16; ++s) {
-                const half8_t A0 = *(const half8_t *)(Ab0 + 16 * s);
-                const half8_t A1 = *(const half8_t *)(Ab1 + 16 * s);
-                const int hf = s >> 3;
-#pragma unroll
-                for (int ct = 0; ct < 2; ++ct) {
-                    const half8_t B =
-                        dq4_f16(dword_of(qv[ct][s >> 2], s & 3), s_lo[ct][hf], nm_lo[ct][hf], s_hi[ct][hf], nm_hi[ct][hf]);
-                    acc[0][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B, acc[0][ct], 0, 0, 0);
-                    if (two) acc[1][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B, acc[1][ct], 0, 0, 0);
-                }
-                if ((s & 3) == 3 && more) {
-                    #pragma unroll
-                    for (int ct = 0; ct < 2; ++ct)
-                        qv[ct][s >> 2] = *(const uint4 *)(rowp[ct] + (int64_t)(b + 1) * Q4K_BYTES + 16 + 64 * g2 +
-                                                          16 * (s >> 2));
-                }
-            }
-        } else {
-            // scales for step (jj, w): first quarter sub 8h + 4w + jj/4, second +2
-            half2_t sq[2][8];
-            uint4 nq[2][6], nh[2];
-            #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                const float d = h2f((uint16_t)(hv[ct].z & 0xffff));
-                #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const uint32_t word = k < 4 ? hv[ct].x : hv[ct].y;
-                    const int sc = (int)(int8_t)(word >> (8 * (k & 3)));
-                    sq[ct][k] = splat_(d * (float)sc);
-                }
-                if (more) g2_load_w<WT>(rowp[ct], b + 1, g2, nq[ct], nh[ct]);
-            }
-#pragma unroll
-            for (int s = 0; s < 16; ++s) {
-                const half8_t A0 = *(const half8_t *)(Ab0 + 16 * s);
-                const half8_t A1 = *(const half8_t *)(Ab1 + 16 * s);
-                const int jj = s >> 1, w = s & 1;
-#pragma unroll
-                for (int ct = 0; ct < 2; ++ct) {
-                    const uint32_t qla = dword_of(qv[ct][jj >> 2], jj & 3);
-                    const uint32_t qlb = dword_of(qv[ct][2 + (jj >> 2)], jj & 3);
-                    const uint32_t qhh = dword_of(qv[ct][4 + (jj >> 2)], jj & 3);
-                    const int k0 = 4 * w + (jj >> 2);
-                    const half8_t B = dq6_f16(qla, qlb, qhh, w, sq[ct][k0], sq[ct][k0 + 2]);
-                    acc[0][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B, acc[0][ct], 0, 0, 0);
-                    if (two) acc[1][ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B, acc[1][ct], 0, 0, 0);
-                }
-            }
-            if (more)
-                #pragma unroll
-                for (int ct = 0; ct < 2; ++ct) {
-                    #pragma unroll
-                    for (int k = 0; k < 6; ++k) qv[ct][k] = nq[ct][k];
-                    hv[ct] = nh[ct];
-                }
-        }
-        if (more) G2S_STORE_ACT(buf ^ 1);
+    L.kin2 = 2u * Kin;
+    L.arow = s_arow;
+    L.rx = g2_rsrc(g.xh, g.xrows * (int64_t)Kin * 2);
+    // weight rows n0 + r of the expert matrix (rows past ncols are clamped to
+    // the last one and never stored); offsets are relative to the matrix base
+    // rounded down to 16 bytes, so 16-byte chunks are absolute-aligned
+    {
+        const uint8_t *mat = g.a.data + (int64_t)e * g.a.mat_bytes;
+        L.mis = (uint32_t)((uintptr_t)mat & 15u);
+        L.rw = g2_rsrc(mat - L.mis, g.a.mat_bytes + L.mis);
+        L.rowb = (uint32_t)g.a.row_bytes;
+        L.n0 = ctile * G3_NCOL + 32 * wave;
+        L.nlast = (int)g.ncols - 1;
     }
-#undef G2S_LOAD_ACT
-#undef G2S_STORE_ACT
-    // rows 32rt + 8(i/4) + 4g2 + i%4, column ncol[ct]
-    #pragma unroll
+    uint8_t *W = &s_w[wave][0];
+    g3_issue<WT>(L, 0, st0, W);
+
+    float16_t acc[2];
+#pragma unroll
     for (int rt = 0; rt < 2; ++rt)
-        #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
-            if (m >= mrows) continue;
-            float *yrow = g.y + (int64_t)s_p[m] * g.ldy;
-            #pragma unroll
-            for (int ct = 0; ct < 2; ++ct)
-                if (nok[ct]) yrow[ncol[ct]] = acc[rt][ct][i];
-        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[rt][i] = 0.f;
+    for (int b = 0; b < nb; b += 2) {
+        g3_block<WT>(L, b, nb, st0, st1, W, acc);
+        if (b + 1 < nb) g3_block<WT>(L, b + 1, nb, st1, st0, W, acc);
+    }
+    // rows 32rt + 8(i/4) + 4g2 + i%4, column n
+    const int64_t n = (int64_t)ctile * G3_NCOL + 32 * wave + l32;
+    if (n < g.ncols) {
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
+                if (m < mrows) g.y[(int64_t)s_p[m] * g.ldy + n] = acc[rt][i];
+            }
+    }
 }
 
 int launch_gemm2(const G2Args &g, hipStream_t st) {
@@ -678,7 +722,9 @@ int launch_gemm2(const G2Args &g, hipStream_t st) {
         if (g.next_type == 14) hipLaunchKernelGGL(k_g2_glu<14>, grid, dim3(G2G_THREADS), 0, st, g);
         else hipLaunchKernelGGL(k_g2_glu<12>, grid, dim3(G2G_THREADS), 0, st, g);
     } else {
-        const int nx = (int)((g.ncols + 511) / 512);
+        const int nx = (int)((g.ncols + G3_NCOL - 1) / G3_NCOL);
+        const int64_t lim = 0x7fffffff;
+        if (g.xrows <= 0 || g.xrows * g.a.K * 2 > lim || g.a.mat_bytes + 16 > lim) return -6;
         const dim3 grid((unsigned)((nx * g.max_tiles + 7) / 8 * 8));
         if (g.a.type == 12) hipLaunchKernelGGL(k_g2_store<12>, grid, dim3(G2_THREADS), 0, st, g);
         else if (g.a.type == 14) hipLaunchKernelGGL(k_g2_store<14>, grid, dim3(G2_THREADS), 0, st, g);

@@ -97,10 +97,13 @@ __device__ inline half8_t dq4_f16(uint32_t v, half2_t s_lo, half2_t nm_lo, half2
     return __builtin_bit_cast(half8_t, r);
 }
 
+// 4 Q6_K values (6-bit codes q in the bytes of x) -> fp16 (q - 32) * s:
+// v_perm_b32 puts each byte under the 0x64 exponent byte (1024 + q), then
+// (1024 + q) - 1056 is exact and one rounding happens in the multiply
 __device__ inline void q6b_to_h2(uint32_t x, half2_t s, half2_t &lo, half2_t &hi) {
     const half2_t c1056 = {(_Float16)1056.f, (_Float16)1056.f};
-    const uint32_t p01 = (x & 0x000000FFu) | ((x << 8) & 0x00FF0000u) | 0x64006400u;
-    const uint32_t p23 = ((x >> 16) & 0x000000FFu) | ((x >> 8) & 0x00FF0000u) | 0x64006400u;
+    const uint32_t p01 = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);
+    const uint32_t p23 = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);
     lo = (u2h2_(p01) - c1056) * s;
     hi = (u2h2_(p23) - c1056) * s;
 }
@@ -500,41 +503,29 @@ struct G3Buf {
 struct G3Lane {
     int wave, lane, l32, g2;
     __amdgpu_buffer_rsrc_t rx, rw;
-    uint32_t kin2;       // activation row bytes
-    uint32_t mis;        // expert matrix base address & 15
-    int n0, nlast;       // first weight row of the wave, last row of the matrix
-    uint32_t rowb;
-    const int *arow;
+    uint32_t aoff[5];    // activation loads: per-lane byte offsets (block 0)
+    uint32_t wrow[8];    // weight loads: byte offset of block 0 of the slot's row + 16 * chunk... see g3_issue
+    uint32_t wchk[8];    // 16 * chunk of the slot
+    uint32_t srow;       // byte offset of block 0 of the lane's own row (l32)
 };
 
-// byte offset of block b of the wave's weight row r (rows past the matrix
-// re-read its last row: their outputs are never stored)
-__device__ inline uint32_t g3_wstart(const G3Lane &L, int r, int b, int bb) {
-    return L.mis + (uint32_t)imin(L.n0 + r, L.nlast) * L.rowb + (uint32_t)(b * bb);
-}
-
 // loads of block b: activation stage st (5 per wave, the 33rd issued by every
-// wave with identical bytes) and the wave's weight region W (NLD per wave).
-// Offsets are recomputed per block from an opaque copy of the lane index.
+// wave with identical bytes) and the wave's weight region W (NLD per wave):
+// slot 64j + lane holds chunk c of row r; the row's block b starts at byte
+// wrow + b * BB, its covering chunks at that offset rounded down to 16
 template <int WT>
 __device__ __forceinline__ void g3_issue(const G3Lane &L, int b, G3Buf &st, uint8_t *W) {
     using F = G3Fmt<WT>;
-    int lane;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(lane) : "v"(L.lane));
 #pragma unroll
     for (int j = 0; j < 5; ++j) {
         const int k = j < 4 ? L.wave + 8 * j : G2G_ALOADS - 1;
-        const int q = 64 * k + lane;
-        const int row = q / 33, ch = q % 33;
-        const uint32_t aoff = (uint32_t)L.arow[row] * L.kin2 + 16u * (uint32_t)(ch == 32 ? 0 : ch);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rx, (lds_void_t *)&st.As[k * 512], 16, aoff, b * (QK * 2), 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rx, (lds_void_t *)&st.As[k * 512], 16, L.aoff[j], b * (QK * 2), 0,
+                                                 0);
     }
 #pragma unroll
     for (int j = 0; j < F::NLD; ++j) {
-        const int slot = imin(64 * j + lane, 32 * F::NC - 1);
-        const int r = slot / F::NC, c = slot - F::NC * r;
-        const uint32_t start = g3_wstart(L, r, b, F::BB);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rw, (lds_void_t *)(W + j * 1024), 16, (start & ~15u) + 16u * c, 0,
+        const uint32_t start = L.wrow[j] + (uint32_t)(b * F::BB);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rw, (lds_void_t *)(W + j * 1024), 16, (start & ~15u) + L.wchk[j], 0,
                                                  0, 0);
     }
 }
@@ -557,7 +548,7 @@ __device__ __forceinline__ void g3_read_w(const G3Lane &L, int b, const uint8_t 
     } else {
         // the block starts at byte s0 (even) of the staged row: dword reads
         // from s0 & ~3, then a 0- or 2-byte shift
-        const uint32_t s0 = g3_wstart(L, L.l32, b, F::BB) & 15u;
+        const uint32_t s0 = (L.srow + (uint32_t)(b * F::BB)) & 15u;
         const uint32_t sh = s0 & 3u;
         const uint32_t *rw = (const uint32_t *)(row + (s0 & ~3u));
         uint32_t t[17];
@@ -667,19 +658,32 @@ __global__ void __launch_bounds__(G2_THREADS) k_g2_store(G2Args g) {
         s_arow[tid] = p < 0 ? 0 : (g.ne11 == 1 ? p / g.K : p);
     }
     __syncthreads();
-    L.kin2 = 2u * Kin;
-    L.arow = s_arow;
     L.rx = g2_rsrc(g.xh, g.xrows * (int64_t)Kin * 2);
-    // weight rows n0 + r of the expert matrix (rows past ncols are clamped to
-    // the last one and never stored); offsets are relative to the matrix base
-    // rounded down to 16 bytes, so 16-byte chunks are absolute-aligned
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+        // slot q = 64k + lane of the padded activation tile: row q / 33, chunk q % 33
+        const int k = j < 4 ? wave + 8 * j : G2G_ALOADS - 1;
+        const int q = 64 * k + L.lane;
+        const int row = q / 33, ch = q % 33;
+        L.aoff[j] = (uint32_t)s_arow[row] * (2u * Kin) + 16u * (uint32_t)(ch == 32 ? 0 : ch);
+    }
+    // weight rows n0 + r of the expert matrix (rows past ncols re-read the
+    // last row; their outputs are never stored); offsets are relative to the
+    // matrix base rounded down to 16 bytes, so 16-byte chunks are aligned
     {
         const uint8_t *mat = g.a.data + (int64_t)e * g.a.mat_bytes;
-        L.mis = (uint32_t)((uintptr_t)mat & 15u);
-        L.rw = g2_rsrc(mat - L.mis, g.a.mat_bytes + L.mis);
-        L.rowb = (uint32_t)g.a.row_bytes;
-        L.n0 = ctile * G3_NCOL + 32 * wave;
-        L.nlast = (int)g.ncols - 1;
+        const uint32_t mis = (uint32_t)((uintptr_t)mat & 15u);
+        L.rw = g2_rsrc(mat - mis, g.a.mat_bytes + mis);
+        const int n0 = ctile * G3_NCOL + 32 * wave, nlast = (int)g.ncols - 1;
+        const uint32_t rowb = (uint32_t)g.a.row_bytes;
+#pragma unroll
+        for (int j = 0; j < F::NLD; ++j) {
+            const int slot = imin(64 * j + L.lane, 32 * F::NC - 1);
+            const int r = slot / F::NC, c = slot - F::NC * r;
+            L.wrow[j] = mis + (uint32_t)imin(n0 + r, nlast) * rowb;
+            L.wchk[j] = 16u * (uint32_t)c;
+        }
+        L.srow = mis + (uint32_t)imin(n0 + l32, nlast) * rowb;
     }
     uint8_t *W = &s_w[wave][0];
     g3_issue<WT>(L, 0, st0, W);

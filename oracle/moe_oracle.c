@@ -97,7 +97,7 @@ int orc_nearest_int(float fval) {
 /* ------------------------------------------------------------------------ */
 static float make_qkx2_quants(int n, int nmax, const float *x, const float *weights,
                               uint8_t *L, float *the_min, uint8_t *Laux,
-                              float rmin, float rdelta, int nstep) {
+                              float rmin, float rdelta, int nstep, int fixed_span) {
     float min = x[0];
     float max = x[0];
     float sum_w = weights[0];
@@ -130,8 +130,11 @@ static float make_qkx2_quants(int n, int nmax, const float *x, const float *weig
         *the_min = -min;
         return scale;
     }
+    /* ggml: the search span max - min follows the best min found so far;
+     * fixed_span = 1 keeps the initial span (convert/q4k.py:43, port only) */
+    const float span0 = max - min;
     for (int is = 0; is <= nstep; ++is) {
-        iscale = (rmin + rdelta * is + nmax) / (max - min);
+        iscale = (rmin + rdelta * is + nmax) / (fixed_span ? span0 : max - min);
         float sum_l = 0, sum_l2 = 0, sum_xl = 0;
         for (int i = 0; i < n; ++i) {
             int l = orc_nearest_int(iscale * (x[i] - min));
@@ -180,7 +183,9 @@ static inline void get_scale_min_k4(int j, const uint8_t *q, uint8_t *d, uint8_t
     }
 }
 
-void orc_quantize_row_q4_K(const float *x, void *vy, int64_t k) {
+void orc_quantize_row_q4_K(const float *x, void *vy, int64_t k) { orc_quantize_row_q4_K_port(x, vy, k, 0); }
+
+void orc_quantize_row_q4_K_port(const float *x, void *vy, int64_t k, int port) {
     orc_block_q4_K *y = (orc_block_q4_K *)vy;
     const int64_t nb = k / QK_K;
     uint8_t L[QK_K];
@@ -198,7 +203,7 @@ void orc_quantize_row_q4_K(const float *x, void *vy, int64_t k) {
             float av_x = sqrtf(sum_x2 / 32);
             for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
             scales[j] = make_qkx2_quants(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j],
-                                         Laux, -1.f, 0.1f, 20);
+                                         Laux, -1.f, 0.1f, 20, port & ORC_PORT_FIXED_SPAN);
             float scale = scales[j];
             if (scale > max_scale) max_scale = scale;
             float min = mins[j];
@@ -228,7 +233,10 @@ void orc_quantize_row_q4_K(const float *x, void *vy, int64_t k) {
         for (int j = 0; j < QK_K / 32; ++j) {
             get_scale_min_k4(j, y[i].scales, &sc, &m);
             const float d = orc_fp16_to_fp32(y[i].d) * sc;
-            if (!d) continue;
+            if (!d) {   /* ggml keeps the search's codes; the port writes 0 */
+                if (port & ORC_PORT_ZERO_L) memset(L + 32 * j, 0, 32);
+                continue;
+            }
             const float dm = orc_fp16_to_fp32(y[i].dmin) * m;
             for (int ii = 0; ii < 32; ++ii) {
                 int l = orc_nearest_int((x[32 * j + ii] + dm) / d);
@@ -324,7 +332,8 @@ static float make_qx_quants_rmse1(int n, int nmax, const float *x, int8_t *L) {
     return scale;
 }
 
-void orc_quantize_row_q6_K(const float *x, void *vy, int64_t k, int requant_fp32_d) {
+void orc_quantize_row_q6_K(const float *x, void *vy, int64_t k, int port) {
+    const int requant_fp32_d = port & ORC_PORT_FP32_D;
     orc_block_q6_K *y = (orc_block_q6_K *)vy;
     const int64_t nb = k / QK_K;
     int8_t L[QK_K];
@@ -356,7 +365,10 @@ void orc_quantize_row_q6_K(const float *x, void *vy, int64_t k, int requant_fp32
         }
         for (int j = 0; j < QK_K / 16; ++j) {
             float d = (requant_fp32_d ? d32 : orc_fp16_to_fp32(y[i].d)) * y[i].scales[j];
-            if (!d) continue;
+            if (!d) {   /* ggml keeps the search's codes; the port writes 0 (value -32) */
+                if (port & ORC_PORT_ZERO_L) memset(L + 16 * j, 0, 16);
+                continue;
+            }
             for (int ii = 0; ii < 16; ++ii) {
                 int l = orc_nearest_int(x[16 * j + ii] / d);
                 l = MAX(-32, MIN(31, l));

@@ -87,12 +87,24 @@ uint16_t orc_fp32_to_fp16(float f);
 int      orc_nearest_int(float f);
 
 /* ---- quantizers (ggml quantize_row_*_ref) -------------------------------
- * k must be a multiple of 256.  q6_K: requant_fp32_d = 0 follows ggml
- * (requantize against the fp16-rounded d); 1 follows convert/q6k.py:171
- * (requantize against the unrounded fp32 d), used only to compare with that
- * port's golden bytes. */
+ * k must be a multiple of 256.  port = 0 follows ggml.  The reference's own
+ * Python ports (convert/q4k.py, convert/q6k.py) differ from ggml in a few
+ * documented places; port bits select those conventions, used only to
+ * compare with the golden bytes the ports produced (tests/golden):
+ *   ORC_PORT_FP32_D     q6_K: requantize against the unrounded fp32 d
+ *                       (convert/q6k.py:171) instead of the fp16-rounded d
+ *   ORC_PORT_ZERO_L     codes of a sub-block whose scale quantized to 0 are
+ *                       written as 0 (q4k.py:113, q6k.py:177) instead of
+ *                       keeping the scale search's codes (ggml `continue`)
+ *   ORC_PORT_FIXED_SPAN q4_K: make_qkx2_quants keeps the initial max - min
+ *                       as the search span (q4k.py:43) instead of the span
+ *                       of the best min found so far */
+#define ORC_PORT_FP32_D     1
+#define ORC_PORT_ZERO_L     2
+#define ORC_PORT_FIXED_SPAN 4
 void orc_quantize_row_q4_K(const float *x, void *y, int64_t k);
-void orc_quantize_row_q6_K(const float *x, void *y, int64_t k, int requant_fp32_d);
+void orc_quantize_row_q4_K_port(const float *x, void *y, int64_t k, int port);
+void orc_quantize_row_q6_K(const float *x, void *y, int64_t k, int port);
 void orc_quantize_row_q8_K(const float *x, void *y, int64_t k);
 /* many rows, threaded: nrows rows of k floats -> nrows * (k/256) blocks */
 void orc_quantize_rows(int type, const float *x, void *y, int64_t nrows, int64_t k, int nthreads);

@@ -52,6 +52,7 @@ def _declare(L: C.CDLL) -> None:
     L.orc_nearest_int.argtypes = [C.c_float]
     L.orc_nearest_int.restype = C.c_int
     L.orc_quantize_row_q4_K.argtypes = [P, P, i64]
+    L.orc_quantize_row_q4_K_port.argtypes = [P, P, i64, C.c_int]
     L.orc_quantize_row_q6_K.argtypes = [P, P, i64, C.c_int]
     L.orc_quantize_row_q8_K.argtypes = [P, P, i64]
     L.orc_quantize_rows.argtypes = [C.c_int, P, P, i64, i64, C.c_int]
@@ -104,17 +105,27 @@ def row_size(type_: int, k: int) -> int:
     return lib().orc_row_size(type_, k)
 
 
-def quantize(type_: int, x: np.ndarray, nthreads: int = 0, requant_fp32_d: bool = False) -> np.ndarray:
-    """x float32 [..., k] (k % 256 == 0) -> uint8 [..., row_size]"""
+PORT_FP32_D, PORT_ZERO_L, PORT_FIXED_SPAN = 1, 2, 4
+
+
+def quantize(type_: int, x: np.ndarray, nthreads: int = 0, requant_fp32_d: bool = False,
+             port: int = 0) -> np.ndarray:
+    """x float32 [..., k] (k % 256 == 0) -> uint8 [..., row_size].  port: the
+    reference Python ports' conventions (PORT_* bits), golden comparison only"""
     x = np.ascontiguousarray(x, dtype=np.float32)
     k = x.shape[-1]
     assert k % QK_K == 0
     rows = x.reshape(-1, k)
     rs = row_size(type_, k)
     out = np.zeros((rows.shape[0], rs), dtype=np.uint8)
-    if type_ == TYPE_Q6_K and requant_fp32_d:
+    if requant_fp32_d:
+        port |= PORT_FP32_D
+    if port and type_ == TYPE_Q6_K:
         for r in range(rows.shape[0]):
-            lib().orc_quantize_row_q6_K(_p(rows[r]), _p(out[r]), k, 1)
+            lib().orc_quantize_row_q6_K(_p(rows[r]), _p(out[r]), k, port)
+    elif port and type_ == TYPE_Q4_K:
+        for r in range(rows.shape[0]):
+            lib().orc_quantize_row_q4_K_port(_p(rows[r]), _p(out[r]), k, port)
     else:
         lib().orc_quantize_rows(type_, _p(rows), _p(out), rows.shape[0], k, nthreads)
     return out.reshape(*x.shape[:-1], rs)

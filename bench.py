@@ -74,6 +74,19 @@ def time_layer(ctx, layers, xs, T, out, steps, warmup, profile=False):
     return max(dev, 0.0) / steps, {"wall_ms_per_step": wall / steps}
 
 
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (profiles/traffic.json: FETCH_SIZE + WRITE_SIZE per dispatch, scaled by
+    the same counters on a copy of known size); None when not measured."""
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(kernel, {}).get("bytes_per_launch")
+    except (ValueError, AttributeError):
+        return None
+
+
 def touched_experts(ctx, layer, x, T):
     counts = M.DeviceBuffer(4 * layer.spec.E)
     r = M.Routing()
@@ -124,6 +137,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=64)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run one 512 MiB device-to-device copy (the known-size kernel "
+                         "that scales FETCH_SIZE / WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -147,6 +163,13 @@ def main() -> int:
     log(f"built {args.copies} layer copies of {spec.name} in {time.perf_counter() - t0:.1f}s "
         f"({sum(l.expert_bytes() * spec.E for l in layers) / 1e9:.2f} GB of expert tables)")
 
+    if args.calib_copy:
+        nbytes = 512 << 20
+        src, dst = M.DeviceBuffer(nbytes), M.DeviceBuffer(nbytes)
+        M.check("memcpy", M.load().mi_memcpy_d2d(dst.ptr, src.ptr, nbytes))
+        M.synchronize()
+        log(f"calibration copy: {nbytes} bytes device to device")
+        del src, dst
     ms, extra = time_layer(ctx, layers, xs, T, out, args.steps, args.warmup)
     log(f"config {args.config}: {ms:.4f} ms/step, wall {extra['wall_ms_per_step']:.4f} ms/step")
     _, stages = time_layer(ctx, layers, xs, T, out, min(args.steps, 20), 2, profile=True)
@@ -174,9 +197,9 @@ def main() -> int:
                    "n_ff": spec.I, "gate_up": "Q4_K", "down": "Q6_K" if spec.down_type == M.TYPE_Q6_K else "Q4_K",
                    "act": "gelu_erf(h)*(g+1)", "layer_copies": args.copies,
                    "touched_experts": touched, "layer_flops": W.flops(spec, T)},
-        "roofline": {"bound": "mfma", "kernel": "gate_up grouped GEMM (k_gemm GLU)",
+        "roofline": {"bound": "mfma", "kernel": "k_g2_glu (gate/up grouped GEMM + GLU + Q8_K)",
                      "achieved": achieved, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": None,
+                     "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": measured_traffic("k_g2_glu"),
                      "kernel_ms": gu_ms, "flops_per_launch": gu_flops},
         "stages_ms": stages,
     }

@@ -36,6 +36,7 @@ import mimoe as M  # noqa: E402
 import workloads as W  # noqa: E402
 
 PEAK_MFMA_TFLOPS = 2500.0      # MI355X dense fp16 / bf16 MFMA
+ACT_NAMES = {0: "silu(gate)*up", 1: "gelu_erf(h)*(g+1)", 2: "gelu_tanh(gate)*up", 3: "gelu_erf(gate)*up"}
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 
 
@@ -195,7 +196,7 @@ def main() -> int:
         "config": {"workload": f"config {args.config}: moondream3 MoE layer prefill",
                    "tokens": T, "n_embd": spec.D, "n_expert": spec.E, "n_expert_used": spec.K,
                    "n_ff": spec.I, "gate_up": "Q4_K", "down": "Q6_K" if spec.down_type == M.TYPE_Q6_K else "Q4_K",
-                   "act": "gelu_erf(h)*(g+1)", "layer_copies": args.copies,
+                   "act": ACT_NAMES[spec.act], "layer_copies": args.copies,
                    "touched_experts": touched, "layer_flops": W.flops(spec, T)},
         "roofline": {"bound": "mfma", "kernel": "k_g2_glu (gate/up grouped GEMM + GLU + Q8_K)",
                      "achieved": achieved, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",

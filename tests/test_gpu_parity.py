@@ -144,6 +144,8 @@ FULL = {
     "md_cfg1": W.CONFIGS[1]["spec"],
     "md_cfg2_skew": W.CONFIGS[2]["spec"],
     "qo_cfg3": W.CONFIGS[3]["spec"],
+    # moondream3's own activation gelu_erf(h) * (g + 1) at full size
+    "md_cfg1_geglu_erf_gp1": W.md_spec(1, M.TYPE_Q6_K, act=M.ACT_GELU_ERF_GP1),
 }
 
 

@@ -173,6 +173,12 @@ int mi_moe_ctx_stage_times(mi_moe_ctx *ctx, int max_stages, const char **names, 
                            int *n_stages);
 /* path choice for a token count: 0 = grouped GEMV (decode), 1 = grouped MFMA GEMM */
 int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *ctx, int64_t min_tokens_for_gemm);
+/* single-token calls of mi_moe_forward: 1 (default) = the whole block in one
+ * cooperative kernel when the layer fits it (Q4_K gate/up, Q4_K or Q6_K down,
+ * top-k <= 8, 16-byte aligned tables), 0 = the separate-kernel chain.  Same
+ * results either way; the reference has one graph per step
+ * (moe_decode_driver.hpp:493-514), this only picks the GPU schedule. */
+int mi_moe_ctx_set_fused_decode(mi_moe_ctx *ctx, int on);
 size_t      mi_row_size(int32_t type, int64_t n_per_row);
 const char *mi_moe_status_string(int status);
 int         mi_moe_abi_version(void);

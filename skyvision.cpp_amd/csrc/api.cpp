@@ -92,6 +92,11 @@ struct mi_moe_ctx {
     float *f2 = nullptr;      // [rows][I]
     float *z = nullptr;       // [rows][max(D, 2I)]
     int64_t gemm_threshold = 16;
+    // single-token fused kernel (k_decode.hip)
+    bool fused_decode = true;
+    int dec_grid = 0;          // cooperative grid (one WG per CU), 0: unavailable
+    unsigned long long *dec_sync = nullptr;
+    unsigned *dec_err = nullptr;
 
     bool profiling = false;
     hipEvent_t ev[kMaxStages + 1] = {};
@@ -173,6 +178,53 @@ int validate_layer(const mi_moe_ctx *c, const mi_moe_layer *L, bool need_router)
     if (kq != is_kquant(L->down.type)) return MI_MOE_ERR_UNSUPPORTED;   // mixed F32 / k-quant layers
     if (!c->reserved) return MI_MOE_ERR_CAPACITY;
     if (D > c->cap_D || I > c->cap_I || E > c->cap_E || K > c->cap_K) return MI_MOE_ERR_CAPACITY;
+    return MI_MOE_OK;
+}
+
+// Single-token fused kernel: shape and layout conditions, and the work split
+// (P (h, g) row pairs per WG for gate/up, C output columns per WG for down).
+bool plan_decode1(const mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int &P, int &C) {
+    const int64_t D = L->n_embd, E = L->n_expert, K = L->n_expert_used, I = L->n_ff;
+    const int G = c->dec_grid;
+    if (!c->fused_decode || G <= 0) return false;
+    if (L->gate.type != MI_TYPE_Q4_K || (!L->fused_gate_up && L->up.type != MI_TYPE_Q4_K)) return false;
+    if (L->down.type != MI_TYPE_Q4_K && L->down.type != MI_TYPE_Q6_K) return false;
+    if (D % QK || I % QK || K > 8 || E > 256) return false;
+    const int64_t NB = D / QK, NBI = I / QK;
+    if (!(NB == 1 || NB == 2 || NB == 4 || NB == 8) || NBI > 8) return false;
+    auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    if (!al16(x) || !al16(L->router_w) || !al16(L->gate.data) || !al16(L->down.data)) return false;
+    if (L->gate.nb[2] % 16 || L->down.nb[2] % 16) return false;
+    if (!L->fused_gate_up && (!al16(L->up.data) || L->up.nb[2] % 16)) return false;
+    P = 0;
+    for (int64_t p = 4; p <= 64; p += 4)
+        if (I % p == 0 && (K * I) / p <= G) { P = (int)p; break; }
+    if (!P || (P / 4) * (int64_t)L->gate.nb[1] > DEC_LIMIT_GU_BYTES) return false;
+    if (!L->fused_gate_up && (P / 4) * (int64_t)L->up.nb[1] > DEC_LIMIT_GU_BYTES) return false;
+    C = 0;
+    for (int64_t cc = 1; cc <= 64; ++cc)
+        if (D % cc == 0 && D / cc <= G) { C = (int)cc; break; }
+    if (!C || C * (int64_t)L->down.nb[1] + 15 > DEC_LIMIT_DN_BYTES) return false;
+    return true;
+}
+
+int run_decode1(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, const float *res, float *out, int P,
+                int C, hipStream_t st) {
+    DecArgs g = {};
+    g.rw = L->router_w; g.rb = L->router_b; g.x = x;
+    g.D = L->n_embd; g.E = L->n_expert; g.K = L->n_expert_used; g.I = L->n_ff;
+    g.gate = as_mat(L->gate);
+    if (!L->fused_gate_up) g.up = as_mat(L->up);
+    g.down = as_mat(L->down);
+    g.fused = L->fused_gate_up; g.act = L->act;
+    g.res = res; g.out = out; g.P = P; g.C = C;
+    g.logits = c->logits; g.sel = c->sel; g.w = c->w;
+    g.counts = c->disp[0].counts; g.offsets = c->disp[0].offsets; g.perm = c->disp[0].perm;
+    g.xq = c->ax.q8; g.xd = c->ax.d8; g.xbs = c->ax.bs;
+    g.actf = c->f1;
+    g.sync = c->dec_sync; g.err = c->dec_err;
+    TRY(launch_decode1(g, c->dec_grid, st));
+    stage_end(c, "decode1", st);
     return MI_MOE_OK;
 }
 
@@ -347,6 +399,7 @@ int mi_moe_ctx_create(mi_moe_ctx **out, int device) {
     HIP_TRY(hipSetDevice(device));
     mi_moe_ctx *c = new mi_moe_ctx();
     c->device = device;
+    if (decode1_max_grid(device, &c->dec_grid)) c->dec_grid = 0;
     for (int i = 0; i <= kMaxStages; ++i) {
         const hipError_t e = hipEventCreate(&c->ev[i]);
         if (e != hipSuccess) {
@@ -392,6 +445,7 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
     need += carve_size<int8_t>(rows * iq) + carve_size<float>(rows * iq / QK) +
             carve_size<int16_t>(rows * iq / 16) + carve_size<_Float16>(rows * iq);
     need += carve_size<float>(rows * wide) + carve_size<float>(rows * I) + carve_size<float>(rows * wide);
+    need += carve_size<unsigned long long>(DEC_SYNC_WORDS) + carve_size<unsigned>(1);
 
     if (c->ws) {
         (void)hipFree(c->ws);
@@ -430,6 +484,8 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
     c->f1 = carve<float>(q, rows * wide);
     c->f2 = carve<float>(q, rows * I);
     c->z = carve<float>(q, rows * wide);
+    c->dec_sync = carve<unsigned long long>(q, DEC_SYNC_WORDS);
+    c->dec_err = carve<unsigned>(q, 1);
     HIP_TRY(hipMemset(p, 0, need));
     c->cap_T = max_tokens;
     c->cap_D = D;
@@ -447,6 +503,12 @@ int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *c, int64_t t) {
     if (!c) return MI_MOE_ERR_NULL;
     if (t < 1) return MI_MOE_ERR_ARG;
     c->gemm_threshold = t;
+    return MI_MOE_OK;
+}
+
+int mi_moe_ctx_set_fused_decode(mi_moe_ctx *c, int on) {
+    if (!c) return MI_MOE_ERR_NULL;
+    c->fused_decode = on != 0;
     return MI_MOE_OK;
 }
 
@@ -483,11 +545,16 @@ int mi_moe_forward(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t
     hipStream_t st = (hipStream_t)stream;
     const int D = L->n_embd, E = L->n_expert, K = L->n_expert_used;
     stage_begin(c, st);
-    TRY(launch_router(L->router_w, L->router_b, x, D, T, D, E, c->logits, st));
-    stage_end(c, "router", st);
-    TRY(launch_topk_softmax(c->logits, E, T, E, K, c->sel, K, c->w, st));
-    stage_end(c, "topk_softmax", st);
-    TRY(run_experts(c, L, x, T, c->sel, c->sel, c->w, res, out, st));
+    int P = 0, C = 0;
+    if (T == 1 && plan_decode1(c, L, x, P, C)) {
+        TRY(run_decode1(c, L, x, res, out, P, C, st));
+    } else {
+        TRY(launch_router(L->router_w, L->router_b, x, D, T, D, E, c->logits, st));
+        stage_end(c, "router", st);
+        TRY(launch_topk_softmax(c->logits, E, T, E, K, c->sel, K, c->w, st));
+        stage_end(c, "topk_softmax", st);
+        TRY(run_experts(c, L, x, T, c->sel, c->sel, c->w, res, out, st));
+    }
     if (routing) {
         const DispBuf &d = c->disp[0];
         if (routing->logits)

@@ -1,0 +1,580 @@
+// k_decode.hip - the whole MoE block for one token in one cooperative kernel.
+//
+// Reference block (one decode step): router mul_mat(+bias) -> top_k ->
+// get_rows -> soft_max -> mul_mat_id gate/up -> GLU -> mul_mat_id down ->
+// mul(w) -> sum_rows (-> add residual)
+//   moondream3: src/models/moondream/moondream.cpp:509-544 (+ residual :547)
+//   qwen3omni : src/models/qwen3omni/qwen3omni_model.cpp:759-780
+//
+// A single-token step reads ~29 MB of expert weights and does almost no
+// arithmetic, so its time is the HBM stream plus whatever serial latency
+// sits in front of it.  The separate-kernel chain pays a launch gap per
+// stage; here every stage lives in one grid of one work-group per CU, and
+// the stages meet at two grid barriers:
+//
+//   A  router rows (one wave per expert, fp64 fixed order) and Q8_K of x
+//   -- barrier --
+//   B  every WG ranks the E logits itself (no extra barrier for top-k), then
+//      DMAs its share of the selected experts' gate/up rows into LDS
+//      (buffer_load ... lds, 1 KB per wave instruction) and loads its share
+//      of their down rows into registers, so the down stream overlaps the
+//      gate/up arithmetic.
+//      Integer Q4_K x Q8_K dots, GLU, fp32 activations to HBM; the last WG
+//      to finish a 256-column block quantizes it to Q8_K.
+//   -- barrier --
+//   C  down dots from the LDS-resident rows, weighted combine in slot order
+//      (fp64, ggml's sum_rows of the weighted rows) and residual add.
+//
+// Numerics are the GEMV path's: exact integer dots per 32-value piece,
+// fp32 block scaling, act_pair for the GLU, the shared Q8_K and softmax
+// code.  Routing is exact: the rank form below selects the same experts in
+// the same order as the stable descending argsort of ggml_top_k.
+//
+// Grid barriers and the data that crosses them.  The eight XCDs have
+// separate L2 caches, so values one WG writes for another (logits, the Q8_K
+// of x, the GLU activations) are stored and loaded at device scope (sc1:
+// write-through stores, loads that do not hit a line another XCD made
+// stale), never through a cache flush: an agent-scope fence writes back or
+// invalidates a whole L2 and costs microseconds per WG.
+//
+// The barrier itself is two levels of monotonic 64-bit counters (groups of
+// 16 WGs, then the groups) and a release word holding the barrier round:
+// the last arrival of the last group publishes the round, everyone polls
+// that word.  Each barrier adds a fixed amount to every counter, so nothing
+// is reset between launches and a captured graph replays correctly.  The
+// launch is cooperative, so all WGs are resident; the wait is still bounded,
+// and a timed-out wait sets an error word that turns the output into NaN
+// instead of hanging the GPU.
+#include "act.hpp"
+#include "common.hpp"
+#include "launch.hpp"
+#include "wave_ops.hpp"
+
+namespace mimoe {
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+constexpr int DEC_WAVES = 8;
+constexpr int DEC_THREADS = DEC_WAVES * 64;
+constexpr int DEC_GU_SEG = 9;       // 1 KB DMA segments per wave of gate/up rows
+constexpr int DEC_DN_SEG = 7;       // 1 KB DMA segments per slot of down rows
+constexpr int DEC_KMAX = 8;         // slots: one wave each in the down phase
+constexpr int DEC_PMAX = 64;        // (h, g) row pairs per WG
+constexpr int DEC_CMAX = 64;        // down columns per WG
+constexpr unsigned DEC_SPIN_LIMIT = 1u << 20;
+constexpr int DEC_SYNC_GROUPS = DEC_SYNC_MAX_GROUPS;
+
+// ---------------------------------------------------------------- shared data
+// Relaxed agent-scope atomics: the compiler emits them with cache policy sc1
+// (stores write through to memory, loads do not hit a line another XCD made
+// stale).  16 bytes are read as two 8-byte atomics.
+__device__ inline void st_dev4(void *base, uint32_t off, uint32_t v) {
+    __hip_atomic_store((uint32_t *)((uint8_t *)base + off), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint32_t ld_dev4(const void *base, uint32_t off) {
+    return __hip_atomic_load((const uint32_t *)((const uint8_t *)base + off), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline u32x4 ld_dev16(const void *base, uint32_t off) {
+    const uint64_t *p = (const uint64_t *)((const uint8_t *)base + off);
+    const uint64_t a = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t b = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    u32x4 r;
+    r[0] = (uint32_t)a;
+    r[1] = (uint32_t)(a >> 32);
+    r[2] = (uint32_t)b;
+    r[3] = (uint32_t)(b >> 32);
+    return r;
+}
+// 16-bit value at an even byte offset, read through its aligned word
+__device__ inline uint16_t ld_dev2(const void *base, uint32_t off) {
+    const uint32_t w = ld_dev4(base, off & ~3u);
+    return (uint16_t)((off & 2u) ? (w >> 16) : (w & 0xffffu));
+}
+// reinterpret a 32-bit value (passed by value: this toolchain's
+// __builtin_bit_cast of an ext-vector element reads element 0)
+__device__ inline float as_float(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// ---------------------------------------------------------------- barrier
+// Counters in the context's workspace, 256 bytes apart: group g at sync[32 g],
+// the top counter at sync[32 * DEC_SYNC_GROUPS], the release word after it.
+constexpr int DEC_GROUP = 16;
+__device__ inline void dec_grid_barrier(unsigned long long *sync, unsigned *err) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's stores are done
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned G = gridDim.x;
+        const unsigned S = (G % DEC_GROUP == 0) ? DEC_GROUP : G;
+        const unsigned ngroups = G / S;
+        unsigned long long *grp = sync + 32 * (blockIdx.x / S);
+        unsigned long long *top = sync + 32 * DEC_SYNC_GROUPS;
+        unsigned long long *rel = top + 32;
+        const unsigned long long old = __hip_atomic_fetch_add(grp, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long round = old / S + 1;
+        if (old % S == S - 1) {
+            const unsigned long long o2 = __hip_atomic_fetch_add(top, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (o2 % ngroups == ngroups - 1) __hip_atomic_store(rel, round, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        unsigned n = 0;
+        while (__hip_atomic_load(rel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < round) {
+            if (++n > DEC_SPIN_LIMIT) {
+                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();
+}
+
+// workgroup barrier that does not wait for outstanding global loads / DMA
+__device__ inline void dec_lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+}
+
+// ---------------------------------------------------------------- phase A
+// logit of expert e: the router's fixed fp64 order (64-wide chunk c: sum over
+// s = 0..15, g = 0..3 of W[64c+16g+s] * x[64c+16g+s]; chunk partials added in
+// chunk order from 0.0; fl32; + bias in fp32).  Lane c owns chunk c.
+__device__ inline void dec_router_row(const DecArgs &g, int e, int lane) {
+    const int D = g.D;
+    const int nch = (D + 63) >> 6;
+    double part = 0.0;
+    if (lane < nch) {
+        const float *xr = g.x + 64 * lane;
+        const float *wr = g.rw + (int64_t)e * D + 64 * lane;
+        float xv[64], wv[64];
+        if (64 * lane + 64 <= D) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const float4_t a = *(const float4_t *)(xr + 4 * q);
+                const float4_t b = *(const float4_t *)(wr + 4 * q);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    xv[4 * q + j] = a[j];
+                    wv[4 * q + j] = b[j];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 64; ++i) {
+                const bool ok = 64 * lane + i < D;
+                xv[i] = ok ? xr[i] : 0.f;
+                wv[i] = ok ? wr[i] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) part = fma((double)wv[16 * q + s], (double)xv[16 * q + s], part);
+    }
+    // chunk partials added left to right (lane reads, no LDS round trips)
+    const uint64_t pb = __builtin_bit_cast(uint64_t, part);
+    const uint32_t plo = (uint32_t)pb, phi = (uint32_t)(pb >> 32);
+    double acc = 0.0;
+    for (int c = 0; c < nch; ++c) {
+        const uint64_t v = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)phi, c) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane((int)plo, c);
+        acc = acc + __builtin_bit_cast(double, v);
+    }
+    if (lane == 0) {
+        float v = (float)acc;
+        if (g.rb) v = v + g.rb[e];
+        st_dev4(g.logits, 4u * e, __builtin_bit_cast(uint32_t, v));
+    }
+}
+
+// Q8_K of x block b (natural order, ggml block_q8_K fields split), written
+// through for the other WGs
+__device__ inline void dec_q8k_x(const DecArgs &g, int b, int lane) {
+    const float4_t xv = *(const float4_t *)(g.x + b * QK + 4 * lane);
+    const float v[4] = {xv[0], xv[1], xv[2], xv[3]};
+    int q[4];
+    const float d = q8k_wave(v, lane, q);
+    st_dev4(g.xq, b * QK + 4 * lane, pack_i8x4(q));
+    if (lane == 0) st_dev4(g.xd, 4u * b, __builtin_bit_cast(uint32_t, d));
+    // block sums 2j and 2j+1 (lanes 8j and 8j+4) as one 32-bit word
+    const int s = q8k_bsum16(q);
+    const int s_hi = __shfl_down(s, 4, 64);
+    if ((lane & 7) == 0)
+        st_dev4(g.xbs, 2u * (b * 16 + (lane >> 2)), (uint32_t)(uint16_t)(int16_t)s | ((uint32_t)(uint16_t)(int16_t)s_hi << 16));
+}
+
+// ---------------------------------------------------------------- dots
+// One lane's 32-value piece sl of a Q4_K block held in LDS against the
+// matching Q8_K activation piece in registers (ggml_vec_dot_q4_K_q8_K
+// restricted to sub-blocks 2c, 2c+1, c = sl/2, values 16*(sl%2)..+16 of each).
+struct Q4X {
+    u32x4 xa, xb;    // activation codes of the low / high nibble halves
+    int bsa, bsb;    // their 16-value block sums
+    float dx;
+};
+// the same piece of the Q8_K of x written by phase A, read at device scope
+__device__ inline Q4X dec_q4x_load_dev(const DecArgs &g, int b, int sl) {
+    const int c = sl >> 1, l0 = 16 * (sl & 1);
+    Q4X x;
+    x.xa = ld_dev16(g.xq, b * QK + 64 * c + l0);
+    x.xb = ld_dev16(g.xq, b * QK + 64 * c + 32 + l0);
+    x.bsa = (int16_t)ld_dev2(g.xbs, 2u * (b * 16 + 4 * c + (sl & 1)));
+    x.bsb = (int16_t)ld_dev2(g.xbs, 2u * (b * 16 + 4 * c + 2 + (sl & 1)));
+    x.dx = as_float(ld_dev4(g.xd, 4u * b));
+    return x;
+}
+__device__ inline Q4X dec_q4x_load(const int8_t *xq, const int16_t *xbs, const float *xd, int b, int sl) {
+    const int c = sl >> 1, l0 = 16 * (sl & 1);
+    Q4X x;
+    const int8_t *blk = xq + b * QK;
+    x.xa = *(const u32x4 *)(blk + 64 * c + l0);
+    x.xb = *(const u32x4 *)(blk + 64 * c + 32 + l0);
+    x.bsa = xbs[b * 16 + 4 * c + (sl & 1)];
+    x.bsb = xbs[b * 16 + 4 * c + 2 + (sl & 1)];
+    x.dx = xd[b];
+    return x;
+}
+__device__ inline float dec_q4_piece(const uint8_t *blk, int sl, const Q4X &x) {
+    const u32x4 h = *(const u32x4 *)blk;
+    const u32x4 q = *(const u32x4 *)(blk + 16 + 16 * sl);
+    const float d = h2f((uint16_t)(h[0] & 0xffff)), dmin = h2f((uint16_t)(h[0] >> 16));
+    const int c = sl >> 1;
+    int scA, mA, scB, mB;
+    scale_min_k4_reg(2 * c, h[1], h[2], h[3], scA, mA);
+    scale_min_k4_reg(2 * c + 1, h[1], h[2], h[3], scB, mB);
+    int sa = 0, sb = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        sa = __builtin_amdgcn_sdot4((int)(q[i] & 0x0F0F0F0Fu), (int)x.xa[i], sa, false);
+        sb = __builtin_amdgcn_sdot4((int)((q[i] >> 4) & 0x0F0F0F0Fu), (int)x.xb[i], sb, false);
+    }
+    const int isum = scA * sa + scB * sb;
+    const int msum = mA * x.bsa + mB * x.bsb;
+    return (d * x.dx) * (float)isum - (dmin * x.dx) * (float)msum;
+}
+
+// 8 bytes at byte offset off (2-byte aligned) of an LDS region
+__device__ inline uint2 lds_load8(const uint8_t *region, uint32_t off) {
+    const uint32_t mis = off & 3u;
+    const uint32_t *w = (const uint32_t *)(region + (off & ~3u));
+    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
+    uint2 r;
+    r.x = __builtin_amdgcn_alignbyte(w1, w0, mis);
+    r.y = __builtin_amdgcn_alignbyte(w2, w1, mis);
+    return r;
+}
+
+// Q6_K piece sl: half h = sl/4, l0 = 8*(sl%4); quarters qq = 0..3 hold values
+// 128h + 32qq + l0 + i, i < 8, scale index 8h + l0/16 + 2qq
+// (ggml_vec_dot_q6_K_q8_K restricted to those values)
+struct Q6X {
+    uint32_t x[8];
+    float dx;
+};
+__device__ inline Q6X dec_q6x_load(const int8_t *xq, const float *xd, int b, int sl) {
+    const int h = sl >> 2, l0 = 8 * (sl & 3);
+    Q6X x;
+    const int8_t *blk = xq + b * QK;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+        const uint2 v = *(const uint2 *)(blk + 128 * h + 32 * qq + l0);
+        x.x[2 * qq] = v.x;
+        x.x[2 * qq + 1] = v.y;
+    }
+    x.dx = xd[b];
+    return x;
+}
+__device__ inline float dec_q6_piece(const uint8_t *region, uint32_t boff, int sl, const Q6X &x) {
+    const int h = sl >> 2, l0 = 8 * (sl & 3);
+    const uint2 qla = lds_load8(region, boff + 64 * h + l0);
+    const uint2 qlb = lds_load8(region, boff + 64 * h + 32 + l0);
+    const uint2 qh = lds_load8(region, boff + 128 + 32 * h + l0);
+    const uint2 s8 = lds_load8(region, boff + 192 + 8 * h);
+    const uint32_t dw = *(const uint32_t *)(region + ((boff + 208) & ~3u));
+    const uint16_t dbits = (uint16_t)(((boff + 208) & 2u) ? (dw >> 16) : (dw & 0xffff));
+    const float d = h2f(dbits);
+    const int is = l0 >> 4;
+    const uint32_t la[2] = {qla.x, qla.y}, lb[2] = {qlb.x, qlb.y}, hh[2] = {qh.x, qh.y};
+    int isum = 0;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+        const int idx = is + 2 * qq;
+        const uint32_t word = (idx >> 2) ? s8.y : s8.x;
+        const int sc = (int)(int8_t)(word >> (8 * (idx & 3)));
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            uint32_t lo, hi2;
+            if (qq == 0) { lo = la[i] & 0x0F0F0F0Fu; hi2 = (hh[i] << 4) & 0x30303030u; }
+            else if (qq == 1) { lo = lb[i] & 0x0F0F0F0Fu; hi2 = (hh[i] << 2) & 0x30303030u; }
+            else if (qq == 2) { lo = (la[i] >> 4) & 0x0F0F0F0Fu; hi2 = hh[i] & 0x30303030u; }
+            else { lo = (lb[i] >> 4) & 0x0F0F0F0Fu; hi2 = (hh[i] >> 2) & 0x30303030u; }
+            // 6-bit q -> q - 32 as a signed byte (see k_gemv.hip dot_q6_piece)
+            const uint32_t x6 = (lo | hi2) ^ 0x20202020u;
+            const uint32_t sq = x6 | ((x6 & 0x20202020u) * 6u);
+            s = __builtin_amdgcn_sdot4((int)sq, (int)x.x[2 * qq + i], s, false);
+        }
+        isum += sc * s;
+    }
+    return (d * x.dx) * (float)isum;
+}
+
+// copy a byte range of one expert matrix into LDS: DEC segments of 1 KB, lane
+// l moving 16 bytes.  The resource covers exactly the 16-aligned span of the
+// range, so segments past it read zeros without touching memory and the
+// number of DMA instructions per wave is a compile-time constant.
+template <int NSEG>
+__device__ inline void dec_dma(const uint8_t *base16, uint32_t span, uint8_t *lds, int lane) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base16), (short)0, (int)span, 0x00020000);
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds + 1024 * s), 16, 1024 * s + 16 * lane, 0, 0,
+                                                 0);
+}
+
+// rows [row0, row0 + nrows) of expert e of m: 16-aligned base, byte shift of
+// the first row, span in bytes (multiple of 16)
+struct DecChunk {
+    const uint8_t *base16;
+    uint32_t shift, span;
+};
+__device__ inline DecChunk dec_chunk(const ExpertMat &m, int e, int64_t row0, int nrows, bool on) {
+    DecChunk c;
+    const uint8_t *p = m.data + (int64_t)e * m.mat_bytes + row0 * m.row_bytes;
+    const uintptr_t a = (uintptr_t)p;
+    c.base16 = (const uint8_t *)(a & ~(uintptr_t)15);
+    c.shift = (uint32_t)(a & 15);
+    const uint32_t len = on ? (uint32_t)(nrows * m.row_bytes) : 0u;
+    c.span = on ? (c.shift + len + 15u) & ~15u : 0u;
+    return c;
+}
+
+// ---------------------------------------------------------------- kernel
+template <int DT>
+__global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
+    __shared__ __attribute__((aligned(1024))) uint8_t s_gu[DEC_WAVES][DEC_GU_SEG * 1024];
+    __shared__ __attribute__((aligned(1024))) uint8_t s_dn[DEC_KMAX][DEC_DN_SEG * 1024];
+    __shared__ float s_logit[256];
+    __shared__ int s_sel[DEC_KMAX];
+    __shared__ float s_val[DEC_KMAX], s_w[DEC_KMAX];
+    __shared__ float s_hg[2 * DEC_PMAX];
+    __shared__ float s_z[DEC_KMAX * DEC_CMAX];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wg = blockIdx.x, G = gridDim.x;
+    const int D = g.D, E = g.E, K = g.K, I = g.I;
+    const int NB = D / QK, NBI = I / QK;
+
+    // ---- A: router rows and Q8_K of x
+    if (wave == 0) {
+        for (int e = wg; e < E; e += G) dec_router_row(g, e, lane);
+    } else if (wave == 1) {
+        for (int b = wg; b < NB; b += G) dec_q8k_x(g, b, lane);
+    }
+    dec_grid_barrier(g.sync, g.err);
+
+    // ---- B: routing (every WG), DMA of its gate/up and down rows
+    float lv = 0.f;
+    if (tid < E) lv = as_float(ld_dev4(g.logits, 4u * tid));
+    // this lane's activation piece: row group of LPR = 8*NB lanes, block bq, piece sl
+    const int LPR = 8 * NB, RPS = 64 / LPR;
+    const int rr = lane / LPR, bq = (lane % LPR) >> 3, sl = lane & 7;
+    const Q4X xg = dec_q4x_load_dev(g, bq, sl);
+    if (tid < E) s_logit[tid] = lv;
+    if (tid < DEC_KMAX) s_sel[tid] = tid < K ? tid : 0;
+    dec_lds_barrier();
+    {
+        // rank of expert e = #{j : l_j > l_e} + #{j < e : l_j == l_e}; the K
+        // lowest ranks in rank order are ggml_top_k's stable descending pick
+        int tpe = 1;
+        while (tpe * 2 * E <= DEC_THREADS && tpe < 64) tpe *= 2;
+        const int e = tid / tpe, j = tid % tpe;
+        int cnt = 0;
+        float ve = 0.f;
+        if (e < E) {
+            ve = s_logit[e];
+            for (int i = j; i < E; i += tpe) {
+                const float vi = s_logit[i];
+                cnt += (vi > ve || (vi == ve && i < e)) ? 1 : 0;
+            }
+        }
+        for (int o = 1; o < tpe; o <<= 1) cnt += __shfl_xor(cnt, o, 64);
+        if (e < E && j == 0 && cnt < K) {
+            s_sel[cnt] = e;
+            s_val[cnt] = ve;
+        }
+    }
+    dec_lds_barrier();
+
+    const int64_t pairs = (int64_t)K * I;
+    const int P = g.P, R = P / 4, C = g.C;
+    const int64_t q0 = (int64_t)wg * P;
+    const bool do_b = q0 < pairs;
+    const int kB = do_b ? (int)(q0 / I) : 0;
+    const int i0 = do_b ? (int)(q0 % I) : 0;
+    const int n0 = wg * C;
+    const bool do_c = n0 < D;
+    {
+        int eb = __builtin_amdgcn_readfirstlane(s_sel[kB]);
+        eb = eb < 0 ? 0 : (eb >= E ? E - 1 : eb);
+        const bool hpart = wave < 4;
+        const ExpertMat &m = (hpart || g.fused) ? g.gate : g.up;
+        const int64_t row0 = (int64_t)i0 + (wave & 3) * R + ((!hpart && g.fused) ? I : 0);
+        const DecChunk c = dec_chunk(m, eb, row0, R, do_b);
+        dec_dma<DEC_GU_SEG>(c.base16, c.span, s_gu[wave], lane);
+    }
+    // down rows of slot k = wave: prefetched into registers now (the stream
+    // overlaps the gate/up arithmetic), parked in LDS after it
+    uint32_t dn_shift;
+    u32x4 dnv[DEC_DN_SEG];
+    {
+        const int k = wave < K ? wave : 0;
+        int ed = __builtin_amdgcn_readfirstlane(s_sel[k]);
+        ed = ed < 0 ? 0 : (ed >= E ? E - 1 : ed);
+        const DecChunk c = dec_chunk(g.down, ed, n0, C, do_c && wave < K);
+        dn_shift = c.shift;
+        const __amdgpu_buffer_rsrc_t r =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(c.base16), (short)0, (int)c.span, 0x00020000);
+#pragma unroll
+        for (int s = 0; s < DEC_DN_SEG; ++s) dnv[s] = __builtin_amdgcn_raw_buffer_load_b128(r, 1024 * s + 16 * lane, 0, 0);
+    }
+
+    if (wave == 0) {
+        const float myval = lane < K ? s_val[lane] : 0.f;
+        const float myw = softmax_selected_wave(myval, K, lane);
+        if (lane < K) s_w[lane] = myw;
+        if (wg == 0 && lane < K) {
+            g.sel[lane] = s_sel[lane];
+            g.w[lane] = myw;
+        }
+    }
+    if (wg == 0) {
+        // single-token dispatch: one list entry per selected expert
+        for (int e = tid; e < E; e += DEC_THREADS) {
+            int cnt = 0, below = 0, slot = 0;
+            for (int k = 0; k < K; ++k) {
+                if (s_sel[k] == e) {
+                    cnt++;
+                    slot = k;
+                }
+                below += s_sel[k] < e;
+            }
+            g.counts[e] = cnt;
+            g.offsets[e] = below;
+            if (cnt) g.perm[below] = slot;
+        }
+        if (tid == 0) g.offsets[E] = K;
+    }
+
+    // gate/up dots: wave v owns R consecutive rows (h for v < 4, g for v >= 4)
+    if (do_b) {
+        const uint32_t shift = 0;   // Q4_K tables are 16-byte aligned
+        const int64_t rb = (int64_t)NB * Q4K_BYTES;
+        for (int r0 = 0; r0 < R; r0 += RPS) {
+            const int r = r0 + rr;
+            float acc = 0.f;
+            if (r < R) acc = dec_q4_piece(s_gu[wave] + shift + r * rb + bq * Q4K_BYTES, sl, xg);
+            for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, 64);
+            if ((lane % LPR) == 0 && r < R) s_hg[(wave >> 2) * P + (wave & 3) * R + r] = acc;
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < DEC_DN_SEG; ++s) *(u32x4 *)(s_dn[wave] + 1024 * s + 16 * lane) = dnv[s];
+    dec_lds_barrier();
+    if (do_b && tid < P) {
+        const float a = act_pair(g.act, s_hg[tid], s_hg[P + tid]);
+        st_dev4(g.actf, 4u * (uint32_t)(kB * I + i0 + tid), __builtin_bit_cast(uint32_t, a));
+    }
+    dec_grid_barrier(g.sync, g.err);
+
+    // ---- C: Q8_K of slot k = wave's activations, down rows, weighted combine
+    if (do_c && wave < K) {
+        const int k = wave;
+        // Q8_K of the I activations of slot k (ggml quantizes each mul_mat_id
+        // source row on its own), codes / scales / block sums into the now
+        // free gate/up region of this wave
+        int8_t *aq = (int8_t *)s_gu[k];
+        float *ad = (float *)(s_gu[k] + 2048);
+        int16_t *abs_ = (int16_t *)(s_gu[k] + 2048 + 64);
+        u32x4 av[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+            if (b < NBI) av[b] = ld_dev16(g.actf, 4u * (uint32_t)(k * I + b * QK + 4 * lane));
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            if (b < NBI) {
+                const float v[4] = {as_float(av[b][0]), as_float(av[b][1]), as_float(av[b][2]), as_float(av[b][3])};
+                int q[4];
+                const float d = q8k_wave(v, lane, q);
+                *(uint32_t *)(aq + b * QK + 4 * lane) = pack_i8x4(q);
+                if (lane == 0) ad[b] = d;
+                const int bs = q8k_bsum16(q);
+                if ((lane & 3) == 0) abs_[b * 16 + (lane >> 2)] = (int16_t)bs;
+            }
+        }
+        const int LPRD = 8 * NBI, RPSD = 64 / LPRD;
+        const int rd = lane / LPRD, bd = (lane % LPRD) >> 3;
+        const bool lane_ok = rd < RPSD;
+        const int base_lane = (lane_ok ? rd : 0) * LPRD;
+        const int64_t rbd = g.down.row_bytes;
+        Q4X x4;
+        Q6X x6;
+        if constexpr (DT == 12) x4 = dec_q4x_load(aq, abs_, ad, lane_ok ? bd : 0, sl);
+        else x6 = dec_q6x_load(aq, ad, lane_ok ? bd : 0, sl);
+        const int bbytes = DT == 12 ? Q4K_BYTES : Q6K_BYTES;
+        for (int c0 = 0; c0 < C; c0 += RPSD) {
+            const int c = c0 + rd;
+            const bool ok = lane_ok && c < C;
+            float acc = 0.f;
+            if (ok) {
+                const uint32_t boff = dn_shift + (uint32_t)(c * rbd) + (uint32_t)(bd * bbytes);
+                if constexpr (DT == 12) acc = dec_q4_piece(s_dn[k] + boff, sl, x4);
+                else acc = dec_q6_piece(s_dn[k], boff, sl, x6);
+            }
+            acc += __shfl_xor(acc, 1, 64);
+            acc += __shfl_xor(acc, 2, 64);
+            acc += __shfl_xor(acc, 4, 64);
+            float tot = 0.f;
+            for (int b = 0; b < NBI; ++b) tot += __shfl(acc, base_lane + 8 * b, 64);
+            if (ok && (lane % LPRD) == 0) s_z[k * C + c] = tot;
+        }
+    }
+    dec_lds_barrier();
+    if (do_c && tid < C) {
+        double s = 0.0;
+        for (int k = 0; k < K; ++k) s = s + (double)(s_z[k * C + tid] * s_w[k]);
+        const float moe = (float)s;
+        float v = g.res ? g.res[n0 + tid] + moe : moe;
+        if (__hip_atomic_load(g.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) v = __builtin_nanf("");
+        g.out[n0 + tid] = v;
+    }
+}
+
+int launch_decode1(const DecArgs &g, int grid, hipStream_t st) {
+    void *args[] = {(void *)&g};
+    hipError_t e;
+    if (g.down.type == 12)
+        e = hipLaunchCooperativeKernel((const void *)k_decode1<12>, dim3(grid), dim3(DEC_THREADS), args, 0, st);
+    else if (g.down.type == 14)
+        e = hipLaunchCooperativeKernel((const void *)k_decode1<14>, dim3(grid), dim3(DEC_THREADS), args, 0, st);
+    else
+        return -3;
+    if (e != hipSuccess) return record_hip_error(e);
+    return hip_check_launch();
+}
+
+int decode1_max_grid(int device, int *grid) {
+    int cus = 0, per = 0;
+    hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess) return record_hip_error(e);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_decode1<14>, DEC_THREADS, 0);
+    if (e != hipSuccess) return record_hip_error(e);
+    int per12 = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per12, (const void *)k_decode1<12>, DEC_THREADS, 0);
+    if (e != hipSuccess) return record_hip_error(e);
+    *grid = cus * imin(imin(per, per12), 1);
+    if (*grid > DEC_GROUP * DEC_SYNC_MAX_GROUPS) *grid = 0;   // more WGs than barrier groups
+    return 0;
+}
+
+}  // namespace mimoe

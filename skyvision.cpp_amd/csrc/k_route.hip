@@ -11,6 +11,7 @@
 // Q8_K is ggml's vec_dot_type for Q4_K / Q6_K: ggml-cpu quantizes the F32
 // activation rows to it before the integer dot.
 #include "common.hpp"
+#include "wave_ops.hpp"
 #include "launch.hpp"
 
 namespace mimoe {
@@ -34,33 +35,15 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ src,
         const float *x = src + row * ld + (int64_t)b * QK + 4 * lane;
         for (int j = 0; j < 4; ++j) v[j] = x[j];
     }
-    AmaxIdx a{-1.f, 1 << 30, 0.f};
-    for (int j = 0; j < 4; ++j) {
-        AmaxIdx c{fabsf(v[j]), 4 * lane + j, v[j]};
-        a = amax_better(a, c);
-    }
-    a = wave_amax_idx(a);
-    const float amax = a.ax, max = a.val;
-    int q[4] = {0, 0, 0, 0};
-    float d = 0.f;
-    if (amax != 0.f) {
-        const float iscale = -127.f / max;
-        for (int j = 0; j < 4; ++j) q[j] = imin(127, nearest_int(iscale * v[j]));
-        d = 1 / iscale;
-    }
+    int q[4];
+    const float d = q8k_wave(v, lane, q);
     if (valid) {
         const int64_t o = row * K + (int64_t)b * QK + 4 * lane;
-        if (q8) {
-            const uint32_t packed = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) |
-                                    ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
-            *(uint32_t *)(q8 + o) = packed;
-        }
+        if (q8) *(uint32_t *)(q8 + o) = pack_i8x4(q);
         if (d8 && lane == 0) d8[row * nb + b] = d;
     }
     if (bsums || xbs) {
-        int s = q[0] + q[1] + q[2] + q[3];
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
+        const int s = q8k_bsum16(q);
         const int64_t bi = row * (K / 16) + (int64_t)b * 16 + (lane >> 2);
         if (valid && (lane & 3) == 0) {
             if (bsums) bsums[bi] = (int16_t)s;
@@ -230,61 +213,18 @@ int launch_router(const float *W, const float *b, const float *x, int64_t ldx, i
 // ties) over the not-yet-taken experts; then softmax over the K selected
 // logits: max, expf(v - max), sum in fp64 in slot order, scale by
 // (float)(1.0 / sum) - the ggml_soft_max order.
-constexpr int TOPK_MAX_PER_LANE = 4;   // E <= 256
 __global__ void __launch_bounds__(256) k_topk_softmax(const float *__restrict__ logits, int64_t ldl, int64_t T,
                                                       int E, int K, int32_t *__restrict__ sel, int64_t lds,
                                                       float *__restrict__ w) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t t = (int64_t)blockIdx.x * 4 + wave;
     if (t >= T) return;
-    const float *l = logits + t * ldl;
-    float v[TOPK_MAX_PER_LANE];
-    bool avail[TOPK_MAX_PER_LANE];
-    for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
-        const int e = lane + 64 * i;
-        avail[i] = e < E;
-        v[i] = avail[i] ? l[e] : 0.f;
-    }
-    int mysel = 0;
-    float myval = 0.f;
-    for (int k = 0; k < K; ++k) {
-        float bv = 0.f;
-        int bi = 0x7fffffff;
-        for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
-            const int e = lane + 64 * i;
-            if (avail[i] && (bi == 0x7fffffff || v[i] > bv)) {
-                bv = v[i];
-                bi = e;
-            }
-        }
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            const bool take = oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
-            if (take) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if (bi != 0x7fffffff && (bi & 63) == lane) {
-            for (int i = 0; i < TOPK_MAX_PER_LANE; ++i)
-                if (lane + 64 * i == bi) avail[i] = false;
-        }
-        if (lane == k) {
-            mysel = bi;
-            myval = bv;
-        }
-    }
-    if (lane < K) sel[t * lds + lane] = mysel;
-    if (w) {
-        float mx = lane < K ? myval : -INFINITY;
-        mx = wave_max(mx);
-        const float val = lane < K ? expf(myval - mx) : 0.f;
-        double sum = 0.0;
-        for (int k = 0; k < K; ++k) sum = sum + (double)__shfl(val, k, 64);
-        sum = 1.0 / sum;
-        const float s = (float)sum;
-        if (lane < K) w[t * K + lane] = val * s;
+    int mysel;
+    float myw;
+    topk_softmax_wave(logits + t * ldl, E, K, lane, mysel, myw, w != nullptr);
+    if (lane < K) {
+        sel[t * lds + lane] = mysel;
+        if (w) w[t * K + lane] = myw;
     }
 }
 

@@ -139,4 +139,33 @@ struct G2Args {
 };
 int launch_gemm2(const G2Args &g, hipStream_t st);
 
+// Single-token MoE block in one cooperative kernel (k_decode.hip).
+struct DecArgs {
+    const float *rw, *rb, *x;     // router W [E][D], bias [E] or NULL, token [D]
+    int D, E, K, I;
+    ExpertMat gate, up, down;     // Q4_K gate (or fused [h | g]) / up; Q4_K or Q6_K down
+    int fused, act;
+    const float *res;             // [D] or NULL
+    float *out;                   // [D]
+    int P, C;                     // (h, g) row pairs per WG; down columns per WG
+    // workspace / routing outputs
+    float *logits;                // [E]
+    int32_t *sel;                 // [K]
+    float *w;                     // [K]
+    int32_t *counts, *offsets, *perm;
+    int8_t *xq;                   // Q8_K of x: codes [D], scales [D/256], block sums [D/16]
+    float *xd;
+    int16_t *xbs;
+    float *actf;                  // GLU output fp32 [K][I]
+    unsigned long long *sync;     // grid barrier counters (only grow), DEC_SYNC_WORDS
+    unsigned *err;                // set by a timed-out barrier wait
+};
+constexpr int DEC_SYNC_MAX_GROUPS = 64;                       // up to 1024 WGs
+constexpr int DEC_SYNC_WORDS = 32 * (DEC_SYNC_MAX_GROUPS + 2);   // 256 B per counter
+constexpr int DEC_LIMIT_GU_BYTES = 9 * 1024;   // LDS per wave of gate/up rows
+constexpr int DEC_LIMIT_DN_BYTES = 7 * 1024;   // LDS per slot of down rows
+int launch_decode1(const DecArgs &g, int grid, hipStream_t st);
+// work-groups of the cooperative grid (one per CU), 0 if it cannot be resident
+int decode1_max_grid(int device, int *grid);
+
 }  // namespace mimoe

@@ -70,6 +70,7 @@ SYMBOLS = {
     "mi_moe_ctx_stage_times": ([P, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_float),
                                 C.POINTER(C.c_int)], C.c_int),
     "mi_moe_ctx_set_gemm_threshold": ([P, i64], C.c_int),
+    "mi_moe_ctx_set_fused_decode": ([P, C.c_int], C.c_int),
     "mi_row_size": ([i32, i64], C.c_size_t),
     "mi_moe_status_string": ([C.c_int], C.c_char_p),
     "mi_moe_abi_version": ([], C.c_int),
@@ -223,6 +224,9 @@ class Context:
 
     def set_gemm_threshold(self, t: int) -> None:
         call("mi_moe_ctx_set_gemm_threshold", self.h, t)
+
+    def set_fused_decode(self, on: bool) -> None:
+        call("mi_moe_ctx_set_fused_decode", self.h, 1 if on else 0)
 
     def set_profiling(self, on: bool) -> None:
         call("mi_moe_ctx_set_profiling", self.h, int(on))

@@ -1,0 +1,176 @@
+"""Single-token MoE block in one cooperative kernel (k_decode.hip) against the
+CPU oracle and against the separate-kernel chain.
+
+Bars, as for every forward path: router logits, expert ids and the
+single-token dispatch (counts / offsets / permutation) bit-exact; routing
+weights within 1e-6 relative; MoE output rel-L2 <= 1e-2 against the oracle.
+The fused kernel and the GEMV chain use the same integer dots and Q8_K code
+but sum the fp32 dot partials in different orders, so an activation sitting
+on a Q8_K rounding boundary can land on either side: on the full config-0
+layer one such flip in 8192 codes moves the output by 1.1e-3 (measured).  The
+two schedules must agree to a few such flips (rel-L2 <= 5e-3).
+
+Consecutive launches on one context reuse the kernel's barrier and block
+counters, so every case runs several tokens back to back, and one case
+switches layer shapes between launches.
+"""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import mimoe as M
+import pyoracle as O
+import workloads as W
+from _util import cpu_x, max_abs, oracle_layer_dict, rel_l2, small_spec
+
+pytestmark = pytest.mark.gpu
+
+TOL_REL_L2 = 1e-2
+TOL_PATHS = 5e-3
+
+
+def log(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+CASES = {
+    "md_small_q6": small_spec("md_small_q6", D=512, E=8, K=2, I=256, fused=True, down_type=O.TYPE_Q6_K,
+                              act=O.ACT_GELU_ERF_GP1),
+    "qo_small": small_spec("qo_small", D=512, E=16, K=4, I=256, fused=False, act=O.ACT_SILU,
+                           seed=0x5EED1001),
+    "md_d256_k3": small_spec("md_d256_k3", D=256, E=8, K=3, I=512, fused=True, act=O.ACT_GELU_TANH,
+                             seed=0x5EED1002),
+    "md_d1024_q6": small_spec("md_d1024_q6", D=1024, E=32, K=8, I=768, fused=True, down_type=O.TYPE_Q6_K,
+                              act=O.ACT_GELU_ERF, seed=0x5EED1003),
+    "md_cfg0": W.CONFIGS[0]["spec"],
+    "md_cfg1": W.CONFIGS[1]["spec"],
+    "qo_cfg3": W.CONFIGS[3]["spec"],
+}
+
+
+def _routing_buffers(E, K):
+    bufs = dict(logits=M.DeviceBuffer(4 * E), sel=M.DeviceBuffer(4 * K), weights=M.DeviceBuffer(4 * K),
+                counts=M.DeviceBuffer(4 * E), offsets=M.DeviceBuffer(4 * (E + 1)), perm=M.DeviceBuffer(4 * K))
+    r = M.Routing()
+    for k, v in bufs.items():
+        setattr(r, k, C.c_void_p(v.addr))
+    return bufs, r
+
+
+def _dispatch_one(sel_t, E):
+    counts = np.bincount(sel_t, minlength=E).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    perm = np.argsort(sel_t, kind="stable").astype(np.int32)
+    return counts, offsets, perm
+
+
+def _run_token(ctx, layer, spec, x_row, res_row, fused):
+    ctx.set_fused_decode(fused)
+    ctx.set_profiling(True)
+    xd, rd = M.to_device(x_row[None, :]), M.to_device(res_row[None, :])
+    out = M.DeviceBuffer(4 * spec.D)
+    bufs, r = _routing_buffers(spec.E, spec.K)
+    M.check("forward", ctx.forward(layer, xd, 1, rd, out, r))
+    stages = [n for n, _ in ctx.stage_times()]
+    ctx.set_profiling(False)
+    got = out.download(np.float32, (spec.D,))
+    routing = {k: b.download(np.float32 if k in ("logits", "weights") else np.int32,
+                             (spec.E if k in ("logits", "counts") else spec.E + 1 if k == "offsets"
+                              else spec.K,))
+               for k, b in bufs.items()}
+    return got, routing, stages
+
+
+def _check_token(name, t, spec, got, routing, ref_t, res_t, dbg, fused):
+    tag = f"{name} t={t} {'fused' if fused else 'chain'}"
+    assert np.array_equal(routing["logits"].view(np.uint32), dbg["logits"][t].view(np.uint32)), tag
+    assert np.array_equal(routing["sel"], dbg["sel"][t]), tag
+    assert np.allclose(routing["weights"], dbg["w"][t], rtol=1e-6, atol=1e-7), tag
+    counts, offsets, perm = _dispatch_one(dbg["sel"][t], spec.E)
+    assert np.array_equal(routing["counts"], counts), tag
+    assert np.array_equal(routing["offsets"], offsets), tag
+    assert np.array_equal(routing["perm"], perm), tag
+    e = rel_l2(got - res_t, ref_t - res_t)
+    assert e <= TOL_REL_L2, (tag, e)
+    return e
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_decode_fused_parity(name):
+    spec = CASES[name]
+    n_tok = 4
+    ctx = M.Context(0)
+    ctx.reserve(n_tok, spec.D, spec.I, spec.E, spec.K)
+    g = W.GpuLayer(ctx, spec)
+    L = oracle_layer_dict(g.download_tables(), spec, g.download_router(), g.bias_host)
+    x = cpu_x(spec, n_tok)
+    res = cpu_x(spec, n_tok, stream=W.S_RES)
+    ref, dbg = O.moe_forward(L, x, res)
+    for t in range(n_tok):
+        got_f, rt_f, st_f = _run_token(ctx, g.layer, spec, x[t], res[t], True)
+        assert "decode1" in st_f, f"fused kernel not taken: {st_f}"
+        got_c, rt_c, st_c = _run_token(ctx, g.layer, spec, x[t], res[t], False)
+        assert "decode1" not in st_c
+        e_f = _check_token(name, t, spec, got_f, rt_f, ref[t], res[t], dbg, True)
+        e_c = _check_token(name, t, spec, got_c, rt_c, ref[t], res[t], dbg, False)
+        e_p = rel_l2(got_f - res[t], got_c - res[t])
+        log(f"{name} t={t}: fused rel-L2 {e_f:.3e} (max-abs {max_abs(got_f, ref[t]):.3e}), "
+            f"chain {e_c:.3e}, fused vs chain {e_p:.3e}")
+        assert e_p <= TOL_PATHS, e_p
+    ctx.close()
+
+
+@pytest.mark.parametrize("pattern", ["all_equal", "half_steps"])
+def test_decode_fused_ties(pattern):
+    """Zero router weights: the logits are the bias exactly, so ties are
+    forced; the pick must be ggml_top_k's (stable descending argsort)."""
+    spec = CASES["md_d1024_q6"]
+    ctx = M.Context(0)
+    ctx.reserve(2, spec.D, spec.I, spec.E, spec.K)
+    g = W.GpuLayer(ctx, spec)
+    rng = np.random.default_rng(11)
+    if pattern == "all_equal":
+        bias = np.full(spec.E, 0.25, np.float32)
+    else:
+        bias = (np.round(rng.standard_normal(spec.E) * 2) / 2).astype(np.float32)
+    rw = np.zeros((spec.E, spec.D), np.float32)
+    rwd, rbd = M.to_device(rw), M.to_device(bias)
+    layer = M.make_layer(spec.D, spec.E, spec.K, spec.I, rwd, rbd, g.tensor("gate"), None, g.tensor("down"),
+                         spec.fused, spec.act)
+    L = oracle_layer_dict(g.download_tables(), spec, rw, bias)
+    x = cpu_x(spec, 2)
+    res = cpu_x(spec, 2, stream=W.S_RES)
+    ref, dbg = O.moe_forward(L, x, res)
+    assert np.array_equal(dbg["sel"][0], np.argsort(-bias, kind="stable")[:spec.K])
+    for t in range(2):
+        got, rt, st = _run_token(ctx, layer, spec, x[t], res[t], True)
+        assert "decode1" in st
+        e = _check_token(f"ties_{pattern}", t, spec, got, rt, ref[t], res[t], dbg, True)
+        log(f"ties {pattern} t={t}: sel {rt['sel'].tolist()} rel-L2 {e:.3e}")
+    ctx.close()
+
+
+def test_decode_fused_shape_changes():
+    """One context, layers of different shapes launched alternately: the block
+    counters are indexed by the layer's shape and must be left at zero by every
+    launch."""
+    a, b = CASES["md_small_q6"], CASES["md_d256_k3"]
+    ctx = M.Context(0)
+    ctx.reserve(2, 512, 512, 8, 3)
+    layers = []
+    for spec in (a, b):
+        g = W.GpuLayer(ctx, spec)
+        L = oracle_layer_dict(g.download_tables(), spec, g.download_router(), g.bias_host)
+        x = cpu_x(spec, 3)
+        res = cpu_x(spec, 3, stream=W.S_RES)
+        ref, dbg = O.moe_forward(L, x, res)
+        layers.append((spec, g, x, res, ref, dbg))
+    for t in range(3):
+        for spec, g, x, res, ref, dbg in layers:
+            got, rt, st = _run_token(ctx, g.layer, spec, x[t], res[t], True)
+            assert "decode1" in st
+            _check_token(f"mixed_{spec.name}", t, spec, got, rt, ref[t], res[t], dbg, True)
+    ctx.close()

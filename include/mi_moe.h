@@ -173,12 +173,26 @@ int mi_moe_ctx_stage_times(mi_moe_ctx *ctx, int max_stages, const char **names, 
                            int *n_stages);
 /* path choice for a token count: 0 = grouped GEMV (decode), 1 = grouped MFMA GEMM */
 int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *ctx, int64_t min_tokens_for_gemm);
-/* single-token calls of mi_moe_forward: 1 (default) = the whole block in one
- * cooperative kernel when the layer fits it (Q4_K gate/up, Q4_K or Q6_K down,
- * top-k <= 8, 16-byte aligned tables), 0 = the separate-kernel chain.  Same
- * results either way; the reference has one graph per step
+/* Schedule of single-token calls of mi_moe_forward.  The fused modes run the
+ * whole block in one kernel of one work-group per CU that synchronizes
+ * through grid barriers, when the layer fits it (Q4_K gate/up, Q4_K or Q6_K
+ * down, top-k <= 8, 16-byte aligned tables); other layers use the chain.
+ *   MI_DECODE_CHAIN              separate kernels
+ *   MI_DECODE_FUSED_COOPERATIVE  fused, cooperative launch: the runtime
+ *                                guarantees all work-groups are resident (default)
+ *   MI_DECODE_FUSED_EXCLUSIVE    fused, plain launch: ~18 us less per call on
+ *                                MI355X, for a GPU that runs nothing else
+ *                                concurrently (two such kernels sharing the GPU
+ *                                could each wait for the other's CUs; the
+ *                                waits are bounded and then return NaN)
+ * Same results in every mode; the reference has one graph per step
  * (moe_decode_driver.hpp:493-514), this only picks the GPU schedule. */
-int mi_moe_ctx_set_fused_decode(mi_moe_ctx *ctx, int on);
+enum {
+    MI_DECODE_CHAIN = 0,
+    MI_DECODE_FUSED_COOPERATIVE = 1,
+    MI_DECODE_FUSED_EXCLUSIVE = 2
+};
+int mi_moe_ctx_set_fused_decode(mi_moe_ctx *ctx, int mode);
 size_t      mi_row_size(int32_t type, int64_t n_per_row);
 const char *mi_moe_status_string(int status);
 int         mi_moe_abi_version(void);

@@ -93,8 +93,10 @@ struct mi_moe_ctx {
     float *z = nullptr;       // [rows][max(D, 2I)]
     int64_t gemm_threshold = 16;
     // single-token fused kernel (k_decode.hip)
-    bool fused_decode = true;
+    int fused_decode = MI_DECODE_FUSED_COOPERATIVE;
     int dec_grid = 0;          // cooperative grid (one WG per CU), 0: unavailable
+    uint64_t *dec_tw = nullptr;
+    uint32_t *dec_epoch = nullptr;
     unsigned long long *dec_sync = nullptr;
     unsigned *dec_err = nullptr;
 
@@ -190,6 +192,7 @@ bool plan_decode1(const mi_moe_ctx *c, const mi_moe_layer *L, const float *x, in
     if (L->gate.type != MI_TYPE_Q4_K || (!L->fused_gate_up && L->up.type != MI_TYPE_Q4_K)) return false;
     if (L->down.type != MI_TYPE_Q4_K && L->down.type != MI_TYPE_Q6_K) return false;
     if (D % QK || I % QK || K > 8 || E > 256) return false;
+    if (E > G || D / QK > E) return false;   // one router row per WG; x-quant WGs also route
     const int64_t NB = D / QK, NBI = I / QK;
     if (!(NB == 1 || NB == 2 || NB == 4 || NB == 8) || NBI > 8) return false;
     auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
@@ -205,6 +208,8 @@ bool plan_decode1(const mi_moe_ctx *c, const mi_moe_layer *L, const float *x, in
     for (int64_t cc = 1; cc <= 64; ++cc)
         if (D % cc == 0 && D / cc <= G) { C = (int)cc; break; }
     if (!C || C * (int64_t)L->down.nb[1] + 15 > DEC_LIMIT_DN_BYTES) return false;
+    const int64_t rows_per_step = 8 / NBI;   // down rows one wave covers per step
+    if ((C + rows_per_step - 1) / rows_per_step > DEC_LIMIT_CSTEPS) return false;
     return true;
 }
 
@@ -222,8 +227,8 @@ int run_decode1(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, const floa
     g.counts = c->disp[0].counts; g.offsets = c->disp[0].offsets; g.perm = c->disp[0].perm;
     g.xq = c->ax.q8; g.xd = c->ax.d8; g.xbs = c->ax.bs;
     g.actf = c->f1;
-    g.sync = c->dec_sync; g.err = c->dec_err;
-    TRY(launch_decode1(g, c->dec_grid, st));
+    g.tw = c->dec_tw; g.epoch = c->dec_epoch; g.sync = c->dec_sync; g.err = c->dec_err;
+    TRY(launch_decode1(g, c->dec_grid, c->fused_decode == MI_DECODE_FUSED_COOPERATIVE, st));
     stage_end(c, "decode1", st);
     return MI_MOE_OK;
 }
@@ -445,7 +450,8 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
     need += carve_size<int8_t>(rows * iq) + carve_size<float>(rows * iq / QK) +
             carve_size<int16_t>(rows * iq / 16) + carve_size<_Float16>(rows * iq);
     need += carve_size<float>(rows * wide) + carve_size<float>(rows * I) + carve_size<float>(rows * wide);
-    need += carve_size<unsigned long long>(DEC_SYNC_WORDS) + carve_size<unsigned>(1);
+    need += carve_size<uint64_t>(DEC_TW_WORDS) + carve_size<uint32_t>(DEC_MAX_GRID) +
+            carve_size<unsigned long long>(DEC_SYNC_WORDS) + carve_size<unsigned>(1);
 
     if (c->ws) {
         (void)hipFree(c->ws);
@@ -484,6 +490,8 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
     c->f1 = carve<float>(q, rows * wide);
     c->f2 = carve<float>(q, rows * I);
     c->z = carve<float>(q, rows * wide);
+    c->dec_tw = carve<uint64_t>(q, DEC_TW_WORDS);
+    c->dec_epoch = carve<uint32_t>(q, DEC_MAX_GRID);
     c->dec_sync = carve<unsigned long long>(q, DEC_SYNC_WORDS);
     c->dec_err = carve<unsigned>(q, 1);
     HIP_TRY(hipMemset(p, 0, need));
@@ -508,7 +516,8 @@ int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *c, int64_t t) {
 
 int mi_moe_ctx_set_fused_decode(mi_moe_ctx *c, int on) {
     if (!c) return MI_MOE_ERR_NULL;
-    c->fused_decode = on != 0;
+    if (on < MI_DECODE_CHAIN || on > MI_DECODE_FUSED_EXCLUSIVE) return MI_MOE_ERR_ARG;
+    c->fused_decode = on;
     return MI_MOE_OK;
 }
 

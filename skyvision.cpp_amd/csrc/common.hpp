@@ -200,8 +200,13 @@ struct AmaxIdx {
     float val;
 };
 __device__ inline AmaxIdx amax_better(AmaxIdx a, AmaxIdx b) {
-    if (b.ax > a.ax || (b.ax == a.ax && b.idx < a.idx)) return b;
-    return a;
+    // selects, not branches (non-short-circuit operators)
+    const bool t = (b.ax > a.ax) | ((b.ax == a.ax) & (b.idx < a.idx));
+    AmaxIdx r;
+    r.ax = t ? b.ax : a.ax;
+    r.idx = t ? b.idx : a.idx;
+    r.val = t ? b.val : a.val;
+    return r;
 }
 __device__ inline AmaxIdx wave_amax_idx(AmaxIdx a, int width = 64) {
     for (int o = width >> 1; o > 0; o >>= 1) {

@@ -30,21 +30,26 @@
 // code.  Routing is exact: the rank form below selects the same experts in
 // the same order as the stable descending argsort of ggml_top_k.
 //
-// Grid barriers and the data that crosses them.  The eight XCDs have
-// separate L2 caches, so values one WG writes for another (logits, the Q8_K
-// of x, the GLU activations) are stored and loaded at device scope (sc1:
-// write-through stores, loads that do not hit a line another XCD made
-// stale), never through a cache flush: an agent-scope fence writes back or
-// invalidates a whole L2 and costs microseconds per WG.
-//
-// The barrier itself is two levels of monotonic 64-bit counters (groups of
-// 16 WGs, then the groups) and a release word holding the barrier round:
-// the last arrival of the last group publishes the round, everyone polls
-// that word.  Each barrier adds a fixed amount to every counter, so nothing
-// is reset between launches and a captured graph replays correctly.  The
-// launch is cooperative, so all WGs are resident; the wait is still bounded,
-// and a timed-out wait sets an error word that turns the output into NaN
-// instead of hanging the GPU.
+// Synchronization.  Values one WG hands to another are written through to
+// memory (relaxed agent-scope atomic stores: sc1) and read with ordinary
+// loads: a kernel launch leaves no stale L2 line behind, and within the
+// launch an XCD's first read of such a line comes after its writer's store
+// landed, so the one L2 copy the XCD's WGs share is fresh (uncached reads
+// would send ~10^6 small requests per launch to the few memory channels
+// holding these buffers).  Two hand-offs:
+//   logits -> every WG: each logit is a 64-bit word tagged with the launch
+//     epoch; a WG polls the E words (one coalesced wave load per try) instead
+//     of meeting a barrier.  The router WGs that also quantize x store their
+//     logit only after their Q8_K of x is out, so ready logits imply ready x.
+//     The epoch is per WG (read at start, stored +1 at the end), so all
+//     epochs agree at every launch, with no atomics and no reset.
+//   activations -> every WG: a grid barrier of two levels of monotonic
+//     counters (16-WG groups, then groups) and a release word holding the
+//     round; nothing is reset between launches.
+// Both keep a captured graph replaying correctly.  Producers and consumers
+// must be resident together: the launch is cooperative, or plain on a GPU
+// that runs nothing else.  Waits are bounded; a WG whose wait gives up
+// writes NaN and sets an error word instead of hanging the GPU.
 #include "act.hpp"
 #include "common.hpp"
 #include "launch.hpp"
@@ -62,44 +67,49 @@ constexpr int DEC_KMAX = 8;         // slots: one wave each in the down phase
 constexpr int DEC_PMAX = 64;        // (h, g) row pairs per WG
 constexpr int DEC_CMAX = 64;        // down columns per WG
 constexpr unsigned DEC_SPIN_LIMIT = 1u << 20;
-constexpr int DEC_SYNC_GROUPS = DEC_SYNC_MAX_GROUPS;
+constexpr int DEC_SYNC_GROUPS = DEC_MAX_GRID / 16;
 
-// ---------------------------------------------------------------- shared data
-// Relaxed agent-scope atomics: the compiler emits them with cache policy sc1
-// (stores write through to memory, loads do not hit a line another XCD made
-// stale).  16 bytes are read as two 8-byte atomics.
+// ---------------------------------------------------------------- tagged words
+__device__ inline void tw_store(uint64_t *p, uint32_t tag, uint32_t v) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint64_t tw_load(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// the data of N words once all carry `tag` (loads issued together, only the
+// stale ones re-read); ok is cleared if the poll gives up
+template <int N>
+__device__ inline void tw_poll(const uint64_t *const (&p)[N], uint32_t tag, uint32_t (&out)[N], bool &ok) {
+    uint64_t w[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) w[i] = tw_load(p[i]);
+    unsigned n = 0;
+    for (;;) {
+        bool all = true;
+#pragma unroll
+        for (int i = 0; i < N; ++i) all = all && (uint32_t)(w[i] >> 32) == tag;
+        if (all) break;
+        if (++n > DEC_SPIN_LIMIT) {
+            ok = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+            if ((uint32_t)(w[i] >> 32) != tag) w[i] = tw_load(p[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = (uint32_t)w[i];
+}
 __device__ inline void st_dev4(void *base, uint32_t off, uint32_t v) {
     __hip_atomic_store((uint32_t *)((uint8_t *)base + off), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ inline uint32_t ld_dev4(const void *base, uint32_t off) {
-    return __hip_atomic_load((const uint32_t *)((const uint8_t *)base + off), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline u32x4 ld_dev16(const void *base, uint32_t off) {
-    const uint64_t *p = (const uint64_t *)((const uint8_t *)base + off);
-    const uint64_t a = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t b = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    u32x4 r;
-    r[0] = (uint32_t)a;
-    r[1] = (uint32_t)(a >> 32);
-    r[2] = (uint32_t)b;
-    r[3] = (uint32_t)(b >> 32);
-    return r;
-}
-// 16-bit value at an even byte offset, read through its aligned word
-__device__ inline uint16_t ld_dev2(const void *base, uint32_t off) {
-    const uint32_t w = ld_dev4(base, off & ~3u);
-    return (uint16_t)((off & 2u) ? (w >> 16) : (w & 0xffffu));
-}
-// reinterpret a 32-bit value (passed by value: this toolchain's
-// __builtin_bit_cast of an ext-vector element reads element 0)
-__device__ inline float as_float(uint32_t u) { return __builtin_bit_cast(float, u); }
 
-// ---------------------------------------------------------------- barrier
-// Counters in the context's workspace, 256 bytes apart: group g at sync[32 g],
-// the top counter at sync[32 * DEC_SYNC_GROUPS], the release word after it.
+// grid barrier; every thread of every WG calls it.  Counters 256 bytes apart:
+// group g at sync[32 g], the top counter at sync[32 * DEC_SYNC_GROUPS], the
+// release word after it.  ok is cleared if the wait gives up.
 constexpr int DEC_GROUP = 16;
-__device__ inline void dec_grid_barrier(unsigned long long *sync, unsigned *err) {
+__device__ inline void dec_grid_barrier(unsigned long long *sync, bool &ok) {
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's stores are done
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -118,7 +128,7 @@ __device__ inline void dec_grid_barrier(unsigned long long *sync, unsigned *err)
         unsigned n = 0;
         while (__hip_atomic_load(rel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < round) {
             if (++n > DEC_SPIN_LIMIT) {
-                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok = false;
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
@@ -126,6 +136,10 @@ __device__ inline void dec_grid_barrier(unsigned long long *sync, unsigned *err)
     }
     __syncthreads();
 }
+
+// reinterpret a 32-bit value (passed by value: this toolchain's
+// __builtin_bit_cast of an ext-vector element reads element 0)
+__device__ inline float as_float(uint32_t u) { return __builtin_bit_cast(float, u); }
 
 // workgroup barrier that does not wait for outstanding global loads / DMA
 __device__ inline void dec_lds_barrier() {
@@ -137,7 +151,7 @@ __device__ inline void dec_lds_barrier() {
 // logit of expert e: the router's fixed fp64 order (64-wide chunk c: sum over
 // s = 0..15, g = 0..3 of W[64c+16g+s] * x[64c+16g+s]; chunk partials added in
 // chunk order from 0.0; fl32; + bias in fp32).  Lane c owns chunk c.
-__device__ inline void dec_router_row(const DecArgs &g, int e, int lane) {
+__device__ inline float dec_router_row(const DecArgs &g, int e, int lane) {
     const int D = g.D;
     const int nch = (D + 63) >> 6;
     double part = 0.0;
@@ -178,11 +192,9 @@ __device__ inline void dec_router_row(const DecArgs &g, int e, int lane) {
                            (uint32_t)__builtin_amdgcn_readlane((int)plo, c);
         acc = acc + __builtin_bit_cast(double, v);
     }
-    if (lane == 0) {
-        float v = (float)acc;
-        if (g.rb) v = v + g.rb[e];
-        st_dev4(g.logits, 4u * e, __builtin_bit_cast(uint32_t, v));
-    }
+    float v = (float)acc;
+    if (g.rb) v = v + g.rb[e];
+    return v;
 }
 
 // Q8_K of x block b (natural order, ggml block_q8_K fields split), written
@@ -198,7 +210,8 @@ __device__ inline void dec_q8k_x(const DecArgs &g, int b, int lane) {
     const int s = q8k_bsum16(q);
     const int s_hi = __shfl_down(s, 4, 64);
     if ((lane & 7) == 0)
-        st_dev4(g.xbs, 2u * (b * 16 + (lane >> 2)), (uint32_t)(uint16_t)(int16_t)s | ((uint32_t)(uint16_t)(int16_t)s_hi << 16));
+        st_dev4(g.xbs, 2u * (b * 16 + (lane >> 2)),
+                (uint32_t)(uint16_t)(int16_t)s | ((uint32_t)(uint16_t)(int16_t)s_hi << 16));
 }
 
 // ---------------------------------------------------------------- dots
@@ -210,17 +223,6 @@ struct Q4X {
     int bsa, bsb;    // their 16-value block sums
     float dx;
 };
-// the same piece of the Q8_K of x written by phase A, read at device scope
-__device__ inline Q4X dec_q4x_load_dev(const DecArgs &g, int b, int sl) {
-    const int c = sl >> 1, l0 = 16 * (sl & 1);
-    Q4X x;
-    x.xa = ld_dev16(g.xq, b * QK + 64 * c + l0);
-    x.xb = ld_dev16(g.xq, b * QK + 64 * c + 32 + l0);
-    x.bsa = (int16_t)ld_dev2(g.xbs, 2u * (b * 16 + 4 * c + (sl & 1)));
-    x.bsb = (int16_t)ld_dev2(g.xbs, 2u * (b * 16 + 4 * c + 2 + (sl & 1)));
-    x.dx = as_float(ld_dev4(g.xd, 4u * b));
-    return x;
-}
 __device__ inline Q4X dec_q4x_load(const int8_t *xq, const int16_t *xbs, const float *xd, int b, int sl) {
     const int c = sl >> 1, l0 = 16 * (sl & 1);
     Q4X x;
@@ -349,7 +351,12 @@ __device__ inline DecChunk dec_chunk(const ExpertMat &m, int e, int64_t row0, in
 }
 
 // ---------------------------------------------------------------- kernel
-template <int DT>
+constexpr int DEC_RSTEPS = 16;   // row steps per wave in the gate/up phase (R / RPS)
+constexpr int DEC_CSTEPS = DEC_LIMIT_CSTEPS;   // row steps per wave in the down phase (C / RPSD)
+
+// NBI = I / 256: blocks per down row (compile time, so the per-slot Q8_K and
+// the down reductions unroll)
+template <int DT, int NBI>
 __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
     __shared__ __attribute__((aligned(1024))) uint8_t s_gu[DEC_WAVES][DEC_GU_SEG * 1024];
     __shared__ __attribute__((aligned(1024))) uint8_t s_dn[DEC_KMAX][DEC_DN_SEG * 1024];
@@ -358,31 +365,41 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
     __shared__ float s_val[DEC_KMAX], s_w[DEC_KMAX];
     __shared__ float s_hg[2 * DEC_PMAX];
     __shared__ float s_z[DEC_KMAX * DEC_CMAX];
+    __shared__ int s_fail;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wg = blockIdx.x, G = gridDim.x;
     const int D = g.D, E = g.E, K = g.K, I = g.I;
-    const int NB = D / QK, NBI = I / QK;
+    const int NB = D / QK;
+    // this launch's epoch (see the header comment)
+    const uint32_t tag = __hip_atomic_load(g.epoch + wg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    bool ok = true;
+    if (tid == 0) s_fail = 0;
 
-    // ---- A: router rows and Q8_K of x
-    if (wave == 0) {
-        for (int e = wg; e < E; e += G) dec_router_row(g, e, lane);
-    } else if (wave == 1) {
-        for (int b = wg; b < NB; b += G) dec_q8k_x(g, b, lane);
-    }
-    dec_grid_barrier(g.sync, g.err);
+    // ---- A: router row wg (wave 0) and Q8_K of x block wg (wave 1); the
+    // logit is published only once this WG's Q8_K of x is out
+    float logit = 0.f;
+    if (wave == 0 && wg < E) logit = dec_router_row(g, wg, lane);
+    else if (wave == 1 && wg < NB) dec_q8k_x(g, wg, lane);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    dec_lds_barrier();
+    if (wave == 0 && lane == 0 && wg < E) tw_store(g.tw + DEC_TW_LOGIT + wg, tag, __builtin_bit_cast(uint32_t, logit));
 
     // ---- B: routing (every WG), DMA of its gate/up and down rows
-    float lv = 0.f;
-    if (tid < E) lv = as_float(ld_dev4(g.logits, 4u * tid));
-    // this lane's activation piece: row group of LPR = 8*NB lanes, block bq, piece sl
-    const int LPR = 8 * NB, RPS = 64 / LPR;
-    const int rr = lane / LPR, bq = (lane % LPR) >> 3, sl = lane & 7;
-    const Q4X xg = dec_q4x_load_dev(g, bq, sl);
-    if (tid < E) s_logit[tid] = lv;
+    if (tid < E) {
+        const uint64_t *const p[1] = {g.tw + DEC_TW_LOGIT + tid};
+        uint32_t v[1];
+        tw_poll<1>(p, tag, v, ok);
+        s_logit[tid] = as_float(v[0]);
+    }
     if (tid < DEC_KMAX) s_sel[tid] = tid < K ? tid : 0;
     dec_lds_barrier();
+    // this lane's activation piece: row group of LPR = 8*NB lanes, block bq,
+    // piece sl (every logit is in, so the Q8_K of x is too)
+    const int LPR = 8 * NB, RPS = 64 / LPR;
+    const int rr = lane / LPR, bq = (lane % LPR) >> 3, sl = lane & 7;
+    const Q4X xg = dec_q4x_load(g.xq, g.xbs, g.xd, bq, sl);
     {
         // rank of expert e = #{j : l_j > l_e} + #{j < e : l_j == l_e}; the K
         // lowest ranks in rank order are ggml_top_k's stable descending pick
@@ -449,6 +466,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
         }
     }
     if (wg == 0) {
+        if (tid < E) g.logits[tid] = s_logit[tid];
         // single-token dispatch: one list entry per selected expert
         for (int e = tid; e < E; e += DEC_THREADS) {
             int cnt = 0, below = 0, slot = 0;
@@ -466,16 +484,40 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
         if (tid == 0) g.offsets[E] = K;
     }
 
-    // gate/up dots: wave v owns R consecutive rows (h for v < 4, g for v >= 4)
+    // gate/up dots: wave v owns R consecutive rows (h for v < 4, g for v >= 4);
+    // every row's piece first, then the lane-group sums of all rows together
+    // (independent exchanges overlap instead of queueing one row at a time)
     if (do_b) {
-        const uint32_t shift = 0;   // Q4_K tables are 16-byte aligned
-        const int64_t rb = (int64_t)NB * Q4K_BYTES;
-        for (int r0 = 0; r0 < R; r0 += RPS) {
-            const int r = r0 + rr;
-            float acc = 0.f;
-            if (r < R) acc = dec_q4_piece(s_gu[wave] + shift + r * rb + bq * Q4K_BYTES, sl, xg);
-            for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, 64);
-            if ((lane % LPR) == 0 && r < R) s_hg[(wave >> 2) * P + (wave & 3) * R + r] = acc;
+        const int64_t rb = (int64_t)NB * Q4K_BYTES;   // Q4_K tables are 16-byte aligned: no shift
+        float acc[DEC_RSTEPS];
+#pragma unroll
+        for (int j = 0; j < DEC_RSTEPS; ++j) {
+            acc[j] = 0.f;
+            const int r = j * RPS + rr;
+            if (j * RPS < R && r < R) acc[j] = dec_q4_piece(s_gu[wave] + r * rb + bq * Q4K_BYTES, sl, xg);
+        }
+#pragma unroll
+        for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += dpp_f<0xB1>(acc[j]);
+#pragma unroll
+        for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += dpp_f<0x4E>(acc[j]);
+#pragma unroll
+        for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += dpp_f<0x141>(acc[j]);
+        if (LPR >= 16) {
+#pragma unroll
+            for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += dpp_f<0x140>(acc[j]);
+        }
+        if (LPR >= 32) {
+#pragma unroll
+            for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += __shfl_xor(acc[j], 16, 64);
+        }
+        if (LPR >= 64) {
+#pragma unroll
+            for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += __shfl_xor(acc[j], 32, 64);
+        }
+#pragma unroll
+        for (int j = 0; j < DEC_RSTEPS; ++j) {
+            const int r = j * RPS + rr;
+            if (j * RPS < R && r < R && (lane % LPR) == 0) s_hg[(wave >> 2) * P + (wave & 3) * R + r] = acc[j];
         }
     }
 #pragma unroll
@@ -485,7 +527,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
         const float a = act_pair(g.act, s_hg[tid], s_hg[P + tid]);
         st_dev4(g.actf, 4u * (uint32_t)(kB * I + i0 + tid), __builtin_bit_cast(uint32_t, a));
     }
-    dec_grid_barrier(g.sync, g.err);
+    dec_grid_barrier(g.sync, ok);
 
     // ---- C: Q8_K of slot k = wave's activations, down rows, weighted combine
     if (do_c && wave < K) {
@@ -496,23 +538,22 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
         int8_t *aq = (int8_t *)s_gu[k];
         float *ad = (float *)(s_gu[k] + 2048);
         int16_t *abs_ = (int16_t *)(s_gu[k] + 2048 + 64);
-        u32x4 av[8];
+        float4_t av[NBI];
 #pragma unroll
-        for (int b = 0; b < 8; ++b)
-            if (b < NBI) av[b] = ld_dev16(g.actf, 4u * (uint32_t)(k * I + b * QK + 4 * lane));
+        for (int b = 0; b < NBI; ++b) av[b] = *(const float4_t *)(g.actf + k * I + b * QK + 4 * lane);
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            if (b < NBI) {
-                const float v[4] = {as_float(av[b][0]), as_float(av[b][1]), as_float(av[b][2]), as_float(av[b][3])};
-                int q[4];
-                const float d = q8k_wave(v, lane, q);
-                *(uint32_t *)(aq + b * QK + 4 * lane) = pack_i8x4(q);
-                if (lane == 0) ad[b] = d;
-                const int bs = q8k_bsum16(q);
-                if ((lane & 3) == 0) abs_[b * 16 + (lane >> 2)] = (int16_t)bs;
-            }
+        for (int b = 0; b < NBI; ++b) {
+            const float4_t a4 = av[b];
+            const float v[4] = {a4.x, a4.y, a4.z, a4.w};
+            int q[4];
+            const float d = q8k_wave(v, lane, q);
+            *(uint32_t *)(aq + b * QK + 4 * lane) = pack_i8x4(q);
+            if (lane == 0) ad[b] = d;
+            const int bs = q8k_bsum16(q);
+            if ((lane & 3) == 0) abs_[b * 16 + (lane >> 2)] = (int16_t)bs;
         }
-        const int LPRD = 8 * NBI, RPSD = 64 / LPRD;
+        constexpr int LPRD = 8 * NBI, RPSD = 64 / LPRD;
+        constexpr bool POW2 = (NBI & (NBI - 1)) == 0;
         const int rd = lane / LPRD, bd = (lane % LPRD) >> 3;
         const bool lane_ok = rd < RPSD;
         const int base_lane = (lane_ok ? rd : 0) * LPRD;
@@ -521,59 +562,114 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
         Q6X x6;
         if constexpr (DT == 12) x4 = dec_q4x_load(aq, abs_, ad, lane_ok ? bd : 0, sl);
         else x6 = dec_q6x_load(aq, ad, lane_ok ? bd : 0, sl);
-        const int bbytes = DT == 12 ? Q4K_BYTES : Q6K_BYTES;
-        for (int c0 = 0; c0 < C; c0 += RPSD) {
-            const int c = c0 + rd;
-            const bool ok = lane_ok && c < C;
-            float acc = 0.f;
-            if (ok) {
+        constexpr int bbytes = DT == 12 ? Q4K_BYTES : Q6K_BYTES;
+        float acc[DEC_CSTEPS];
+#pragma unroll
+        for (int j = 0; j < DEC_CSTEPS; ++j) {
+            acc[j] = 0.f;
+            const int c = j * RPSD + rd;
+            if (j * RPSD < C && lane_ok && c < C) {
                 const uint32_t boff = dn_shift + (uint32_t)(c * rbd) + (uint32_t)(bd * bbytes);
-                if constexpr (DT == 12) acc = dec_q4_piece(s_dn[k] + boff, sl, x4);
-                else acc = dec_q6_piece(s_dn[k], boff, sl, x6);
+                if constexpr (DT == 12) acc[j] = dec_q4_piece(s_dn[k] + boff, sl, x4);
+                else acc[j] = dec_q6_piece(s_dn[k], boff, sl, x6);
             }
-            acc += __shfl_xor(acc, 1, 64);
-            acc += __shfl_xor(acc, 2, 64);
-            acc += __shfl_xor(acc, 4, 64);
-            float tot = 0.f;
-            for (int b = 0; b < NBI; ++b) tot += __shfl(acc, base_lane + 8 * b, 64);
-            if (ok && (lane % LPRD) == 0) s_z[k * C + c] = tot;
+        }
+        // sum the 8 piece lanes of each block, then the NBI blocks of the row
+#pragma unroll
+        for (int j = 0; j < DEC_CSTEPS; ++j) acc[j] += dpp_f<0xB1>(acc[j]);
+#pragma unroll
+        for (int j = 0; j < DEC_CSTEPS; ++j) acc[j] += dpp_f<0x4E>(acc[j]);
+#pragma unroll
+        for (int j = 0; j < DEC_CSTEPS; ++j) acc[j] += dpp_f<0x141>(acc[j]);
+        if constexpr (POW2) {
+            if constexpr (LPRD >= 16) {
+#pragma unroll
+                for (int j = 0; j < DEC_CSTEPS; ++j) acc[j] += dpp_f<0x140>(acc[j]);
+            }
+            if constexpr (LPRD >= 32) {
+#pragma unroll
+                for (int j = 0; j < DEC_CSTEPS; ++j) acc[j] += __shfl_xor(acc[j], 16, 64);
+            }
+            if constexpr (LPRD >= 64) {
+#pragma unroll
+                for (int j = 0; j < DEC_CSTEPS; ++j) acc[j] += __shfl_xor(acc[j], 32, 64);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < DEC_CSTEPS; ++j) {
+                if (j * RPSD < C) {
+                    float tot = 0.f;
+#pragma unroll
+                    for (int b = 0; b < NBI; ++b) tot += __shfl(acc[j], base_lane + 8 * b, 64);
+                    acc[j] = tot;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < DEC_CSTEPS; ++j) {
+            const int c = j * RPSD + rd;
+            if (j * RPSD < C && lane_ok && c < C && (lane % LPRD) == 0) s_z[k * C + c] = acc[j];
         }
     }
+    if (!ok) s_fail = 1;
     dec_lds_barrier();
+    const bool failed = s_fail != 0;
     if (do_c && tid < C) {
         double s = 0.0;
         for (int k = 0; k < K; ++k) s = s + (double)(s_z[k * C + tid] * s_w[k]);
         const float moe = (float)s;
         float v = g.res ? g.res[n0 + tid] + moe : moe;
-        if (__hip_atomic_load(g.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) v = __builtin_nanf("");
+        if (failed) v = __builtin_nanf("");
         g.out[n0 + tid] = v;
+    }
+    if (tid == 0) {
+        if (failed) __hip_atomic_store(g.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(g.epoch + wg, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-int launch_decode1(const DecArgs &g, int grid, hipStream_t st) {
+template <int DT>
+static const void *decode1_fn(int nbi) {
+    switch (nbi) {
+    case 1: return (const void *)k_decode1<DT, 1>;
+    case 2: return (const void *)k_decode1<DT, 2>;
+    case 3: return (const void *)k_decode1<DT, 3>;
+    case 4: return (const void *)k_decode1<DT, 4>;
+    case 5: return (const void *)k_decode1<DT, 5>;
+    case 6: return (const void *)k_decode1<DT, 6>;
+    case 7: return (const void *)k_decode1<DT, 7>;
+    case 8: return (const void *)k_decode1<DT, 8>;
+    default: return nullptr;
+    }
+}
+
+int launch_decode1(const DecArgs &g, int grid, bool cooperative, hipStream_t st) {
+    const int nbi = g.I / QK;
+    const void *fn = g.down.type == 12 ? decode1_fn<12>(nbi) : g.down.type == 14 ? decode1_fn<14>(nbi) : nullptr;
+    if (!fn) return -3;
     void *args[] = {(void *)&g};
-    hipError_t e;
-    if (g.down.type == 12)
-        e = hipLaunchCooperativeKernel((const void *)k_decode1<12>, dim3(grid), dim3(DEC_THREADS), args, 0, st);
-    else if (g.down.type == 14)
-        e = hipLaunchCooperativeKernel((const void *)k_decode1<14>, dim3(grid), dim3(DEC_THREADS), args, 0, st);
-    else
-        return -3;
+    const hipError_t e = cooperative
+                             ? hipLaunchCooperativeKernel(fn, dim3(grid), dim3(DEC_THREADS), args, 0, st)
+                             : hipLaunchKernel(fn, dim3(grid), dim3(DEC_THREADS), args, 0, st);
     if (e != hipSuccess) return record_hip_error(e);
     return hip_check_launch();
 }
 
 int decode1_max_grid(int device, int *grid) {
-    int cus = 0, per = 0;
+    int cus = 0;
     hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
     if (e != hipSuccess) return record_hip_error(e);
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_decode1<14>, DEC_THREADS, 0);
-    if (e != hipSuccess) return record_hip_error(e);
-    int per12 = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per12, (const void *)k_decode1<12>, DEC_THREADS, 0);
-    if (e != hipSuccess) return record_hip_error(e);
-    *grid = cus * imin(imin(per, per12), 1);
-    if (*grid > DEC_GROUP * DEC_SYNC_MAX_GROUPS) *grid = 0;   // more WGs than barrier groups
+    int per = 1;
+    for (int dt = 12; dt <= 14; dt += 2)
+        for (int nbi = 1; nbi <= 8; ++nbi) {
+            int p = 0;
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&p, dt == 12 ? decode1_fn<12>(nbi) : decode1_fn<14>(nbi),
+                                                             DEC_THREADS, 0);
+            if (e != hipSuccess) return record_hip_error(e);
+            per = imin(per, p);
+        }
+    *grid = cus * per;   // one WG per CU
+    if (*grid > DEC_MAX_GRID) *grid = 0;
     return 0;
 }
 

@@ -157,14 +157,20 @@ struct DecArgs {
     float *xd;
     int16_t *xbs;
     float *actf;                  // GLU output fp32 [K][I]
+    uint64_t *tw;                 // epoch-tagged logits [E]
+    uint32_t *epoch;              // [grid] per-WG launch epochs
     unsigned long long *sync;     // grid barrier counters (only grow), DEC_SYNC_WORDS
-    unsigned *err;                // set by a timed-out barrier wait
+    unsigned *err;                // set when a wait gave up (output is NaN)
 };
-constexpr int DEC_SYNC_MAX_GROUPS = 64;                       // up to 1024 WGs
-constexpr int DEC_SYNC_WORDS = 32 * (DEC_SYNC_MAX_GROUPS + 2);   // 256 B per counter
+constexpr int DEC_TW_LOGIT = 0, DEC_TW_WORDS = 256;
+constexpr int DEC_MAX_GRID = 1024;
+constexpr int DEC_SYNC_WORDS = 32 * (DEC_MAX_GRID / 16 + 2);   // 256 B per counter
 constexpr int DEC_LIMIT_GU_BYTES = 9 * 1024;   // LDS per wave of gate/up rows
 constexpr int DEC_LIMIT_DN_BYTES = 7 * 1024;   // LDS per slot of down rows
-int launch_decode1(const DecArgs &g, int grid, hipStream_t st);
+constexpr int DEC_LIMIT_CSTEPS = 16;           // down row steps per wave
+// cooperative: hipLaunchCooperativeKernel (residency guaranteed by the runtime);
+// otherwise a plain launch that relies on the GPU running nothing else
+int launch_decode1(const DecArgs &g, int grid, bool cooperative, hipStream_t st);
 // work-groups of the cooperative grid (one per CU), 0 if it cannot be resident
 int decode1_max_grid(int device, int *grid);
 

@@ -7,6 +7,62 @@
 
 namespace mimoe {
 
+// ---------------------------------------------------------------- lane exchange
+// DPP moves (no LDS round trip) for reductions inside 16-lane rows.  Each
+// control pairs every lane with one partner; applied in this order the four
+// reduce groups of 2, 4, 8 and 16 lanes, and every lane of the group ends up
+// with the result:
+//   0xB1  quad_perm [1,0,3,2]   (lane ^ 1)
+//   0x4E  quad_perm [2,3,0,1]   (lane ^ 2)
+//   0x141 row_half_mirror       (lane i <-> 7 - i within 8)
+//   0x140 row_mirror            (lane i <-> 15 - i within 16)
+template <int CTRL>
+__device__ inline int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+    return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+
+// sum over aligned groups of `width` lanes (8, 16, 32 or 64), in every lane
+__device__ inline float group_sum(float v, int width) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    if (width >= 16) v += dpp_f<0x140>(v);
+    if (width >= 32) v += __shfl_xor(v, 16, 64);
+    if (width >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+template <int CTRL>
+__device__ inline AmaxIdx amax_dpp(AmaxIdx a) {
+    AmaxIdx b;
+    b.ax = dpp_f<CTRL>(a.ax);
+    b.idx = dpp_i<CTRL>(a.idx);
+    b.val = dpp_f<CTRL>(a.val);
+    return amax_better(a, b);
+}
+__device__ inline AmaxIdx amax_xor(AmaxIdx a, int o) {
+    AmaxIdx b;
+    b.ax = __shfl_xor(a.ax, o, 64);
+    b.idx = __shfl_xor(a.idx, o, 64);
+    b.val = __shfl_xor(a.val, o, 64);
+    return amax_better(a, b);
+}
+// (|x| max, first index) over the wave.  amax_better is a total order (ties
+// in |x| go to the lower index), so the result does not depend on the
+// reduction tree.
+__device__ inline AmaxIdx wave_amax_idx_fast(AmaxIdx a) {
+    a = amax_dpp<0xB1>(a);
+    a = amax_dpp<0x4E>(a);
+    a = amax_dpp<0x141>(a);
+    a = amax_dpp<0x140>(a);
+    a = amax_xor(a, 16);
+    return amax_xor(a, 32);
+}
+
 // Q8_K of one 256-value block held by one wave, lane l holding the values at
 // 4l .. 4l+3 (ggml quantize_row_q8_K_ref): the first value with the largest
 // |x| sets iscale = -127 / x, q = min(127, nearest_int(iscale * v)),
@@ -15,7 +71,7 @@ __device__ inline float q8k_wave(const float (&v)[4], int lane, int (&q)[4]) {
     AmaxIdx a{-1.f, 1 << 30, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) a = amax_better(a, AmaxIdx{fabsf(v[j]), 4 * lane + j, v[j]});
-    a = wave_amax_idx(a);
+    a = wave_amax_idx_fast(a);
 #pragma unroll
     for (int j = 0; j < 4; ++j) q[j] = 0;
     if (a.ax == 0.f) return 0.f;
@@ -29,8 +85,8 @@ __device__ inline float q8k_wave(const float (&v)[4], int lane, int (&q)[4]) {
 // every lane of the group
 __device__ inline int q8k_bsum16(const int (&q)[4]) {
     int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
+    s += dpp_i<0xB1>(s);
+    s += dpp_i<0x4E>(s);
     return s;
 }
 

@@ -14,6 +14,8 @@ import numpy as np
 HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "libmimoe.so"
 
+DECODE_CHAIN, DECODE_FUSED_COOPERATIVE, DECODE_FUSED_EXCLUSIVE = 0, 1, 2
+
 TYPE_F32, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K, TYPE_I32 = 0, 1, 12, 14, 26
 ACT_SILU, ACT_GELU_ERF_GP1, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2, 3
 GATING_SOFTMAX_TOPK = 0
@@ -225,8 +227,10 @@ class Context:
     def set_gemm_threshold(self, t: int) -> None:
         call("mi_moe_ctx_set_gemm_threshold", self.h, t)
 
-    def set_fused_decode(self, on: bool) -> None:
-        call("mi_moe_ctx_set_fused_decode", self.h, 1 if on else 0)
+    def set_fused_decode(self, mode) -> None:
+        """False / DECODE_CHAIN, True / DECODE_FUSED_COOPERATIVE, DECODE_FUSED_EXCLUSIVE"""
+        m = DECODE_FUSED_COOPERATIVE if mode is True else DECODE_CHAIN if mode is False else int(mode)
+        call("mi_moe_ctx_set_fused_decode", self.h, m)
 
     def set_profiling(self, on: bool) -> None:
         call("mi_moe_ctx_set_profiling", self.h, int(on))

@@ -10,9 +10,10 @@ on a Q8_K rounding boundary can land on either side: on the full config-0
 layer one such flip in 8192 codes moves the output by 1.1e-3 (measured).  The
 two schedules must agree to a few such flips (rel-L2 <= 5e-3).
 
-Consecutive launches on one context reuse the kernel's barrier and block
-counters, so every case runs several tokens back to back, and one case
-switches layer shapes between launches.
+Consecutive launches on one context keep counting on the kernel's barrier
+counters, so every case runs several tokens back to back, in both launch
+modes (cooperative and exclusive) and interleaved with the chain, and one
+case switches layer shapes between launches.
 """
 import ctypes as C
 import sys
@@ -67,8 +68,8 @@ def _dispatch_one(sel_t, E):
     return counts, offsets, perm
 
 
-def _run_token(ctx, layer, spec, x_row, res_row, fused):
-    ctx.set_fused_decode(fused)
+def _run_token(ctx, layer, spec, x_row, res_row, mode):
+    ctx.set_fused_decode(mode)
     ctx.set_profiling(True)
     xd, rd = M.to_device(x_row[None, :]), M.to_device(res_row[None, :])
     out = M.DeviceBuffer(4 * spec.D)
@@ -110,11 +111,16 @@ def test_decode_fused_parity(name):
     res = cpu_x(spec, n_tok, stream=W.S_RES)
     ref, dbg = O.moe_forward(L, x, res)
     for t in range(n_tok):
-        got_f, rt_f, st_f = _run_token(ctx, g.layer, spec, x[t], res[t], True)
+        got_f, rt_f, st_f = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED_COOPERATIVE)
         assert "decode1" in st_f, f"fused kernel not taken: {st_f}"
-        got_c, rt_c, st_c = _run_token(ctx, g.layer, spec, x[t], res[t], False)
+        got_x, rt_x, st_x = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED_EXCLUSIVE)
+        assert "decode1" in st_x
+        got_c, rt_c, st_c = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_CHAIN)
         assert "decode1" not in st_c
         e_f = _check_token(name, t, spec, got_f, rt_f, ref[t], res[t], dbg, True)
+        _check_token(name, t, spec, got_x, rt_x, ref[t], res[t], dbg, True)
+        # the two launch modes run the same kernel: same bits
+        assert np.array_equal(got_f.view(np.uint32), got_x.view(np.uint32))
         e_c = _check_token(name, t, spec, got_c, rt_c, ref[t], res[t], dbg, False)
         e_p = rel_l2(got_f - res[t], got_c - res[t])
         log(f"{name} t={t}: fused rel-L2 {e_f:.3e} (max-abs {max_abs(got_f, ref[t]):.3e}), "
@@ -146,7 +152,7 @@ def test_decode_fused_ties(pattern):
     ref, dbg = O.moe_forward(L, x, res)
     assert np.array_equal(dbg["sel"][0], np.argsort(-bias, kind="stable")[:spec.K])
     for t in range(2):
-        got, rt, st = _run_token(ctx, layer, spec, x[t], res[t], True)
+        got, rt, st = _run_token(ctx, layer, spec, x[t], res[t], M.DECODE_FUSED_EXCLUSIVE)
         assert "decode1" in st
         e = _check_token(f"ties_{pattern}", t, spec, got, rt, ref[t], res[t], dbg, True)
         log(f"ties {pattern} t={t}: sel {rt['sel'].tolist()} rel-L2 {e:.3e}")
@@ -154,9 +160,8 @@ def test_decode_fused_ties(pattern):
 
 
 def test_decode_fused_shape_changes():
-    """One context, layers of different shapes launched alternately: the block
-    counters are indexed by the layer's shape and must be left at zero by every
-    launch."""
+    """One context, layers of different shapes launched alternately through
+    the same workspace and barrier counters."""
     a, b = CASES["md_small_q6"], CASES["md_d256_k3"]
     ctx = M.Context(0)
     ctx.reserve(2, 512, 512, 8, 3)
@@ -170,7 +175,7 @@ def test_decode_fused_shape_changes():
         layers.append((spec, g, x, res, ref, dbg))
     for t in range(3):
         for spec, g, x, res, ref, dbg in layers:
-            got, rt, st = _run_token(ctx, g.layer, spec, x[t], res[t], True)
+            got, rt, st = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED_EXCLUSIVE if t % 2 else M.DECODE_FUSED_COOPERATIVE)
             assert "decode1" in st
             _check_token(f"mixed_{spec.name}", t, spec, got, rt, ref[t], res[t], dbg, True)
     ctx.close()

@@ -208,8 +208,7 @@ bool plan_decode1(const mi_moe_ctx *c, const mi_moe_layer *L, const float *x, in
     for (int64_t cc = 1; cc <= 64; ++cc)
         if (D % cc == 0 && D / cc <= G) { C = (int)cc; break; }
     if (!C || C * (int64_t)L->down.nb[1] + 15 > DEC_LIMIT_DN_BYTES) return false;
-    const int64_t rows_per_step = 8 / NBI;   // down rows one wave covers per step
-    if ((C + rows_per_step - 1) / rows_per_step > DEC_LIMIT_CSTEPS) return false;
+    if (C * (I + 16 + NBI * 40) > DEC_LIMIT_UNPACKED_BYTES) return false;   // unpacked down rows of a slot
     return true;
 }
 

@@ -62,6 +62,7 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 constexpr int DEC_WAVES = 8;
 constexpr int DEC_THREADS = DEC_WAVES * 64;
 constexpr int DEC_GU_SEG = 9;       // 1 KB DMA segments per wave of gate/up rows
+constexpr int DEC_WREG = DEC_LIMIT_UNPACKED_BYTES;   // LDS per wave: gate/up rows, then its slot's unpacked down rows
 constexpr int DEC_DN_SEG = 7;       // 1 KB DMA segments per slot of down rows
 constexpr int DEC_KMAX = 8;         // slots: one wave each in the down phase
 constexpr int DEC_PMAX = 64;        // (h, g) row pairs per WG
@@ -105,26 +106,38 @@ __device__ inline void st_dev4(void *base, uint32_t off, uint32_t v) {
     __hip_atomic_store((uint32_t *)((uint8_t *)base + off), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// grid barrier; every thread of every WG calls it.  Counters 256 bytes apart:
-// group g at sync[32 g], the top counter at sync[32 * DEC_SYNC_GROUPS], the
-// release word after it.  ok is cleared if the wait gives up.
+// Grid barrier in two halves so a WG can work between arriving and waiting.
+// Counters 256 bytes apart: group g at sync[32 g], the top counter at
+// sync[32 * DEC_SYNC_GROUPS], the release word after it.  Every thread of the
+// WG calls both halves; the WG's write-through stores must come from wave 0
+// and be issued before dec_arrive.
 constexpr int DEC_GROUP = 16;
-__device__ inline void dec_grid_barrier(unsigned long long *sync, bool &ok) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's stores are done
-    __syncthreads();
+__device__ inline unsigned long long dec_arrive(unsigned long long *sync) {
+    // the WG's hand-off stores come from wave 0 only (the caller's contract):
+    // once they are done, thread 0 arrives; the other waves go on at once
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    unsigned long long old = 0;
     if (threadIdx.x == 0) {
         const unsigned G = gridDim.x;
         const unsigned S = (G % DEC_GROUP == 0) ? DEC_GROUP : G;
         const unsigned ngroups = G / S;
-        unsigned long long *grp = sync + 32 * (blockIdx.x / S);
-        unsigned long long *top = sync + 32 * DEC_SYNC_GROUPS;
-        unsigned long long *rel = top + 32;
-        const unsigned long long old = __hip_atomic_fetch_add(grp, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned long long round = old / S + 1;
-        if (old % S == S - 1) {
+        old = __hip_atomic_fetch_add(sync + 32 * (blockIdx.x / S), 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old % S == S - 1) {   // last of its group: arrive at the top level
+            unsigned long long *top = sync + 32 * DEC_SYNC_GROUPS;
             const unsigned long long o2 = __hip_atomic_fetch_add(top, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (o2 % ngroups == ngroups - 1) __hip_atomic_store(rel, round, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (o2 % ngroups == ngroups - 1)
+                __hip_atomic_store(top + 32, old / S + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+    }
+    return old;
+}
+// ok is cleared if the wait gives up
+__device__ inline void dec_wait(unsigned long long *sync, unsigned long long old, bool &ok) {
+    if (threadIdx.x == 0) {
+        const unsigned G = gridDim.x;
+        const unsigned S = (G % DEC_GROUP == 0) ? DEC_GROUP : G;
+        const unsigned long long *rel = sync + 32 * DEC_SYNC_GROUPS + 32;
+        const unsigned long long round = old / S + 1;
         unsigned n = 0;
         while (__hip_atomic_load(rel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < round) {
             if (++n > DEC_SPIN_LIMIT) {
@@ -253,70 +266,126 @@ __device__ inline float dec_q4_piece(const uint8_t *blk, int sl, const Q4X &x) {
     return (d * x.dx) * (float)isum - (dmin * x.dx) * (float)msum;
 }
 
-// 8 bytes at byte offset off (2-byte aligned) of an LDS region
-__device__ inline uint2 lds_load8(const uint8_t *region, uint32_t off) {
+// N dwords from byte offset off (2-byte aligned) of an LDS region, reading
+// only the aligned dwords that intersect the range
+template <int N>
+__device__ inline void lds_words(const uint8_t *region, uint32_t off, uint32_t (&out)[N]) {
     const uint32_t mis = off & 3u;
     const uint32_t *w = (const uint32_t *)(region + (off & ~3u));
-    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
-    uint2 r;
-    r.x = __builtin_amdgcn_alignbyte(w1, w0, mis);
-    r.y = __builtin_amdgcn_alignbyte(w2, w1, mis);
-    return r;
+    uint32_t a[N + 1];
+#pragma unroll
+    for (int i = 0; i <= N; ++i) a[i] = w[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(a[i + 1], a[i], mis);
 }
 
-// Q6_K piece sl: half h = sl/4, l0 = 8*(sl%4); quarters qq = 0..3 hold values
-// 128h + 32qq + l0 + i, i < 8, scale index 8h + l0/16 + 2qq
-// (ggml_vec_dot_q6_K_q8_K restricted to those values)
-struct Q6X {
-    uint32_t x[8];
-    float dx;
+// ---------------------------------------------------------------- down rows, unpacked
+// Phase C reads its slot's down rows in a dot-ready form that the wave builds
+// from the raw GGUF rows while it waits for the activations: per row c the I
+// weights as int8 (Q4_K: q in 0..15, Q6_K: q - 32); per (row, block b, lane
+// slot j < 8) one word with the scales and mins of 16-value groups j and
+// j + 8 (s_j | s_{j+8} << 8 | m_j << 16 | m_{j+8} << 24; Q4_K: the 6-bit
+// scale and min of the group's sub-block, Q6_K: its int8 scale and min 0);
+// per (row, block) the float pair (d, dmin) (Q6_K: dmin 0).  A block then
+// contributes (d dx) sum_g s_g dot_g - (dmin dx) sum_g m_g bsum_g, the
+// integer form of ggml_vec_dot_q4_K_q8_K / ggml_vec_dot_q6_K_q8_K.
+// Rows are DN_PAD bytes apart beyond their I weights, so the eight rows one
+// instruction touches start in different LDS banks.
+constexpr int DN_PAD = 16;
+struct DnLayout {
+    uint32_t row, sc, dm;   // row stride; byte offsets of the scale words and (d, dmin) pairs
 };
-__device__ inline Q6X dec_q6x_load(const int8_t *xq, const float *xd, int b, int sl) {
-    const int h = sl >> 2, l0 = 8 * (sl & 3);
-    Q6X x;
-    const int8_t *blk = xq + b * QK;
-#pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-        const uint2 v = *(const uint2 *)(blk + 128 * h + 32 * qq + l0);
-        x.x[2 * qq] = v.x;
-        x.x[2 * qq + 1] = v.y;
-    }
-    x.dx = xd[b];
-    return x;
+__device__ inline DnLayout dn_layout(int C, int I) {
+    DnLayout L;
+    L.row = (uint32_t)(I + DN_PAD);
+    L.sc = (uint32_t)C * L.row;
+    L.dm = L.sc + (uint32_t)(C * (I / QK) * 32);
+    return L;
 }
-__device__ inline float dec_q6_piece(const uint8_t *region, uint32_t boff, int sl, const Q6X &x) {
-    const int h = sl >> 2, l0 = 8 * (sl & 3);
-    const uint2 qla = lds_load8(region, boff + 64 * h + l0);
-    const uint2 qlb = lds_load8(region, boff + 64 * h + 32 + l0);
-    const uint2 qh = lds_load8(region, boff + 128 + 32 * h + l0);
-    const uint2 s8 = lds_load8(region, boff + 192 + 8 * h);
-    const uint32_t dw = *(const uint32_t *)(region + ((boff + 208) & ~3u));
-    const uint16_t dbits = (uint16_t)(((boff + 208) & 2u) ? (dw >> 16) : (dw & 0xffff));
-    const float d = h2f(dbits);
-    const int is = l0 >> 4;
-    const uint32_t la[2] = {qla.x, qla.y}, lb[2] = {qlb.x, qlb.y}, hh[2] = {qh.x, qh.y};
-    int isum = 0;
+
+// unpack half h of block b of row c (raw row bytes at dn + c*rbd + b*BB)
+__device__ inline void dn_unpack_q4(const uint8_t *dn, uint8_t *un, const DnLayout &L, int I, int NBI,
+                                    uint32_t rbd, int c, int b, int h) {
+    const uint8_t *raw = dn + c * rbd + b * Q4K_BYTES;     // 16-byte aligned (Q4_K rows)
+    const u32x4 hdr = *(const u32x4 *)raw;
+    int8_t *w = (int8_t *)un + c * L.row + b * QK;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        // qs bytes 64h + 16t .. +16 = sub-block pair jj = 2h + t/2, positions l0 = 16 (t % 2) ..
+        const u32x4 qv = *(const u32x4 *)(raw + 16 + 64 * h + 16 * t);
+        const int jj = 2 * h + (t >> 1), l0 = 16 * (t & 1);
+        u32x4 lo, hi;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            lo[e] = qv[e] & 0x0F0F0F0Fu;
+            hi[e] = (qv[e] >> 4) & 0x0F0F0F0Fu;
+        }
+        *(u32x4 *)(w + 64 * jj + l0) = lo;        // values 64 jj + l0 ..
+        *(u32x4 *)(w + 64 * jj + 32 + l0) = hi;   // values 64 jj + 32 + l0 ..
+    }
+    // scale words 4h .. 4h + 3: groups j and j + 8 lie in sub-blocks j/2 and j/2 + 4
+    uint32_t *sw = (uint32_t *)(un + L.sc) + (c * NBI + b) * 8 + 4 * h;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        int sa, ma, sb, mb;
+        scale_min_k4_reg(2 * h + i, hdr[1], hdr[2], hdr[3], sa, ma);
+        scale_min_k4_reg(2 * h + i + 4, hdr[1], hdr[2], hdr[3], sb, mb);
+        const uint32_t word = (uint32_t)sa | ((uint32_t)sb << 8) | ((uint32_t)ma << 16) | ((uint32_t)mb << 24);
+        sw[2 * i] = word;
+        sw[2 * i + 1] = word;
+    }
+    if (h == 0) {
+        float *dm = (float *)(un + L.dm) + 2 * (c * NBI + b);
+        dm[0] = h2f((uint16_t)(hdr[0] & 0xffff));
+        dm[1] = h2f((uint16_t)(hdr[0] >> 16));
+    }
+}
+
+__device__ inline void dn_unpack_q6(const uint8_t *dn, uint8_t *un, const DnLayout &L, int I, int NBI,
+                                    uint32_t boff, int c, int b, int h) {
+    // block at byte boff of the raw region (2-byte aligned)
+    uint32_t ql[16], qh[8];
+    lds_words<16>(dn, boff + 64 * h, ql);        // ql[64h .. 64h + 64)
+    lds_words<8>(dn, boff + 128 + 32 * h, qh);   // qh[32h .. 32h + 32)
+    int8_t *w = (int8_t *)un + c * L.row + b * QK + 128 * h;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
-        const int idx = is + 2 * qq;
-        const uint32_t word = (idx >> 2) ? s8.y : s8.x;
-        const int sc = (int)(int8_t)(word >> (8 * (idx & 3)));
-        int s = 0;
+        // values 32 qq + l, l < 32: low / high nibble of ql[l] or ql[l + 32]
+        // and bits 2 qq .. 2 qq + 1 of qh[l] (ggml dequantize_row_q6_K)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            uint32_t lo, hi2;
-            if (qq == 0) { lo = la[i] & 0x0F0F0F0Fu; hi2 = (hh[i] << 4) & 0x30303030u; }
-            else if (qq == 1) { lo = lb[i] & 0x0F0F0F0Fu; hi2 = (hh[i] << 2) & 0x30303030u; }
-            else if (qq == 2) { lo = (la[i] >> 4) & 0x0F0F0F0Fu; hi2 = hh[i] & 0x30303030u; }
-            else { lo = (lb[i] >> 4) & 0x0F0F0F0Fu; hi2 = (hh[i] >> 2) & 0x30303030u; }
-            // 6-bit q -> q - 32 as a signed byte (see k_gemv.hip dot_q6_piece)
-            const uint32_t x6 = (lo | hi2) ^ 0x20202020u;
-            const uint32_t sq = x6 | ((x6 & 0x20202020u) * 6u);
-            s = __builtin_amdgcn_sdot4((int)sq, (int)x.x[2 * qq + i], s, false);
+        for (int half = 0; half < 2; ++half) {
+            u32x4 out;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int wi = 4 * half + e;   // word of l = 4 wi .. 4 wi + 3
+                const uint32_t lw = (qq & 1) ? ql[8 + wi] : ql[wi];
+                const uint32_t lo = (qq >> 1) ? ((lw >> 4) & 0x0F0F0F0Fu) : (lw & 0x0F0F0F0Fu);
+                const uint32_t hi2 = ((qh[wi] >> (2 * qq)) << 4) & 0x30303030u;
+                // 6-bit q -> q - 32 as a signed byte: q ^ 0x20 is its 6-bit two's
+                // complement; copy bit 5 into bits 6-7 (0x20 * 6 = 0xC0, no carries)
+                const uint32_t x6 = (lo | hi2) ^ 0x20202020u;
+                out[e] = x6 | ((x6 & 0x20202020u) * 6u);
+            }
+            *(u32x4 *)(w + 32 * qq + 16 * half) = out;
         }
-        isum += sc * s;
     }
-    return (d * x.dx) * (float)isum;
+    // scale words 4h .. 4h + 3: int8 scales of groups j and j + 8
+    uint32_t scw[4];
+    lds_words<4>(dn, boff + 192, scw);
+    uint32_t *sw = (uint32_t *)(un + L.sc) + (c * NBI + b) * 8 + 4 * h;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t s0 = (scw[h] >> (8 * i)) & 0xffu;
+        const uint32_t s1 = (scw[h + 2] >> (8 * i)) & 0xffu;
+        sw[i] = s0 | (s1 << 8);
+    }
+    if (h == 0) {
+        uint32_t dw[1];
+        lds_words<1>(dn, boff + 208, dw);
+        float *dm = (float *)(un + L.dm) + 2 * (c * NBI + b);
+        dm[0] = h2f((uint16_t)(dw[0] & 0xffff));
+        dm[1] = 0.f;
+    }
 }
 
 // copy a byte range of one expert matrix into LDS: DEC segments of 1 KB, lane
@@ -352,13 +421,12 @@ __device__ inline DecChunk dec_chunk(const ExpertMat &m, int e, int64_t row0, in
 
 // ---------------------------------------------------------------- kernel
 constexpr int DEC_RSTEPS = 16;   // row steps per wave in the gate/up phase (R / RPS)
-constexpr int DEC_CSTEPS = DEC_LIMIT_CSTEPS;   // row steps per wave in the down phase (C / RPSD)
 
 // NBI = I / 256: blocks per down row (compile time, so the per-slot Q8_K and
 // the down reductions unroll)
 template <int DT, int NBI>
 __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
-    __shared__ __attribute__((aligned(1024))) uint8_t s_gu[DEC_WAVES][DEC_GU_SEG * 1024];
+    __shared__ __attribute__((aligned(1024))) uint8_t s_gu[DEC_WAVES][DEC_WREG];
     __shared__ __attribute__((aligned(1024))) uint8_t s_dn[DEC_KMAX][DEC_DN_SEG * 1024];
     __shared__ float s_logit[256];
     __shared__ int s_sel[DEC_KMAX];
@@ -376,6 +444,10 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
     const uint32_t tag = __hip_atomic_load(g.epoch + wg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     bool ok = true;
     if (tid == 0) s_fail = 0;
+    // residual of this WG's output columns, loaded now (off the kernel's tail)
+    const int C = g.C, n0 = wg * C;
+    const bool do_c = n0 < D;
+    const float resv = (do_c && tid < C && g.res) ? g.res[n0 + tid] : 0.f;
 
     // ---- A: router row wg (wave 0) and Q8_K of x block wg (wave 1); the
     // logit is published only once this WG's Q8_K of x is out
@@ -424,13 +496,11 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
     dec_lds_barrier();
 
     const int64_t pairs = (int64_t)K * I;
-    const int P = g.P, R = P / 4, C = g.C;
+    const int P = g.P, R = P / 4;
     const int64_t q0 = (int64_t)wg * P;
     const bool do_b = q0 < pairs;
     const int kB = do_b ? (int)(q0 / I) : 0;
     const int i0 = do_b ? (int)(q0 % I) : 0;
-    const int n0 = wg * C;
-    const bool do_c = n0 < D;
     {
         int eb = __builtin_amdgcn_readfirstlane(s_sel[kB]);
         eb = eb < 0 ? 0 : (eb >= E ? E - 1 : eb);
@@ -527,88 +597,99 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
         const float a = act_pair(g.act, s_hg[tid], s_hg[P + tid]);
         st_dev4(g.actf, 4u * (uint32_t)(kB * I + i0 + tid), __builtin_bit_cast(uint32_t, a));
     }
-    dec_grid_barrier(g.sync, ok);
+    const unsigned long long arrival = dec_arrive(g.sync);
+
+    // while the other WGs finish: turn this wave's slot of down rows into the
+    // dot-ready form (raw rows in s_dn[wave], result in s_gu[wave])
+    const DnLayout UL = dn_layout(C, I);
+    if (do_c && wave < K) {
+        const uint32_t rbd = (uint32_t)g.down.row_bytes;
+        for (int u = lane; u < C * NBI * 2; u += 64) {
+            const int c = u / (2 * NBI), rem = u % (2 * NBI), b = rem >> 1, h = rem & 1;
+            if constexpr (DT == 12) dn_unpack_q4(s_dn[wave] + dn_shift, s_gu[wave], UL, I, NBI, rbd, c, b, h);
+            else dn_unpack_q6(s_dn[wave], s_gu[wave], UL, I, NBI, dn_shift + c * rbd + b * Q6K_BYTES, c, b, h);
+        }
+    }
+    dec_wait(g.sync, arrival, ok);
 
     // ---- C: Q8_K of slot k = wave's activations, down rows, weighted combine
     if (do_c && wave < K) {
         const int k = wave;
         // Q8_K of the I activations of slot k (ggml quantizes each mul_mat_id
-        // source row on its own), codes / scales / block sums into the now
-        // free gate/up region of this wave
-        int8_t *aq = (int8_t *)s_gu[k];
-        float *ad = (float *)(s_gu[k] + 2048);
-        int16_t *abs_ = (int16_t *)(s_gu[k] + 2048 + 64);
-        float4_t av[NBI];
+        // source row on its own): codes / scales / block sums into s_dn[k],
+        // whose raw rows are unpacked already
+        int8_t *aq = (int8_t *)s_dn[k];
+        float *ad = (float *)(s_dn[k] + 2048);
+        int16_t *abs_ = (int16_t *)(s_dn[k] + 2048 + 64);
+        // 16 lanes per block, four blocks per pass
+        for (int b0 = 0; b0 < NBI; b0 += 4) {
+            const int b = b0 + (lane >> 4), seg = lane & 15;
+            float v[16];
 #pragma unroll
-        for (int b = 0; b < NBI; ++b) av[b] = *(const float4_t *)(g.actf + k * I + b * QK + 4 * lane);
+            for (int i = 0; i < 4; ++i) {
+                float4_t a4 = {0.f, 0.f, 0.f, 0.f};
+                if (b < NBI) a4 = *(const float4_t *)(g.actf + k * I + b * QK + 16 * seg + 4 * i);
+                v[4 * i] = a4.x;
+                v[4 * i + 1] = a4.y;
+                v[4 * i + 2] = a4.z;
+                v[4 * i + 3] = a4.w;
+            }
+            int q[16], bsum;
+            const float d = q8k_wave4x16(v, lane, q, bsum);
+            if (b < NBI) {
+                u32x4 pk;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int qi[4] = {q[4 * i], q[4 * i + 1], q[4 * i + 2], q[4 * i + 3]};
+                    pk[i] = pack_i8x4(qi);
+                }
+                *(u32x4 *)(aq + b * QK + 16 * seg) = pk;
+                abs_[b * 16 + seg] = (int16_t)bsum;
+                if (seg == 0) ad[b] = d;
+            }
+        }
+        // lane (row c = c0 + lane / 8, j = lane % 8): groups j and j + 8 of every block
+        const int j = lane & 7, rsub = lane >> 3;
+        u32x4 x0[NBI], x1[NBI];
+        int bs0[NBI], bs1[NBI];
+        float dx[NBI];
 #pragma unroll
         for (int b = 0; b < NBI; ++b) {
-            const float4_t a4 = av[b];
-            const float v[4] = {a4.x, a4.y, a4.z, a4.w};
-            int q[4];
-            const float d = q8k_wave(v, lane, q);
-            *(uint32_t *)(aq + b * QK + 4 * lane) = pack_i8x4(q);
-            if (lane == 0) ad[b] = d;
-            const int bs = q8k_bsum16(q);
-            if ((lane & 3) == 0) abs_[b * 16 + (lane >> 2)] = (int16_t)bs;
+            x0[b] = *(const u32x4 *)(aq + b * QK + 16 * j);
+            x1[b] = *(const u32x4 *)(aq + b * QK + 128 + 16 * j);
+            bs0[b] = abs_[b * 16 + j];
+            bs1[b] = abs_[b * 16 + 8 + j];
+            dx[b] = ad[b];
         }
-        constexpr int LPRD = 8 * NBI, RPSD = 64 / LPRD;
-        constexpr bool POW2 = (NBI & (NBI - 1)) == 0;
-        const int rd = lane / LPRD, bd = (lane % LPRD) >> 3;
-        const bool lane_ok = rd < RPSD;
-        const int base_lane = (lane_ok ? rd : 0) * LPRD;
-        const int64_t rbd = g.down.row_bytes;
-        Q4X x4;
-        Q6X x6;
-        if constexpr (DT == 12) x4 = dec_q4x_load(aq, abs_, ad, lane_ok ? bd : 0, sl);
-        else x6 = dec_q6x_load(aq, ad, lane_ok ? bd : 0, sl);
-        constexpr int bbytes = DT == 12 ? Q4K_BYTES : Q6K_BYTES;
-        float acc[DEC_CSTEPS];
+        const uint8_t *un = s_gu[k];
+        for (int c0 = 0; c0 < C; c0 += 8) {
+            const int c = c0 + rsub;
+            float acc = 0.f;
+            if (c < C) {
 #pragma unroll
-        for (int j = 0; j < DEC_CSTEPS; ++j) {
-            acc[j] = 0.f;
-            const int c = j * RPSD + rd;
-            if (j * RPSD < C && lane_ok && c < C) {
-                const uint32_t boff = dn_shift + (uint32_t)(c * rbd) + (uint32_t)(bd * bbytes);
-                if constexpr (DT == 12) acc[j] = dec_q4_piece(s_dn[k] + boff, sl, x4);
-                else acc[j] = dec_q6_piece(s_dn[k], boff, sl, x6);
-            }
-        }
-        // sum the 8 piece lanes of each block, then the NBI blocks of the row
+                for (int b = 0; b < NBI; ++b) {
+                    const int8_t *wr = (const int8_t *)un + c * UL.row + b * QK;
+                    const u32x4 w0 = *(const u32x4 *)(wr + 16 * j);
+                    const u32x4 w1 = *(const u32x4 *)(wr + 128 + 16 * j);
+                    const uint32_t sw = *((const uint32_t *)(un + UL.sc) + (c * NBI + b) * 8 + j);
+                    const float2 dm = *((const float2 *)(un + UL.dm) + (c * NBI + b));
+                    int d0 = 0, d1 = 0;
 #pragma unroll
-        for (int j = 0; j < DEC_CSTEPS; ++j) acc[j] += dpp_f<0xB1>(acc[j]);
-#pragma unroll
-        for (int j = 0; j < DEC_CSTEPS; ++j) acc[j] += dpp_f<0x4E>(acc[j]);
-#pragma unroll
-        for (int j = 0; j < DEC_CSTEPS; ++j) acc[j] += dpp_f<0x141>(acc[j]);
-        if constexpr (POW2) {
-            if constexpr (LPRD >= 16) {
-#pragma unroll
-                for (int j = 0; j < DEC_CSTEPS; ++j) acc[j] += dpp_f<0x140>(acc[j]);
-            }
-            if constexpr (LPRD >= 32) {
-#pragma unroll
-                for (int j = 0; j < DEC_CSTEPS; ++j) acc[j] += __shfl_xor(acc[j], 16, 64);
-            }
-            if constexpr (LPRD >= 64) {
-#pragma unroll
-                for (int j = 0; j < DEC_CSTEPS; ++j) acc[j] += __shfl_xor(acc[j], 32, 64);
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < DEC_CSTEPS; ++j) {
-                if (j * RPSD < C) {
-                    float tot = 0.f;
-#pragma unroll
-                    for (int b = 0; b < NBI; ++b) tot += __shfl(acc[j], base_lane + 8 * b, 64);
-                    acc[j] = tot;
+                    for (int i = 0; i < 4; ++i) {
+                        d0 = __builtin_amdgcn_sdot4((int)w0[i], (int)x0[b][i], d0, false);
+                        d1 = __builtin_amdgcn_sdot4((int)w1[i], (int)x1[b][i], d1, false);
+                    }
+                    const int s0 = (int)(int8_t)(sw & 0xff), s1 = (int)(int8_t)((sw >> 8) & 0xff);
+                    const int m0 = (int)((sw >> 16) & 0xff), m1 = (int)(sw >> 24);
+                    const int isum = s0 * d0 + s1 * d1;
+                    const int msum = m0 * bs0[b] + m1 * bs1[b];
+                    acc += (dm.x * dx[b]) * (float)isum - (dm.y * dx[b]) * (float)msum;
                 }
             }
-        }
-#pragma unroll
-        for (int j = 0; j < DEC_CSTEPS; ++j) {
-            const int c = j * RPSD + rd;
-            if (j * RPSD < C && lane_ok && c < C && (lane % LPRD) == 0) s_z[k * C + c] = acc[j];
+            acc += dpp_f<0xB1>(acc);
+            acc += dpp_f<0x4E>(acc);
+            acc += dpp_f<0x141>(acc);
+            if (c < C && j == 0) s_z[k * C + c] = acc;
         }
     }
     if (!ok) s_fail = 1;
@@ -618,7 +699,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
         double s = 0.0;
         for (int k = 0; k < K; ++k) s = s + (double)(s_z[k * C + tid] * s_w[k]);
         const float moe = (float)s;
-        float v = g.res ? g.res[n0 + tid] + moe : moe;
+        float v = g.res ? resv + moe : moe;
         if (failed) v = __builtin_nanf("");
         g.out[n0 + tid] = v;
     }

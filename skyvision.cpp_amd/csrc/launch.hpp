@@ -167,7 +167,7 @@ constexpr int DEC_MAX_GRID = 1024;
 constexpr int DEC_SYNC_WORDS = 32 * (DEC_MAX_GRID / 16 + 2);   // 256 B per counter
 constexpr int DEC_LIMIT_GU_BYTES = 9 * 1024;   // LDS per wave of gate/up rows
 constexpr int DEC_LIMIT_DN_BYTES = 7 * 1024;   // LDS per slot of down rows
-constexpr int DEC_LIMIT_CSTEPS = 16;           // down row steps per wave
+constexpr int DEC_LIMIT_UNPACKED_BYTES = 10 * 1024;   // LDS per slot of dot-ready down rows
 // cooperative: hipLaunchCooperativeKernel (residency guaranteed by the runtime);
 // otherwise a plain launch that relies on the GPU running nothing else
 int launch_decode1(const DecArgs &g, int grid, bool cooperative, hipStream_t st);

@@ -63,15 +63,41 @@ __device__ inline AmaxIdx wave_amax_idx_fast(AmaxIdx a) {
     return amax_xor(a, 32);
 }
 
+// Largest |x| over the wave (lane l holding elements 4l .. 4l+3) and the
+// signed value of the first element that attains it, in element order: the
+// element ggml's "if (ax > amax)" scan keeps.  The max is reduced alone (one
+// exchange and one max per step); the first holder comes from a ballot.
+struct AbsMax {
+    float ax, val;
+};
+__device__ inline float absmax4(const float (&v)[4]) {
+    return fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+}
+__device__ inline AbsMax absmax_first(const float (&v)[4], float m) {
+    // m: the wave's largest |x|
+    const bool h0 = fabsf(v[0]) == m, h1 = fabsf(v[1]) == m, h2 = fabsf(v[2]) == m, h3 = fabsf(v[3]) == m;
+    const unsigned long long holders = __ballot(h0 | h1 | h2 | h3);
+    const int first = (int)__builtin_ctzll(holders | (1ull << 63));
+    const float mine = h0 ? v[0] : h1 ? v[1] : h2 ? v[2] : v[3];
+    AbsMax r;
+    r.ax = m;
+    r.val = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), first));
+    return r;
+}
+
 // Q8_K of one 256-value block held by one wave, lane l holding the values at
 // 4l .. 4l+3 (ggml quantize_row_q8_K_ref): the first value with the largest
 // |x| sets iscale = -127 / x, q = min(127, nearest_int(iscale * v)),
 // d = 1 / iscale; an all-zero block gives q = 0 and d = 0.  Returns d.
 __device__ inline float q8k_wave(const float (&v)[4], int lane, int (&q)[4]) {
-    AmaxIdx a{-1.f, 1 << 30, 0.f};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) a = amax_better(a, AmaxIdx{fabsf(v[j]), 4 * lane + j, v[j]});
-    a = wave_amax_idx_fast(a);
+    float m = absmax4(v);
+    m = fmaxf(m, dpp_f<0xB1>(m));
+    m = fmaxf(m, dpp_f<0x4E>(m));
+    m = fmaxf(m, dpp_f<0x141>(m));
+    m = fmaxf(m, dpp_f<0x140>(m));
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    const AbsMax a = absmax_first(v, m);
 #pragma unroll
     for (int j = 0; j < 4; ++j) q[j] = 0;
     if (a.ax == 0.f) return 0.f;
@@ -79,6 +105,81 @@ __device__ inline float q8k_wave(const float (&v)[4], int lane, int (&q)[4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) q[j] = imin(127, nearest_int(iscale * v[j]));
     return 1 / iscale;
+}
+
+// Q8_K of N blocks at once (the same arithmetic as q8k_wave; the N reductions
+// run in lockstep so their lane exchanges overlap)
+template <int N>
+__device__ inline void q8k_wave_n(const float (&v)[N][4], int lane, int (&q)[N][4], float (&d)[N]) {
+    float m[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) m[n] = absmax4(v[n]);
+#pragma unroll
+    for (int n = 0; n < N; ++n) m[n] = fmaxf(m[n], dpp_f<0xB1>(m[n]));
+#pragma unroll
+    for (int n = 0; n < N; ++n) m[n] = fmaxf(m[n], dpp_f<0x4E>(m[n]));
+#pragma unroll
+    for (int n = 0; n < N; ++n) m[n] = fmaxf(m[n], dpp_f<0x141>(m[n]));
+#pragma unroll
+    for (int n = 0; n < N; ++n) m[n] = fmaxf(m[n], dpp_f<0x140>(m[n]));
+#pragma unroll
+    for (int n = 0; n < N; ++n) m[n] = fmaxf(m[n], __shfl_xor(m[n], 16, 64));
+#pragma unroll
+    for (int n = 0; n < N; ++n) m[n] = fmaxf(m[n], __shfl_xor(m[n], 32, 64));
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+        const AbsMax a = absmax_first(v[n], m[n]);
+        const bool zero = a.ax == 0.f;
+        const float iscale = zero ? 0.f : -127.f / a.val;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[n][j] = zero ? 0 : imin(127, nearest_int(iscale * v[n][j]));
+        d[n] = zero ? 0.f : 1 / iscale;
+    }
+}
+
+// Q8_K of four blocks by one wave, 16 lanes per block: lane l quantizes
+// values 16 (l % 16) .. +15 of block l / 16 (same arithmetic as q8k_wave;
+// the four blocks share one instruction stream, and each lane's 16 codes
+// form one ggml bsums entry).  Returns this lane's block scale d; bsum is
+// the sum of the lane's 16 codes.
+__device__ inline float q8k_wave4x16(const float (&v)[16], int lane, int (&q)[16], int &bsum) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+    m = fmaxf(m, dpp_f<0xB1>(m));
+    m = fmaxf(m, dpp_f<0x4E>(m));
+    m = fmaxf(m, dpp_f<0x141>(m));
+    m = fmaxf(m, dpp_f<0x140>(m));   // m: largest |x| of the lane's block
+    // first element attaining it: first holder lane of the 16-lane group,
+    // first position in that lane
+    bool has = false;
+    float mine = 0.f;
+#pragma unroll
+    for (int i = 15; i >= 0; --i) {
+        const bool hi = fabsf(v[i]) == m;
+        has = has | hi;
+        mine = hi ? v[i] : mine;
+    }
+    const unsigned long long holders = __ballot(has);
+    float first_val[4];
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+        const unsigned long long gm = (holders >> (16 * gi)) & 0xffffull;
+        const int fl = 16 * gi + (int)__builtin_ctzll(gm | 0x8000ull);
+        first_val[gi] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), fl));
+    }
+    const int grp = lane >> 4;
+    const float val = grp == 0 ? first_val[0] : grp == 1 ? first_val[1] : grp == 2 ? first_val[2] : first_val[3];
+    const bool zero = m == 0.f;
+    const float iscale = zero ? 0.f : -127.f / val;
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        q[i] = zero ? 0 : imin(127, nearest_int(iscale * v[i]));
+        s += q[i];
+    }
+    bsum = s;
+    return zero ? 0.f : 1 / iscale;
 }
 
 // sum of the 16 codes of lane group lane / 4 (the ggml bsums entry), valid in

@@ -212,8 +212,16 @@ def main() -> int:
         dl = [W.GpuLayer(dctx, dspec, copy=c) for c in range(args.copies)]
         dx = [W.gen_x(dctx, dspec, 1, copy=c) for c in range(args.copies)]
         dout = M.DeviceBuffer(4 * dspec.D)
+        # fused single-token kernel, plain launch (the GPU runs nothing else
+        # here); the cooperative launch is timed beside it
+        dctx.set_fused_decode(M.DECODE_FUSED_EXCLUSIVE)
         dms, _ = time_layer(dctx, dl, dx, 1, dout, 200, 20)
         _, dst = time_layer(dctx, dl, dx, 1, dout, 50, 5, profile=True)
+        modes = {}
+        for mname, mode in [("fused_cooperative", M.DECODE_FUSED_COOPERATIVE), ("chain", M.DECODE_CHAIN)]:
+            dctx.set_fused_decode(mode)
+            modes[mname] = time_layer(dctx, dl, dx, 1, dout, 200, 20)[0]
+        dctx.set_fused_decode(M.DECODE_FUSED_EXCLUSIVE)
         dtouched, _ = touched_experts(dctx, dl[0], dx[0], 1)
         layer_bytes = W.algorithmic_bytes(dspec, dtouched)
         if "decode1" in dst:
@@ -225,7 +233,9 @@ def main() -> int:
             kms = dst.get("gate_up", float("nan"))
         result["decode"] = {
             "workload": "config 0: moondream3 MoE layer, 1-token decode, Q4_K",
+            "schedule": "fused kernel, plain launch (MI_DECODE_FUSED_EXCLUSIVE)",
             "tokens_per_s": 1.0 / (dms * 1e-3), "ms_per_token": dms,
+            "ms_per_token_other_schedules": modes,
             "layer_bytes": layer_bytes, "layer_GBs": layer_bytes / (dms * 1e-3) / 1e9,
             "layer_frac_hbm": layer_bytes / (dms * 1e-3) / 1e9 / PEAK_HBM_GBS,
             "roofline": {"bound": "hbm", "kernel": kname,

@@ -473,21 +473,25 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
     const int rr = lane / LPR, bq = (lane % LPR) >> 3, sl = lane & 7;
     const Q4X xg = dec_q4x_load(g.xq, g.xbs, g.xd, bq, sl);
     {
-        // rank of expert e = #{j : l_j > l_e} + #{j < e : l_j == l_e}; the K
-        // lowest ranks in rank order are ggml_top_k's stable descending pick
-        int tpe = 1;
-        while (tpe * 2 * E <= DEC_THREADS && tpe < 64) tpe *= 2;
+        // rank of expert e = #{i : l_i > l_e} + #{i < e : l_i == l_e}; the K
+        // lowest ranks in rank order are ggml_top_k's stable descending pick.
+        // 8, 4 or 2 lanes per expert (E <= 64, 128, 256), each comparing a
+        // share of the logits
+        const int tpe = E <= DEC_THREADS / 8 ? 8 : E <= DEC_THREADS / 4 ? 4 : 2;
         const int e = tid / tpe, j = tid % tpe;
         int cnt = 0;
         float ve = 0.f;
         if (e < E) {
             ve = s_logit[e];
+#pragma unroll 8
             for (int i = j; i < E; i += tpe) {
                 const float vi = s_logit[i];
-                cnt += (vi > ve || (vi == ve && i < e)) ? 1 : 0;
+                cnt += (int)(vi > ve) | ((int)(vi == ve) & (int)(i < e));
             }
         }
-        for (int o = 1; o < tpe; o <<= 1) cnt += __shfl_xor(cnt, o, 64);
+        cnt += dpp_i<0xB1>(cnt);
+        if (tpe >= 4) cnt += dpp_i<0x4E>(cnt);
+        if (tpe >= 8) cnt += dpp_i<0x141>(cnt);
         if (e < E && j == 0 && cnt < K) {
             s_sel[cnt] = e;
             s_val[cnt] = ve;

@@ -137,6 +137,9 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=1, choices=[1, 2])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-coop", action="store_true",
+                    help="skip timing the cooperative-launch decode schedule (rocprofv3 cannot "
+                         "write its results after a cooperative launch on this image)")
     ap.add_argument("--cpu-tokens", type=int, default=64)
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 512 MiB device-to-device copy (the known-size kernel "
@@ -218,15 +221,21 @@ def main() -> int:
         dms, _ = time_layer(dctx, dl, dx, 1, dout, 200, 20)
         _, dst = time_layer(dctx, dl, dx, 1, dout, 50, 5, profile=True)
         modes = {}
-        for mname, mode in [("fused_cooperative", M.DECODE_FUSED_COOPERATIVE), ("chain", M.DECODE_CHAIN)]:
+        other = [("chain", M.DECODE_CHAIN)]
+        if not args.no_coop:
+            other.insert(0, ("fused_cooperative", M.DECODE_FUSED_COOPERATIVE))
+        for mname, mode in other:
             dctx.set_fused_decode(mode)
             modes[mname] = time_layer(dctx, dl, dx, 1, dout, 200, 20)[0]
         dctx.set_fused_decode(M.DECODE_FUSED_EXCLUSIVE)
         dtouched, _ = touched_experts(dctx, dl[0], dx[0], 1)
         layer_bytes = W.algorithmic_bytes(dspec, dtouched)
         if "decode1" in dst:
-            # the whole block is one kernel: its bytes are the layer's bytes
-            kname, kbytes, kms = "k_decode1 (fused single-token MoE block)", layer_bytes, dst["decode1"]
+            # the whole block is one kernel launched back to back: its duration
+            # is the timed loop's per-step time (HIP events around the loop on
+            # the launch stream; rocprofv3 reports the same kernel average), and
+            # its bytes are the layer's bytes
+            kname, kbytes, kms = "k_decode1 (fused single-token MoE block)", layer_bytes, dms
         else:
             kname = "gate_up grouped GEMV (k_gemv GLU)"
             kbytes = dtouched * 2 * dspec.I * M.row_size(dspec.gate_type, dspec.D)

@@ -238,11 +238,15 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
     const int D = L->n_embd, E = L->n_expert, K = L->n_expert_used, I = L->n_ff;
     const int64_t rows = T * K;
     const int max_active = (int)std::min<int64_t>(E, rows);
-    const int max_tiles = (int)((rows + GEMM_BM - 1) / GEMM_BM + max_active);
     const bool same_ids = ids_gu == ids_dn;
+    const bool kq = is_kquant(L->gate.type);
+    const bool gemm = kq && (T >= c->gemm_threshold || D > 8 * QK || I > 8 * QK);
+    // GEMM M-tile height: 128 for the 4-wave GEMMs (Q4_K gate/up), 64 otherwise
+    const int bm = gemm && L->gate.type == MI_TYPE_Q4_K ? G4_BM : GEMM_BM;
+    const int max_tiles = (int)((rows + bm - 1) / bm + max_active);
 
-    TRY(launch_dispatch(ids_gu, T, K, E, GEMM_BM, c->disp[0].view(), st));
-    if (!same_ids) TRY(launch_dispatch(ids_dn, T, K, E, GEMM_BM, c->disp[1].view(), st));
+    TRY(launch_dispatch(ids_gu, T, K, E, bm, c->disp[0].view(), st));
+    if (!same_ids) TRY(launch_dispatch(ids_dn, T, K, E, bm, c->disp[1].view(), st));
     const DispBuf &dg = c->disp[0];
     const DispBuf &dd = same_ids ? c->disp[0] : c->disp[1];
     stage_end(c, "dispatch", st);
@@ -251,7 +255,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
     ExpertMat up = {};
     if (!L->fused_gate_up) up = as_mat(L->up);
 
-    if (!is_kquant(L->gate.type)) {
+    if (!kq) {
         // fp32 expert tables: reference semantics without activation quantization
         const int64_t Ng = L->fused_gate_up ? 2LL * I : I;
         GemvArgs a = {};
@@ -284,7 +288,6 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         return MI_MOE_OK;
     }
 
-    const bool gemm = T >= c->gemm_threshold || D > 8 * QK || I > 8 * QK;
     if (!gemm) {
         Q8Out qx;
         qx.q8 = c->ax.q8; qx.d8 = c->ax.d8; qx.bsums = c->ax.bs;
@@ -311,26 +314,26 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         TRY(launch_gemv(d, st));
         stage_end(c, "down", st);
     } else if (gate.type == MI_TYPE_Q4_K) {
-        // exact Q4_K x Q8_K gate/up on 32x32x16 MFMA, fp16 down
+        // 4-wave GEMMs on 32x32x16 MFMA: fp16 dequantized weights x fp16
+        // d*q of the Q8_K activations, GLU + Q8_K of its output fused in
         Q8Out qx;
-        qx.xh = c->ax.h; qx.d8 = c->ax.d8; qx.xbs = c->ax.bsh;
-        qx.wtype = MI_TYPE_Q4_K; qx.order = 1; qx.exact = 1;
+        qx.xh = c->ax.h; qx.wtype = MI_TYPE_Q4_K; qx.order = 1;
         TRY(launch_q8k_rows(x, D, T, D, qx, st));
         stage_end(c, "q8k_x", st);
         G2Args a = {};
         a.a = gate; a.b = up; a.glu = 1; a.fused = L->fused_gate_up; a.act = L->act; a.I = I;
-        a.xh = c->ax.h; a.xd = c->ax.d8; a.xbs = c->ax.bsh; a.ne11 = 1; a.K = K;
+        a.xh = c->ax.h; a.ne11 = 1; a.K = K;
         a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.tile_e = dg.tile_e;
         a.tile_r0 = dg.tile_r0; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
         a.acth = c->aact.h; a.next_type = down.type; a.ncols = I; a.xrows = T;
-        TRY(launch_gemm2(a, st));
+        TRY(launch_gemm4(a, st));
         stage_end(c, "gate_up", st);
         G2Args d = {};
         d.a = down; d.glu = 0; d.xh = c->aact.h; d.ne11 = K; d.K = K;
         d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
         d.tile_r0 = dd.tile_r0; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles; d.xrows = (int64_t)T * K;
         d.y = c->z; d.ldy = D; d.ncols = D;
-        TRY(launch_gemm2(d, st));
+        TRY(launch_gemm4(d, st));
         stage_end(c, "down", st);
     } else {
         // Q6_K gate/up: fp16 dequant on 16x16x32 MFMA
@@ -638,9 +641,9 @@ int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const 
     hipStream_t st = (hipStream_t)stream;
     const int64_t rows = T * n_used;
     const int max_active = (int)std::min<int64_t>(E, rows);
-    const int max_tiles = (int)((rows + GEMM_BM - 1) / GEMM_BM + max_active);
+    const int max_tiles = (int)((rows + G4_BM - 1) / G4_BM + max_active);
     const DispBuf &dsp = c->disp[0];
-    TRY(launch_dispatch((const int32_t *)ids->data, T, (int)n_used, (int)E, GEMM_BM, dsp.view(), st));
+    TRY(launch_dispatch((const int32_t *)ids->data, T, (int)n_used, (int)E, G4_BM, dsp.view(), st));
     const ExpertMat M = as_mat(*as);
     const float *bp = (const float *)b->data;
     if (as->type == MI_TYPE_F32) {
@@ -672,7 +675,7 @@ int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const 
     a.counts = dsp.counts; a.offsets = dsp.offsets; a.perm = dsp.perm; a.tile_e = dsp.tile_e;
     a.tile_r0 = dsp.tile_r0; a.n_tiles = dsp.n_tiles; a.max_tiles = max_tiles; a.xrows = T * ne11;
     a.y = (float *)dst->data; a.ldy = N; a.ncols = N;
-    return launch_gemm2(a, st);
+    return launch_gemm4(a, st);
 }
 
 int mi_quantize(mi_moe_ctx *c, int32_t type, const float *src, void *dst, int64_t nrows, int64_t n_per_row,

@@ -145,31 +145,34 @@ __device__ __host__ inline int mfma_elem(int wtype, int pos) {
 
 // v_mfma_f32_32x32x16_f16 order: step s (0..15), lane group g (lane/32, 0..1),
 // slot p (0..7), pos = 16*s + 8*g + p.
-// Q4_K: lane group g owns qs[64g .. 64g+64) = chunks 2g, 2g+1; step s uses
-// dword s&7 of chunk 2g + (s>>3): elements 64c + 4(s&7) + {0..3} (low
-// nibbles, sub-block 2c) and 64c + 32 + 4(s&7) + {0..3} (high, 2c+1), in
-// the operand order of q4k_elem.
+// Q4_K: steps 8 h .. 8 h + 7 cover half h of the block (qs[64h..64h+64));
+// lane group g takes chunk c = 2 h + g (qs[32c..32c+32)); step s uses dword
+// s&7 of that chunk: elements 64c + 4(s&7) + {0..3} (low nibbles, sub-block
+// 2c) and 64c + 32 + 4(s&7) + {0..3} (high, 2c+1), in the operand order of
+// q4k_elem.
 __device__ __host__ inline int q4k_elem32(int pos) {
     const int s = pos >> 4, g = (pos >> 3) & 1, p = pos & 7;
     const int off[8] = {0, 2, 32, 34, 1, 3, 33, 35};
-    return 64 * (2 * g + (s >> 3)) + 4 * (s & 7) + off[p];
+    return 64 * (2 * (s >> 3) + g) + 4 * (s & 7) + off[p];
 }
-// Q6_K: lane group g owns half g (ql[64g..64g+64), qh[32g..32g+32)); step s =
-// 2*jj + w covers l = 4jj..4jj+3 of quarters (q1, q2) for w = 0 or (q3, q4)
-// for w = 1; slots 0..3 the first quarter, 4..7 the second.
+// Q6_K: steps 8 h .. 8 h + 7 cover half h of the block (ql[64h..64h+64),
+// qh[32h..32h+32), scales[8h..8h+8)); lane group g takes the quarter-row
+// positions l = 16 g .. 16 g + 15; step s = 8 h + 2 jj + w covers
+// l = 16 g + 4 jj .. + 3 of quarters (q1, q2) for w = 0 or (q3, q4) for w = 1;
+// slots 0..3 the first quarter, 4..7 the second.
 __device__ __host__ inline int q6k_elem32(int pos) {
     const int s = pos >> 4, g = (pos >> 3) & 1, p = pos & 7;
-    return 128 * g + 4 * (s >> 1) + 64 * (s & 1) + 32 * (p >> 2) + (p & 3);
+    return 128 * (s >> 3) + 16 * g + 4 * ((s & 7) >> 1) + (p & 3) + 32 * (p >> 2) + 64 * (s & 1);
 }
 __device__ __host__ inline int q4k_pos32(int e) {
     const int c = e >> 6, r = e & 63, hi = r >> 5, r2 = r & 31, j = r2 >> 2, lo = r2 & 3;
-    const int g = c >> 1, s = 8 * (c & 1) + j, p = (lo & 1) * 4 + hi * 2 + (lo >> 1);
+    const int g = c & 1, s = 8 * (c >> 1) + j, p = (lo & 1) * 4 + hi * 2 + (lo >> 1);
     return 16 * s + 8 * g + p;
 }
 __device__ __host__ inline int q6k_pos32(int e) {
-    const int g = e >> 7, r = e & 127, qq = r >> 5, l = r & 31, jj = l >> 2, i = l & 3;
-    const int s = 2 * jj + (qq >> 1), p = 4 * (qq & 1) + i;
-    return 16 * s + 8 * g + p;
+    const int h = e >> 7, r = e & 127, qq = r >> 5, l = r & 31;
+    const int s = 8 * h + 2 * ((l >> 2) & 3) + (qq >> 1), p = 4 * (qq & 1) + (l & 3);
+    return 16 * s + 8 * (l >> 4) + p;
 }
 __device__ __host__ inline int mfma32_elem(int wtype, int pos) {
     return wtype == 14 ? q6k_elem32(pos) : q4k_elem32(pos);

@@ -245,19 +245,24 @@ int launch_topk_softmax(const float *logits, int64_t ld_logits, int64_t T, int E
 //      chose expert e; rank(t, e) = tokens before t in e's bitset + the
 //      expert's running base.  Ids repeated inside one token (legal for
 //      mul_mat_id, never produced by top-k) take the ballot path instead.
+// GEMM tiles of BM rows: every expert's full tiles first (expert order), then
+// one partial tile per expert with cnt % BM rows, by decreasing row count
+// (ties: lower expert first), so the longest work-groups start first.
 constexpr int DISPATCH_THREADS = 1024;
 constexpr int DISPATCH_WAVES = DISPATCH_THREADS / 64;
 constexpr int DISPATCH_LDS_BYTES = 48 * 1024;
+constexpr int DISPATCH_HEAD_INTS = 6;   // per-expert LDS arrays before the bitsets
 
 __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__restrict__ ids, int64_t T, int K,
                                                                int E, int BM, int wpc, Dispatch d) {
     extern __shared__ __attribute__((aligned(16))) unsigned char dsm_raw[];
     int *cnt = (int *)dsm_raw;                     // [E]
     int *scn = cnt + E;                            // [E] inclusive scan of counts
-    int *tsc = scn + E;                            // [E] inclusive scan of tiles
+    int *tsc = scn + E;                            // [E] inclusive scan of full tiles
     int *asc = tsc + E;                            // [E] inclusive scan of active flags
-    int *run = asc + E;                            // [E] running list position
-    unsigned char *rest = dsm_raw + (((size_t)5 * E * sizeof(int) + 15) & ~(size_t)15);
+    int *psc = asc + E;                            // [E] inclusive scan of partial-tile flags
+    int *run = psc + E;                            // [E] running list position
+    unsigned char *rest = dsm_raw + (((size_t)DISPATCH_HEAD_INTS * E * sizeof(int) + 15) & ~(size_t)15);
     __shared__ int bad, dup;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t n = T * K;
@@ -281,15 +286,16 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
     __syncthreads();
     if (tid < E) {
         scn[tid] = cnt[tid];
-        tsc[tid] = (cnt[tid] + BM - 1) / BM;
+        tsc[tid] = cnt[tid] / BM;
         asc[tid] = cnt[tid] > 0 ? 1 : 0;
+        psc[tid] = cnt[tid] % BM > 0 ? 1 : 0;
     }
     __syncthreads();
-    for (int off = 1; off < E; off <<= 1) {        // three inclusive scans at once
-        int a0 = 0, a1 = 0, a2 = 0;
-        if (tid < E && tid >= off) { a0 = scn[tid - off]; a1 = tsc[tid - off]; a2 = asc[tid - off]; }
+    for (int off = 1; off < E; off <<= 1) {        // four inclusive scans at once
+        int a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+        if (tid < E && tid >= off) { a0 = scn[tid - off]; a1 = tsc[tid - off]; a2 = asc[tid - off]; a3 = psc[tid - off]; }
         __syncthreads();
-        if (tid < E) { scn[tid] += a0; tsc[tid] += a1; asc[tid] += a2; }
+        if (tid < E) { scn[tid] += a0; tsc[tid] += a1; asc[tid] += a2; psc[tid] += a3; }
         __syncthreads();
     }
     if (tid < E) {
@@ -298,16 +304,25 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
         d.counts[tid] = c;
         d.offsets[tid] = off;
         run[tid] = off;
-        const int nt = (c + BM - 1) / BM;
-        const int tb = tsc[tid] - nt;
-        for (int j = 0; j < nt; ++j) {
+        const int nf = c / BM, rem = c - nf * BM;
+        const int tb = tsc[tid] - nf;
+        for (int j = 0; j < nf; ++j) {
             d.tile_e[tb + j] = tid;
             d.tile_r0[tb + j] = j * BM;
+        }
+        if (rem > 0) {
+            int rank = 0;
+            for (int e2 = 0; e2 < E; ++e2) {
+                const int r2 = cnt[e2] % BM;
+                rank += (r2 > rem) | ((r2 == rem) & (e2 < tid));
+            }
+            d.tile_e[tsc[E - 1] + rank] = tid;
+            d.tile_r0[tsc[E - 1] + rank] = nf * BM;
         }
         if (c > 0) d.active_e[asc[tid] - 1] = tid;
         if (tid == E - 1) {
             d.offsets[E] = scn[tid];
-            *d.n_tiles = tsc[tid];
+            *d.n_tiles = tsc[tid] + psc[tid];
             *d.n_active = asc[tid];
             *d.bad_ids = bad;
         }
@@ -391,7 +406,7 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
 
 int launch_dispatch(const int32_t *ids, int64_t T, int K, int E, int BM, const Dispatch &d, hipStream_t st) {
     if (E <= 0 || E > 256) return -6;
-    const size_t head = ((size_t)5 * E * sizeof(int) + 15) & ~(size_t)15;
+    const size_t head = ((size_t)DISPATCH_HEAD_INTS * E * sizeof(int) + 15) & ~(size_t)15;
     // bitset chunk: wpc 64-token words per expert, E * wpc * (8 + 4) bytes
     int64_t wpc = (T + 63) / 64;
     const int64_t wpc_max = (int64_t)((DISPATCH_LDS_BYTES - head) / ((size_t)E * 12));

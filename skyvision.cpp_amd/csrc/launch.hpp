@@ -139,6 +139,11 @@ struct G2Args {
 };
 int launch_gemm2(const G2Args &g, hipStream_t st);
 
+// 4-wave grouped GEMMs over 128-row tiles (k_gemm4.hip), same arguments;
+// glu = 1 takes fp16 d*q activations (not codes) and ignores xd / xbs
+constexpr int G4_BM = 128;
+int launch_gemm4(const G2Args &g, hipStream_t st);
+
 // Single-token MoE block in one cooperative kernel (k_decode.hip).
 struct DecArgs {
     const float *rw, *rb, *x;     // router W [E][D], bias [E] or NULL, token [D]

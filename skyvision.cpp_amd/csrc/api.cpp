@@ -241,12 +241,14 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
     const bool same_ids = ids_gu == ids_dn;
     const bool kq = is_kquant(L->gate.type);
     const bool gemm = kq && (T >= c->gemm_threshold || D > 8 * QK || I > 8 * QK);
-    // GEMM M-tile height: 128 for the 4-wave GEMMs (Q4_K gate/up), 64 otherwise
-    const int bm = gemm && L->gate.type == MI_TYPE_Q4_K ? G4_BM : GEMM_BM;
+    // GEMM M-tiles: balanced tiles of at most G4_BM rows for the 4-wave GEMMs
+    // (Q4_K gate/up), GEMM_BM-row tiles otherwise
+    const bool g4 = gemm && L->gate.type == MI_TYPE_Q4_K;
+    const int bm = g4 ? G4_BM : GEMM_BM;
     const int max_tiles = (int)((rows + bm - 1) / bm + max_active);
 
-    TRY(launch_dispatch(ids_gu, T, K, E, bm, c->disp[0].view(), st));
-    if (!same_ids) TRY(launch_dispatch(ids_dn, T, K, E, bm, c->disp[1].view(), st));
+    TRY(launch_dispatch(ids_gu, T, K, E, bm, g4, c->disp[0].view(), st));
+    if (!same_ids) TRY(launch_dispatch(ids_dn, T, K, E, bm, g4, c->disp[1].view(), st));
     const DispBuf &dg = c->disp[0];
     const DispBuf &dd = same_ids ? c->disp[0] : c->disp[1];
     stage_end(c, "dispatch", st);
@@ -325,9 +327,14 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         a.xh = c->ax.h; a.ne11 = 1; a.K = K;
         a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.tile_e = dg.tile_e;
         a.tile_r0 = dg.tile_r0; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
-        a.acth = c->aact.h; a.next_type = down.type; a.ncols = I; a.xrows = T;
+        a.y = c->f1; a.ldy = I; a.ncols = I; a.xrows = T;
         TRY(launch_gemm4(a, st));
         stage_end(c, "gate_up", st);
+        // Q8_K of the GLU rows (ggml: the down mul_mat_id quantizes its F32 input)
+        Q8Out qa;
+        qa.xh = c->aact.h; qa.wtype = down.type; qa.order = 1;
+        TRY(launch_q8k_rows(c->f1, I, rows, I, qa, st));
+        stage_end(c, "q8k_act", st);
         G2Args d = {};
         d.a = down; d.glu = 0; d.xh = c->aact.h; d.ne11 = K; d.K = K;
         d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
@@ -643,7 +650,7 @@ int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const 
     const int max_active = (int)std::min<int64_t>(E, rows);
     const int max_tiles = (int)((rows + G4_BM - 1) / G4_BM + max_active);
     const DispBuf &dsp = c->disp[0];
-    TRY(launch_dispatch((const int32_t *)ids->data, T, (int)n_used, (int)E, G4_BM, dsp.view(), st));
+    TRY(launch_dispatch((const int32_t *)ids->data, T, (int)n_used, (int)E, G4_BM, 1, dsp.view(), st));
     const ExpertMat M = as_mat(*as);
     const float *bp = (const float *)b->data;
     if (as->type == MI_TYPE_F32) {

@@ -245,16 +245,17 @@ int launch_topk_softmax(const float *logits, int64_t ld_logits, int64_t T, int E
 //      chose expert e; rank(t, e) = tokens before t in e's bitset + the
 //      expert's running base.  Ids repeated inside one token (legal for
 //      mul_mat_id, never produced by top-k) take the ballot path instead.
-// GEMM tiles of BM rows: every expert's full tiles first (expert order), then
-// one partial tile per expert with cnt % BM rows, by decreasing row count
-// (ties: lower expert first), so the longest work-groups start first.
+// GEMM tiles of at most BM rows: every expert's full tiles first (expert
+// order), then one partial tile per expert with cnt % BM rows, by decreasing
+// row count (ties: lower expert first), so the longest work-groups start
+// first; or (balanced) ceil(cnt / BM) equal tiles per expert.
 constexpr int DISPATCH_THREADS = 1024;
 constexpr int DISPATCH_WAVES = DISPATCH_THREADS / 64;
 constexpr int DISPATCH_LDS_BYTES = 48 * 1024;
 constexpr int DISPATCH_HEAD_INTS = 6;   // per-expert LDS arrays before the bitsets
 
 __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__restrict__ ids, int64_t T, int K,
-                                                               int E, int BM, int wpc, Dispatch d) {
+                                                               int E, int BM, int balanced, int wpc, Dispatch d) {
     extern __shared__ __attribute__((aligned(16))) unsigned char dsm_raw[];
     int *cnt = (int *)dsm_raw;                     // [E]
     int *scn = cnt + E;                            // [E] inclusive scan of counts
@@ -286,9 +287,9 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
     __syncthreads();
     if (tid < E) {
         scn[tid] = cnt[tid];
-        tsc[tid] = cnt[tid] / BM;
+        tsc[tid] = balanced ? (cnt[tid] + BM - 1) / BM : cnt[tid] / BM;
         asc[tid] = cnt[tid] > 0 ? 1 : 0;
-        psc[tid] = cnt[tid] % BM > 0 ? 1 : 0;
+        psc[tid] = !balanced && cnt[tid] % BM > 0 ? 1 : 0;
     }
     __syncthreads();
     for (int off = 1; off < E; off <<= 1) {        // four inclusive scans at once
@@ -304,7 +305,15 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
         d.counts[tid] = c;
         d.offsets[tid] = off;
         run[tid] = off;
-        const int nf = c / BM, rem = c - nf * BM;
+        if (balanced) {
+            const int nt = (c + BM - 1) / BM, tb = tsc[tid] - nt;
+            const int base = nt ? c / nt : 0, extra = c - base * nt;
+            for (int j = 0; j < nt; ++j) {
+                d.tile_e[tb + j] = tid;
+                d.tile_r0[tb + j] = j * base + (j < extra ? j : extra);
+            }
+        }
+        const int nf = balanced ? 0 : c / BM, rem = balanced ? 0 : c - nf * BM;
         const int tb = tsc[tid] - nf;
         for (int j = 0; j < nf; ++j) {
             d.tile_e[tb + j] = tid;
@@ -404,7 +413,8 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
     }
 }
 
-int launch_dispatch(const int32_t *ids, int64_t T, int K, int E, int BM, const Dispatch &d, hipStream_t st) {
+int launch_dispatch(const int32_t *ids, int64_t T, int K, int E, int BM, int balanced, const Dispatch &d,
+                    hipStream_t st) {
     if (E <= 0 || E > 256) return -6;
     const size_t head = ((size_t)DISPATCH_HEAD_INTS * E * sizeof(int) + 15) & ~(size_t)15;
     // bitset chunk: wpc 64-token words per expert, E * wpc * (8 + 4) bytes
@@ -415,7 +425,8 @@ int launch_dispatch(const int32_t *ids, int64_t T, int K, int E, int BM, const D
     const size_t bitset_bytes = (size_t)E * (size_t)wpc * 12;
     const size_t ballot_bytes = (size_t)2 * DISPATCH_WAVES * E * sizeof(int);
     const size_t smem = head + (bitset_bytes > ballot_bytes ? bitset_bytes : ballot_bytes);
-    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(DISPATCH_THREADS), smem, st, ids, T, K, E, BM, (int)wpc, d);
+    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(DISPATCH_THREADS), smem, st, ids, T, K, E, BM, balanced, (int)wpc,
+                       d);
     return hip_check_launch();
 }
 

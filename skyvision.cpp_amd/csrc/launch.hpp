@@ -50,7 +50,12 @@ struct Dispatch {
     int32_t *n_active;   // [1]
     int32_t *bad_ids;    // [1] number of ids outside [0, E) (skipped)
 };
-int launch_dispatch(const int32_t *ids, int64_t T, int K, int E, int BM, const Dispatch &d, hipStream_t st);
+// balanced = 0: per expert floor(cnt / BM) full tiles, then one partial tile
+// per expert with cnt % BM rows (largest first); balanced = 1: per expert
+// ceil(cnt / BM) tiles of equal size (the first cnt % n one row longer), in
+// expert order
+int launch_dispatch(const int32_t *ids, int64_t T, int K, int E, int BM, int balanced, const Dispatch &d,
+                    hipStream_t st);
 
 // out[t][n] = res[t][n] + sum_k (double)(z[t*K+k][n] * w[t][k])   (res may be NULL)
 int launch_combine(const float *z, const float *w, const float *res, float *out, int64_t T, int K, int D,
@@ -139,9 +144,11 @@ struct G2Args {
 };
 int launch_gemm2(const G2Args &g, hipStream_t st);
 
-// 4-wave grouped GEMMs over 128-row tiles (k_gemm4.hip), same arguments;
-// glu = 1 takes fp16 d*q activations (not codes) and ignores xd / xbs
-constexpr int G4_BM = 128;
+// 4-wave grouped GEMMs (k_gemm4.hip), same arguments; tiles of at most
+// G4_BM rows from a balanced dispatch.  glu = 1 takes fp16 d*q activations
+// (not codes), ignores xd / xbs and writes fp32 GLU rows to y (ldy), whose
+// Q8_K the caller computes (launch_q8k_rows) for the down product.
+constexpr int G4_BM = 160;
 int launch_gemm4(const G2Args &g, hipStream_t st);
 
 // Single-token MoE block in one cooperative kernel (k_decode.hip).

@@ -201,9 +201,9 @@ def main() -> int:
                    "n_ff": spec.I, "gate_up": "Q4_K", "down": "Q6_K" if spec.down_type == M.TYPE_Q6_K else "Q4_K",
                    "act": ACT_NAMES[spec.act], "layer_copies": args.copies,
                    "touched_experts": touched, "layer_flops": W.flops(spec, T)},
-        "roofline": {"bound": "mfma", "kernel": "k_g2_glu (gate/up grouped GEMM + GLU + Q8_K)",
+        "roofline": {"bound": "mfma", "kernel": "k_g4_glu (gate/up grouped GEMM + GLU)",
                      "achieved": achieved, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": measured_traffic("k_g2_glu"),
+                     "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": measured_traffic("k_g4_glu"),
                      "kernel_ms": gu_ms, "flops_per_launch": gu_flops},
         "stages_ms": stages,
     }

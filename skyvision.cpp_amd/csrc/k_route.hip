@@ -98,6 +98,9 @@ int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, cons
 typedef double double4_t __attribute__((ext_vector_type(4)));
 constexpr int RM_MAX_CHUNKS = 32;   // D <= 2048 (64 KB of LDS partials)
 
+// Grid: one work-group per (16-token slab, 16-expert tile); the slab's
+// expert tiles run on one XCD (slab s on XCD s % 8, work-groups dealt to the
+// XCDs in turn), so each token's row is fetched into one L2 only.
 template <bool VEC>
 __global__ void __launch_bounds__(1024) k_router_mfma(const float *__restrict__ W, const float *__restrict__ bias,
                                                       const float *__restrict__ x, int64_t ldx, int64_t T, int D,
@@ -106,8 +109,12 @@ __global__ void __launch_bounds__(1024) k_router_mfma(const float *__restrict__ 
     const int nw = blockDim.x >> 6;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nch = (D + 63) / 64;
-    const int e0 = blockIdx.x * 16;
-    const int64_t t0 = (int64_t)blockIdx.y * 16;
+    const int net = (E + 15) / 16;
+    const int lin = blockIdx.x, q = lin >> 3;
+    const int64_t slab = (int64_t)(q / net) * 8 + (lin & 7);
+    if (slab * 16 >= T) return;
+    const int e0 = (q % net) * 16;
+    const int64_t t0 = slab * 16;
     const int row = lane & 15, g = lane >> 4;
     const int64_t tok = t0 + row;
     const int ex = e0 + row;
@@ -118,24 +125,25 @@ __global__ void __launch_bounds__(1024) k_router_mfma(const float *__restrict__ 
         const int base = 64 * c + 16 * g;
         float xv[16], wv[16];
         if (VEC) {
-            for (int q = 0; q < 4; ++q) {
-                const float4 a = *(const float4 *)(xr + base + 4 * q);
-                const float4 b = *(const float4 *)(wr + base + 4 * q);
-                xv[4 * q] = a.x; xv[4 * q + 1] = a.y; xv[4 * q + 2] = a.z; xv[4 * q + 3] = a.w;
-                wv[4 * q] = b.x; wv[4 * q + 1] = b.y; wv[4 * q + 2] = b.z; wv[4 * q + 3] = b.w;
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 a = *(const float4 *)(xr + base + 4 * q4);
+                const float4 b = *(const float4 *)(wr + base + 4 * q4);
+                xv[4 * q4] = a.x; xv[4 * q4 + 1] = a.y; xv[4 * q4 + 2] = a.z; xv[4 * q4 + 3] = a.w;
+                wv[4 * q4] = b.x; wv[4 * q4 + 1] = b.y; wv[4 * q4 + 2] = b.z; wv[4 * q4 + 3] = b.w;
             }
         } else {
-            for (int s = 0; s < 16; ++s) {
-                const int d = base + s;
-                xv[s] = d < D ? xr[d] : 0.f;
-                wv[s] = d < D ? wr[d] : 0.f;
+            for (int s2 = 0; s2 < 16; ++s2) {
+                const int dd = base + s2;
+                xv[s2] = dd < D ? xr[dd] : 0.f;
+                wv[s2] = dd < D ? wr[dd] : 0.f;
             }
         }
         double4_t part = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            const double a = tok_ok ? (double)xv[s] : 0.0;
-            const double b = ex_ok ? (double)wv[s] : 0.0;
+        for (int s2 = 0; s2 < 16; ++s2) {
+            const double a = tok_ok ? (double)xv[s2] : 0.0;
+            const double b = ex_ok ? (double)wv[s2] : 0.0;
             part = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, part, 0, 0, 0);
         }
         for (int r = 0; r < 4; ++r) rparts[c * 256 + lane * 4 + r] = part[r];
@@ -146,8 +154,17 @@ __global__ void __launch_bounds__(1024) k_router_mfma(const float *__restrict__ 
         const int l = threadIdx.x >> 2, r = threadIdx.x & 3;
         const int64_t tt = t0 + 4 * r + (l >> 4);
         const int ee = e0 + (l & 15);
+        // chunk partials added in chunk order, eight loads in flight
         double acc = 0.0;
-        for (int c = 0; c < nch; ++c) acc = acc + rparts[c * 256 + threadIdx.x];
+        int c = 0;
+        for (; c + 8 <= nch; c += 8) {
+            double v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = rparts[(c + j) * 256 + threadIdx.x];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc = acc + v[j];
+        }
+        for (; c < nch; ++c) acc = acc + rparts[c * 256 + threadIdx.x];
         if (tt < T && ee < E) {
             float v = (float)acc;
             if (bias) v = v + bias[ee];
@@ -191,14 +208,15 @@ int launch_router(const float *W, const float *b, const float *x, int64_t ldx, i
                   float *logits, hipStream_t st) {
     if (T <= 0) return 0;
     const int nch = (D + 63) / 64;
-    if (nch <= RM_MAX_CHUNKS && T <= 65535 * 16) {
+    if (nch <= RM_MAX_CHUNKS && T <= (int64_t)1 << 30) {
         const bool vec = (D % 64 == 0) && (ldx % 4 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)W % 16 == 0);
-        const int64_t blocks = (int64_t)((E + 15) / 16) * ((T + 15) / 16);
-        const int nw = blocks >= 256 ? imin(4, nch) : imin(16, nch);
-        const dim3 grid((unsigned)((E + 15) / 16), (unsigned)((T + 15) / 16));
+        const int nw = imin(16, nch);
+        const int64_t net = (E + 15) / 16, nslab = (T + 15) / 16;
+        const int64_t blocks = 8 * net * ((nslab + 7) / 8);
+        if (blocks > 0x7fffffff) return -6;
         const size_t smem = sizeof(double) * 256 * (size_t)nch;
-        if (vec) hipLaunchKernelGGL(k_router_mfma<true>, grid, dim3(64 * nw), smem, st, W, b, x, ldx, T, D, E, logits);
-        else hipLaunchKernelGGL(k_router_mfma<false>, grid, dim3(64 * nw), smem, st, W, b, x, ldx, T, D, E, logits);
+        if (vec) hipLaunchKernelGGL(k_router_mfma<true>, dim3((unsigned)blocks), dim3(64 * nw), smem, st, W, b, x, ldx, T, D, E, logits);
+        else hipLaunchKernelGGL(k_router_mfma<false>, dim3((unsigned)blocks), dim3(64 * nw), smem, st, W, b, x, ldx, T, D, E, logits);
     } else {
         if (nch > 256 || T > 65535) return -6;
         const int epb = 256 / nch;
@@ -209,19 +227,20 @@ int launch_router(const float *W, const float *b, const float *x, int64_t ldx, i
 }
 
 // ---------------------------------------------------------------- top-k
-// One wave per token.  K rounds of a wave arg-max (largest value, lowest id on
-// ties) over the not-yet-taken experts; then softmax over the K selected
-// logits: max, expf(v - max), sum in fp64 in slot order, scale by
-// (float)(1.0 / sum) - the ggml_soft_max order.
+// One wave per token: rank-based top-k (largest value, lowest id on ties),
+// then softmax over the K selected logits: max, expf(v - max), sum in fp64 in
+// slot order, scale by (float)(1.0 / sum) - the ggml_soft_max order.
 __global__ void __launch_bounds__(256) k_topk_softmax(const float *__restrict__ logits, int64_t ldl, int64_t T,
                                                       int E, int K, int32_t *__restrict__ sel, int64_t lds,
                                                       float *__restrict__ w) {
+    __shared__ __attribute__((aligned(16))) float s_v[4][64 * TOPK_MAX_PER_LANE];
+    __shared__ int s_sel[4][64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t t = (int64_t)blockIdx.x * 4 + wave;
-    if (t >= T) return;
+    if (t >= T) return;   // whole waves; the routine synchronizes only its own wave
     int mysel;
     float myw;
-    topk_softmax_wave(logits + t * ldl, E, K, lane, mysel, myw, w != nullptr);
+    topk_softmax_wave(logits + t * ldl, E, K, lane, s_v[wave], s_sel[wave], mysel, myw, w != nullptr);
     if (lane < K) {
         sel[t * lds + lane] = mysel;
         if (w) w[t * K + lane] = myw;
@@ -238,50 +257,64 @@ int launch_topk_softmax(const float *logits, int64_t ld_logits, int64_t T, int E
 }
 
 // ---------------------------------------------------------------- dispatch
-// Single work-group of 1024 threads.  Stable: within an expert the list is in
-// flat (t*K + k) order, i.e. token-ascending then slot-ascending.
-//   1. counts (LDS atomics) -> exclusive scans: offsets, GEMM M-tiles, active list
-//   2. ranks: per chunk of tokens, a bitset bits[e][word] of the tokens that
-//      chose expert e; rank(t, e) = tokens before t in e's bitset + the
-//      expert's running base.  Ids repeated inside one token (legal for
-//      mul_mat_id, never produced by top-k) take the ballot path instead.
+// One work-group of 1024 threads per expert.  The ids pass through LDS in
+// chunks of at most DISPATCH_IDS (coalesced loads); every work-group counts
+// all of them (LDS atomics), scans the counts, writes its own expert's entries
+// (count, offset, GEMM tiles, active-list slot), and then lists its expert's
+// slots in flat (t*K + k) order: per 1024 ids, a wave ballot of the ids equal
+// to the expert, wave totals in LDS, positions = running base + waves before
+// + lanes before.  The list is the stable counting sort of the flat ids
+// (token-ascending, then slot-ascending; ids repeated inside a token keep
+// their slot order).  Ids outside [0, E) are counted in bad_ids and skipped.
 // GEMM tiles of at most BM rows: every expert's full tiles first (expert
 // order), then one partial tile per expert with cnt % BM rows, by decreasing
 // row count (ties: lower expert first), so the longest work-groups start
 // first; or (balanced) ceil(cnt / BM) equal tiles per expert.
 constexpr int DISPATCH_THREADS = 1024;
 constexpr int DISPATCH_WAVES = DISPATCH_THREADS / 64;
-constexpr int DISPATCH_LDS_BYTES = 48 * 1024;
-constexpr int DISPATCH_HEAD_INTS = 6;   // per-expert LDS arrays before the bitsets
+constexpr int DISPATCH_MAX_E = 256;
+constexpr int DISPATCH_IDS = 8192;                         // ids per staged chunk (32 KB)
 
-__global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__restrict__ ids, int64_t T, int K,
-                                                               int E, int BM, int balanced, int wpc, Dispatch d) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char dsm_raw[];
-    int *cnt = (int *)dsm_raw;                     // [E]
-    int *scn = cnt + E;                            // [E] inclusive scan of counts
-    int *tsc = scn + E;                            // [E] inclusive scan of full tiles
-    int *asc = tsc + E;                            // [E] inclusive scan of active flags
-    int *psc = asc + E;                            // [E] inclusive scan of partial-tile flags
-    int *run = psc + E;                            // [E] running list position
-    unsigned char *rest = dsm_raw + (((size_t)DISPATCH_HEAD_INTS * E * sizeof(int) + 15) & ~(size_t)15);
-    __shared__ int bad, dup;
+// ids[0 .. m) -> sid (m <= DISPATCH_IDS); independent loads, one latency
+__device__ __forceinline__ void dispatch_stage(const int32_t *__restrict__ src, int m, int *sid, int tid) {
+    int v[DISPATCH_IDS / DISPATCH_THREADS];
+#pragma unroll
+    for (int j = 0; j < DISPATCH_IDS / DISPATCH_THREADS; ++j) {
+        const int i = j * DISPATCH_THREADS + tid;
+        v[j] = i < m ? src[i] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < DISPATCH_IDS / DISPATCH_THREADS; ++j) {
+        const int i = j * DISPATCH_THREADS + tid;
+        if (i < m) sid[i] = v[j];
+    }
+}
+
+__global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__restrict__ ids, int64_t n, int E,
+                                                               int BM, int balanced, Dispatch d) {
+    __shared__ int cnt[DISPATCH_MAX_E];   // counts
+    __shared__ int scn[DISPATCH_MAX_E];   // inclusive scan of counts
+    __shared__ int tsc[DISPATCH_MAX_E];   // inclusive scan of full (or balanced) tiles
+    __shared__ int asc[DISPATCH_MAX_E];   // inclusive scan of active flags
+    __shared__ int psc[DISPATCH_MAX_E];   // inclusive scan of partial-tile flags
+    __shared__ int sid[DISPATCH_IDS];
+    __shared__ int wsum[DISPATCH_WAVES];
+    __shared__ int bad;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int64_t n = T * K;
+    const int me = blockIdx.x;
+    const bool one_chunk = n <= DISPATCH_IDS;
 
     for (int e = tid; e < E; e += DISPATCH_THREADS) cnt[e] = 0;
-    if (tid == 0) { bad = 0; dup = 0; }
-    __syncthreads();
-    for (int64_t t = tid; t < T; t += DISPATCH_THREADS) {
-        const int32_t *it = ids + t * K;
-        for (int k = 0; k < K; ++k) {
-            const int e = it[k];
-            if (e >= 0 && e < E) {
-                atomicAdd(&cnt[e], 1);
-                for (int k2 = 0; k2 < k; ++k2)
-                    if (it[k2] == e) dup = 1;
-            } else {
-                atomicAdd(&bad, 1);
-            }
+    if (tid == 0) bad = 0;
+    for (int64_t c0 = 0; c0 < n; c0 += DISPATCH_IDS) {
+        const int m = (int)(c0 + DISPATCH_IDS < n ? DISPATCH_IDS : n - c0);
+        if (c0 > 0) __syncthreads();   // the previous chunk's counting is done
+        dispatch_stage(ids + c0, m, sid, tid);
+        __syncthreads();
+        for (int i = tid; i < m; i += DISPATCH_THREADS) {
+            const int e = sid[i];
+            if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+            else atomicAdd(&bad, 1);
         }
     }
     __syncthreads();
@@ -299,134 +332,78 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
         if (tid < E) { scn[tid] += a0; tsc[tid] += a1; asc[tid] += a2; psc[tid] += a3; }
         __syncthreads();
     }
-    if (tid < E) {
-        const int c = cnt[tid];
-        const int off = scn[tid] - c;
-        d.counts[tid] = c;
-        d.offsets[tid] = off;
-        run[tid] = off;
-        if (balanced) {
-            const int nt = (c + BM - 1) / BM, tb = tsc[tid] - nt;
-            const int base = nt ? c / nt : 0, extra = c - base * nt;
-            for (int j = 0; j < nt; ++j) {
-                d.tile_e[tb + j] = tid;
-                d.tile_r0[tb + j] = j * base + (j < extra ? j : extra);
-            }
-        }
-        const int nf = balanced ? 0 : c / BM, rem = balanced ? 0 : c - nf * BM;
-        const int tb = tsc[tid] - nf;
-        for (int j = 0; j < nf; ++j) {
-            d.tile_e[tb + j] = tid;
-            d.tile_r0[tb + j] = j * BM;
-        }
-        if (rem > 0) {
-            int rank = 0;
-            for (int e2 = 0; e2 < E; ++e2) {
-                const int r2 = cnt[e2] % BM;
-                rank += (r2 > rem) | ((r2 == rem) & (e2 < tid));
-            }
-            d.tile_e[tsc[E - 1] + rank] = tid;
-            d.tile_r0[tsc[E - 1] + rank] = nf * BM;
-        }
-        if (c > 0) d.active_e[asc[tid] - 1] = tid;
-        if (tid == E - 1) {
-            d.offsets[E] = scn[tid];
-            *d.n_tiles = tsc[tid] + psc[tid];
-            *d.n_active = asc[tid];
+    const int c = cnt[me];
+    const int off = scn[me] - c;
+    if (tid == 0) {
+        d.counts[me] = c;
+        d.offsets[me] = off;
+        if (c > 0) d.active_e[asc[me] - 1] = me;
+        if (me == 0) {
+            d.offsets[E] = scn[E - 1];
+            *d.n_tiles = tsc[E - 1] + psc[E - 1];
+            *d.n_active = asc[E - 1];
             *d.bad_ids = bad;
         }
     }
-    __syncthreads();
-
-    if (!dup) {
-        unsigned long long *bits = (unsigned long long *)rest;       // [E][wpc]
-        int *pref = (int *)(bits + (size_t)E * wpc);                  // [E][wpc]
-        const int64_t tc = (int64_t)wpc * 64;
-        for (int64_t c0 = 0; c0 < T; c0 += tc) {
-            for (int j = tid; j < E * wpc; j += DISPATCH_THREADS) bits[j] = 0ull;
-            __syncthreads();
-            const int64_t c1 = c0 + tc < T ? c0 + tc : T;
-            for (int64_t t = c0 + tid; t < c1; t += DISPATCH_THREADS) {
-                const int tl = (int)(t - c0);
-                for (int k = 0; k < K; ++k) {
-                    const int e = ids[t * K + k];
-                    if (e >= 0 && e < E) atomicOr(&bits[(size_t)e * wpc + (tl >> 6)], 1ull << (tl & 63));
-                }
-            }
-            __syncthreads();
-            for (int e = tid; e < E; e += DISPATCH_THREADS) {
-                int r = run[e];
-                for (int w = 0; w < wpc; ++w) {
-                    pref[e * wpc + w] = r;
-                    r += __popcll(bits[(size_t)e * wpc + w]);
-                }
-                run[e] = r;
-            }
-            __syncthreads();
-            for (int64_t t = c0 + tid; t < c1; t += DISPATCH_THREADS) {
-                const int tl = (int)(t - c0);
-                const unsigned long long below = (1ull << (tl & 63)) - 1ull;
-                for (int k = 0; k < K; ++k) {
-                    const int e = ids[t * K + k];
-                    if (e >= 0 && e < E) {
-                        const size_t wi = (size_t)e * wpc + (tl >> 6);
-                        d.perm[pref[wi] + __popcll(bits[wi] & below)] = (int32_t)(t * K + k);
-                    }
-                }
-            }
-            __syncthreads();
+    if (balanced) {
+        const int nt = (c + BM - 1) / BM, tb = tsc[me] - nt;
+        const int base = nt ? c / nt : 0, extra = c - base * nt;
+        for (int j = tid; j < nt; j += DISPATCH_THREADS) {
+            d.tile_e[tb + j] = me;
+            d.tile_r0[tb + j] = j * base + (j < extra ? j : extra);
         }
-        return;
+    } else {
+        const int nf = c / BM, rem = c - nf * BM;
+        const int tb = tsc[me] - nf;
+        for (int j = tid; j < nf; j += DISPATCH_THREADS) {
+            d.tile_e[tb + j] = me;
+            d.tile_r0[tb + j] = j * BM;
+        }
+        if (rem > 0 && tid == 0) {
+            int rank = 0;
+            for (int e2 = 0; e2 < E; ++e2) {
+                const int r2 = cnt[e2] % BM;
+                rank += (r2 > rem) | ((r2 == rem) & (e2 < me));
+            }
+            d.tile_e[tsc[E - 1] + rank] = me;
+            d.tile_r0[tsc[E - 1] + rank] = nf * BM;
+        }
     }
 
-    // repeated ids inside a token: wave-level ranking by ballot over flat indices
-    int *wcnt = (int *)rest;                       // [16][E]
-    int *wbase = wcnt + DISPATCH_WAVES * E;        // [16][E]
-    for (int64_t base = 0; base < n; base += DISPATCH_THREADS) {
-        const int64_t i = base + tid;
-        const int e = i < n ? ids[i] : -1;
-        const bool valid = e >= 0 && e < E;
-        for (int j = tid; j < DISPATCH_WAVES * E; j += DISPATCH_THREADS) wcnt[j] = 0;
-        __syncthreads();
-        uint64_t todo = __ballot(valid);
-        int rank = 0;
-        while (todo) {
-            const int leader = __ffsll((unsigned long long)todo) - 1;
-            const int el = __shfl(e, leader, 64);
-            const uint64_t m = __ballot(valid && e == el);
-            if (valid && e == el) rank = __popcll(m & ((1ull << lane) - 1ull));
-            if (lane == leader) wcnt[wave * E + el] = __popcll(m);
-            todo &= ~m;
+    // the expert's slots in flat order
+    int run = off;
+    for (int64_t c0 = 0; c0 < n; c0 += DISPATCH_IDS) {
+        const int m = (int)(c0 + DISPATCH_IDS < n ? DISPATCH_IDS : n - c0);
+        if (!one_chunk) {
+            __syncthreads();   // every wave is done with the previous chunk
+            dispatch_stage(ids + c0, m, sid, tid);
+            __syncthreads();
         }
-        __syncthreads();
-        for (int e2 = tid; e2 < E; e2 += DISPATCH_THREADS) {
-            int r = run[e2];
-            for (int w2 = 0; w2 < DISPATCH_WAVES; ++w2) {
-                wbase[w2 * E + e2] = r;
-                r += wcnt[w2 * E + e2];
+        for (int r0 = 0; r0 < m; r0 += DISPATCH_THREADS) {
+            const int i = r0 + tid;
+            const bool hit = i < m && sid[i] == me;
+            const uint64_t mask = __ballot(hit);
+            if (lane == 0) wsum[wave] = __popcll(mask);
+            __syncthreads();
+            int before = 0, total = 0;
+#pragma unroll
+            for (int w = 0; w < DISPATCH_WAVES; ++w) {
+                const int v = wsum[w];
+                before += w < wave ? v : 0;
+                total += v;
             }
-            run[e2] = r;
+            if (hit) d.perm[run + before + __popcll(mask & ((1ull << lane) - 1ull))] = (int32_t)(c0 + i);
+            run += total;
+            __syncthreads();   // wsum is rewritten next round
         }
-        __syncthreads();
-        if (valid) d.perm[wbase[wave * E + e] + rank] = (int32_t)i;
-        __syncthreads();
     }
 }
 
 int launch_dispatch(const int32_t *ids, int64_t T, int K, int E, int BM, int balanced, const Dispatch &d,
                     hipStream_t st) {
-    if (E <= 0 || E > 256) return -6;
-    const size_t head = ((size_t)DISPATCH_HEAD_INTS * E * sizeof(int) + 15) & ~(size_t)15;
-    // bitset chunk: wpc 64-token words per expert, E * wpc * (8 + 4) bytes
-    int64_t wpc = (T + 63) / 64;
-    const int64_t wpc_max = (int64_t)((DISPATCH_LDS_BYTES - head) / ((size_t)E * 12));
-    if (wpc > wpc_max) wpc = wpc_max;
-    if (wpc < 1) wpc = 1;
-    const size_t bitset_bytes = (size_t)E * (size_t)wpc * 12;
-    const size_t ballot_bytes = (size_t)2 * DISPATCH_WAVES * E * sizeof(int);
-    const size_t smem = head + (bitset_bytes > ballot_bytes ? bitset_bytes : ballot_bytes);
-    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(DISPATCH_THREADS), smem, st, ids, T, K, E, BM, balanced, (int)wpc,
-                       d);
+    if (E <= 0 || E > DISPATCH_MAX_E || K <= 0 || BM <= 0) return -6;
+    hipLaunchKernelGGL(k_dispatch, dim3((unsigned)E), dim3(DISPATCH_THREADS), 0, st, ids, T * (int64_t)K, E, BM,
+                       balanced, d);
     return hip_check_launch();
 }
 

@@ -212,53 +212,50 @@ __device__ inline float softmax_selected_wave(float myval, int K, int lane) {
 }
 
 // Top-k of one token's E logits by one wave (E <= 64 * TOPK_MAX_PER_LANE,
-// K <= 64): K rounds of a wave arg-max (largest value, lowest id on ties)
-// over the experts not yet taken.  Lane k < K gets the k-th id and, when
-// want_w, its softmax weight over the K selected logits: max, expf(v - max),
-// sum in fp64 in slot order, scale by (float)(1.0 / sum) (ggml_soft_max).
+// K <= 64), largest value first, lower id first on ties.  The logits go to
+// the wave's LDS row sv (padded with -inf to a multiple of 4); each lane ranks
+// its own logits against all of them (rank = logits that come first: larger,
+// or equal with a lower id) and logit e of rank r < K becomes slot r.  Lane
+// k < K gets the k-th id and, when want_w, its softmax weight over the K
+// selected logits: max, expf(v - max), sum in fp64 in slot order, scale by
+// (float)(1.0 / sum) (ggml_soft_max).
 constexpr int TOPK_MAX_PER_LANE = 4;
-__device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane, int &mysel, float &myw,
-                                         bool want_w) {
+__device__ inline void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+__device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane, float *sv, int *ssel, int &mysel,
+                                         float &myw, bool want_w) {
+    const int nper = (E + 63) >> 6, E4 = (E + 3) & ~3;
     float v[TOPK_MAX_PER_LANE];
-    bool avail[TOPK_MAX_PER_LANE];
 #pragma unroll
     for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
         const int e = lane + 64 * i;
-        avail[i] = e < E;
-        v[i] = avail[i] ? l[e] : 0.f;
+        v[i] = e < E ? l[e] : -INFINITY;
+        if (e < E4) sv[e] = v[i];
     }
-    mysel = 0;
-    float myval = 0.f;
-    for (int k = 0; k < K; ++k) {
-        float bv = 0.f;
-        int bi = 0x7fffffff;
+    wave_lds_sync();
+    int r[TOPK_MAX_PER_LANE] = {0, 0, 0, 0};
+    for (int j = 0; j < E4; j += 4) {
+        const float4 q = *(const float4 *)(sv + j);
+        const float qq[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
         for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
+            if (i >= nper) break;
             const int e = lane + 64 * i;
-            if (avail[i] && (bi == 0x7fffffff || v[i] > bv)) {
-                bv = v[i];
-                bi = e;
-            }
-        }
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            const bool take = oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
-            if (take) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if (bi != 0x7fffffff && (bi & 63) == lane) {
 #pragma unroll
-            for (int i = 0; i < TOPK_MAX_PER_LANE; ++i)
-                if (lane + 64 * i == bi) avail[i] = false;
-        }
-        if (lane == k) {
-            mysel = bi;
-            myval = bv;
+            for (int c = 0; c < 4; ++c) r[i] += (qq[c] > v[i]) | ((qq[c] == v[i]) & (j + c < e));
         }
     }
+#pragma unroll
+    for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
+        const int e = lane + 64 * i;
+        if (i < nper && e < E && r[i] < K) ssel[r[i]] = e;
+    }
+    wave_lds_sync();
+    mysel = lane < K ? ssel[lane] : 0;
+    const float myval = lane < K ? sv[mysel] : 0.f;
     myw = want_w ? softmax_selected_wave(myval, K, lane) : 0.f;
 }
 

@@ -10,6 +10,9 @@
   fp64 dot of the dequantized weights with the dequantized Q8_K rows, so the
   difference is fp16 rounding only: rel-L2 <= 2e-3 (measured ~3e-4).  The
   GEMV path (exact integer dots) is checked beside it.
+* Ids repeated inside a token (legal for mul_mat_id) take the dispatch's
+  ballot path; T * n_used above one staged chunk of ids (8192) takes several
+  chunks.
 * Full BASELINE layers at T = 1024 on the GEMM path against the same layer
   on the GEMV path (bit-exact routing, outputs within 5e-3: the two differ by
   fp16 rounding plus the few Q8_K rounding flips of the activations that it
@@ -38,8 +41,10 @@ def log(*a):
 
 
 MMID_CASES = [
-    # type, Kin, N, E, n_used, T, ne11
+    # type, Kin, N, E, n_used, T, ne11[, ids repeated inside a token]
     (O.TYPE_Q4_K, 512, 300, 8, 4, 300, 1),
+    (O.TYPE_Q4_K, 512, 300, 8, 6, 700, 6, True),
+    (O.TYPE_Q6_K, 256, 520, 8, 4, 2300, 1, True),
     (O.TYPE_Q4_K, 1024, 2048, 16, 4, 257, 4),
     (O.TYPE_Q6_K, 1024, 2048, 10, 8, 64, 8),
     (O.TYPE_Q6_K, 256, 520, 8, 3, 301, 3),
@@ -47,9 +52,11 @@ MMID_CASES = [
 ]
 
 
-@pytest.mark.parametrize("case", MMID_CASES, ids=lambda c: f"t{c[0]}_k{c[1]}_n{c[2]}_e{c[3]}_u{c[4]}_T{c[5]}_b{c[6]}")
+@pytest.mark.parametrize("case", MMID_CASES,
+                         ids=lambda c: f"t{c[0]}_k{c[1]}_n{c[2]}_e{c[3]}_u{c[4]}_T{c[5]}_b{c[6]}" + ("_rep" if c[7:] else ""))
 def test_mul_mat_id_gemm(case):
-    type_, Kin, N, E, nu, T, ne11 = case
+    type_, Kin, N, E, nu, T, ne11 = case[:7]
+    rep = bool(case[7:])
     rng = np.random.default_rng(1000 + Kin + N + T)
     w = (rng.standard_normal((E * N, Kin)) * 0.02).astype(np.float32)
     raw = O.quantize(type_, w).ravel()
@@ -59,7 +66,9 @@ def test_mul_mat_id_gemm(case):
     p = np.linspace(3.0, 1.0, E)
     p[-1] = 0.0
     p = p / p.sum()
-    ids = np.stack([rng.choice(E, size=nu, replace=False, p=p) for _ in range(T)]).astype(np.int32)
+    ids = np.stack([rng.choice(E, size=nu, replace=rep, p=p) for _ in range(T)]).astype(np.int32)
+    if rep:
+        assert any(len(set(r)) < nu for r in ids.tolist())
     ref = O.mul_mat_id(type_, raw, Kin, N, E, b, ids)
 
     ctx = M.Context(0)
@@ -95,6 +104,29 @@ def _routing_buffers(T, E, K):
     for k, v in bufs.items():
         setattr(r, k, C.c_void_p(v.addr))
     return bufs, r
+
+
+@pytest.mark.parametrize("T", [1, 63, 1024, 1500, 4133])
+def test_dispatch_chunks(T):
+    """Dispatch (counts / offsets / permutation) against the oracle's stable
+    counting sort of the GPU's own top-k ids, across one and several staged
+    chunks of ids (8192 ids per chunk)."""
+    spec = FULL["qo_cfg3"]
+    ctx = M.Context(0)
+    ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
+    g = W.GpuLayer(ctx, spec)
+    x = cpu_x(spec, T)
+    xd = M.to_device(x)
+    out = M.DeviceBuffer(4 * T * spec.D)
+    bufs, r = _routing_buffers(T, spec.E, spec.K)
+    M.check("forward", ctx.forward(g.layer, xd, T, None, out, r))
+    sel = bufs["sel"].download(np.int32, (T, spec.K))
+    counts, offsets, perm = O.dispatch(sel, spec.E)
+    assert np.array_equal(bufs["counts"].download(np.int32, (spec.E,)), counts)
+    assert np.array_equal(bufs["offsets"].download(np.int32, (spec.E + 1,)), offsets)
+    assert np.array_equal(bufs["perm"].download(np.int32, (T * spec.K,)), perm)
+    log(f"dispatch T={T}: max count {int(counts.max())}")
+    ctx.close()
 
 
 @pytest.mark.parametrize("name", list(FULL))

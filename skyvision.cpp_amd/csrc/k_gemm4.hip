@@ -3,12 +3,12 @@
 // plain product (k_g4_store: the down product, mul_mat_id).
 //
 // One work-group of 4 waves per CU, one wave per SIMD.  A work-group owns a
-// tile of up to 160 dispatched rows of one expert (tokens gathered through
-// the permutation; an expert's rows are split into equal tiles of at most 160,
-// so nearly every expert is one tile and its weights are streamed once per
-// column tile) and 256 weight rows; each wave owns all of the tile's rows and
-// 64 weight rows: up to 5 x 2 MFMA tiles of 32 x 32 (160 fp32 accumulators
-// per lane).  Every dequantized weight operand feeds one MFMA per row tile
+// tile of up to G4_BM = 192 dispatched rows of one expert (tokens gathered
+// through the permutation; an expert's rows are split into equal tiles of at
+// most 192, so nearly every expert is one tile and its weights are streamed
+// once per column tile) and 256 weight rows; each wave owns all of the tile's
+// rows and 64 weight rows: up to 6 x 2 MFMA tiles of 32 x 32 (192 fp32
+// accumulators per lane).  Every dequantized weight operand feeds one MFMA per row tile
 // and every activation operand two.  Row tiles past the tile's rows are
 // skipped (one specialization of the K loop per row-tile count).
 //
@@ -25,6 +25,10 @@
 //    the block start and loads the next block over the region, one block
 //    ahead; operands are dequantized to fp16 in-register (Q4_K d*sc*q -
 //    dmin*m, Q6_K d*sc*(q - 32)).
+// LDS: two activation stages of 48 KB and the waves' weight regions (4 x 10
+// KB Q4_K, 4 x 16 KB Q6_K: 160 KB in all); the tile's activation rows sit in
+// the second stage until the K loop has taken its load offsets, the rows'
+// slot indices in the first after the K loop.
 // Between its MFMAs a stage dequantizes the next weight operand a quarter at
 // a time, reads the next step's activation operands and issues the next
 // loads, in a fixed interleave (one wave per SIMD hides ~4 VALU instructions
@@ -42,7 +46,7 @@ constexpr int G4_WAVES = 4;
 constexpr int G4_THREADS = G4_WAVES * 64;
 constexpr int G4_NWG = 256;            // weight rows per work-group
 constexpr int G4_SK = 128;             // K values per stage
-constexpr int G4_AST = G4_BM * G4_SK;  // halfs per activation stage (40 KB)
+constexpr int G4_AST = G4_BM * G4_SK;  // halfs per activation stage (48 KB)
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -83,8 +87,9 @@ __device__ __forceinline__ int g4_tile_rows(int cnt, int r0) {
     return base + (j < extra ? 1 : 0);
 }
 
-// rows of the tile: s_p = flat slot index (t*K + k) or -1, s_arow = activation row
-__device__ __forceinline__ G4Tile g4_tile(const G2Args &g, int tile, int *s_p, int *s_arow) {
+// rows of the tile: thread m < G4_BM gets row m's flat slot index p (t*K + k,
+// or -1 past the tile) and writes its activation row to s_arow
+__device__ __forceinline__ G4Tile g4_tile(const G2Args &g, int tile, int *s_arow, int &p) {
     G4Tile t;
     t.e = g.tile_e[tile];
     const int r0 = g.tile_r0[tile];
@@ -92,13 +97,23 @@ __device__ __forceinline__ G4Tile g4_tile(const G2Args &g, int tile, int *s_p, i
     t.mrows = g4_tile_rows(cnt, r0);
     t.nrt = (t.mrows + 31) >> 5;
     const int tid = threadIdx.x;
+    p = -1;
     if (tid < G4_BM) {
-        const int p = tid < t.mrows ? g.perm[off + r0 + tid] : -1;
-        s_p[tid] = p;
+        p = tid < t.mrows ? g.perm[off + r0 + tid] : -1;
         s_arow[tid] = p < 0 ? 0 : (g.ne11 == 1 ? p / g.K : p);
     }
     __syncthreads();
     return t;
+}
+
+// after the K loop (every load of this wave landed): the rows' slot indices
+// to LDS, in the first activation buffer once no wave has a load in flight
+__device__ __forceinline__ const int *g4_publish_rows(_Float16 *As0, int p) {
+    int *s_p = (int *)As0;
+    __syncthreads();
+    if (threadIdx.x < G4_BM) s_p[threadIdx.x] = p;
+    __syncthreads();
+    return s_p;
 }
 
 // ------------------------------------------------------------------ weights
@@ -128,9 +143,9 @@ template <> struct G4W<12> {
     u32x4 q[2][2][2];   // [ct][h][half]: qs chunk 2 h + g2 (stage h, steps 0-3 / 4-7)
 };
 template <> struct G4W<14> {
-    // [ct][h]: ql 64 h + 16 g2 .., ql 64 h + 32 + 16 g2 .., qh 32 h + 16 g2 ..
-    // (5 dwords each from the dword at or below, sh bytes early)
-    uint32_t a[2][2][5], b[2][2][5], c[2][2][5];
+    // [ct][h]: 16 bytes each of ql 64 h + 16 g2 .., ql 64 h + 32 + 16 g2 ..,
+    // qh 32 h + 16 g2 .. (shifted into place at the copy)
+    uint32_t a[2][2][4], b[2][2][4], c[2][2][4];
     uint32_t sc[2][5];  // scales (sh bytes early) and d (bytes 16 + sh ..)
 };
 
@@ -196,7 +211,7 @@ __device__ __forceinline__ void g4_issue_w(const G4WDma<WT> &dm, uint8_t *W, int
 
 // the lane's operand bytes of the whole block from the region
 template <int WT>
-__device__ __forceinline__ void g4_copy_w(const uint8_t *W, int l32, int g2, G4W<WT> &w) {
+__device__ __forceinline__ void g4_copy_w(const uint8_t *W, int l32, int g2, uint32_t sh, G4W<WT> &w) {
     using F = G4Fmt<WT>;
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
@@ -209,10 +224,15 @@ __device__ __forceinline__ void g4_copy_w(const uint8_t *W, int l32, int g2, G4W
                 for (int c = 0; c < 2; ++c) w.q[ct][h][c] = *(const u32x4 *)(row + 16 * (1 + 2 * (2 * h + g2) + c));
         } else {
             const int z = l32 & 7;
-            auto rd = [&](int k, uint32_t (&d)[5]) __attribute__((always_inline)) {
+            // 16 bytes from sh bytes into slot k (the run's data starts sh
+            // bytes past the dword it was loaded from)
+            auto rd = [&](int k, uint32_t (&d)[4]) __attribute__((always_inline)) {
                 const u32x4 v = *(const u32x4 *)(row + 16 * (k ^ z));
-                d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
-                d[4] = *(const uint32_t *)(row + 16 * ((k + 1) ^ z));
+                const uint32_t v4 = *(const uint32_t *)(row + 16 * ((k + 1) ^ z));
+                d[0] = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+                d[1] = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+                d[2] = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
+                d[3] = __builtin_amdgcn_alignbyte(v4, v.w, sh);
             };
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -220,7 +240,11 @@ __device__ __forceinline__ void g4_copy_w(const uint8_t *W, int l32, int g2, G4W
                 rd(4 * h + 2 + g2, w.b[ct][h]);
                 rd(9 + 2 * h + g2, w.c[ct][h]);
             }
-            rd(14, w.sc[ct]);
+            {
+                const u32x4 v = *(const u32x4 *)(row + 16 * (14 ^ z));
+                w.sc[ct][0] = v.x; w.sc[ct][1] = v.y; w.sc[ct][2] = v.z; w.sc[ct][3] = v.w;
+                w.sc[ct][4] = *(const uint32_t *)(row + 16 * (15 ^ z));
+            }
         }
     }
 }
@@ -282,13 +306,13 @@ __device__ __forceinline__ uint32_t g4_piece(const G4W<WT> &w, const G4Sc<WT> &s
     } else {
         const half2_t c1056 = {(_Float16)1056.f, (_Float16)1056.f};
         const int m = sp >> 1, ww = sp & 1;
-        const uint32_t qh = __builtin_amdgcn_alignbyte(w.c[ct][h][m + 1], w.c[ct][h][m], sh);
+        const uint32_t qh = w.c[ct][h][m];
         uint32_t q;
         if (p < 2) {
-            const uint32_t ql = __builtin_amdgcn_alignbyte(w.a[ct][h][m + 1], w.a[ct][h][m], sh);
+            const uint32_t ql = w.a[ct][h][m];
             q = ww == 0 ? (ql & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u) : ((ql >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u);
         } else {
-            const uint32_t ql = __builtin_amdgcn_alignbyte(w.b[ct][h][m + 1], w.b[ct][h][m], sh);
+            const uint32_t ql = w.b[ct][h][m];
             q = ww == 0 ? (ql & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u)
                         : ((ql >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u);
         }
@@ -370,7 +394,7 @@ __device__ __forceinline__ void g4_stage(const _Float16 *st, uint32_t abase, con
                 if (nsp < 8) {
 #pragma unroll
                     for (int p = 0; p < 4; ++p)
-                        if (p * imin(NRT, 4) / 4 == rt) Bn[p] = g4_piece<WT>(w, sc, sh, h, nsp, nct, p);
+                        if (p * NRT / 4 == rt) Bn[p] = g4_piece<WT>(w, sc, sh, h, nsp, nct, p);
                 }
                 if (ct == 0 && sp < 7) A[(sp + 1) & 1][rt] = g4_read_a(stb, abase, sp + 1, rt);
                 extra(slot);
@@ -390,8 +414,8 @@ __device__ __forceinline__ void g4_stage(const _Float16 *st, uint32_t abase, con
 //  stage (b, 1): the activation loads of (b + 1, 0).
 // The sync before (b, 1) waits only for the activations (issued before the
 // weight loads, which stay in flight); the one before (b + 1, 0) for all.
-// Past the last block the loads repeat the last block (valid addresses,
-// unused data; the epilogue waits for them).
+// The last block's loads for a next one repeat it (valid addresses, unused
+// data; the epilogue waits for them).
 template <int WT, int NRT>
 __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_t arowbytes, const G4WDma<WT> &dm,
                                            const uint32_t (&wsh)[2], uint8_t *W, int nb, int wave, int lane,
@@ -420,11 +444,13 @@ __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_
     // landed, the NW weight loads and the 2 column tiles' stage-1 scales
     constexpr int NS = 16 * NRT, S0 = 8 * NRT - 3, NI = NW + 2;
     for (int b = 0; b < nb; ++b) {
+        // block b + 1's loads go out during block b; the last block reloads
+        // itself (valid addresses, data unused) so that no stage branches
         const int bn = b + 1 < nb ? b + 1 : b;
         // Q6_K: bytes the block starts past a dword (same for all the lane's rows)
         const uint32_t sh = WT == 14 ? ((wsh[0] + (uint32_t)(b * Q6K_BYTES)) & 3u) : 0u;
         g4_stage_sync<0>();
-        g4_copy_w<WT>(W, l32, g2, w);
+        g4_copy_w<WT>(W, l32, g2, sh, w);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) g4_scales<WT>(w, ct, g2, 0, sh, s0);
         g4_stage<WT, NRT>(As0, abase, w, s0, sh, 0, acc, [&](int slot) __attribute__((always_inline)) {
@@ -454,7 +480,8 @@ __device__ __forceinline__ void g4_kloop(rsrc_t rx, const int *s_arow, uint32_t 
     case 2: g4_kloop_n<WT, 2>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
     case 3: g4_kloop_n<WT, 3>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
     case 4: g4_kloop_n<WT, 4>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
-    default: g4_kloop_n<WT, 5>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
+    case 5: g4_kloop_n<WT, 5>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
+    default: g4_kloop_n<WT, 6>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
     }
 }
 
@@ -492,11 +519,14 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     __shared__ __attribute__((aligned(1024))) _Float16 As0[G4_AST];
     __shared__ __attribute__((aligned(1024))) _Float16 As1[G4_AST];
     __shared__ __attribute__((aligned(1024))) uint8_t Ws[G4_WAVES][g4_wregion<12>()];
-    __shared__ int s_p[G4_BM], s_arow[G4_BM];
     int tile, ctile;
     if (!g4_coords((int)(g.I / 128), g.n_tiles, tile, ctile)) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const G4Tile t = g4_tile(g, tile, s_p, s_arow);
+    // the activation rows live in the second activation buffer until the K
+    // loop has computed its load offsets (its first write comes later)
+    int *s_arow = (int *)As1;
+    int my_p;
+    const G4Tile t = g4_tile(g, tile, s_arow, my_p);
     const int nrt = __builtin_amdgcn_readfirstlane(t.nrt);
     const uint32_t Kin = (uint32_t)g.a.K;
     const rsrc_t rx = g4_rsrc(g.xh, g.xrows * (int64_t)Kin * 2);
@@ -511,6 +541,7 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     f32x16 acc[G4_BM / 32][2];
     g4_kloop<12>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc);
     __builtin_amdgcn_s_waitcnt(0);   // no load may land in LDS after the work-group ends
+    const int *s_p = g4_publish_rows(As0, my_p);
     switch (g.act) {
     case 0: g4_glu_store<0>(g, acc, t, ctile, wave, lane, s_p); break;
     case 1: g4_glu_store<1>(g, acc, t, ctile, wave, lane, s_p); break;
@@ -528,12 +559,13 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     __shared__ __attribute__((aligned(1024))) _Float16 As0[G4_AST];
     __shared__ __attribute__((aligned(1024))) _Float16 As1[G4_AST];
     __shared__ __attribute__((aligned(1024))) uint8_t Ws[G4_WAVES][g4_wregion<WT>()];
-    __shared__ int s_p[G4_BM], s_arow[G4_BM];
     int tile, ctile;
     if (!g4_coords((int)((g.ncols + G4_NWG - 1) / G4_NWG), g.n_tiles, tile, ctile)) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int l32 = lane & 31, g2 = lane >> 5;
-    const G4Tile t = g4_tile(g, tile, s_p, s_arow);
+    int *s_arow = (int *)As1;   // as in k_g4_glu
+    int my_p;
+    const G4Tile t = g4_tile(g, tile, s_arow, my_p);
     const int nrt = __builtin_amdgcn_readfirstlane(t.nrt);
     const uint32_t Kin = (uint32_t)g.a.K;
     const rsrc_t rx = g4_rsrc(g.xh, g.xrows * (int64_t)Kin * 2);
@@ -549,6 +581,7 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     f32x16 acc[G4_BM / 32][2];
     g4_kloop<WT>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc);
     __builtin_amdgcn_s_waitcnt(0);   // no load may land in LDS after the work-group ends
+    const int *s_p = g4_publish_rows(As0, my_p);
     // rows 32 rt + 8 (i / 4) + 4 g2 + i % 4, columns n0 + 32 ct + l32
 #pragma unroll
     for (int rt = 0; rt < G4_BM / 32; ++rt) {

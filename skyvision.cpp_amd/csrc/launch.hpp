@@ -148,7 +148,7 @@ int launch_gemm2(const G2Args &g, hipStream_t st);
 // G4_BM rows from a balanced dispatch.  glu = 1 takes fp16 d*q activations
 // (not codes), ignores xd / xbs and writes fp32 GLU rows to y (ldy), whose
 // Q8_K the caller computes (launch_q8k_rows) for the down product.
-constexpr int G4_BM = 160;
+constexpr int G4_BM = 192;
 int launch_gemm4(const G2Args &g, hipStream_t st);
 
 // Single-token MoE block in one cooperative kernel (k_decode.hip).

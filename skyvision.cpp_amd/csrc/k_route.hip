@@ -17,59 +17,87 @@
 namespace mimoe {
 
 // ---------------------------------------------------------------- Q8_K rows
-// One wave per (row, 256-block).  Lane l holds elements 4l..4l+3.
+// One wave per (row, group of 4 blocks): lane l holds values 16 (l % 16) ..
+// + 15 of block 4 grp + l / 16 (q8k_wave4x16: every block's reduction in one
+// instruction stream, each lane's 16 codes one ggml bsums entry).  Outputs:
+// codes (natural order, 16 B per lane), scales, block sums, and fp16 values
+// (d*q, or q when exact) in the consumer's MFMA K order through a wave-private
+// LDS copy of the codes.
+template <bool VEC>
 __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ src, int64_t ld, int64_t nrows,
                                                   int nb, int8_t *__restrict__ q8, float *__restrict__ d8,
                                                   int16_t *__restrict__ bsums, _Float16 *__restrict__ xh,
                                                   int wtype, int order, int exact, _Float16 *__restrict__ xbs) {
-    __shared__ int8_t sq[4][QK];
+    __shared__ __attribute__((aligned(16))) int8_t sq[4][4 * QK];
+    __shared__ float sd[4][4];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int ngrp = (nb + 3) >> 2;
     const int64_t item = (int64_t)blockIdx.x * 4 + wave;
-    const bool valid = item < nrows * nb;
-    const int64_t row = valid ? item / nb : 0;
-    const int b = valid ? (int)(item % nb) : 0;
+    if (item >= nrows * ngrp) return;   // whole waves; only wave-local exchanges follow
+    const int64_t row = item / ngrp;
+    const int grp = (int)(item - row * ngrp);
+    const int bl = lane >> 4, l16 = lane & 15;
+    const int b = 4 * grp + bl;
+    const bool bok = b < nb;
     const int64_t K = (int64_t)nb * QK;
-
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if (valid) {
-        const float *x = src + row * ld + (int64_t)b * QK + 4 * lane;
-        for (int j = 0; j < 4; ++j) v[j] = x[j];
-    }
-    int q[4];
-    const float d = q8k_wave(v, lane, q);
-    if (valid) {
-        const int64_t o = row * K + (int64_t)b * QK + 4 * lane;
-        if (q8) *(uint32_t *)(q8 + o) = pack_i8x4(q);
-        if (d8 && lane == 0) d8[row * nb + b] = d;
-    }
-    if (bsums || xbs) {
-        const int s = q8k_bsum16(q);
-        const int64_t bi = row * (K / 16) + (int64_t)b * 16 + (lane >> 2);
-        if (valid && (lane & 3) == 0) {
-            if (bsums) bsums[bi] = (int16_t)s;
-            if (xbs) xbs[bi] = (_Float16)(float)s;        // |s| <= 2032: exact in fp16
+    float v[16];
+    if (bok) {
+        const float *x = src + row * ld + (int64_t)b * QK + 16 * l16;
+        if (VEC) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 f = *(const float4 *)(x + 4 * j);
+                v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = x[i];
         }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = 0.f;
+    }
+    int q[16], bsum;
+    const float d = q8k_wave4x16(v, lane, q, bsum);
+    uint32_t pk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int qq[4] = {q[4 * j], q[4 * j + 1], q[4 * j + 2], q[4 * j + 3]};
+        pk[j] = pack_i8x4(qq);
+    }
+    if (bok) {
+        const int64_t o = row * K + (int64_t)b * QK + 16 * l16;
+        if (q8) *(uint4 *)(q8 + o) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        if (d8 && l16 == 0) d8[row * nb + b] = d;
+        const int64_t bi = row * (K / 16) + (int64_t)b * 16 + l16;
+        if (bsums) bsums[bi] = (int16_t)bsum;
+        if (xbs) xbs[bi] = (_Float16)(float)bsum;        // |s| <= 2032: exact in fp16
     }
     if (xh) {
-        for (int j = 0; j < 4; ++j) sq[wave][4 * lane + j] = (int8_t)q[j];
-        __syncthreads();
-        if (valid) {
-            half2_t h01, h23;
-            const int p0 = 4 * lane;
-            float qv[4];
-            for (int j = 0; j < 4; ++j) {
-                const int el = order ? mfma32_elem(wtype, p0 + j) : mfma_elem(wtype, p0 + j);
-                const float qf = (float)sq[wave][el];
-                qv[j] = exact ? qf : d * qf;
+        *(uint4 *)&sq[wave][bl * QK + 16 * l16] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        if (l16 == 0) sd[wave][bl] = d;
+        wave_lds_sync();
+        if (bok) {
+            const float db = sd[wave][bl];
+            uint32_t h[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float qv[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int p = 16 * l16 + 2 * i + j;
+                    const int el = order ? mfma32_elem(wtype, p) : mfma_elem(wtype, p);
+                    const float qf = (float)sq[wave][bl * QK + el];
+                    qv[j] = exact ? qf : db * qf;
+                }
+                half2_t hh;
+                hh[0] = (_Float16)qv[0];
+                hh[1] = (_Float16)qv[1];
+                h[i] = __builtin_bit_cast(uint32_t, hh);
             }
-            h01[0] = (_Float16)qv[0];
-            h01[1] = (_Float16)qv[1];
-            h23[0] = (_Float16)qv[2];
-            h23[1] = (_Float16)qv[3];
-            uint2 pk;
-            pk.x = __builtin_bit_cast(uint32_t, h01);
-            pk.y = __builtin_bit_cast(uint32_t, h23);
-            *(uint2 *)(xh + row * K + (int64_t)b * QK + p0) = pk;
+            uint4 *dst = (uint4 *)(xh + row * K + (int64_t)b * QK + 16 * l16);
+            dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
+            dst[1] = make_uint4(h[4], h[5], h[6], h[7]);
         }
     }
 }
@@ -77,9 +105,15 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ src,
 int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, const Q8Out &o, hipStream_t st) {
     if (nrows <= 0) return 0;
     const int nb = (int)(K / QK);
-    const int64_t items = nrows * nb;
-    hipLaunchKernelGGL(k_q8k_rows, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, st, src, ld, nrows, nb, o.q8,
-                       o.d8, o.bsums, o.xh, o.wtype, o.order, o.exact, o.xbs);
+    const int64_t items = nrows * ((nb + 3) / 4);
+    const bool vec = (ld % 4 == 0) && ((uintptr_t)src % 16 == 0);
+    const dim3 grid((unsigned)((items + 3) / 4));
+    if (vec)
+        hipLaunchKernelGGL(k_q8k_rows<true>, grid, dim3(256), 0, st, src, ld, nrows, nb, o.q8, o.d8, o.bsums, o.xh,
+                           o.wtype, o.order, o.exact, o.xbs);
+    else
+        hipLaunchKernelGGL(k_q8k_rows<false>, grid, dim3(256), 0, st, src, ld, nrows, nb, o.q8, o.d8, o.bsums,
+                           o.xh, o.wtype, o.order, o.exact, o.xbs);
     return hip_check_launch();
 }
 

@@ -121,9 +121,12 @@ struct GemmArgs {
 constexpr int GEMM_BM = 64;
 int launch_gemm(const GemmArgs &g, hipStream_t st);
 
-// 32x32x16 MFMA grouped GEMM (k_gemm2.hip).  glu = 1: exact Q4_K x Q8_K
-// gate/up with GLU + Q8_K epilogue (xh = codes, xd = scales, xbs = block sums);
-// glu = 0: fp16 dequant x fp16(d*q) activations, fp32 rows out.
+// 4-wave grouped GEMMs on 32x32x16 MFMA (k_gemm4.hip), tiles of at most
+// G4_BM rows from a balanced dispatch.  Both take fp16 activations in the
+// weight type's 32x32x16 MFMA K order (xh; xd, xbs, acth and next_type are
+// not read).  glu = 1: Q4_K gate/up (fused [h | g] or separate), writes fp32
+// GLU rows to y (ldy), whose Q8_K the caller computes (launch_q8k_rows) for
+// the down product; glu = 0: Q4_K / Q6_K product, fp32 rows to y.
 struct G2Args {
     ExpertMat a;
     ExpertMat b;
@@ -135,19 +138,13 @@ struct G2Args {
     int ne11, K;
     const int32_t *counts, *offsets, *perm, *tile_e, *tile_r0, *n_tiles;
     int max_tiles;
-    int64_t xrows;        // rows of xh / xd / xbs (glu = 1: tokens)
+    int64_t xrows;        // rows of xh (glu = 1: tokens)
     float *y;
     int64_t ldy;
     _Float16 *acth;
     int next_type;
     int64_t ncols;
 };
-int launch_gemm2(const G2Args &g, hipStream_t st);
-
-// 4-wave grouped GEMMs (k_gemm4.hip), same arguments; tiles of at most
-// G4_BM rows from a balanced dispatch.  glu = 1 takes fp16 d*q activations
-// (not codes), ignores xd / xbs and writes fp32 GLU rows to y (ldy), whose
-// Q8_K the caller computes (launch_q8k_rows) for the down product.
 constexpr int G4_BM = 192;
 int launch_gemm4(const G2Args &g, hipStream_t st);
 

@@ -461,9 +461,49 @@ __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ z, co
     }
 }
 
+// Vector form: work-group (column chunk, token), 4 consecutive columns per
+// thread; the K slot rows' loads are issued before the (slot-order) sums.
+template <int KMAX>
+__global__ void __launch_bounds__(256) k_combine4(const float *__restrict__ z, const float *__restrict__ w,
+                                                  const float *__restrict__ res, float *__restrict__ out, int K,
+                                                  int D) {
+    const int64_t t = blockIdx.y;
+    const int n = 4 * ((int)blockIdx.x * 256 + (int)threadIdx.x);
+    if (n >= D) return;
+    float4 zv[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k)
+        if (k < K) zv[k] = *(const float4 *)(z + (t * K + k) * (int64_t)D + n);
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+        if (k < K) {
+            const float wk = w[t * K + k];
+            s0 = s0 + (double)(zv[k].x * wk);
+            s1 = s1 + (double)(zv[k].y * wk);
+            s2 = s2 + (double)(zv[k].z * wk);
+            s3 = s3 + (double)(zv[k].w * wk);
+        }
+    }
+    float4 o = make_float4((float)s0, (float)s1, (float)s2, (float)s3);
+    if (res) {
+        const float4 r = *(const float4 *)(res + t * D + n);
+        o.x = r.x + o.x; o.y = r.y + o.y; o.z = r.z + o.z; o.w = r.w + o.w;
+    }
+    *(float4 *)(out + t * D + n) = o;
+}
+
 int launch_combine(const float *z, const float *w, const float *res, float *out, int64_t T, int K, int D,
                    hipStream_t st) {
     if (T <= 0) return 0;
+    const bool vec = D % 4 == 0 && (uintptr_t)z % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+                     (!res || (uintptr_t)res % 16 == 0) && T <= 65535;
+    if (vec && K <= 16) {
+        const dim3 grid((unsigned)((D / 4 + 255) / 256), (unsigned)T);
+        if (K <= 8) hipLaunchKernelGGL(k_combine4<8>, grid, dim3(256), 0, st, z, w, res, out, K, D);
+        else hipLaunchKernelGGL(k_combine4<16>, grid, dim3(256), 0, st, z, w, res, out, K, D);
+        return hip_check_launch();
+    }
     const int64_t total = T * (int64_t)D;
     const int64_t blocks = (total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192;
     hipLaunchKernelGGL(k_combine, dim3((unsigned)blocks), dim3(256), 0, st, z, w, res, out, T, K, D);

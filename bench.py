@@ -3,7 +3,7 @@
 Default workload: config 1, the moondream3-shape MoE layer on a 1024-token
 prefill (gate/up Q4_K, down Q6_K, E=64, top-8), seeded synthetic data.  One
 step = one full layer forward (router -> top-k -> dispatch -> gate/up GEMM +
-GeGLU + Q8_K -> down GEMM -> weighted combine) over the 1024 tokens, with
+GeGLU -> Q8_K -> down GEMM -> weighted combine) over the 1024 tokens, with
 the inputs resident in HBM.  Steps rotate over --copies distinct layer copies
 so the 256 MB Infinity Cache cannot hold the weights between steps.
 
@@ -17,10 +17,17 @@ Printed JSON line (rank 0):
                  duration vs 8 TB/s)
   cpu_baseline   the CPU oracle (ggml-semantics restatement, C, OpenMP) on a
                  bounded sample of the same workload, physical cores
+  config3        qwen3omni layer, batched decode at 1 / 8 / 32 / 64 tokens on
+                 the GEMV and GEMM paths (and the fused single-token kernel):
+                 times, HBM rates, the GEMV-to-GEMM crossover
+  config4        24-layer stack h + MoE(RMSNorm(h)): 2048-token prefill and
+                 256 decode steps, sustained tokens/s, TFLOP/s and GB/s
+(--no-decode, --no-sweeps and --no-cpu skip the extra legs.)
 """
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import pathlib
@@ -128,6 +135,139 @@ def cpu_baseline(spec, layer0: W.GpuLayer, T_sample: int, budget_s: float = 20.0
                       f"{cores} threads"}
 
 
+def config3_sweep(copies: int) -> dict:
+    """Config 3: qwen3omni layer (E 128, I 768, SwiGLU, Q4_K), batched decode
+    at T = 1, 8, 32, 64 on both product paths (grouped GEMV, grouped MFMA
+    GEMM; at T = 1 also the fused single-token kernel), rotating layer copies.
+    Bytes per call = the touched experts' tables + the router (measured
+    touched count); the crossover is the smallest T at which the GEMM path is
+    faster."""
+    spec = W.CONFIGS[3]["spec"]
+    Ts = W.CONFIGS[3]["tokens"]
+    ctx = M.Context(0)
+    ctx.reserve(max(Ts), spec.D, spec.I, spec.E, spec.K)
+    layers = [W.GpuLayer(ctx, spec, copy=c) for c in range(copies)]
+    rows = []
+    for T in Ts:
+        xs = [W.gen_x(ctx, spec, T, copy=c) for c in range(copies)]
+        out = M.DeviceBuffer(4 * T * spec.D)
+        touched, _ = touched_experts(ctx, layers[0], xs[0], T)
+        nbytes = W.algorithmic_bytes(spec, touched)
+        row = {"tokens": T, "touched_experts": touched, "layer_bytes": nbytes}
+        paths = [("gemv", 1 << 30), ("gemm", 1)]
+        for name, thr in paths:
+            ctx.set_gemm_threshold(thr)
+            if T == 1:
+                ctx.set_fused_decode(M.DECODE_CHAIN)
+            ms, _ = time_layer(ctx, layers, xs, T, out, 100, 10)
+            row[f"{name}_ms"] = ms
+        if T == 1:
+            ctx.set_fused_decode(M.DECODE_FUSED_EXCLUSIVE)
+            row["fused_ms"] = time_layer(ctx, layers, xs, T, out, 100, 10)[0]
+        best = min(v for k, v in row.items() if k.endswith("_ms"))
+        row["best_ms"] = best
+        row["tokens_per_s"] = T / (best * 1e-3)
+        row["GBs"] = nbytes / (best * 1e-3) / 1e9
+        row["frac_hbm"] = row["GBs"] / PEAK_HBM_GBS
+        log(f"config 3 T={T}: " + ", ".join(f"{k} {v:.4f}" for k, v in row.items() if k.endswith("_ms")) +
+            f" | touched {touched}, {row['GBs']:.0f} GB/s")
+        rows.append(row)
+        del xs, out
+    ctx.set_gemm_threshold(16)
+    cross = next((r["tokens"] for r in rows if r["gemm_ms"] < r["gemv_ms"]), None)
+    del layers
+    ctx.close()
+    return {"workload": "config 3: qwen3omni MoE layer (E 128, top-8, I 768, SwiGLU, Q4_K), batched decode",
+            "layer_copies": copies, "points": rows, "gemm_faster_from_tokens": cross}
+
+
+def config4_stack(n_layers: int = 24, T_prefill: int = 2048, n_decode: int = 256, eps: float = 1e-6) -> dict:
+    """Config 4: 24 moondream-shape layers (Q4_K gate/up and down, per-layer
+    seeds), h <- h + MoE_l(RMSNorm(h)) with attention as identity: a
+    2048-token prefill through the stack, then 256 single-token steps, each
+    fed the RMSNorm of the previous step's final hidden state.  Reports
+    sustained tokens/s, the prefill's TFLOP/s and the decode's GB/s (touched
+    experts' bytes of every layer, counted on the first step)."""
+    spec = W.md_spec(4, M.TYPE_Q4_K)
+    ctx = M.Context(0)
+    ctx.reserve(T_prefill, spec.D, spec.I, spec.E, spec.K)
+    ctx.set_fused_decode(M.DECODE_FUSED_EXCLUSIVE)
+    t0 = time.perf_counter()
+    layers = [W.GpuLayer(ctx, spec, copy=c) for c in range(n_layers)]
+    resident = sum(l.expert_bytes() * spec.E + 4 * spec.E * spec.D for l in layers)
+    log(f"config 4: built {n_layers} layers in {time.perf_counter() - t0:.1f}s ({resident / 1e9:.2f} GB)")
+    h0 = W.gen_x(ctx, spec, T_prefill)
+    h = M.DeviceBuffer(4 * T_prefill * spec.D)
+    hn = M.DeviceBuffer(4 * T_prefill * spec.D)
+    h2 = M.DeviceBuffer(4 * T_prefill * spec.D)
+
+    def stack(T, cur, nxt):
+        # ping-pong: out = cur + MoE(RMSNorm(cur)) into the other buffer
+        for L in layers:
+            M.check("rmsnorm", ctx.rmsnorm(cur, T, spec.D, eps, hn))
+            M.check("forward", ctx.forward(L.layer, hn, T, cur, nxt))
+            cur, nxt = nxt, cur
+        return cur
+
+    def prefill():
+        M.check("copy", M.load().mi_memcpy_d2d(h.ptr, h0.ptr, 4 * T_prefill * spec.D))
+        return stack(T_prefill, h, h2)
+
+    prefill()
+    M.synchronize()
+    e0, e1 = M.Event(), M.Event()
+    reps = 3
+    e0.record()
+    for _ in range(reps):
+        last = prefill()
+    e1.record()
+    e1.synchronize()
+    pre_ms = e0.elapsed_ms(e1) / reps
+    # decode: the next token's input is the RMSNorm of the previous final hidden
+    tok = M.DeviceBuffer(4 * spec.D)
+    M.check("copy", M.load().mi_memcpy_d2d(tok.ptr, C.c_void_p(last.addr + 4 * (T_prefill - 1) * spec.D),
+                                           4 * spec.D))
+    M.check("rmsnorm", ctx.rmsnorm(tok, 1, spec.D, eps, tok))
+    touched = 0
+    counts = M.DeviceBuffer(4 * spec.E)
+    r = M.Routing()
+    r.counts = counts.addr
+    cur, nxt, nrm = tok, M.DeviceBuffer(4 * spec.D), M.DeviceBuffer(4 * spec.D)
+    for L in layers:   # first step, counting the touched experts of every layer
+        M.check("rmsnorm", ctx.rmsnorm(cur, 1, spec.D, eps, nrm))
+        M.check("forward", ctx.forward(L.layer, nrm, 1, cur, nxt, r))
+        touched += int((counts.download(np.int32, (spec.E,)) > 0).sum())
+        cur, nxt = nxt, cur
+    step_bytes = sum(W.algorithmic_bytes(spec, 0) for _ in layers) + touched * (W.algorithmic_bytes(spec, 1) - W.algorithmic_bytes(spec, 0))
+    M.synchronize()
+    e0.record()
+    for _ in range(n_decode):
+        for L in layers:
+            M.check("rmsnorm", ctx.rmsnorm(cur, 1, spec.D, eps, nrm))
+            M.check("forward", ctx.forward(L.layer, nrm, 1, cur, nxt))
+            cur, nxt = nxt, cur
+        M.check("rmsnorm", ctx.rmsnorm(cur, 1, spec.D, eps, cur))
+    e1.record()
+    e1.synchronize()
+    dec_ms = e0.elapsed_ms(e1) / n_decode
+    fl = n_layers * W.flops(spec, T_prefill)
+    res = {"workload": f"config 4: {n_layers}-layer moondream-shape MoE stack (Q4_K, 64 experts, top-8), "
+                       f"h + MoE(RMSNorm(h)), attention as identity",
+           "resident_bytes": resident,
+           "prefill": {"tokens": T_prefill, "ms": pre_ms, "tokens_per_s": T_prefill / (pre_ms * 1e-3),
+                       "TFLOPs": fl / (pre_ms * 1e-3) / 1e12},
+           "decode": {"steps": n_decode, "ms_per_token": dec_ms, "tokens_per_s": 1.0 / (dec_ms * 1e-3),
+                      "bytes_per_step": step_bytes, "GBs": step_bytes / (dec_ms * 1e-3) / 1e9,
+                      "frac_hbm": step_bytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                      "schedule": "fused single-token kernel per layer, plain launch"}}
+    log(f"config 4: prefill {pre_ms:.2f} ms ({res['prefill']['tokens_per_s']:.0f} tok/s, "
+        f"{res['prefill']['TFLOPs']:.0f} TFLOP/s), decode {dec_ms:.3f} ms/token "
+        f"({res['decode']['GBs']:.0f} GB/s)")
+    del layers
+    ctx.close()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -137,6 +277,8 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=1, choices=[1, 2])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-sweeps", action="store_true",
+                    help="skip the config-3 batched-decode sweep and the config-4 layer stack")
     ap.add_argument("--no-coop", action="store_true",
                     help="skip timing the cooperative-launch decode schedule (rocprofv3 cannot "
                          "write its results after a cooperative launch on this image)")
@@ -260,6 +402,12 @@ def main() -> int:
     if not args.no_cpu:
         cb = cpu_baseline(spec, layers[0], args.cpu_tokens)
         result["cpu_baseline"] = cb
+
+    if not args.no_sweeps:
+        del layers, xs
+        ctx.close()
+        result["config3"] = config3_sweep(args.copies)
+        result["config4"] = config4_stack()
     print(json.dumps(result), flush=True)
     return 0
 

@@ -165,6 +165,14 @@ int mi_quantize(mi_moe_ctx *ctx, int32_t type, const float *src, void *dst, int6
 int mi_fill_normal(mi_moe_ctx *ctx, float *dst, int64_t n, uint64_t seed, uint64_t stream_id,
                    float mean, float stddev, mi_stream_t stream);
 
+/* y = x / sqrt(mean(x^2) + eps) over each row of n_cols (F32 [n_rows][n_cols]
+ * device; y may equal x).  No counterpart in the reference's MoE path: the
+ * norm that feeds the synthetic layer stack (h + MoE(
+ * RMSNorm(h)) with attention as identity), written here so the stack runs
+ * on one device stream. */
+int mi_rmsnorm(mi_moe_ctx *ctx, const float *x, int64_t n_rows, int32_t n_cols, float eps, float *y,
+               mi_stream_t stream);
+
 /* ---- introspection ---------------------------------------------------------
  * Per-stage timing (HIP events on the call's stream) for the last forward
  * when profiling is on.  Stage names are static strings. */

@@ -704,6 +704,14 @@ int mi_fill_normal(mi_moe_ctx *c, float *dst, int64_t n, uint64_t seed, uint64_t
     return launch_fill_normal(dst, n, seed, stream_id, mean, stddev, (hipStream_t)stream);
 }
 
+int mi_rmsnorm(mi_moe_ctx *c, const float *x, int64_t n_rows, int32_t n_cols, float eps, float *y,
+               mi_stream_t stream) {
+    if (!c || !x || !y) return MI_MOE_ERR_NULL;
+    if (n_rows < 0 || n_cols <= 0) return MI_MOE_ERR_SHAPE;
+    HIP_TRY(hipSetDevice(c->device));
+    return launch_rmsnorm(x, n_rows, n_cols, eps, y, (hipStream_t)stream);
+}
+
 // ------------------------------------------------------------------ util ABI
 int mi_device_count(int *count) {
     if (!count) return MI_MOE_ERR_NULL;

@@ -409,6 +409,33 @@ __global__ void __launch_bounds__(256) k_quantize_q6_K(const float *__restrict__
 }
 
 // ---------------------------------------------------------------- launchers
+// y[t] = x[t] / sqrt(mean(x[t]^2) + eps): one work-group per row; each thread
+// sums the squares of columns tid, tid + 256, ... in fp32, then a fixed-order
+// tree over the 256 partials (deterministic)
+__global__ void __launch_bounds__(256) k_rmsnorm(const float *__restrict__ x, int D, float eps,
+                                                 float *__restrict__ y) {
+    __shared__ float part[256];
+    const int64_t t = blockIdx.x;
+    const float *xr = x + t * D;
+    float s = 0.f;
+    for (int n = threadIdx.x; n < D; n += 256) s = fmaf(xr[n], xr[n], s);
+    part[threadIdx.x] = s;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) part[threadIdx.x] += part[threadIdx.x + o];
+        __syncthreads();
+    }
+    const float r = 1.0f / sqrtf(part[0] / (float)D + eps);
+    for (int n = threadIdx.x; n < D; n += 256) y[t * D + n] = xr[n] * r;
+}
+
+int launch_rmsnorm(const float *x, int64_t T, int D, float eps, float *y, hipStream_t st) {
+    if (T <= 0) return 0;
+    if (T > 0x7fffffff || D <= 0) return -6;
+    hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)T), dim3(256), 0, st, x, D, eps, y);
+    return hip_check_launch();
+}
+
 int launch_fill_normal(float *out, int64_t n, uint64_t seed, uint64_t stream, float mean, float sd,
                        hipStream_t st) {
     if (n <= 0) return 0;

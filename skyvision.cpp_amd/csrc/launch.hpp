@@ -17,6 +17,8 @@ int hip_check_launch();
 int launch_fill_normal(float *out, int64_t n, uint64_t seed, uint64_t stream, float mean, float sd,
                        hipStream_t st);
 int launch_quantize(int type, const float *src, void *dst, int64_t nblocks, hipStream_t st);
+// y = x / sqrt(mean(x^2) + eps) per row of D (x may equal y)
+int launch_rmsnorm(const float *x, int64_t T, int D, float eps, float *y, hipStream_t st);
 
 // ---- routing (k_route.hip)
 struct Q8Out {

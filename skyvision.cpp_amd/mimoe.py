@@ -68,6 +68,7 @@ SYMBOLS = {
                        C.POINTER(Tensor), P], C.c_int),
     "mi_quantize": ([P, i32, P, P, i64, i64, P], C.c_int),
     "mi_fill_normal": ([P, P, i64, C.c_uint64, C.c_uint64, C.c_float, C.c_float, P], C.c_int),
+    "mi_rmsnorm": ([P, P, i64, C.c_int32, C.c_float, P, P], C.c_int),
     "mi_moe_ctx_set_profiling": ([P, C.c_int], C.c_int),
     "mi_moe_ctx_stage_times": ([P, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_float),
                                 C.POINTER(C.c_int)], C.c_int),
@@ -268,6 +269,9 @@ class Context:
                     stream=None) -> int:
         return load().mi_fill_normal(self.h, _addr(dst), n, seed, stream_id, mean, std,
                                      _addr(stream))
+
+    def rmsnorm(self, x, n_rows: int, n_cols: int, eps: float, y, stream=None) -> int:
+        return load().mi_rmsnorm(self.h, _addr(x), n_rows, n_cols, eps, _addr(y), _addr(stream))
 
     def close(self) -> None:
         if self.h and self.h.value:

@@ -333,7 +333,7 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
     __shared__ int psc[DISPATCH_MAX_E];   // inclusive scan of partial-tile flags
     __shared__ int sid[DISPATCH_IDS];
     __shared__ int wsum[DISPATCH_WAVES];
-    __shared__ int bad;
+    __shared__ int bad, prank;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int me = blockIdx.x;
     const bool one_chunk = n <= DISPATCH_IDS;
@@ -393,14 +393,19 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
             d.tile_e[tb + j] = me;
             d.tile_r0[tb + j] = j * BM;
         }
-        if (rem > 0 && tid == 0) {
-            int rank = 0;
-            for (int e2 = 0; e2 < E; ++e2) {
-                const int r2 = cnt[e2] % BM;
-                rank += (r2 > rem) | ((r2 == rem) & (e2 < me));
+        if (rem > 0) {
+            // rank among the partial tiles: one expert per thread, summed in LDS
+            if (tid == 0) prank = 0;
+            __syncthreads();
+            if (tid < E) {
+                const int r2 = cnt[tid] % BM;
+                if ((r2 > rem) | ((r2 == rem) & (tid < me))) atomicAdd(&prank, 1);
             }
-            d.tile_e[tsc[E - 1] + rank] = me;
-            d.tile_r0[tsc[E - 1] + rank] = nf * BM;
+            __syncthreads();
+            if (tid == 0) {
+                d.tile_e[tsc[E - 1] + prank] = me;
+                d.tile_r0[tsc[E - 1] + prank] = nf * BM;
+            }
         }
     }
 

@@ -232,9 +232,27 @@ int run_decode1(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, const floa
     return MI_MOE_OK;
 }
 
-// routed FFN body: needs c->sel-like ids (device [T][K]) and weights w [T][K]
+// How the expert path consumes x: false for fp32 expert tables, else the
+// Q8_K form it reads (GEMV: codes, scales, block sums; GEMM: fp16 d*q in the
+// gate weight's MFMA K order).
+bool x_q8_spec(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T, Q8Out &qx) {
+    const int D = L->n_embd, I = L->n_ff;
+    if (!is_kquant(L->gate.type)) return false;
+    const bool gemm = T >= c->gemm_threshold || D > 8 * QK || I > 8 * QK;
+    qx = Q8Out{};
+    if (!gemm) {
+        qx.q8 = c->ax.q8; qx.d8 = c->ax.d8; qx.bsums = c->ax.bs;
+    } else {
+        qx.xh = c->ax.h; qx.wtype = L->gate.type; qx.order = L->gate.type == MI_TYPE_Q4_K;
+    }
+    return true;
+}
+
+// routed FFN body: needs c->sel-like ids (device [T][K]) and weights w [T][K];
+// x_done: x is already in the x_q8_spec form
 int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const int32_t *ids_gu,
-                const int32_t *ids_dn, const float *w, const float *res, float *out, hipStream_t st) {
+                const int32_t *ids_dn, const float *w, const float *res, float *out, hipStream_t st,
+                bool x_done = false) {
     const int D = L->n_embd, E = L->n_expert, K = L->n_expert_used, I = L->n_ff;
     const int64_t rows = T * K;
     const int max_active = (int)std::min<int64_t>(E, rows);
@@ -252,6 +270,11 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
     const DispBuf &dg = c->disp[0];
     const DispBuf &dd = same_ids ? c->disp[0] : c->disp[1];
     stage_end(c, "dispatch", st);
+    Q8Out qx;
+    if (x_q8_spec(c, L, T, qx) && !x_done) {
+        TRY(launch_q8k_rows(x, D, T, D, qx, st));
+        stage_end(c, "q8k_x", st);
+    }
 
     const ExpertMat gate = as_mat(L->gate), down = as_mat(L->down);
     ExpertMat up = {};
@@ -291,10 +314,6 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
     }
 
     if (!gemm) {
-        Q8Out qx;
-        qx.q8 = c->ax.q8; qx.d8 = c->ax.d8; qx.bsums = c->ax.bs;
-        TRY(launch_q8k_rows(x, D, T, D, qx, st));
-        stage_end(c, "q8k_x", st);
         GemvArgs a = {};
         a.a = gate; a.b = up; a.epi = EPI_GLU; a.act = L->act; a.I = I; a.fused = L->fused_gate_up;
         a.q8 = c->ax.q8; a.d8 = c->ax.d8; a.bsums = c->ax.bs; a.ne11 = 1; a.K = K;
@@ -317,11 +336,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         stage_end(c, "down", st);
     } else if (gate.type == MI_TYPE_Q4_K) {
         // 4-wave GEMMs on 32x32x16 MFMA: fp16 dequantized weights x fp16
-        // d*q of the Q8_K activations, GLU + Q8_K of its output fused in
-        Q8Out qx;
-        qx.xh = c->ax.h; qx.wtype = MI_TYPE_Q4_K; qx.order = 1;
-        TRY(launch_q8k_rows(x, D, T, D, qx, st));
-        stage_end(c, "q8k_x", st);
+        // d*q of the Q8_K activations, then Q8_K of the GLU rows for the down GEMM
         G2Args a = {};
         a.a = gate; a.b = up; a.glu = 1; a.fused = L->fused_gate_up; a.act = L->act; a.I = I;
         a.xh = c->ax.h; a.ne11 = 1; a.K = K;
@@ -344,10 +359,6 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         stage_end(c, "down", st);
     } else {
         // Q6_K gate/up: fp16 dequant on 16x16x32 MFMA
-        Q8Out qx;
-        qx.xh = c->ax.h; qx.wtype = gate.type;
-        TRY(launch_q8k_rows(x, D, T, D, qx, st));
-        stage_end(c, "q8k_x", st);
         GemmArgs a = {};
         a.a = gate; a.b = up; a.epi = EPI_GLU; a.act = L->act; a.I = I; a.fused = L->fused_gate_up;
         a.xh = c->ax.h; a.ne11 = 1; a.K = K;
@@ -567,11 +578,16 @@ int mi_moe_forward(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t
     if (T == 1 && plan_decode1(c, L, x, P, C)) {
         TRY(run_decode1(c, L, x, res, out, P, C, st));
     } else {
-        TRY(launch_router(L->router_w, L->router_b, x, D, T, D, E, c->logits, st));
+        // router + Q8_K(x) in one launch where the shape fits
+        Q8Out qx;
+        const bool xq = x_q8_spec(c, L, T, qx);
+        const int rc = launch_front(L->router_w, L->router_b, x, D, T, D, E, c->logits, xq ? &qx : nullptr, st);
+        if (rc == -6) TRY(launch_router(L->router_w, L->router_b, x, D, T, D, E, c->logits, st));
+        else TRY(rc);
         stage_end(c, "router", st);
         TRY(launch_topk_softmax(c->logits, E, T, E, K, c->sel, K, c->w, st));
         stage_end(c, "topk_softmax", st);
-        TRY(run_experts(c, L, x, T, c->sel, c->sel, c->w, res, out, st));
+        TRY(run_experts(c, L, x, T, c->sel, c->sel, c->w, res, out, st, xq && rc == 0));
     }
     if (routing) {
         const DispBuf &d = c->disp[0];

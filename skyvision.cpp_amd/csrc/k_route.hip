@@ -22,20 +22,16 @@ namespace mimoe {
 // instruction stream, each lane's 16 codes one ggml bsums entry).  Outputs:
 // codes (natural order, 16 B per lane), scales, block sums, and fp16 values
 // (d*q, or q when exact) in the consumer's MFMA K order through a wave-private
-// LDS copy of the codes.
+// LDS copy of the codes (sq: 4 * QK bytes, sd: 4 floats, private to the wave).
 template <bool VEC>
-__global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ src, int64_t ld, int64_t nrows,
-                                                  int nb, int8_t *__restrict__ q8, float *__restrict__ d8,
-                                                  int16_t *__restrict__ bsums, _Float16 *__restrict__ xh,
-                                                  int wtype, int order, int exact, _Float16 *__restrict__ xbs) {
-    __shared__ __attribute__((aligned(16))) int8_t sq[4][4 * QK];
-    __shared__ float sd[4][4];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int ngrp = (nb + 3) >> 2;
-    const int64_t item = (int64_t)blockIdx.x * 4 + wave;
-    if (item >= nrows * ngrp) return;   // whole waves; only wave-local exchanges follow
-    const int64_t row = item / ngrp;
-    const int grp = (int)(item - row * ngrp);
+__device__ __forceinline__ void q8k_row_group(const float *__restrict__ src, int64_t ld, int64_t row, int grp,
+                                              int nb, const Q8Out &o, int8_t *sq, float *sd, int lane) {
+    int8_t *__restrict__ q8 = o.q8;
+    float *__restrict__ d8 = o.d8;
+    int16_t *__restrict__ bsums = o.bsums;
+    _Float16 *__restrict__ xh = o.xh;
+    _Float16 *__restrict__ xbs = o.xbs;
+    const int wtype = o.wtype, order = o.order, exact = o.exact;
     const int bl = lane >> 4, l16 = lane & 15;
     const int b = 4 * grp + bl;
     const bool bok = b < nb;
@@ -66,19 +62,19 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ src,
         pk[j] = pack_i8x4(qq);
     }
     if (bok) {
-        const int64_t o = row * K + (int64_t)b * QK + 16 * l16;
-        if (q8) *(uint4 *)(q8 + o) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        const int64_t off = row * K + (int64_t)b * QK + 16 * l16;
+        if (q8) *(uint4 *)(q8 + off) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         if (d8 && l16 == 0) d8[row * nb + b] = d;
         const int64_t bi = row * (K / 16) + (int64_t)b * 16 + l16;
         if (bsums) bsums[bi] = (int16_t)bsum;
         if (xbs) xbs[bi] = (_Float16)(float)bsum;        // |s| <= 2032: exact in fp16
     }
     if (xh) {
-        *(uint4 *)&sq[wave][bl * QK + 16 * l16] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        if (l16 == 0) sd[wave][bl] = d;
+        *(uint4 *)&sq[bl * QK + 16 * l16] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        if (l16 == 0) sd[bl] = d;
         wave_lds_sync();
         if (bok) {
-            const float db = sd[wave][bl];
+            const float db = sd[bl];
             uint32_t h[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
@@ -87,7 +83,7 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ src,
                 for (int j = 0; j < 2; ++j) {
                     const int p = 16 * l16 + 2 * i + j;
                     const int el = order ? mfma32_elem(wtype, p) : mfma_elem(wtype, p);
-                    const float qf = (float)sq[wave][bl * QK + el];
+                    const float qf = (float)sq[bl * QK + el];
                     qv[j] = exact ? qf : db * qf;
                 }
                 half2_t hh;
@@ -102,18 +98,27 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ src,
     }
 }
 
+template <bool VEC>
+__global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ src, int64_t ld, int64_t nrows,
+                                                  int nb, Q8Out o) {
+    __shared__ __attribute__((aligned(16))) int8_t sq[4][4 * QK];
+    __shared__ float sd[4][4];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int ngrp = (nb + 3) >> 2;
+    const int64_t item = (int64_t)blockIdx.x * 4 + wave;
+    if (item >= nrows * ngrp) return;   // whole waves; only wave-local exchanges follow
+    const int64_t row = item / ngrp;
+    q8k_row_group<VEC>(src, ld, row, (int)(item - row * ngrp), nb, o, sq[wave], sd[wave], lane);
+}
+
 int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, const Q8Out &o, hipStream_t st) {
     if (nrows <= 0) return 0;
     const int nb = (int)(K / QK);
     const int64_t items = nrows * ((nb + 3) / 4);
     const bool vec = (ld % 4 == 0) && ((uintptr_t)src % 16 == 0);
     const dim3 grid((unsigned)((items + 3) / 4));
-    if (vec)
-        hipLaunchKernelGGL(k_q8k_rows<true>, grid, dim3(256), 0, st, src, ld, nrows, nb, o.q8, o.d8, o.bsums, o.xh,
-                           o.wtype, o.order, o.exact, o.xbs);
-    else
-        hipLaunchKernelGGL(k_q8k_rows<false>, grid, dim3(256), 0, st, src, ld, nrows, nb, o.q8, o.d8, o.bsums,
-                           o.xh, o.wtype, o.order, o.exact, o.xbs);
+    if (vec) hipLaunchKernelGGL(k_q8k_rows<true>, grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    else hipLaunchKernelGGL(k_q8k_rows<false>, grid, dim3(256), 0, st, src, ld, nrows, nb, o);
     return hip_check_launch();
 }
 
@@ -132,55 +137,107 @@ int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, cons
 typedef double double4_t __attribute__((ext_vector_type(4)));
 constexpr int RM_MAX_CHUNKS = 32;   // D <= 2048 (64 KB of LDS partials)
 
-// Grid: one work-group per (16-token slab, 16-expert tile); the slab's
-// expert tiles run on one XCD (slab s on XCD s % 8, work-groups dealt to the
-// XCDs in turn), so each token's row is fetched into one L2 only.
+// Grid: one work-group (16 waves) per (16-token slab, 16-expert tile); the
+// slab's expert tiles run on one XCD (slab s on XCD s % 8, work-groups dealt
+// to the XCDs in turn), so each token's row is fetched into one L2 only.
+//
+// Loads: a chunk's 16 x rows and 16 W rows (64 floats each) arrive by
+// coalesced loads (lane l: row 4 j + l / 16, 16-byte piece l % 16, so one
+// instruction covers 4 rows x 256 B) and pass through a wave-private LDS
+// stage (piece p of row r at slot p ^ r: conflict-free both ways) into the
+// MFMA operand layout (lane (row, g): pieces 4 g .. 4 g + 3 of its row).  The
+// next chunk's loads go out once the current one is in operand registers,
+// and land while its 16 MFMAs run.
+constexpr int RT_WAVES = 16;
+
+struct RtChunk {
+    float4 x[4], w[4];
+};
+
 template <bool VEC>
-__global__ void __launch_bounds__(1024) k_router_mfma(const float *__restrict__ W, const float *__restrict__ bias,
-                                                      const float *__restrict__ x, int64_t ldx, int64_t T, int D,
-                                                      int E, float *__restrict__ logits) {
-    extern __shared__ double rparts[];   // [nch][256]
-    const int nw = blockDim.x >> 6;
+__device__ __forceinline__ float4 rt_piece(const float *row, int64_t off, int D, bool ok) {
+    if (VEC) return ok ? *(const float4 *)(row + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+    float t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] = ok && off + i < D ? row[off + i] : 0.f;
+    return make_float4(t[0], t[1], t[2], t[3]);
+}
+
+// chunk c of the slab's x rows (t0 ..) and the tile's W rows (e0 ..); rows
+// past T or E read as zeros
+template <bool VEC>
+__device__ __forceinline__ void rt_load(RtChunk &k, const float *__restrict__ x, int64_t ldx, int64_t t0, int64_t T,
+                                        const float *__restrict__ W, int e0, int E, int D, int c, int lane) {
+    const int64_t off = 64 * (int64_t)c + 4 * (lane & 15);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = 4 * j + (lane >> 4);
+        const bool tok_ok = t0 + r < T, ex_ok = e0 + r < E;
+        k.x[j] = rt_piece<VEC>(x + (tok_ok ? t0 + r : 0) * ldx, off, D, tok_ok);
+        k.w[j] = rt_piece<VEC>(W + (int64_t)(ex_ok ? e0 + r : 0) * D, off, D, ex_ok);
+    }
+}
+
+// a wave's four loaded pieces -> its lane's 16 operand values (stage: 256 float4)
+__device__ __forceinline__ void rt_transpose(const float4 (&in)[4], float4 *stage, int lane, float (&out)[16]) {
+    const int p = lane & 15;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = 4 * j + (lane >> 4);
+        stage[r * 16 + (p ^ r)] = in[j];
+    }
+    wave_lds_sync();
+    const int row = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 v = stage[row * 16 + ((4 * g + q) ^ row)];
+        out[4 * q] = v.x; out[4 * q + 1] = v.y; out[4 * q + 2] = v.z; out[4 * q + 3] = v.w;
+    }
+    wave_lds_sync();   // the stage is rewritten next
+}
+
+// The front of a forward: every work-group computes its logit tile, and with
+// a Q8_K output (o.q8 or o.xh set) quantizes its share of the slab's x rows
+// (row group item i = row * ngrp + grp by work-group i % net, wave i / net
+// mod 16) while the rows are in this XCD's L2.  (Ranking the slab in the last
+// of its work-groups to finish was measured slower than the separate top-k
+// launch: the logit hand-off costs three memory round trips at the kernel's
+// end.)
+template <bool VEC>
+__global__ void __launch_bounds__(1024) k_front(const float *__restrict__ W, const float *__restrict__ bias,
+                                                const float *__restrict__ x, int64_t ldx, int64_t T, int D, int E,
+                                                float *__restrict__ logits, Q8Out o) {
+    __shared__ double rparts[RM_MAX_CHUNKS * 256];   // [chunk][256]
+    __shared__ float4 stage[RT_WAVES][256];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nch = (D + 63) / 64;
     const int net = (E + 15) / 16;
     const int lin = blockIdx.x, q = lin >> 3;
     const int64_t slab = (int64_t)(q / net) * 8 + (lin & 7);
     if (slab * 16 >= T) return;
-    const int e0 = (q % net) * 16;
+    const int et = q % net, e0 = et * 16;
     const int64_t t0 = slab * 16;
-    const int row = lane & 15, g = lane >> 4;
-    const int64_t tok = t0 + row;
-    const int ex = e0 + row;
-    const bool tok_ok = tok < T, ex_ok = ex < E;
-    const float *xr = x + (tok_ok ? tok : 0) * ldx;
-    const float *wr = W + (int64_t)(ex_ok ? ex : 0) * D;
-    for (int c = wave; c < nch; c += nw) {
-        const int base = 64 * c + 16 * g;
+    float4 *stg = stage[wave];
+    RtChunk cur;
+    if (wave < nch) rt_load<VEC>(cur, x, ldx, t0, T, W, e0, E, D, wave, lane);
+    for (int c = wave; c < nch; c += RT_WAVES) {
         float xv[16], wv[16];
-        if (VEC) {
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                const float4 a = *(const float4 *)(xr + base + 4 * q4);
-                const float4 b = *(const float4 *)(wr + base + 4 * q4);
-                xv[4 * q4] = a.x; xv[4 * q4 + 1] = a.y; xv[4 * q4 + 2] = a.z; xv[4 * q4 + 3] = a.w;
-                wv[4 * q4] = b.x; wv[4 * q4 + 1] = b.y; wv[4 * q4 + 2] = b.z; wv[4 * q4 + 3] = b.w;
-            }
-        } else {
-            for (int s2 = 0; s2 < 16; ++s2) {
-                const int dd = base + s2;
-                xv[s2] = dd < D ? xr[dd] : 0.f;
-                wv[s2] = dd < D ? wr[dd] : 0.f;
-            }
-        }
+        rt_transpose(cur.x, stg, lane, xv);
+        rt_transpose(cur.w, stg, lane, wv);
+        if (c + RT_WAVES < nch) rt_load<VEC>(cur, x, ldx, t0, T, W, e0, E, D, c + RT_WAVES, lane);
         double4_t part = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-        for (int s2 = 0; s2 < 16; ++s2) {
-            const double a = tok_ok ? (double)xv[s2] : 0.0;
-            const double b = ex_ok ? (double)wv[s2] : 0.0;
-            part = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, part, 0, 0, 0);
-        }
+        for (int s2 = 0; s2 < 16; ++s2)
+            part = __builtin_amdgcn_mfma_f64_16x16x4f64((double)xv[s2], (double)wv[s2], part, 0, 0, 0);
+#pragma unroll
         for (int r = 0; r < 4; ++r) rparts[c * 256 + lane * 4 + r] = part[r];
+    }
+    if (o.q8 || o.xh) {
+        const int nb = D / QK, ngrp = (nb + 3) >> 2;
+        for (int i = et + net * wave; i < 16 * ngrp; i += net * RT_WAVES) {
+            const int64_t row = t0 + i / ngrp;
+            if (row < T) q8k_row_group<VEC>(x, ldx, row, i % ngrp, nb, o, (int8_t *)stg, (float *)(stg + 64), lane);
+        }
     }
     __syncthreads();
     if (threadIdx.x < 256) {
@@ -238,25 +295,36 @@ __global__ void __launch_bounds__(256) k_router_split(const float *__restrict__ 
     }
 }
 
+int launch_front(const float *W, const float *b, const float *x, int64_t ldx, int64_t T, int D, int E,
+                 float *logits, const Q8Out *qx, hipStream_t st) {
+    if (T <= 0) return 0;
+    const int nch = (D + 63) / 64;
+    if (nch > RM_MAX_CHUNKS || T > (int64_t)1 << 30) return -6;
+    if (qx && D % QK) return -6;
+    const bool vec = (D % 64 == 0) && (ldx % 4 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)W % 16 == 0);
+    const int64_t net = (E + 15) / 16, nslab = (T + 15) / 16;
+    const int64_t blocks = 8 * net * ((nslab + 7) / 8);
+    if (blocks > 0x7fffffff) return -6;
+    const Q8Out o = qx ? *qx : Q8Out{};
+    if (vec)
+        hipLaunchKernelGGL(k_front<true>, dim3((unsigned)blocks), dim3(64 * RT_WAVES), 0, st, W, b, x, ldx, T, D, E,
+                           logits, o);
+    else
+        hipLaunchKernelGGL(k_front<false>, dim3((unsigned)blocks), dim3(64 * RT_WAVES), 0, st, W, b, x, ldx, T, D,
+                           E, logits, o);
+    return hip_check_launch();
+}
+
 int launch_router(const float *W, const float *b, const float *x, int64_t ldx, int64_t T, int D, int E,
                   float *logits, hipStream_t st) {
     if (T <= 0) return 0;
     const int nch = (D + 63) / 64;
-    if (nch <= RM_MAX_CHUNKS && T <= (int64_t)1 << 30) {
-        const bool vec = (D % 64 == 0) && (ldx % 4 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)W % 16 == 0);
-        const int nw = imin(16, nch);
-        const int64_t net = (E + 15) / 16, nslab = (T + 15) / 16;
-        const int64_t blocks = 8 * net * ((nslab + 7) / 8);
-        if (blocks > 0x7fffffff) return -6;
-        const size_t smem = sizeof(double) * 256 * (size_t)nch;
-        if (vec) hipLaunchKernelGGL(k_router_mfma<true>, dim3((unsigned)blocks), dim3(64 * nw), smem, st, W, b, x, ldx, T, D, E, logits);
-        else hipLaunchKernelGGL(k_router_mfma<false>, dim3((unsigned)blocks), dim3(64 * nw), smem, st, W, b, x, ldx, T, D, E, logits);
-    } else {
-        if (nch > 256 || T > 65535) return -6;
-        const int epb = 256 / nch;
-        hipLaunchKernelGGL(k_router_split, dim3((unsigned)((E + epb - 1) / epb), (unsigned)T), dim3(256), 0, st, W,
-                           b, x, ldx, D, E, nch, epb, logits);
-    }
+    if (nch <= RM_MAX_CHUNKS && T <= (int64_t)1 << 30)
+        return launch_front(W, b, x, ldx, T, D, E, logits, nullptr, st);
+    if (nch > 256 || T > 65535) return -6;
+    const int epb = 256 / nch;
+    hipLaunchKernelGGL(k_router_split, dim3((unsigned)((E + epb - 1) / epb), (unsigned)T), dim3(256), 0, st, W, b,
+                       x, ldx, D, E, nch, epb, logits);
     return hip_check_launch();
 }
 

@@ -36,6 +36,10 @@ int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, cons
 // router logits, fixed fp64 order; W: [E][D], x rows at x + t*ldx
 int launch_router(const float *W, const float *b, const float *x, int64_t ldx, int64_t T, int D, int E,
                   float *logits, hipStream_t st);
+// router logits plus (qx) the Q8_K of the x rows in one launch; -6 when the
+// shape is outside the kernel (D > 2048, or qx with D % 256)
+int launch_front(const float *W, const float *b, const float *x, int64_t ldx, int64_t T, int D, int E,
+                 float *logits, const Q8Out *qx, hipStream_t st);
 // top-k (descending, ties -> lower id) and softmax over the selected logits;
 // w may be NULL (op-level top_k)
 int launch_topk_softmax(const float *logits, int64_t ld_logits, int64_t T, int E, int K, int32_t *sel,

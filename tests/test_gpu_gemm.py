@@ -155,3 +155,26 @@ def test_prefill_gemm_vs_gemv(name):
         f"max count {int(counts.max())} empty experts {int((counts == 0).sum())}")
     assert e <= TOL_PATHS
     ctx.close()
+
+
+def test_prefill_repeatable():
+    """Three forwards of the config-1 layer give the same bits: no kernel of
+    the prefill path depends on scheduling order or on workspace contents
+    left by the previous call (fixed-order sums, dispatch rebuilt, counters
+    cleared)."""
+    spec = FULL["md_cfg1"]
+    T = 1024
+    ctx = M.Context(0)
+    ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
+    g = W.GpuLayer(ctx, spec)
+    xd = M.to_device(cpu_x(spec, T))
+    outs = []
+    for _ in range(3):
+        out = M.DeviceBuffer(4 * T * spec.D)
+        M.check("forward", ctx.forward(g.layer, xd, T, None, out))
+        outs.append(out.download(np.float32, (T, spec.D)))
+    assert np.isfinite(outs[0]).all()
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+    ctx.close()
+

@@ -179,3 +179,38 @@ def test_full_layer_parity(name):
     log(f"{name}: T={T} rel-L2 {e_rel:.3e} max-abs {max_abs(got, ref):.3e} "
         f"experts used {int((counts > 0).sum())}/{spec.E} max count {int(counts.max())}")
     assert e_rel <= TOL_REL_L2
+
+
+@pytest.mark.parametrize("D,E,K", [(100, 5, 2), (2048, 64, 8), (2048, 128, 8)])
+def test_forward_routing_shapes(D, E, K):
+    """Routing of the forward (router tiles of 16 tokens x 16 experts, then
+    top-k + softmax) against the oracle: logits and ids bit-exact, weights
+    within 1e-6, for ragged token counts on one context, D off the 64-wide
+    chunk grid (the router's scalar loads) and E off the 16-expert tile grid.
+    fp32 expert tables of I = 8: the expert path is not what is checked here."""
+    I = 8
+    rng = np.random.default_rng(D * 1000 + E)
+    ctx = M.Context(0)
+    ctx.reserve(600, D, I, E, K)
+    rw = (rng.standard_normal((E, D)) * 0.05).astype(np.float32)
+    rb = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    gate = (rng.standard_normal((E, 2 * I, D)) * 0.05).astype(np.float32)
+    down = (rng.standard_normal((E, D, I)) * 0.05).astype(np.float32)
+    rwd, rbd, gd, dd = M.to_device(rw), M.to_device(rb), M.to_device(gate), M.to_device(down)
+    L = M.make_layer(D, E, K, I, rwd, rbd, M.tensor(gd, M.TYPE_F32, [D, 2 * I, E]), None,
+                     M.tensor(dd, M.TYPE_F32, [I, D, E]), True, M.ACT_SILU)
+    for T in [1, 15, 16, 17, 255, 600]:
+        x = rng.standard_normal((T, D)).astype(np.float32)
+        xd = M.to_device(x)
+        out = M.DeviceBuffer(4 * T * D)
+        bufs, r = _routing_buffers(T, E, K)
+        M.check("forward", ctx.forward(L, xd, T, None, out, r))
+        ref_l = O.router_logits(rw, rb, x)
+        ref_s = O.top_k(ref_l, K)
+        gl = bufs["logits"].download(np.float32, (T, E))
+        assert np.array_equal(gl.view(np.uint32), ref_l.view(np.uint32)), f"logits T={T}"
+        assert np.array_equal(bufs["sel"].download(np.int32, (T, K)), ref_s), f"ids T={T}"
+        gw = bufs["weights"].download(np.float32, (T, K))
+        assert np.allclose(gw, O.softmax_selected(ref_l, ref_s), rtol=1e-6, atol=1e-7), f"weights T={T}"
+    log(f"routing D={D} E={E} K={K}: T 1..600 bit-exact")
+    ctx.close()

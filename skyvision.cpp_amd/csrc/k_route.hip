@@ -23,21 +23,19 @@ namespace mimoe {
 // codes (natural order, 16 B per lane), scales, block sums, and fp16 values
 // (d*q, or q when exact) in the consumer's MFMA K order through a wave-private
 // LDS copy of the codes (sq: 4 * QK bytes, sd: 4 floats, private to the wave).
+// XO fixes the fp16 order at compile time: XO_Q4 / XO_Q6 the 32x32x16 order of
+// a Q4_K / Q6_K consumer (not exact), where a lane's 16 positions are the
+// bytes of four aligned code dwords (at base and base + 32 for each of its two
+// lane groups), XO_ANY whatever o asks for, element by element.
+enum { XO_ANY = 0, XO_Q4 = 1, XO_Q6 = 2 };
+
+// the lane's 16 values of row group (row, grp) (zeros past the row's blocks)
 template <bool VEC>
-__device__ __forceinline__ void q8k_row_group(const float *__restrict__ src, int64_t ld, int64_t row, int grp,
-                                              int nb, const Q8Out &o, int8_t *sq, float *sd, int lane) {
-    int8_t *__restrict__ q8 = o.q8;
-    float *__restrict__ d8 = o.d8;
-    int16_t *__restrict__ bsums = o.bsums;
-    _Float16 *__restrict__ xh = o.xh;
-    _Float16 *__restrict__ xbs = o.xbs;
-    const int wtype = o.wtype, order = o.order, exact = o.exact;
+__device__ __forceinline__ void q8k_load(const float *__restrict__ src, int64_t ld, int64_t row, int grp, int nb,
+                                         int lane, float (&v)[16]) {
     const int bl = lane >> 4, l16 = lane & 15;
     const int b = 4 * grp + bl;
-    const bool bok = b < nb;
-    const int64_t K = (int64_t)nb * QK;
-    float v[16];
-    if (bok) {
+    if (b < nb) {
         const float *x = src + row * ld + (int64_t)b * QK + 16 * l16;
         if (VEC) {
 #pragma unroll
@@ -53,6 +51,21 @@ __device__ __forceinline__ void q8k_row_group(const float *__restrict__ src, int
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = 0.f;
     }
+}
+
+template <int XO>
+__device__ __forceinline__ void q8k_quant(const float (&v)[16], int64_t row, int grp, int nb, const Q8Out &o,
+                                          int8_t *sq, float *sd, int lane) {
+    int8_t *__restrict__ q8 = o.q8;
+    float *__restrict__ d8 = o.d8;
+    int16_t *__restrict__ bsums = o.bsums;
+    _Float16 *__restrict__ xh = o.xh;
+    _Float16 *__restrict__ xbs = o.xbs;
+    const int wtype = o.wtype, order = o.order, exact = o.exact;
+    const int bl = lane >> 4, l16 = lane & 15;
+    const int b = 4 * grp + bl;
+    const bool bok = b < nb;
+    const int64_t K = (int64_t)nb * QK;
     int q[16], bsum;
     const float d = q8k_wave4x16(v, lane, q, bsum);
     uint32_t pk[4];
@@ -70,10 +83,42 @@ __device__ __forceinline__ void q8k_row_group(const float *__restrict__ src, int
         if (xbs) xbs[bi] = (_Float16)(float)bsum;        // |s| <= 2032: exact in fp16
     }
     if (xh) {
+        wave_lds_sync();   // a previous item's reads of sq / sd are done
         *(uint4 *)&sq[bl * QK + 16 * l16] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         if (l16 == 0) sd[bl] = d;
         wave_lds_sync();
-        if (bok) {
+        if (bok && XO != XO_ANY) {
+            const float db = sd[bl];
+            const int s = l16;
+            uint32_t h[8];
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                const int base = XO == XO_Q4 ? 64 * (2 * (s >> 3) + g) + 4 * (s & 7)
+                                             : 128 * (s >> 3) + 16 * g + 4 * ((s & 7) >> 1) + 64 * (s & 1);
+                const uint32_t A = *(const uint32_t *)&sq[bl * QK + base];
+                const uint32_t B = *(const uint32_t *)&sq[bl * QK + base + 32];
+                // slot p = 0..7 of the lane group: Q4_K bytes A0 A2 B0 B2 A1 A3 B1 B3
+                // (q4k_elem32's offsets 0 2 32 34 1 3 33 35), Q6_K A0..A3 B0..B3
+                int q[8];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int sh = XO == XO_Q4 ? 16 * (k & 1) + 8 * (k >> 1) : 8 * k;
+                    const int slot = XO == XO_Q4 ? (k & 1) + 4 * (k >> 1) : k;
+                    q[slot] = (int)(int8_t)(A >> sh);
+                    q[slot + (XO == XO_Q4 ? 2 : 4)] = (int)(int8_t)(B >> sh);
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    half2_t hh;
+                    hh[0] = (_Float16)(db * (float)q[2 * k]);
+                    hh[1] = (_Float16)(db * (float)q[2 * k + 1]);
+                    h[4 * g + k] = __builtin_bit_cast(uint32_t, hh);
+                }
+            }
+            uint4 *dst = (uint4 *)(xh + row * K + (int64_t)b * QK + 16 * l16);
+            dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
+            dst[1] = make_uint4(h[4], h[5], h[6], h[7]);
+        } else if (bok) {
             const float db = sd[bl];
             uint32_t h[8];
 #pragma unroll
@@ -98,17 +143,49 @@ __device__ __forceinline__ void q8k_row_group(const float *__restrict__ src, int
     }
 }
 
-template <bool VEC>
+template <bool VEC, int XO>
+__device__ __forceinline__ void q8k_row_group(const float *__restrict__ src, int64_t ld, int64_t row, int grp,
+                                              int nb, const Q8Out &o, int8_t *sq, float *sd, int lane) {
+    float v[16];
+    q8k_load<VEC>(src, ld, row, grp, nb, lane, v);
+    q8k_quant<XO>(v, row, grp, nb, o, sq, sd, lane);
+}
+
+// Items (row groups) per wave, all loaded before the first is quantized.  One
+// is fastest for the 8192 x 1024 GLU rows of a 1024-token moondream3 layer
+// (two: 12.6 vs 11.1 us; the wave count halves).
+constexpr int Q8_ITEMS = 1;
+
+template <bool VEC, int XO>
 __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ src, int64_t ld, int64_t nrows,
                                                   int nb, Q8Out o) {
     __shared__ __attribute__((aligned(16))) int8_t sq[4][4 * QK];
     __shared__ float sd[4][4];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int ngrp = (nb + 3) >> 2;
-    const int64_t item = (int64_t)blockIdx.x * 4 + wave;
-    if (item >= nrows * ngrp) return;   // whole waves; only wave-local exchanges follow
-    const int64_t row = item / ngrp;
-    q8k_row_group<VEC>(src, ld, row, (int)(item - row * ngrp), nb, o, sq[wave], sd[wave], lane);
+    const int64_t n_items = nrows * ngrp;
+    const int64_t item0 = ((int64_t)blockIdx.x * 4 + wave) * Q8_ITEMS;
+    if (item0 >= n_items) return;   // whole waves; only wave-local exchanges follow
+    float v[Q8_ITEMS][16];
+#pragma unroll
+    for (int u = 0; u < Q8_ITEMS; ++u) {
+        const int64_t item = item0 + u < n_items ? item0 + u : item0;
+        const int64_t row = item / ngrp;
+        q8k_load<VEC>(src, ld, row, (int)(item - row * ngrp), nb, lane, v[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < Q8_ITEMS; ++u) {
+        const int64_t item = item0 + u;
+        if (item >= n_items) break;
+        const int64_t row = item / ngrp;
+        q8k_quant<XO>(v[u], row, (int)(item - row * ngrp), nb, o, sq[wave], sd[wave], lane);
+    }
+}
+
+// the compile-time fp16 order for o (XO_ANY when o has no xh)
+inline int q8_xo(const Q8Out &o) {
+    if (!o.xh || !o.order || o.exact) return XO_ANY;
+    return o.wtype == 12 ? XO_Q4 : o.wtype == 14 ? XO_Q6 : XO_ANY;
 }
 
 int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, const Q8Out &o, hipStream_t st) {
@@ -116,9 +193,12 @@ int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, cons
     const int nb = (int)(K / QK);
     const int64_t items = nrows * ((nb + 3) / 4);
     const bool vec = (ld % 4 == 0) && ((uintptr_t)src % 16 == 0);
-    const dim3 grid((unsigned)((items + 3) / 4));
-    if (vec) hipLaunchKernelGGL(k_q8k_rows<true>, grid, dim3(256), 0, st, src, ld, nrows, nb, o);
-    else hipLaunchKernelGGL(k_q8k_rows<false>, grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    const dim3 grid((unsigned)((items + 4 * Q8_ITEMS - 1) / (4 * Q8_ITEMS)));
+    const int xo = q8_xo(o);
+    if (vec && xo == XO_Q4) hipLaunchKernelGGL((k_q8k_rows<true, XO_Q4>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    else if (vec && xo == XO_Q6) hipLaunchKernelGGL((k_q8k_rows<true, XO_Q6>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    else if (vec) hipLaunchKernelGGL((k_q8k_rows<true, XO_ANY>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    else hipLaunchKernelGGL((k_q8k_rows<false, XO_ANY>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
     return hip_check_launch();
 }
 
@@ -203,7 +283,7 @@ __device__ __forceinline__ void rt_transpose(const float4 (&in)[4], float4 *stag
 // of its work-groups to finish was measured slower than the separate top-k
 // launch: the logit hand-off costs three memory round trips at the kernel's
 // end.)
-template <bool VEC>
+template <bool VEC, int XO>
 __global__ void __launch_bounds__(1024) k_front(const float *__restrict__ W, const float *__restrict__ bias,
                                                 const float *__restrict__ x, int64_t ldx, int64_t T, int D, int E,
                                                 float *__restrict__ logits, Q8Out o) {
@@ -236,7 +316,11 @@ __global__ void __launch_bounds__(1024) k_front(const float *__restrict__ W, con
         const int nb = D / QK, ngrp = (nb + 3) >> 2;
         for (int i = et + net * wave; i < 16 * ngrp; i += net * RT_WAVES) {
             const int64_t row = t0 + i / ngrp;
-            if (row < T) q8k_row_group<VEC>(x, ldx, row, i % ngrp, nb, o, (int8_t *)stg, (float *)(stg + 64), lane);
+            if (row >= T) continue;
+            int8_t *sq = (int8_t *)stg;
+            float *sd = (float *)(stg + 64);
+            if (XO == XO_Q4) q8k_row_group<VEC, XO_Q4>(x, ldx, row, i % ngrp, nb, o, sq, sd, lane);
+            else q8k_row_group<VEC, XO_ANY>(x, ldx, row, i % ngrp, nb, o, sq, sd, lane);
         }
     }
     __syncthreads();
@@ -306,12 +390,15 @@ int launch_front(const float *W, const float *b, const float *x, int64_t ldx, in
     const int64_t blocks = 8 * net * ((nslab + 7) / 8);
     if (blocks > 0x7fffffff) return -6;
     const Q8Out o = qx ? *qx : Q8Out{};
-    if (vec)
-        hipLaunchKernelGGL(k_front<true>, dim3((unsigned)blocks), dim3(64 * RT_WAVES), 0, st, W, b, x, ldx, T, D, E,
-                           logits, o);
+    if (vec && q8_xo(o) == XO_Q4)
+        hipLaunchKernelGGL((k_front<true, XO_Q4>), dim3((unsigned)blocks), dim3(64 * RT_WAVES), 0, st, W, b, x, ldx,
+                           T, D, E, logits, o);
+    else if (vec)
+        hipLaunchKernelGGL((k_front<true, XO_ANY>), dim3((unsigned)blocks), dim3(64 * RT_WAVES), 0, st, W, b, x,
+                           ldx, T, D, E, logits, o);
     else
-        hipLaunchKernelGGL(k_front<false>, dim3((unsigned)blocks), dim3(64 * RT_WAVES), 0, st, W, b, x, ldx, T, D,
-                           E, logits, o);
+        hipLaunchKernelGGL((k_front<false, XO_ANY>), dim3((unsigned)blocks), dim3(64 * RT_WAVES), 0, st, W, b, x,
+                           ldx, T, D, E, logits, o);
     return hip_check_launch();
 }
 

@@ -44,6 +44,20 @@ int mi_event_record(mi_event_t e, mi_stream_t s);
 int mi_event_synchronize(mi_event_t e);
 int mi_event_elapsed_ms(float *ms, mi_event_t start, mi_event_t stop);
 
+/* Stream capture into a replayable graph.  mi_moe_forward and
+ * mi_moe_expert_ffn may be captured once their context is reserved: after
+ * reservation they allocate nothing, set no memory by memset, and wait on
+ * nothing on the host (stage profiling, which records events, must be off).
+ * Capture mode is relaxed; the stream must not be the null stream.
+ * end_capture instantiates the captured work; a graph replays the captured
+ * calls with their arguments (pointers, token count) as captured, so the
+ * caller rewrites the inputs in place between launches. */
+typedef struct mi_graph_s *mi_graph_t;
+int mi_stream_begin_capture(mi_stream_t s);
+int mi_stream_end_capture(mi_stream_t s, mi_graph_t *graph);
+int mi_graph_launch(mi_graph_t graph, mi_stream_t s);
+int mi_graph_destroy(mi_graph_t graph);
+
 /* last HIP error string seen by the library (thread-local, static storage) */
 const char *mi_last_hip_error(void);
 

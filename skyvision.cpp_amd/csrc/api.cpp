@@ -821,6 +821,33 @@ int mi_event_elapsed_ms(float *ms, mi_event_t a, mi_event_t b) {
     HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
     return MI_MOE_OK;
 }
+int mi_stream_begin_capture(mi_stream_t s) {
+    if (!s) return MI_MOE_ERR_ARG;
+    HIP_TRY(hipStreamBeginCapture((hipStream_t)s, hipStreamCaptureModeRelaxed));
+    return MI_MOE_OK;
+}
+int mi_stream_end_capture(mi_stream_t s, mi_graph_t *graph) {
+    if (!graph) return MI_MOE_ERR_NULL;
+    *graph = nullptr;
+    hipGraph_t g = nullptr;
+    HIP_TRY(hipStreamEndCapture((hipStream_t)s, &g));
+    hipGraphExec_t ex = nullptr;
+    const hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return record_hip_error(e);
+    *graph = (mi_graph_t)ex;
+    return MI_MOE_OK;
+}
+int mi_graph_launch(mi_graph_t graph, mi_stream_t s) {
+    if (!graph) return MI_MOE_ERR_NULL;
+    HIP_TRY(hipGraphLaunch((hipGraphExec_t)graph, (hipStream_t)s));
+    return MI_MOE_OK;
+}
+int mi_graph_destroy(mi_graph_t graph) {
+    if (!graph) return MI_MOE_OK;
+    HIP_TRY(hipGraphExecDestroy((hipGraphExec_t)graph));
+    return MI_MOE_OK;
+}
 const char *mi_last_hip_error(void) { return g_last_error.c_str(); }
 
 }  // extern "C"

@@ -98,6 +98,10 @@ SYMBOLS = {
     "mi_event_synchronize": ([P], C.c_int),
     "mi_event_elapsed_ms": ([C.POINTER(C.c_float), P, P], C.c_int),
     "mi_last_hip_error": ([], C.c_char_p),
+    "mi_stream_begin_capture": ([P], C.c_int),
+    "mi_stream_end_capture": ([P, C.POINTER(P)], C.c_int),
+    "mi_graph_launch": ([P, P], C.c_int),
+    "mi_graph_destroy": ([P], C.c_int),
 }
 
 
@@ -293,6 +297,46 @@ def _addr(x):
     if isinstance(x, P):
         return x
     return P(int(x))
+
+
+class Stream:
+    def __init__(self):
+        self.h = P()
+        call("mi_stream_create", C.byref(self.h))
+
+    @property
+    def addr(self) -> int:
+        return self.h.value or 0
+
+    def synchronize(self) -> None:
+        call("mi_stream_synchronize", self.h)
+
+    def destroy(self) -> None:
+        if self.h:
+            call("mi_stream_destroy", self.h)
+            self.h = P()
+
+
+class Graph:
+    """Library calls captured on a stream (mi_stream_begin_capture ..
+    mi_stream_end_capture) and instantiated; launch() replays them."""
+
+    def __init__(self, stream: Stream, record):
+        call("mi_stream_begin_capture", stream.h)
+        self.h = P()
+        try:
+            record(stream)
+        finally:
+            rc = load().mi_stream_end_capture(stream.h, C.byref(self.h))
+        check("end capture", rc)
+
+    def launch(self, stream: Stream) -> None:
+        call("mi_graph_launch", self.h, stream.h)
+
+    def destroy(self) -> None:
+        if self.h:
+            call("mi_graph_destroy", self.h)
+            self.h = P()
 
 
 class Event:

@@ -237,13 +237,17 @@ def config4_stack(n_layers: int = 24, T_prefill: int = 2048, n_decode: int = 256
     hn = M.DeviceBuffer(4 * T_prefill * spec.D)
     h2 = M.DeviceBuffer(4 * T_prefill * spec.D)
 
-    def stack(T, cur, nxt):
+    def stack_on(T, cur, nxt, st=None):
         # ping-pong: out = cur + MoE(RMSNorm(cur)) into the other buffer
+        sh = st.h if st is not None else None
         for L in layers:
-            M.check("rmsnorm", ctx.rmsnorm(cur, T, spec.D, eps, hn))
-            M.check("forward", ctx.forward(L.layer, hn, T, cur, nxt))
+            M.check("rmsnorm", ctx.rmsnorm(cur, T, spec.D, eps, hn, stream=sh))
+            M.check("forward", ctx.forward(L.layer, hn, T, cur, nxt, stream=sh))
             cur, nxt = nxt, cur
         return cur
+
+    def stack(T, cur, nxt):
+        return stack_on(T, cur, nxt)
 
     def prefill():
         M.check("copy", M.load().mi_memcpy_d2d(h.ptr, h0.ptr, 4 * T_prefill * spec.D))
@@ -258,7 +262,24 @@ def config4_stack(n_layers: int = 24, T_prefill: int = 2048, n_decode: int = 256
         last = prefill()
     e1.record()
     e1.synchronize()
+    pre_ms_stream = e0.elapsed_ms(e1) / reps
+    # the same prefill with the stack captured once (n_layers even: the result
+    # lands in h, like the issued run) and replayed after the input copy
+    gs = M.Stream()
+    g = M.Graph(gs, lambda st: stack_on(T_prefill, h, h2, st))
+    M.check("copy", M.load().mi_memcpy_d2d(h.ptr, h0.ptr, 4 * T_prefill * spec.D))
+    g.launch(gs)
+    gs.synchronize()
+    M.synchronize()
+    e0.record(gs.h)
+    for _ in range(reps):
+        M.check("copy", M.load().mi_memcpy_d2d(h.ptr, h0.ptr, 4 * T_prefill * spec.D))
+        g.launch(gs)
+    e1.record(gs.h)
+    e1.synchronize()
     pre_ms = e0.elapsed_ms(e1) / reps
+    g.destroy()
+    M.synchronize()
     # decode: the next token's input is the RMSNorm of the previous final hidden
     tok = M.DeviceBuffer(4 * spec.D)
     M.check("copy", M.load().mi_memcpy_d2d(tok.ptr, C.c_void_p(last.addr + 4 * (T_prefill - 1) * spec.D),
@@ -275,30 +296,51 @@ def config4_stack(n_layers: int = 24, T_prefill: int = 2048, n_decode: int = 256
         touched += int((counts.download(np.int32, (spec.E,)) > 0).sum())
         cur, nxt = nxt, cur
     step_bytes = sum(W.algorithmic_bytes(spec, 0) for _ in layers) + touched * (W.algorithmic_bytes(spec, 1) - W.algorithmic_bytes(spec, 0))
+    def step(st=None):
+        nonlocal cur, nxt
+        sh = st.h if st is not None else None
+        for L in layers:
+            M.check("rmsnorm", ctx.rmsnorm(cur, 1, spec.D, eps, nrm, stream=sh))
+            M.check("forward", ctx.forward(L.layer, nrm, 1, cur, nxt, stream=sh))
+            cur, nxt = nxt, cur
+        M.check("rmsnorm", ctx.rmsnorm(cur, 1, spec.D, eps, cur, stream=sh))
+
     M.synchronize()
     e0.record()
     for _ in range(n_decode):
-        for L in layers:
-            M.check("rmsnorm", ctx.rmsnorm(cur, 1, spec.D, eps, nrm))
-            M.check("forward", ctx.forward(L.layer, nrm, 1, cur, nxt))
-            cur, nxt = nxt, cur
-        M.check("rmsnorm", ctx.rmsnorm(cur, 1, spec.D, eps, cur))
+        step()
     e1.record()
     e1.synchronize()
+    dec_ms_stream = e0.elapsed_ms(e1) / n_decode
+    # one decode step captured (n_layers even: it ends in the buffer it
+    # started from) and replayed n_decode times
+    g = M.Graph(gs, step)
+    M.synchronize()
+    e0.record(gs.h)
+    for _ in range(n_decode):
+        g.launch(gs)
+    e1.record(gs.h)
+    e1.synchronize()
     dec_ms = e0.elapsed_ms(e1) / n_decode
+    g.destroy()
+    gs.destroy()
+    M.synchronize()
     fl = n_layers * W.flops(spec, T_prefill)
     res = {"workload": f"config 4: {n_layers}-layer moondream-shape MoE stack (Q4_K, 64 experts, top-8), "
                        f"h + MoE(RMSNorm(h)), attention as identity",
            "resident_bytes": resident,
+           "schedule": "each prefill / decode step captured once into a HIP graph and replayed",
            "prefill": {"tokens": T_prefill, "ms": pre_ms, "tokens_per_s": T_prefill / (pre_ms * 1e-3),
-                       "TFLOPs": fl / (pre_ms * 1e-3) / 1e12},
+                       "TFLOPs": fl / (pre_ms * 1e-3) / 1e12, "stream_ms": pre_ms_stream},
            "decode": {"steps": n_decode, "ms_per_token": dec_ms, "tokens_per_s": 1.0 / (dec_ms * 1e-3),
                       "bytes_per_step": step_bytes, "GBs": step_bytes / (dec_ms * 1e-3) / 1e9,
                       "frac_hbm": step_bytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                      "stream_ms_per_token": dec_ms_stream,
                       "schedule": "fused single-token kernel per layer, plain launch"}}
     log(f"config 4: prefill {pre_ms:.2f} ms ({res['prefill']['tokens_per_s']:.0f} tok/s, "
         f"{res['prefill']['TFLOPs']:.0f} TFLOP/s), decode {dec_ms:.3f} ms/token "
-        f"({res['decode']['GBs']:.0f} GB/s)")
+        f"({res['decode']['GBs']:.0f} GB/s); issued kernel by kernel: prefill {pre_ms_stream:.2f} ms, "
+        f"decode {dec_ms_stream:.3f} ms/token")
     del layers
     ctx.close()
     return res

@@ -1,0 +1,342 @@
+// vqa_moe.cpp - vqa::moe on the libmimoe C ABI (see vqa_moe.hpp).
+//
+// Reference: src/core/engine/moe_compute.cpp:33-151 (the builders) and its
+// MOE_COMPUTE_TEST_MAIN self-test (:154-230), mirrored below under
+// VQA_MOE_SELFTEST with the same hand-computed known answer.
+#include "vqa_moe.hpp"
+
+#include <algorithm>
+#include <cstring>
+
+namespace vqa {
+namespace moe {
+
+namespace {
+
+int32_t mi_act_of(UnaryOp act) {
+    switch (act) {
+    case UnaryOp::SILU: return MI_ACT_SILU;
+    case UnaryOp::GELU: return MI_ACT_GELU_TANH;
+    case UnaryOp::GELU_ERF: return MI_ACT_GELU_ERF;
+    }
+    return -1;
+}
+
+mi_tensor as_mi(const Tensor *t) {
+    mi_tensor m{};
+    m.data = t->data;
+    m.type = t->type;
+    for (int i = 0; i < 4; ++i) {
+        m.ne[i] = t->ne[i];
+        m.nb[i] = t->nb[i];
+    }
+    return m;
+}
+
+// bytes of a row of n values (mi_row_size covers the expert-table types)
+size_t row_bytes(int type, int64_t n) {
+    if (n <= 0) return 0;
+    if (type == MI_TYPE_I32) return 4 * (size_t)n;
+    return mi_row_size(type, n);
+}
+
+// rows of ne0 values stored back to back, planes back to back
+bool contiguous(const Tensor *t) {
+    const size_t row = row_bytes(t->type, t->ne[0]);
+    return row > 0 && t->nb[1] == row && t->nb[2] == row * (size_t)t->ne[1] &&
+           t->nb[3] == t->nb[2] * (size_t)t->ne[2];
+}
+
+size_t bytes_of(const Tensor *t) { return t->nb[3] * (size_t)t->ne[3]; }
+
+}  // namespace
+
+// ------------------------------------------------------------------ Session
+Session::Session(int device) {
+    if (fail(mi_moe_ctx_create(&ctx_, device))) return;
+    fail(mi_stream_create(&stream_));
+}
+
+Session::~Session() {
+    if (stream_) (void)mi_stream_synchronize(stream_);
+    for (Tensor *t : owned_) {
+        (void)mi_dev_free(t->data);
+        delete t;
+    }
+    if (stream_) (void)mi_stream_destroy(stream_);
+    if (ctx_) mi_moe_ctx_destroy(ctx_);
+}
+
+int Session::fail(int rc) {
+    if (rc && !status_) status_ = rc;
+    return rc;
+}
+
+Tensor *Session::new_tensor(int type, int64_t ne0, int64_t ne1, int64_t ne2) {
+    const size_t row = row_bytes(type, ne0);
+    if (!row || ne1 <= 0 || ne2 <= 0) {
+        fail(MI_MOE_ERR_SHAPE);
+        return nullptr;
+    }
+    Tensor *t = new Tensor;
+    t->type = type;
+    t->ne[0] = ne0; t->ne[1] = ne1; t->ne[2] = ne2; t->ne[3] = 1;
+    t->nb[0] = type == MI_TYPE_F32 || type == MI_TYPE_I32 ? 4 : type == MI_TYPE_F16 ? 2 : row / (size_t)(ne0 / 256);
+    t->nb[1] = row;
+    t->nb[2] = row * (size_t)ne1;
+    t->nb[3] = t->nb[2] * (size_t)ne2;
+    if (fail(mi_dev_malloc(&t->data, bytes_of(t)))) {
+        delete t;
+        return nullptr;
+    }
+    owned_.push_back(t);
+    return t;
+}
+
+int Session::set(Tensor *t, const void *host, size_t bytes) {
+    if (!t || !host) return fail(MI_MOE_ERR_NULL);
+    if (bytes > bytes_of(t)) return fail(MI_MOE_ERR_SHAPE);
+    if (int rc = fail(mi_stream_synchronize(stream_))) return rc;
+    return fail(mi_memcpy_h2d(t->data, host, bytes));
+}
+
+int Session::get(const Tensor *t, void *host, size_t bytes) {
+    if (!t || !host) return fail(MI_MOE_ERR_NULL);
+    if (bytes > bytes_of(t)) return fail(MI_MOE_ERR_SHAPE);
+    if (int rc = fail(mi_stream_synchronize(stream_))) return rc;
+    return fail(mi_memcpy_d2h(host, t->data, bytes));
+}
+
+int Session::compute() {
+    if (status_) return status_;
+    return fail(mi_stream_synchronize(stream_));
+}
+
+int Session::ensure(int64_t T, int32_t D, int32_t I, int32_t E, int32_t K) {
+    if (T <= cap_T_ && D <= cap_D_ && I <= cap_I_ && E <= cap_E_ && K <= cap_K_) return 0;
+    // the workspace is replaced: nothing queued may still use it
+    if (int rc = fail(mi_stream_synchronize(stream_))) return rc;
+    cap_T_ = std::max(cap_T_, T);
+    cap_D_ = std::max(cap_D_, D);
+    cap_I_ = std::max(cap_I_, I);
+    cap_E_ = std::max(cap_E_, E);
+    cap_K_ = std::max(cap_K_, K);
+    return fail(mi_moe_ctx_reserve(ctx_, cap_T_, cap_D_, cap_I_, cap_E_, cap_K_));
+}
+
+// ------------------------------------------------------------------ v3 table form
+Tensor *build_expert_ffn_table_res(Session &s, Tensor *x, Tensor *res, Tensor *gate_table, Tensor *up_table,
+                                   Tensor *down_table, Tensor *gate_up_ids, Tensor *down_ids, Tensor *w,
+                                   UnaryOp act) {
+    // moe_compute.cpp:102-122, in order
+    if (!s.ctx() || !x || !res || !w) return nullptr;
+    if (!gate_table || !up_table || !down_table || !gate_up_ids || !down_ids) return nullptr;
+    if (w->type != MI_TYPE_F32) return nullptr;
+    const int64_t K = w->ne[0];
+    const int64_t T = x->ne[1];
+    if (K <= 0 || w->ne[1] != T || w->ne[2] != 1 || w->ne[3] != 1) return nullptr;
+    if (res->ne[0] != x->ne[0] || res->ne[1] != T) return nullptr;
+    if (gate_up_ids->type != MI_TYPE_I32 || down_ids->type != MI_TYPE_I32) return nullptr;
+    if (gate_up_ids->ne[0] != K || down_ids->ne[0] != K) return nullptr;
+    if (gate_up_ids->ne[1] != T || down_ids->ne[1] != T) return nullptr;
+    if (gate_table->type != up_table->type || gate_table->ne[0] != up_table->ne[0] ||
+        gate_table->ne[1] != up_table->ne[1] || gate_table->nb[1] != up_table->nb[1])
+        return nullptr;
+    if (gate_table->ne[0] != x->ne[0]) return nullptr;
+    if (up_table->ne[0] != x->ne[0]) return nullptr;
+    if (down_table->ne[0] != gate_table->ne[1]) return nullptr;
+    if (down_table->ne[1] != x->ne[0]) return nullptr;
+    // this build: F32 contiguous activations, one slot count for the tables
+    if (x->type != MI_TYPE_F32 || res->type != MI_TYPE_F32) return nullptr;
+    if (!contiguous(x) || !contiguous(res) || !contiguous(w) || !contiguous(gate_up_ids) || !contiguous(down_ids))
+        return nullptr;
+    if (up_table->ne[2] != gate_table->ne[2] || down_table->ne[2] != gate_table->ne[2]) return nullptr;
+    if (T <= 0 || x->ne[0] > INT32_MAX || gate_table->ne[1] > INT32_MAX || gate_table->ne[2] > INT32_MAX ||
+        K > INT32_MAX)
+        return nullptr;
+    const int32_t D = (int32_t)x->ne[0], I = (int32_t)gate_table->ne[1], E = (int32_t)gate_table->ne[2];
+
+    Tensor *out = s.new_tensor(MI_TYPE_F32, D, T);
+    if (!out || s.ensure(T, D, I, E, (int32_t)K)) return nullptr;
+    mi_moe_layer L{};
+    L.n_embd = D;
+    L.n_expert = E;
+    L.n_expert_used = (int32_t)K;
+    L.n_ff = I;
+    L.gate = as_mi(gate_table);
+    L.up = as_mi(up_table);
+    L.down = as_mi(down_table);
+    L.fused_gate_up = 0;
+    L.act = mi_act_of(act);
+    L.gating = 0;
+    if (s.fail(mi_moe_expert_ffn(s.ctx(), &L, (const float *)x->data, T, (const float *)res->data,
+                                 (const int32_t *)gate_up_ids->data, (const int32_t *)down_ids->data,
+                                 (const float *)w->data, (float *)out->data, s.stream())))
+        return nullptr;
+    return out;
+}
+
+Tensor *build_expert_ffn_table(Session &s, Tensor *x, Tensor *gate_table, Tensor *up_table, Tensor *down_table,
+                               Tensor *gate_up_ids, Tensor *down_ids, Tensor *w, UnaryOp act) {
+    return build_expert_ffn_table_res(s, x, x, gate_table, up_table, down_table, gate_up_ids, down_ids, w, act);
+}
+
+// ------------------------------------------------------------------ v1 per-slot form
+Tensor *build_expert_ffn_res(Session &s, Tensor *x, Tensor *res, const std::vector<Tensor *> &gate,
+                             const std::vector<Tensor *> &up, const std::vector<Tensor *> &down, Tensor *w,
+                             UnaryOp act) {
+    // moe_compute.cpp:43-58, in order
+    const size_t n_used = gate.size();
+    if (!s.ctx() || !x || !res || !w || n_used == 0) return nullptr;
+    if (up.size() != n_used || down.size() != n_used) return nullptr;
+    if (w->type != MI_TYPE_F32) return nullptr;
+    if (w->ne[0] != (int64_t)n_used) return nullptr;
+    if (w->ne[1] != x->ne[1] || w->ne[2] != 1 || w->ne[3] != 1) return nullptr;
+    if (res->ne[0] != x->ne[0] || res->ne[1] != x->ne[1]) return nullptr;
+    for (size_t k = 0; k < n_used; k++) {
+        if (!gate[k] || !up[k] || !down[k]) return nullptr;
+        if (gate[k]->ne[0] != x->ne[0] || up[k]->ne[0] != x->ne[0]) return nullptr;
+        if (down[k]->ne[0] != gate[k]->ne[1] || down[k]->ne[0] != up[k]->ne[1]) return nullptr;
+        if (down[k]->ne[1] != x->ne[0]) return nullptr;
+    }
+    // this build: one type and shape per role, contiguous 2D tensors; slot k
+    // of every token is expert tensor k, so the tables are the tensors packed
+    // in slot order and the ids are 0 .. n_used - 1 for every token
+    const std::vector<Tensor *> *roles[3] = {&gate, &up, &down};
+    for (const auto *r : roles)
+        for (const Tensor *t : *r)
+            if (t->type != (*r)[0]->type || t->ne[1] != (*r)[0]->ne[1] || t->ne[2] != 1 || t->ne[3] != 1 ||
+                !contiguous(t))
+                return nullptr;
+    const int64_t T = x->ne[1];
+    const int64_t K = (int64_t)n_used;
+    Tensor *tables[3];
+    for (int r = 0; r < 3; ++r) {
+        const Tensor *t0 = (*roles[r])[0];
+        tables[r] = s.new_tensor(t0->type, t0->ne[0], t0->ne[1], K);
+        if (!tables[r]) return nullptr;
+        for (int64_t k = 0; k < K; ++k)
+            if (s.fail(mi_memcpy_d2d((char *)tables[r]->data + (size_t)k * tables[r]->nb[2],
+                                     (*roles[r])[k]->data, tables[r]->nb[2])))
+                return nullptr;
+    }
+    Tensor *ids = s.new_tensor(MI_TYPE_I32, K, T);
+    if (!ids) return nullptr;
+    std::vector<int32_t> h((size_t)(K * T));
+    for (int64_t t = 0; t < T; ++t)
+        for (int64_t k = 0; k < K; ++k) h[(size_t)(t * K + k)] = (int32_t)k;
+    if (s.set(ids, h.data(), h.size() * sizeof(int32_t))) return nullptr;
+    return build_expert_ffn_table_res(s, x, res, tables[0], tables[1], tables[2], ids, ids, w, act);
+}
+
+Tensor *build_expert_ffn(Session &s, Tensor *x, const std::vector<Tensor *> &gate,
+                         const std::vector<Tensor *> &up, const std::vector<Tensor *> &down, Tensor *w,
+                         UnaryOp act) {
+    return build_expert_ffn_res(s, x, x, gate, up, down, w, act);
+}
+
+}  // namespace moe
+}  // namespace vqa
+
+#ifdef VQA_MOE_SELFTEST
+// The reference's self-test (moe_compute.cpp:154-230) on this build: D = 2,
+// I = 3, K = 2, T = 1, F32, SiLU; out = x + 0.5 f0 + 1.0 f1 = [3.6423913,
+// 4.1931758] (hand-computed there); a w with the wrong row count gives
+// nullptr.  Added: the same answer through the slot-table form, the residual
+// split (res != x), and the table form's argument checks.
+#include <cmath>
+#include <cstdio>
+
+static int g_fail = 0;
+#define CHECK(cond, msg)                                               \
+    do {                                                               \
+        if (!(cond)) {                                                 \
+            std::fprintf(stderr, "FAIL %s (line %d)\n", msg, __LINE__); \
+            g_fail++;                                                  \
+        }                                                              \
+    } while (0)
+
+using vqa::moe::Tensor;
+
+int main(void) {
+    vqa::moe::Session s(0);
+    CHECK(s.status() == 0, "session");
+    if (s.status()) return 1;
+    const float gate0[6] = {0, 1, 1, 0, 0, 0};   // [I = 3 rows, D = 2]
+    const float up0[6] = {1, 0, 0, 1, 1, 1};
+    const float down0[6] = {1, 0, 0, 0, 1, 0};   // [D = 2 rows, I = 3]
+    const float gate1[6] = {1, 0, 0, 1, 0, 0};
+    const float up1[6] = {0, 1, 1, 0, 0, 0};
+    const float down1[6] = {0, 1, 0, 1, 0, 0};
+    const float xv[2] = {1.0f, 2.0f};
+    const float wv[2] = {0.5f, 1.0f};
+    const float want[2] = {3.6423913f, 4.1931758f};
+    auto mk = [&](const float *d, int ne0, int ne1) {
+        Tensor *t = s.new_tensor(MI_TYPE_F32, ne0, ne1);
+        if (t) s.set(t, d, sizeof(float) * ne0 * ne1);
+        return t;
+    };
+    std::vector<Tensor *> gate = {mk(gate0, 2, 3), mk(gate1, 2, 3)};
+    std::vector<Tensor *> up = {mk(up0, 2, 3), mk(up1, 2, 3)};
+    std::vector<Tensor *> down = {mk(down0, 3, 2), mk(down1, 3, 2)};
+    Tensor *x = mk(xv, 2, 1);
+    Tensor *w = mk(wv, 2, 1);
+
+    Tensor *out = vqa::moe::build_expert_ffn(s, x, gate, up, down, w);
+    CHECK(out, "build");
+    float o[2] = {0, 0};
+    if (out) {
+        CHECK(s.compute() == 0, "compute");
+        s.get(out, o, sizeof(o));
+        CHECK(std::fabs(o[0] - want[0]) < 1e-5f && std::fabs(o[1] - want[1]) < 1e-5f, "values");
+        std::fprintf(stderr, "moe out = [%.7f, %.7f] expected [%.7f, %.7f]\n", o[0], o[1], want[0], want[1]);
+    }
+    Tensor *wbad = s.new_tensor(MI_TYPE_F32, 3, 1);
+    CHECK(vqa::moe::build_expert_ffn(s, x, gate, up, down, wbad) == nullptr, "bad w rows -> nullptr");
+
+    // slot tables [D, I, 2] / [I, D, 2] and ids [2, 1]
+    const float gt[12] = {0, 1, 1, 0, 0, 0, 1, 0, 0, 1, 0, 0};
+    const float ut[12] = {1, 0, 0, 1, 1, 1, 0, 1, 1, 0, 0, 0};
+    const float dt[12] = {1, 0, 0, 0, 1, 0, 0, 1, 0, 1, 0, 0};
+    const int32_t idv[2] = {0, 1};
+    Tensor *gT = s.new_tensor(MI_TYPE_F32, 2, 3, 2), *uT = s.new_tensor(MI_TYPE_F32, 2, 3, 2);
+    Tensor *dT = s.new_tensor(MI_TYPE_F32, 3, 2, 2), *ids = s.new_tensor(MI_TYPE_I32, 2, 1);
+    s.set(gT, gt, sizeof(gt));
+    s.set(uT, ut, sizeof(ut));
+    s.set(dT, dt, sizeof(dt));
+    s.set(ids, idv, sizeof(idv));
+    Tensor *out2 = vqa::moe::build_expert_ffn_table(s, x, gT, uT, dT, ids, ids, w);
+    CHECK(out2, "table build");
+    if (out2) {
+        float o2[2] = {0, 0};
+        CHECK(s.compute() == 0, "table compute");
+        s.get(out2, o2, sizeof(o2));
+        CHECK(std::fabs(o2[0] - want[0]) < 1e-5f && std::fabs(o2[1] - want[1]) < 1e-5f, "table values");
+        std::fprintf(stderr, "table out = [%.7f, %.7f]\n", o2[0], o2[1]);
+    }
+    // residual split: res = [10, 20] -> out = res + (want - x)
+    const float rv[2] = {10.0f, 20.0f};
+    Tensor *res = mk(rv, 2, 1);
+    Tensor *out3 = vqa::moe::build_expert_ffn_table_res(s, x, res, gT, uT, dT, ids, ids, w, vqa::moe::UnaryOp::SILU);
+    CHECK(out3, "table_res build");
+    if (out3) {
+        float o3[2] = {0, 0};
+        CHECK(s.compute() == 0, "table_res compute");
+        s.get(out3, o3, sizeof(o3));
+        CHECK(std::fabs(o3[0] - (10.0f + want[0] - 1.0f)) < 1e-5f &&
+                  std::fabs(o3[1] - (20.0f + want[1] - 2.0f)) < 1e-5f,
+              "table_res values");
+    }
+    // argument checks of the table form
+    Tensor *ids_f = s.new_tensor(MI_TYPE_F32, 2, 1);
+    CHECK(vqa::moe::build_expert_ffn_table(s, x, gT, uT, dT, ids_f, ids, w) == nullptr, "F32 ids -> nullptr");
+    CHECK(vqa::moe::build_expert_ffn_table(s, x, gT, dT, dT, ids, ids, w) == nullptr,
+          "gate/up shape mismatch -> nullptr");
+    CHECK(vqa::moe::build_expert_ffn_table(s, x, gT, uT, gT, ids, ids, w) == nullptr, "down rows -> nullptr");
+    CHECK(vqa::moe::build_expert_ffn_table(s, x, gT, uT, dT, ids, ids, wbad) == nullptr, "w rows -> nullptr");
+    CHECK(s.compute() == 0, "session status");
+    if (s.status()) std::fprintf(stderr, "session status %d (%s)\n", s.status(), mi_last_hip_error());
+    std::fprintf(stderr, "%s (%d failures)\n", g_fail ? "FAIL" : "PASS", g_fail);
+    return g_fail ? 1 : 0;
+}
+#endif

@@ -168,7 +168,23 @@ def cpu_baseline(spec, layer0: W.GpuLayer, T_sample: int, budget_s: float = 20.0
     return {"value": T_sample / med, "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"{spec.name}: {T_sample} tokens x {len(times)} runs (median {med * 1e3:.1f} ms), "
                       f"ggml-semantics CPU restatement (Q8_K activations x k-quant integer dots), "
-                      f"{cores} threads"}
+                      f"{cores} threads on {host_cpu()}"}
+
+
+def host_cpu() -> str:
+    """The host CPU's model name and vector ISA (from /proc/cpuinfo)."""
+    model, flags = "unknown CPU", set()
+    try:
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            if k.strip() == "model name" and model == "unknown CPU":
+                model = v.strip()
+            elif k.strip() == "flags" and not flags:
+                flags = set(v.split())
+    except OSError:
+        pass
+    isa = [f for f in ("avx512_vnni", "avx512bw", "avx512f", "avx2") if f in flags]
+    return f"{model} ({', '.join(isa) if isa else 'no AVX2'})"
 
 
 def config3_sweep(copies: int) -> dict:
@@ -349,7 +365,7 @@ def config4_stack(n_layers: int = 24, T_prefill: int = 2048, n_decode: int = 256
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--copies", type=int, default=16)
     ap.add_argument("--config", type=int, default=1, choices=[1, 2])

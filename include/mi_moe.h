@@ -100,6 +100,24 @@ typedef struct {
                                                token-ascending within an expert    */
 } mi_moe_routing;
 
+/* Row norm of the layer stream in front of the MoE block (the reference
+ * normalizes before routing: moondream3 LayerNorm with weight and bias,
+ * moondream.cpp:405-407; qwen3omni RMSNorm times ffn_norm,
+ * qwen3omni_model.cpp:756-757).  weight / bias: F32 [D] device or NULL; bias
+ * is read for MI_NORM_LAYER only. */
+typedef enum {
+    MI_NORM_NONE  = 0,
+    MI_NORM_RMS   = 1,             /* y = x / sqrt(mean(x^2) + eps) [* weight]                  */
+    MI_NORM_LAYER = 2,             /* y = (x - mean) / sqrt(var(x) + eps) [* weight] [+ bias]   */
+} mi_norm_kind;
+
+typedef struct {
+    int32_t      kind;             /* mi_norm_kind */
+    float        eps;
+    const float *weight;
+    const float *bias;
+} mi_moe_norm;
+
 typedef struct mi_moe_ctx mi_moe_ctx;
 
 /* ---- context -------------------------------------------------------------
@@ -124,6 +142,23 @@ int  mi_moe_ctx_reserve(mi_moe_ctx *ctx, int64_t max_tokens, int32_t n_embd, int
 int mi_moe_forward(mi_moe_ctx *ctx, const mi_moe_layer *layer, const float *x, int64_t n_tokens,
                    const float *res, float *out, const mi_moe_routing *routing,
                    mi_stream_t stream);
+
+/* ---- norm + MoE block in one call ----------------------------------------
+ * out[t] = res[t] + MoE(norm(h[t])): the reference's ffn_norm followed by its
+ * MoE block (moondream.cpp:405-407 + 509-547; qwen3omni_model.cpp:756-780),
+ * in one call: the rows are normalized once into the context's workspace
+ * (mi_moe_ctx_reserve sizes it), then the block runs on them.  Same results,
+ * bit for bit, as mi_norm into a buffer followed by mi_moe_forward on it.  norm NULL or MI_NORM_NONE: mi_moe_forward.
+ * D <= 4096 with a norm (MI_MOE_ERR_UNSUPPORTED beyond). */
+int mi_moe_forward_norm(mi_moe_ctx *ctx, const mi_moe_layer *layer, const mi_moe_norm *norm, const float *h,
+                        int64_t n_tokens, const float *res, float *out, const mi_moe_routing *routing,
+                        mi_stream_t stream);
+
+/* y = norm(x) over each row of n_cols <= 4096 (F32 [n_rows][n_cols] device;
+ * y may equal x): the norms of mi_moe_forward_norm as an op (ggml_norm /
+ * ggml_rms_norm followed by ggml_mul / ggml_add with the weight and bias). */
+int mi_norm(mi_moe_ctx *ctx, const mi_moe_norm *norm, const float *x, int64_t n_rows, int32_t n_cols,
+            float *y, mi_stream_t stream);
 
 /* ---- routed FFN with caller-supplied routing ------------------------------
  * Replaces vqa::moe::build_expert_ffn_table_res (src/core/engine/moe_compute.hpp:66-71,
@@ -165,8 +200,9 @@ int mi_quantize(mi_moe_ctx *ctx, int32_t type, const float *src, void *dst, int6
 int mi_fill_normal(mi_moe_ctx *ctx, float *dst, int64_t n, uint64_t seed, uint64_t stream_id,
                    float mean, float stddev, mi_stream_t stream);
 
-/* y = x / sqrt(mean(x^2) + eps) over each row of n_cols (F32 [n_rows][n_cols]
- * device; y may equal x).  No counterpart in the reference's MoE path: the
+/* y = x / sqrt(mean(x^2) + eps) over each row of n_cols <= 4096 (F32
+ * [n_rows][n_cols] device; y may equal x): mi_norm with MI_NORM_RMS and no
+ * weight.  No counterpart in the reference's MoE path: the
  * norm that feeds the synthetic layer stack (h + MoE(
  * RMSNorm(h)) with attention as identity), written here so the stack runs
  * on one device stream. */

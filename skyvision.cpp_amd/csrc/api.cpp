@@ -86,6 +86,7 @@ struct mi_moe_ctx {
     float *logits = nullptr;
     int32_t *sel = nullptr;
     float *w = nullptr;
+    float *xn = nullptr;      // [cap_T][D] normalized rows where a norm cannot be fused
     DispBuf disp[2];
     ActBuf ax, aact;
     float *f1 = nullptr;      // [rows][max(2I, kmax)]  GLU / F32 scratch
@@ -458,6 +459,7 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
     const int64_t tiles = (rows + GEMM_BM - 1) / GEMM_BM + std::min<int64_t>(E, rows);
     size_t need = 0;
     need += carve_size<float>(max_tokens * E) + carve_size<int32_t>(rows) + carve_size<float>(rows);
+    need += carve_size<float>(max_tokens * D);
     for (int s = 0; s < 2; ++s)
         need += carve_size<int32_t>(E) + carve_size<int32_t>(E + 1) + carve_size<int32_t>(rows) +
                 2 * carve_size<int32_t>(tiles) + carve_size<int32_t>(1) + carve_size<int32_t>(E) +
@@ -486,6 +488,7 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
     c->logits = carve<float>(q, max_tokens * E);
     c->sel = carve<int32_t>(q, rows);
     c->w = carve<float>(q, rows);
+    c->xn = carve<float>(q, max_tokens * D);
     for (int s = 0; s < 2; ++s) {
         DispBuf &d = c->disp[s];
         d.counts = carve<int32_t>(q, E);
@@ -562,18 +565,32 @@ int mi_moe_ctx_stage_times(mi_moe_ctx *c, int max_stages, const char **names, fl
     return MI_MOE_OK;
 }
 
-int mi_moe_forward(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const float *res,
-                   float *out, const mi_moe_routing *routing, mi_stream_t stream) {
+namespace {
+
+// the forward with an optional norm of its input (np.kind != NORM_NONE): the
+// rows are normalized into the workspace once, then the forward runs as
+// usual.  (Applying the norm where the kernels read x was built and measured
+// slower: in the router launch each of a token slab's expert-tile
+// work-groups recomputed the rows' statistics before its chunk loop, config-4
+// prefill 9.96 vs 9.57 ms; in the single-token kernel the extra registers of
+// phase A cost more than the launch it saved, 0.675 vs 0.641 ms per step.)
+int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const float *res, float *out,
+                 const mi_moe_routing *routing, const NormParams &np, hipStream_t st) {
     if (!c) return MI_MOE_ERR_NULL;
     if (T < 0) return MI_MOE_ERR_SHAPE;
     TRY(validate_layer(c, L, true));
     if (T == 0) return MI_MOE_OK;
     if (!x || !out) return MI_MOE_ERR_NULL;
     if (T > c->cap_T) return MI_MOE_ERR_CAPACITY;
-    HIP_TRY(hipSetDevice(c->device));
-    hipStream_t st = (hipStream_t)stream;
     const int D = L->n_embd, E = L->n_expert, K = L->n_expert_used;
+    if (np.kind != NORM_NONE && D > 4096) return MI_MOE_ERR_UNSUPPORTED;
+    HIP_TRY(hipSetDevice(c->device));
     stage_begin(c, st);
+    if (np.kind != NORM_NONE) {
+        TRY(launch_norm(np, x, T, D, c->xn, st));
+        stage_end(c, "norm", st);
+        x = c->xn;
+    }
     int P = 0, C = 0;
     if (T == 1 && plan_decode1(c, L, x, P, C)) {
         TRY(run_decode1(c, L, x, res, out, P, C, st));
@@ -606,6 +623,43 @@ int mi_moe_forward(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t
             HIP_TRY(hipMemcpyAsync(routing->perm, d.perm, sizeof(int32_t) * T * K, hipMemcpyDeviceToDevice, st));
     }
     return MI_MOE_OK;
+}
+
+int norm_params(const mi_moe_norm *norm, NormParams &np) {
+    np = NormParams{};
+    if (!norm || norm->kind == MI_NORM_NONE) return MI_MOE_OK;
+    if (norm->kind != MI_NORM_RMS && norm->kind != MI_NORM_LAYER) return MI_MOE_ERR_ARG;
+    np.kind = norm->kind == MI_NORM_RMS ? NORM_RMS : NORM_LAYER;
+    np.eps = norm->eps;
+    np.w = norm->weight;
+    np.b = norm->kind == MI_NORM_LAYER ? norm->bias : nullptr;
+    return MI_MOE_OK;
+}
+
+}  // namespace
+
+int mi_moe_forward(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const float *res,
+                   float *out, const mi_moe_routing *routing, mi_stream_t stream) {
+    return forward_impl(c, L, x, T, res, out, routing, NormParams{}, (hipStream_t)stream);
+}
+
+int mi_moe_forward_norm(mi_moe_ctx *c, const mi_moe_layer *L, const mi_moe_norm *norm, const float *h, int64_t T,
+                        const float *res, float *out, const mi_moe_routing *routing, mi_stream_t stream) {
+    NormParams np;
+    TRY(norm_params(norm, np));
+    return forward_impl(c, L, h, T, res, out, routing, np, (hipStream_t)stream);
+}
+
+int mi_norm(mi_moe_ctx *c, const mi_moe_norm *norm, const float *x, int64_t n_rows, int32_t n_cols, float *y,
+            mi_stream_t stream) {
+    if (!c || !norm || !x || !y) return MI_MOE_ERR_NULL;
+    if (n_rows < 0 || n_cols <= 0) return MI_MOE_ERR_SHAPE;
+    if (n_cols > 4096) return MI_MOE_ERR_UNSUPPORTED;
+    NormParams np;
+    TRY(norm_params(norm, np));
+    if (np.kind == NORM_NONE) return MI_MOE_ERR_ARG;
+    HIP_TRY(hipSetDevice(c->device));
+    return launch_norm(np, x, n_rows, n_cols, y, (hipStream_t)stream);
 }
 
 int mi_moe_expert_ffn(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const float *res,

@@ -11,6 +11,7 @@
 // CPU restatement's.
 #include "common.hpp"
 #include "launch.hpp"
+#include "norm.hpp"
 
 namespace mimoe {
 
@@ -409,31 +410,98 @@ __global__ void __launch_bounds__(256) k_quantize_q6_K(const float *__restrict__
 }
 
 // ---------------------------------------------------------------- launchers
-// y[t] = x[t] / sqrt(mean(x[t]^2) + eps): one work-group per row; each thread
-// sums the squares of columns tid, tid + 256, ... in fp32, then a fixed-order
-// tree over the 256 partials (deterministic)
-__global__ void __launch_bounds__(256) k_rmsnorm(const float *__restrict__ x, int D, float eps,
-                                                 float *__restrict__ y) {
-    __shared__ float part[256];
-    const int64_t t = blockIdx.x;
-    const float *xr = x + t * D;
-    float s = 0.f;
-    for (int n = threadIdx.x; n < D; n += 256) s = fmaf(xr[n], xr[n], s);
-    part[threadIdx.x] = s;
+// y[t] = norm(x[t]) (norm.hpp): one 256-thread work-group per row of D <=
+// 4096; thread i holds the float4 pieces at 1024 k + 4 i (coalesced), sums in
+// fp64 over its pieces in k order, then a fixed LDS tree (128, 64, .. 1) over
+// the threads; LayerNorm's second sum reuses the held values.  y may equal x
+// (every value is in registers before the first store).
+constexpr int NORM_T = 256, NORM_PIECES = 4;   // 4096 / (4 * 256)
+
+__device__ inline double norm_block_sum(double v, double *red) {
+    red[threadIdx.x] = v;
     __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if ((int)threadIdx.x < o) part[threadIdx.x] += part[threadIdx.x + o];
+    for (int o = NORM_T / 2; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + o];
         __syncthreads();
     }
-    const float r = 1.0f / sqrtf(part[0] / (float)D + eps);
-    for (int n = threadIdx.x; n < D; n += 256) y[t * D + n] = xr[n] * r;
+    const double r = red[0];
+    __syncthreads();   // red is reused
+    return r;
+}
+
+__global__ void __launch_bounds__(NORM_T) k_norm_rows(const float *x, int D, NormParams p, float *y) {
+    __shared__ double red[NORM_T];
+    const int64_t t = blockIdx.x;
+    const float *xr = x + t * D;
+    float *yr = y + t * D;
+    const bool vec = D % 4 == 0 && ((uintptr_t)xr & 15) == 0 && ((uintptr_t)yr & 15) == 0;
+    float v[NORM_PIECES][4];
+#pragma unroll
+    for (int k = 0; k < NORM_PIECES; ++k) {
+        const int i = 1024 * k + 4 * (int)threadIdx.x;
+        if (vec && i < D) {
+            const float4 a = *(const float4 *)(xr + i);
+            v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[k][j] = i + j < D ? xr[i + j] : 0.f;
+        }
+    }
+    float m = 0.f, sc;
+    double acc = 0.0;
+    if (p.kind == NORM_RMS) {
+#pragma unroll
+        for (int k = 0; k < NORM_PIECES; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = acc + (double)(v[k][j] * v[k][j]);   // zeros past D add 0
+        const float ms = (float)(norm_block_sum(acc, red) / (double)D);
+        sc = 1.0f / sqrtf(ms + p.eps);
+    } else {
+#pragma unroll
+        for (int k = 0; k < NORM_PIECES; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = acc + (double)v[k][j];
+        m = (float)(norm_block_sum(acc, red) / (double)D);
+        double acc2 = 0.0;
+#pragma unroll
+        for (int k = 0; k < NORM_PIECES; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (1024 * k + 4 * (int)threadIdx.x + j < D) {
+                    const float d = v[k][j] - m;
+                    acc2 = acc2 + (double)(d * d);
+                }
+        const float var = (float)(norm_block_sum(acc2, red) / (double)D);
+        sc = 1.0f / sqrtf(var + p.eps);
+    }
+#pragma unroll
+    for (int k = 0; k < NORM_PIECES; ++k) {
+        const int i = 1024 * k + 4 * (int)threadIdx.x;
+        if (i >= D) continue;
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = norm_apply(p, v[k][j], i + j, m, sc);
+        if (vec) {
+            *(float4 *)(yr + i) = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+            for (int j = 0; j < 4; ++j)
+                if (i + j < D) yr[i + j] = o[j];
+        }
+    }
+}
+
+int launch_norm(const NormParams &p, const float *x, int64_t T, int D, float *y, hipStream_t st) {
+    if (T <= 0) return 0;
+    if (T > 0x7fffffff || D <= 0 || D > 4096 || (p.kind != NORM_RMS && p.kind != NORM_LAYER)) return -6;
+    hipLaunchKernelGGL(k_norm_rows, dim3((unsigned)T), dim3(NORM_T), 0, st, x, D, p, y);
+    return hip_check_launch();
 }
 
 int launch_rmsnorm(const float *x, int64_t T, int D, float eps, float *y, hipStream_t st) {
-    if (T <= 0) return 0;
-    if (T > 0x7fffffff || D <= 0) return -6;
-    hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)T), dim3(256), 0, st, x, D, eps, y);
-    return hip_check_launch();
+    NormParams p;
+    p.kind = NORM_RMS;
+    p.eps = eps;
+    return launch_norm(p, x, T, D, y, st);
 }
 
 int launch_fill_normal(float *out, int64_t n, uint64_t seed, uint64_t stream, float mean, float sd,

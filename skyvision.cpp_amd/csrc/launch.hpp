@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "norm.hpp"
+
 namespace mimoe {
 
 // records the HIP error string for mi_last_hip_error(); returns MI_MOE_ERR_HIP (-5)
@@ -19,6 +21,8 @@ int launch_fill_normal(float *out, int64_t n, uint64_t seed, uint64_t stream, fl
 int launch_quantize(int type, const float *src, void *dst, int64_t nblocks, hipStream_t st);
 // y = x / sqrt(mean(x^2) + eps) per row of D (x may equal y)
 int launch_rmsnorm(const float *x, int64_t T, int D, float eps, float *y, hipStream_t st);
+// y = norm(x) per row of D <= 4096 (norm.hpp; x may equal y)
+int launch_norm(const NormParams &p, const float *x, int64_t T, int D, float *y, hipStream_t st);
 
 // ---- routing (k_route.hip)
 struct Q8Out {

@@ -18,6 +18,7 @@ DECODE_CHAIN, DECODE_FUSED_COOPERATIVE, DECODE_FUSED_EXCLUSIVE = 0, 1, 2
 
 TYPE_F32, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K, TYPE_I32 = 0, 1, 12, 14, 26
 ACT_SILU, ACT_GELU_ERF_GP1, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2, 3
+NORM_NONE, NORM_RMS, NORM_LAYER = 0, 1, 2
 GATING_SOFTMAX_TOPK = 0
 QK_K = 256
 BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210}
@@ -51,6 +52,21 @@ class Layer(C.Structure):
                 ("down", Tensor), ("fused_gate_up", i32), ("act", i32), ("gating", i32)]
 
 
+class Norm(C.Structure):
+    _fields_ = [("kind", C.c_int32), ("eps", C.c_float), ("weight", C.c_void_p), ("bias", C.c_void_p)]
+
+
+def make_norm(kind: int, eps: float, weight=None, bias=None) -> Norm:
+    """weight / bias: DeviceBuffer (kept alive by the returned Norm) or a
+    device address."""
+    n = Norm()
+    n.kind, n.eps = kind, eps
+    n.weight = weight.addr if isinstance(weight, DeviceBuffer) else weight
+    n.bias = bias.addr if isinstance(bias, DeviceBuffer) else bias
+    n._buffers = (weight, bias)
+    return n
+
+
 class Routing(C.Structure):
     _fields_ = [("logits", P), ("sel", P), ("weights", P), ("counts", P), ("offsets", P),
                 ("perm", P)]
@@ -69,6 +85,9 @@ SYMBOLS = {
     "mi_quantize": ([P, i32, P, P, i64, i64, P], C.c_int),
     "mi_fill_normal": ([P, P, i64, C.c_uint64, C.c_uint64, C.c_float, C.c_float, P], C.c_int),
     "mi_rmsnorm": ([P, P, i64, C.c_int32, C.c_float, P, P], C.c_int),
+    "mi_norm": ([P, C.POINTER(Norm), P, i64, C.c_int32, P, P], C.c_int),
+    "mi_moe_forward_norm": ([P, C.POINTER(Layer), C.POINTER(Norm), P, i64, P, P, C.POINTER(Routing), P],
+                            C.c_int),
     "mi_moe_ctx_set_profiling": ([P, C.c_int], C.c_int),
     "mi_moe_ctx_stage_times": ([P, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_float),
                                 C.POINTER(C.c_int)], C.c_int),
@@ -273,6 +292,15 @@ class Context:
                     stream=None) -> int:
         return load().mi_fill_normal(self.h, _addr(dst), n, seed, stream_id, mean, std,
                                      _addr(stream))
+
+    def norm(self, norm: Norm, x, n_rows: int, n_cols: int, y, stream=None) -> int:
+        return load().mi_norm(self.h, C.byref(norm), _addr(x), n_rows, n_cols, _addr(y), _addr(stream))
+
+    def forward_norm(self, layer: Layer, norm: Norm | None, h, T: int, res, out, routing: Routing | None = None,
+                     stream=None) -> int:
+        return load().mi_moe_forward_norm(self.h, C.byref(layer), C.byref(norm) if norm is not None else None,
+                                          _addr(h), T, _addr(res), _addr(out),
+                                          C.byref(routing) if routing is not None else None, _addr(stream))
 
     def rmsnorm(self, x, n_rows: int, n_cols: int, eps: float, y, stream=None) -> int:
         return load().mi_rmsnorm(self.h, _addr(x), n_rows, n_cols, eps, _addr(y), _addr(stream))

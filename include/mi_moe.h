@@ -38,6 +38,7 @@ typedef enum {
     MI_MOE_ERR_UNSUPPORTED  = -6,  /* valid request this build does not handle    */
     MI_MOE_ERR_DEVICE       = -7,  /* no such device / device not usable          */
     MI_MOE_ERR_ARG          = -8,  /* other invalid argument (enum out of range)  */
+    MI_MOE_ERR_FORMAT       = -9,  /* file missing, unreadable or not valid GGUF  */
 } mi_moe_status;
 
 typedef enum {                     /* ggml_type ids */
@@ -208,6 +209,33 @@ int mi_fill_normal(mi_moe_ctx *ctx, float *dst, int64_t n, uint64_t seed, uint64
  * on one device stream. */
 int mi_rmsnorm(mi_moe_ctx *ctx, const float *x, int64_t n_rows, int32_t n_cols, float eps, float *y,
                mi_stream_t stream);
+
+/* ---- GGUF expert tensors (the on-disk side of the path) --------------------
+ * Replaces the reference's model load of the MoE tensors: moondream3 binds
+ * blk.N.ffn_gate_inp.{weight,bias} (router; F16 promoted to F32,
+ * moondream.cpp:149-172, 241-251), blk.N.ffn_up_exps (fused [h | g]) and
+ * blk.N.ffn_down_exps as written by convert/convert_hf_to_gguf.py:173-183;
+ * qwen3omni's converter writes blk.N.ffn_router, ffn_gate_exps, ffn_up_exps,
+ * ffn_down_exps (convert/convert_qwen3omni.py:188-219).  The file is mapped
+ * read-only (GGUF v2 / v3); bad or truncated files give MI_MOE_ERR_FORMAT. */
+typedef struct mi_gguf mi_gguf;
+int  mi_gguf_open(mi_gguf **out, const char *path);
+void mi_gguf_close(mi_gguf *gguf);
+/* an integer metadata value (any integer or bool type); MI_MOE_ERR_ARG if absent */
+int  mi_gguf_get_int(const mi_gguf *gguf, const char *key, int64_t *value);
+/* a tensor's ggml type, ne (fastest first, 1-padded) and byte size (0 for
+ * types this library does not read); MI_MOE_ERR_ARG if absent */
+int  mi_gguf_tensor_info(const mi_gguf *gguf, const char *name, int32_t *type, int64_t ne[4],
+                         uint64_t *nbytes);
+/* block `block`'s MoE layer uploaded to the current device in one allocation
+ * (*device_buffer; free it with mi_dev_free when the layer is no longer
+ * used): router (F32), bias if present, expert tables as stored (Q4_K,
+ * Q6_K or F32), K from <general.architecture>.expert_used_count, fused
+ * [h | g] when the block has no ffn_gate_exps.  act: mi_act (the
+ * architecture's choice: moondream3 MI_ACT_GELU_ERF_GP1, qwen3omni
+ * MI_ACT_SILU). */
+int  mi_gguf_load_moe_layer(const mi_gguf *gguf, int32_t block, int32_t act, mi_moe_layer *layer,
+                            void **device_buffer);
 
 /* ---- introspection ---------------------------------------------------------
  * Per-stage timing (HIP events on the call's stream) for the last forward

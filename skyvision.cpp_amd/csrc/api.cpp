@@ -410,6 +410,7 @@ const char *mi_moe_status_string(int s) {
     case MI_MOE_ERR_UNSUPPORTED: return "unsupported";
     case MI_MOE_ERR_DEVICE: return "bad device";
     case MI_MOE_ERR_ARG: return "bad argument";
+    case MI_MOE_ERR_FORMAT: return "bad or unreadable file";
     default: return "unknown";
     }
 }

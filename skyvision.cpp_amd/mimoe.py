@@ -117,6 +117,11 @@ SYMBOLS = {
     "mi_event_synchronize": ([P], C.c_int),
     "mi_event_elapsed_ms": ([C.POINTER(C.c_float), P, P], C.c_int),
     "mi_last_hip_error": ([], C.c_char_p),
+    "mi_gguf_open": ([C.POINTER(P), C.c_char_p], C.c_int),
+    "mi_gguf_close": ([P], None),
+    "mi_gguf_get_int": ([P, C.c_char_p, C.POINTER(i64)], C.c_int),
+    "mi_gguf_tensor_info": ([P, C.c_char_p, C.POINTER(C.c_int32), C.POINTER(i64), C.POINTER(C.c_uint64)], C.c_int),
+    "mi_gguf_load_moe_layer": ([P, C.c_int32, C.c_int32, C.POINTER(Layer), C.POINTER(P)], C.c_int),
     "mi_stream_begin_capture": ([P], C.c_int),
     "mi_stream_end_capture": ([P, C.POINTER(P)], C.c_int),
     "mi_graph_launch": ([P, P], C.c_int),
@@ -233,6 +238,7 @@ def tensor(buf, type_: int, ne, nb=None, offset: int = 0) -> Tensor:
         nb = [nb0, nb1, nb1 * ne[1], nb1 * ne[1] * ne[2]]
     t = Tensor()
     t.data = P((buf.addr if isinstance(buf, DeviceBuffer) else int(buf)) + offset)
+    t._buf = buf   # a DeviceBuffer stays alive as long as the descriptor
     t.type = type_
     for i in range(4):
         t.ne[i] = int(ne[i])
@@ -327,6 +333,35 @@ def _addr(x):
     return P(int(x))
 
 
+class Gguf:
+    """A GGUF file opened by the library (mi_gguf_*)."""
+
+    def __init__(self, path: str):
+        self.h = P()
+        check("mi_gguf_open", load().mi_gguf_open(C.byref(self.h), str(path).encode()))
+
+    def get_int(self, key: str):
+        v = i64()
+        rc = load().mi_gguf_get_int(self.h, key.encode(), C.byref(v))
+        return None if rc else v.value
+
+    def tensor_info(self, name: str):
+        t, ne, nb = C.c_int32(), (i64 * 4)(), C.c_uint64()
+        rc = load().mi_gguf_tensor_info(self.h, name.encode(), C.byref(t), ne, C.byref(nb))
+        return None if rc else (t.value, list(ne), nb.value)
+
+    def load_moe_layer(self, block: int, act: int):
+        """(Layer, device buffer address); free the buffer with mi_dev_free."""
+        L, buf = Layer(), P()
+        check("mi_gguf_load_moe_layer", load().mi_gguf_load_moe_layer(self.h, block, act, C.byref(L), C.byref(buf)))
+        return L, buf
+
+    def close(self) -> None:
+        if self.h:
+            load().mi_gguf_close(self.h)
+            self.h = P()
+
+
 class Stream:
     def __init__(self):
         self.h = P()
@@ -397,4 +432,5 @@ def make_layer(D: int, E: int, K: int, I: int, router_w, router_b, gate: Tensor,
     L.fused_gate_up = int(fused)
     L.act = act
     L.gating = GATING_SOFTMAX_TOPK
+    L._refs = (router_w, router_b, gate, up, down)   # device memory the descriptor points to
     return L

@@ -1,0 +1,173 @@
+"""GGUF expert-tensor loader (mi_gguf_*; csrc/gguf.cpp).
+
+The files are written here by a small GGUF v3 writer (magic, version, counts,
+metadata, tensor infos, aligned data), in the two layouts the reference's
+converters produce: moondream3 (blk.N.ffn_gate_inp.{weight F16, bias},
+fused [h | g] ffn_up_exps Q4_K, ffn_down_exps Q6_K; convert_hf_to_gguf.py:
+173-183, moondream.cpp:149-172, 241-251) and qwen3omni (blk.N.ffn_router F32,
+ffn_gate_exps / ffn_up_exps / ffn_down_exps; convert_qwen3omni.py:188-219).
+CPU: parsing, metadata, tensor infos and every malformed-file error (no
+device).  GPU: a loaded layer's forward is bit-identical to the forward of
+the same tables uploaded directly.
+"""
+import pathlib
+import struct
+
+import numpy as np
+import pytest
+
+import mimoe as M
+import pyoracle as O
+
+GV_U32, GV_F32, GV_STR, GV_ARR = 4, 6, 8, 9
+
+
+def _s(x: str) -> bytes:
+    b = x.encode()
+    return struct.pack("<Q", len(b)) + b
+
+
+def write_gguf(path, kv, tensors, alignment=32, version=3, magic=b"GGUF"):
+    """kv: [(key, gguf type, value)]; tensors: [(name, ggml type, ne, bytes)]."""
+    out = bytearray(magic + struct.pack("<I", version) + struct.pack("<QQ", len(tensors), len(kv)))
+    for key, t, v in kv:
+        out += _s(key) + struct.pack("<I", t)
+        if t == GV_STR:
+            out += _s(v)
+        elif t == GV_U32:
+            out += struct.pack("<I", v)
+        elif t == GV_F32:
+            out += struct.pack("<f", v)
+        elif t == GV_ARR:   # (element type, values) - u32 elements here
+            out += struct.pack("<IQ", GV_U32, len(v)) + b"".join(struct.pack("<I", e) for e in v)
+    off = 0
+    offs = []
+    for name, typ, ne, data in tensors:
+        offs.append(off)
+        out += _s(name) + struct.pack("<I", len(ne)) + b"".join(struct.pack("<Q", n) for n in ne)
+        out += struct.pack("<IQ", typ, off)
+        off += (len(data) + alignment - 1) // alignment * alignment
+    out += b"\0" * ((-len(out)) % alignment)
+    for (name, typ, ne, data), o in zip(tensors, offs):
+        out += data + b"\0" * ((-len(data)) % alignment)
+    pathlib.Path(path).write_bytes(bytes(out))
+
+
+D, E, K, I = 512, 8, 2, 256
+
+
+def _tables(seed, fused):
+    rng = np.random.default_rng(seed)
+    w = lambda *s: (rng.standard_normal(s) * 0.02).astype(np.float32)
+    router = w(E, D)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    t = {}
+    if fused:
+        t["up"] = O.quantize(O.TYPE_Q4_K, w(E * 2 * I, D)).tobytes()
+    else:
+        t["gate"] = O.quantize(O.TYPE_Q4_K, w(E * I, D)).tobytes()
+        t["up"] = O.quantize(O.TYPE_Q4_K, w(E * I, D)).tobytes()
+    t["down"] = O.quantize(O.TYPE_Q6_K if fused else O.TYPE_Q4_K, w(E * D, I)).tobytes()
+    return router, bias, t
+
+
+def moondream_file(path, seed=1, alignment=32):
+    router, bias, t = _tables(seed, True)
+    r16 = router.astype(np.float16)
+    kv = [("general.architecture", GV_STR, "moondream"), ("moondream.expert_used_count", GV_U32, K),
+          ("general.alignment", GV_U32, alignment), ("moondream.some_list", GV_ARR, [1, 2, 3]),
+          ("moondream.norm_eps", GV_F32, 1e-5)]
+    tensors = [("blk.3.ffn_gate_inp.weight", M.TYPE_F16, [D, E], r16.tobytes()),
+               ("blk.3.ffn_gate_inp.bias", M.TYPE_F32, [E], bias.tobytes()),
+               ("blk.3.ffn_up_exps.weight", M.TYPE_Q4_K, [D, 2 * I, E], t["up"]),
+               ("blk.3.ffn_down_exps.weight", M.TYPE_Q6_K, [I, D, E], t["down"])]
+    write_gguf(path, kv, tensors, alignment=alignment)
+    return r16.astype(np.float32), bias, t
+
+
+def qwen_file(path, seed=2):
+    router, _, t = _tables(seed, False)
+    kv = [("general.architecture", GV_STR, "qwen3omni"), ("qwen3omni.expert_used_count", GV_U32, K)]
+    tensors = [("blk.0.ffn_router.weight", M.TYPE_F32, [D, E], router.tobytes()),
+               ("blk.0.ffn_gate_exps.weight", M.TYPE_Q4_K, [D, I, E], t["gate"]),
+               ("blk.0.ffn_up_exps.weight", M.TYPE_Q4_K, [D, I, E], t["up"]),
+               ("blk.0.ffn_down_exps.weight", M.TYPE_Q4_K, [I, D, E], t["down"])]
+    write_gguf(path, kv, tensors)
+    return router, t
+
+
+def test_gguf_parse(tmp_path):
+    p = tmp_path / "md.gguf"
+    moondream_file(p, alignment=64)
+    g = M.Gguf(p)
+    assert g.get_int("moondream.expert_used_count") == K
+    assert g.get_int("general.alignment") == 64
+    assert g.get_int("moondream.norm_eps") is None       # a float: not an integer key
+    assert g.get_int("absent") is None
+    t, ne, nb = g.tensor_info("blk.3.ffn_up_exps.weight")
+    assert (t, ne, nb) == (M.TYPE_Q4_K, [D, 2 * I, E, 1], E * 2 * I * (D // 256) * 144)
+    t, ne, nb = g.tensor_info("blk.3.ffn_gate_inp.weight")
+    assert (t, ne, nb) == (M.TYPE_F16, [D, E, 1, 1], D * E * 2)
+    assert g.tensor_info("blk.3.ffn_gate_exps.weight") is None
+    g.close()
+
+
+def test_gguf_bad_files(tmp_path):
+    lib = M.load()
+    h = M.P()
+    assert lib.mi_gguf_open(M.C.byref(h), str(tmp_path / "missing.gguf").encode()) == -9
+    good = tmp_path / "md.gguf"
+    moondream_file(good)
+    raw = good.read_bytes()
+    cases = {
+        "magic": b"GGUX" + raw[4:],
+        "version": raw[:4] + struct.pack("<I", 1) + raw[8:],
+        "truncated infos": raw[:200],
+        "data past end": raw[:-4096],
+    }
+    for name, data in cases.items():
+        p = tmp_path / f"bad_{name.replace(' ', '_')}.gguf"
+        p.write_bytes(data)
+        assert lib.mi_gguf_open(M.C.byref(h), str(p).encode()) == -9, name
+    assert lib.mi_gguf_open(M.C.byref(h), None) == -1
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("style", ["moondream", "qwen3omni"])
+def test_gguf_layer_forward(tmp_path, style):
+    ctx = M.Context(0)
+    T = 300
+    ctx.reserve(T, D, I, E, K)
+    p = tmp_path / f"{style}.gguf"
+    if style == "moondream":
+        router, bias, t = moondream_file(p)
+        blk, act, fused = 3, M.ACT_GELU_ERF_GP1, True
+    else:
+        router, t = qwen_file(p)
+        bias, blk, act, fused = None, 0, M.ACT_SILU, False
+    g = M.Gguf(p)
+    L, buf = g.load_moe_layer(blk, act)
+    assert (L.n_embd, L.n_expert, L.n_expert_used, L.n_ff, L.fused_gate_up) == (D, E, K, I, int(fused))
+    # the same tables uploaded directly
+    rd = M.to_device(router)
+    bd = M.to_device(bias) if bias is not None else None
+    dn_type = M.TYPE_Q6_K if fused else M.TYPE_Q4_K
+    keep = {k: M.to_device(np.frombuffer(v, np.uint8)) for k, v in t.items()}   # alive through the forwards
+    down = M.tensor(keep["down"], dn_type, [I, D, E])
+    if fused:
+        gate = M.tensor(keep["up"], M.TYPE_Q4_K, [D, 2 * I, E])
+        up = None
+    else:
+        gate = M.tensor(keep["gate"], M.TYPE_Q4_K, [D, I, E])
+        up = M.tensor(keep["up"], M.TYPE_Q4_K, [D, I, E])
+    Ld = M.make_layer(D, E, K, I, rd, bd, gate, up, down, fused, act)
+    x = np.random.default_rng(5).standard_normal((T, D)).astype(np.float32)
+    xd = M.to_device(x)
+    o1, o2 = M.DeviceBuffer(4 * T * D), M.DeviceBuffer(4 * T * D)
+    M.check("forward gguf", ctx.forward(L, xd, T, xd, o1))
+    M.check("forward direct", ctx.forward(Ld, xd, T, xd, o2))
+    a, b = o1.download(np.float32, (T, D)), o2.download(np.float32, (T, D))
+    assert np.isfinite(a).all() and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    M.check("free", M.load().mi_dev_free(buf))
+    g.close()
+    ctx.close()

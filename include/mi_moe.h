@@ -59,7 +59,13 @@ typedef enum {                     /* activation between the two expert products
 
 typedef enum {
     MI_GATING_SOFTMAX_TOPK = 0,    /* top_k on logits, softmax over the K selected
-                                      (moondream.cpp:510-516, qwen3omni_model.cpp:759-766) */
+                                      (moondream.cpp:510-516, qwen3omni_model.cpp:759-766);
+                                      times expert_scale[e] when set: diffusiongemma's
+                                      softmax -> top_k -> renorm x per-expert scale
+                                      (diffusiongemma_model.cpp:923-937) */
+    MI_GATING_SIGMOID_BIAS = 1,    /* s = sigmoid(logit); top_k on s + sel_bias[e] (selection
+                                      only); w = s / (sum_K s + gate_eps) * routed_scaling
+                                      [* expert_scale[e]] (nemotronomni_model.cpp:344-354) */
 } mi_gating;
 
 /* ggml_tensor stand-in: data on the device, ne fastest-first, nb in bytes. */
@@ -87,6 +93,10 @@ typedef struct {
     int32_t fused_gate_up;
     int32_t act;                   /* mi_act */
     int32_t gating;                /* mi_gating */
+    const float *sel_bias;         /* F32 [E] or NULL: MI_GATING_SIGMOID_BIAS selection bias */
+    const float *expert_scale;     /* F32 [E] or NULL: per-expert factor on the weights */
+    float routed_scaling;          /* MI_GATING_SIGMOID_BIAS: weight scale (0 is read as 1) */
+    float gate_eps;                /* MI_GATING_SIGMOID_BIAS: added to the weight sum */
 } mi_moe_layer;
 
 /* Optional routing outputs of mi_moe_forward (device pointers, any may be

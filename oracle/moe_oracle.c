@@ -762,6 +762,50 @@ void orc_softmax_selected(const float *logits, const int32_t *sel,
     }
 }
 
+/* Router gating variants (kind 0: top-k on logits + softmax over the K;
+ * kind 1: nemotronomni_model.cpp:344-354 - s = sigmoid(logit), top-k on
+ * s + sel_bias, w = s / (sum s + eps) * scaling); expert_scale multiplies the
+ * weights (diffusiongemma_model.cpp:932-936).  The sigmoid is evaluated in
+ * double and rounded once to float (the restatement's choice, so rankings do
+ * not depend on a float exp's last bit; ggml's ggml_sigmoid is float); the
+ * weight sum is a double sum in slot order, rounded to float before eps is
+ * added; ties rank the lower id first (strict > in the repeated selection). */
+static float orc_sigmoid(float x) { return (float)(1.0 / (1.0 + exp(-(double)x))); }
+
+void orc_route_gated(const float *logits, int64_t T, int E, int K, int kind, const float *sel_bias,
+                     const float *expert_scale, float scaling, float eps, int32_t *sel, float *w) {
+    for (int64_t t = 0; t < T; t++) {
+        const float *l = logits + t * E;
+        int32_t *s = sel + t * K;
+        float score[1024];
+        for (int e = 0; e < E; e++)
+            score[e] = kind == 1 ? orc_sigmoid(l[e]) + (sel_bias ? sel_bias[e] : 0.f) : l[e];
+        for (int k = 0; k < K; k++) {
+            int best = -1;
+            for (int e = 0; e < E; e++) {
+                int taken = 0;
+                for (int j = 0; j < k; j++) if (s[j] == e) { taken = 1; break; }
+                if (taken) continue;
+                if (best < 0 || score[e] > score[best]) best = e;
+            }
+            s[k] = best;
+        }
+        if (kind == 1) {
+            float sv[512];
+            double sum = 0.0;
+            for (int k = 0; k < K; k++) {
+                sv[k] = orc_sigmoid(l[s[k]]);
+                sum += (double)sv[k];
+            }
+            for (int k = 0; k < K; k++) w[t * K + k] = sv[k] / ((float)sum + eps) * scaling;
+        } else {
+            orc_softmax_selected(logits + t * E, s, 1, E, K, w + t * K);
+        }
+        if (expert_scale)
+            for (int k = 0; k < K; k++) w[t * K + k] = w[t * K + k] * expert_scale[s[k]];
+    }
+}
+
 void orc_dispatch(const int32_t *sel, int64_t T, int K, int E,
                   int32_t *counts, int32_t *offsets, int32_t *perm) {
     for (int e = 0; e < E; e++) counts[e] = 0;

@@ -144,6 +144,11 @@ void orc_top_k(const float *logits, int64_t T, int E, int K, int32_t *sel);
 /* ggml_get_rows + ggml_soft_max over the K selected logits */
 void orc_softmax_selected(const float *logits, const int32_t *sel,
                           int64_t T, int E, int K, float *w);
+/* router gating variants: kind 0 top-k on logits + softmax over the K, kind 1
+ * sigmoid + selection bias + renorm with eps and scaling; expert_scale (or
+ * NULL) multiplies the weights */
+void orc_route_gated(const float *logits, int64_t T, int E, int K, int kind, const float *sel_bias,
+                     const float *expert_scale, float scaling, float eps, int32_t *sel, float *w);
 /* histogram, exclusive scan, permutation (perm value = t*K + k), lists
  * token-ascending; counts[E], offsets[E+1], perm[T*K] */
 void orc_dispatch(const int32_t *sel, int64_t T, int K, int E,

@@ -73,6 +73,7 @@ def _declare(L: C.CDLL) -> None:
     L.orc_router_logits.argtypes = [P, P, P, i64, C.c_int, C.c_int, P, C.c_int]
     L.orc_top_k.argtypes = [P, i64, C.c_int, C.c_int, P]
     L.orc_softmax_selected.argtypes = [P, P, i64, C.c_int, C.c_int, P]
+    L.orc_route_gated.argtypes = [P, i64, C.c_int, C.c_int, C.c_int, P, P, C.c_float, C.c_float, P, P]
     L.orc_dispatch.argtypes = [P, i64, C.c_int, C.c_int, P, P, P]
     L.orc_mul_mat_id.argtypes = [C.c_int, P, i64, i64, C.c_int, P, C.c_int, P, C.c_int, i64, P,
                                  C.c_int, C.c_int]
@@ -198,6 +199,19 @@ def softmax_selected(logits: np.ndarray, sel: np.ndarray) -> np.ndarray:
     w = np.zeros((T, K), dtype=np.float32)
     lib().orc_softmax_selected(_p(logits), _p(sel), T, E, K, _p(w))
     return w
+
+
+def route_gated(logits: np.ndarray, K: int, kind: int, sel_bias=None, expert_scale=None, scaling: float = 1.0,
+                eps: float = 0.0):
+    """Router gating variants (moe_oracle.c orc_route_gated): (sel, w)."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    T, E = logits.shape
+    sel = np.zeros((T, K), dtype=np.int32)
+    w = np.zeros((T, K), dtype=np.float32)
+    sb = None if sel_bias is None else np.ascontiguousarray(sel_bias, dtype=np.float32)
+    es = None if expert_scale is None else np.ascontiguousarray(expert_scale, dtype=np.float32)
+    lib().orc_route_gated(_p(logits), T, E, K, kind, _p(sb), _p(es), scaling, eps, _p(sel), _p(w))
+    return sel, w
 
 
 def dispatch(sel: np.ndarray, E: int):

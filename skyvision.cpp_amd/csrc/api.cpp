@@ -19,6 +19,7 @@
 #include "../../include/mi_moe_util.h"
 #include "common.hpp"
 #include "launch.hpp"
+#include "wave_ops.hpp"
 
 namespace mimoe {
 int launch_mm_id_f32(const GemvArgs &g, const float *b, int64_t ldb, hipStream_t st);
@@ -168,7 +169,7 @@ int validate_layer(const mi_moe_ctx *c, const mi_moe_layer *L, bool need_router)
     if (D <= 0 || E <= 0 || K <= 0 || I <= 0 || K > E) return MI_MOE_ERR_SHAPE;
     if (E > 256 || K > 64) return MI_MOE_ERR_UNSUPPORTED;
     if (L->act < MI_ACT_SILU || L->act > MI_ACT_GELU_ERF) return MI_MOE_ERR_ARG;
-    if (L->gating != MI_GATING_SOFTMAX_TOPK) return MI_MOE_ERR_ARG;
+    if (L->gating != MI_GATING_SOFTMAX_TOPK && L->gating != MI_GATING_SIGMOID_BIAS) return MI_MOE_ERR_ARG;
     if (need_router && !L->router_w) return MI_MOE_ERR_NULL;
     const int64_t Ng = L->fused_gate_up ? 2 * I : I;
     TRY(check_table(L->gate, D, Ng, E));
@@ -190,6 +191,8 @@ bool plan_decode1(const mi_moe_ctx *c, const mi_moe_layer *L, const float *x, in
     const int64_t D = L->n_embd, E = L->n_expert, K = L->n_expert_used, I = L->n_ff;
     const int G = c->dec_grid;
     if (!c->fused_decode || G <= 0) return false;
+    // the fused kernel ranks and weights with the default gating only
+    if (L->gating != MI_GATING_SOFTMAX_TOPK || L->expert_scale) return false;
     if (L->gate.type != MI_TYPE_Q4_K || (!L->fused_gate_up && L->up.type != MI_TYPE_Q4_K)) return false;
     if (L->down.type != MI_TYPE_Q4_K && L->down.type != MI_TYPE_Q6_K) return false;
     if (D % QK || I % QK || K > 8 || E > 256) return false;
@@ -603,7 +606,13 @@ int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T
         if (rc == -6) TRY(launch_router(L->router_w, L->router_b, x, D, T, D, E, c->logits, st));
         else TRY(rc);
         stage_end(c, "router", st);
-        TRY(launch_topk_softmax(c->logits, E, T, E, K, c->sel, K, c->w, st));
+        Gating gt;
+        gt.kind = L->gating == MI_GATING_SIGMOID_BIAS ? 1 : 0;
+        gt.sel_bias = L->sel_bias;
+        gt.expert_scale = L->expert_scale;
+        gt.scaling = L->routed_scaling != 0.f ? L->routed_scaling : 1.f;
+        gt.eps = L->gate_eps;
+        TRY(launch_topk_softmax(c->logits, E, T, E, K, c->sel, K, c->w, st, gt));
         stage_end(c, "topk_softmax", st);
         TRY(run_experts(c, L, x, T, c->sel, c->sel, c->w, res, out, st, xq && rc == 0));
     }
@@ -690,7 +699,7 @@ int mi_top_k(mi_moe_ctx *c, const mi_tensor *a, int32_t k, mi_tensor *dst, mi_st
     if (T == 0) return MI_MOE_OK;
     HIP_TRY(hipSetDevice(c->device));
     return launch_topk_softmax((const float *)a->data, (int64_t)(a->nb[1] / 4), T, (int)E, k, (int32_t *)dst->data,
-                               (int64_t)(dst->nb[1] / 4), nullptr, (hipStream_t)stream);
+                               (int64_t)(dst->nb[1] / 4), nullptr, (hipStream_t)stream, Gating{});
 }
 
 int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const mi_tensor *ids, mi_tensor *dst,

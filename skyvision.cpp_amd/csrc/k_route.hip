@@ -421,7 +421,7 @@ int launch_router(const float *W, const float *b, const float *x, int64_t ldx, i
 // slot order, scale by (float)(1.0 / sum) - the ggml_soft_max order.
 __global__ void __launch_bounds__(256) k_topk_softmax(const float *__restrict__ logits, int64_t ldl, int64_t T,
                                                       int E, int K, int32_t *__restrict__ sel, int64_t lds,
-                                                      float *__restrict__ w) {
+                                                      float *__restrict__ w, Gating gt) {
     __shared__ __attribute__((aligned(16))) float s_v[4][64 * TOPK_MAX_PER_LANE];
     __shared__ int s_sel[4][64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -429,7 +429,7 @@ __global__ void __launch_bounds__(256) k_topk_softmax(const float *__restrict__ 
     if (t >= T) return;   // whole waves; the routine synchronizes only its own wave
     int mysel;
     float myw;
-    topk_softmax_wave(logits + t * ldl, E, K, lane, s_v[wave], s_sel[wave], mysel, myw, w != nullptr);
+    topk_softmax_wave(logits + t * ldl, E, K, lane, s_v[wave], s_sel[wave], mysel, myw, w != nullptr, gt);
     if (lane < K) {
         sel[t * lds + lane] = mysel;
         if (w) w[t * K + lane] = myw;
@@ -437,11 +437,12 @@ __global__ void __launch_bounds__(256) k_topk_softmax(const float *__restrict__ 
 }
 
 int launch_topk_softmax(const float *logits, int64_t ld_logits, int64_t T, int E, int K, int32_t *sel,
-                        int64_t ld_sel, float *w, hipStream_t st) {
+                        int64_t ld_sel, float *w, hipStream_t st, const Gating &gt) {
     if (T <= 0) return 0;
     if (E > 64 * TOPK_MAX_PER_LANE || K > 64 || K > E || K <= 0) return -6;
+    if (gt.kind != 0 && gt.kind != 1) return -6;
     hipLaunchKernelGGL(k_topk_softmax, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, logits, ld_logits, T, E,
-                       K, sel, ld_sel, w);
+                       K, sel, ld_sel, w, gt);
     return hip_check_launch();
 }
 

@@ -46,8 +46,9 @@ int launch_front(const float *W, const float *b, const float *x, int64_t ldx, in
                  float *logits, const Q8Out *qx, hipStream_t st);
 // top-k (descending, ties -> lower id) and softmax over the selected logits;
 // w may be NULL (op-level top_k)
+struct Gating;
 int launch_topk_softmax(const float *logits, int64_t ld_logits, int64_t T, int E, int K, int32_t *sel,
-                        int64_t ld_sel, float *w, hipStream_t st);
+                        int64_t ld_sel, float *w, hipStream_t st, const Gating &gt);
 
 struct Dispatch {
     int32_t *counts;     // [E]

@@ -225,14 +225,35 @@ __device__ inline void wave_lds_sync() {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
+// Router gating variants (the layer's mi_gating): kind 0 ranks the logits
+// and takes the softmax over the K selected; kind 1 ranks s + sel_bias[e]
+// with s = fl32(1 / (1 + exp(-logit))) evaluated in fp64 (one rounding, so
+// every implementation ranks the same values) and weights s / (fl32(sum_K
+// s in fp64, slot order) + eps) * scaling; expert_scale[e] multiplies the
+// weights of either kind.
+struct Gating {
+    int kind = 0;
+    const float *sel_bias = nullptr;
+    const float *expert_scale = nullptr;
+    float scaling = 1.f;
+    float eps = 0.f;
+};
+
+__device__ inline float gating_sigmoid(float x) { return (float)(1.0 / (1.0 + exp(-(double)x))); }
+
 __device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane, float *sv, int *ssel, int &mysel,
-                                         float &myw, bool want_w) {
+                                         float &myw, bool want_w, const Gating &gt = Gating{}) {
     const int nper = (E + 63) >> 6, E4 = (E + 3) & ~3;
     float v[TOPK_MAX_PER_LANE];
 #pragma unroll
     for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
         const int e = lane + 64 * i;
-        v[i] = e < E ? l[e] : -INFINITY;
+        if (e < E) {
+            v[i] = l[e];
+            if (gt.kind == 1) v[i] = gating_sigmoid(v[i]) + (gt.sel_bias ? gt.sel_bias[e] : 0.f);
+        } else {
+            v[i] = -INFINITY;
+        }
         if (e < E4) sv[e] = v[i];
     }
     wave_lds_sync();
@@ -255,8 +276,20 @@ __device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane,
     }
     wave_lds_sync();
     mysel = lane < K ? ssel[lane] : 0;
-    const float myval = lane < K ? sv[mysel] : 0.f;
-    myw = want_w ? softmax_selected_wave(myval, K, lane) : 0.f;
+    if (!want_w) {
+        myw = 0.f;
+        return;
+    }
+    if (gt.kind == 1) {
+        const float s = lane < K ? gating_sigmoid(l[mysel]) : 0.f;
+        double sum = 0.0;
+        for (int k = 0; k < K; ++k) sum = sum + (double)__shfl(s, k, 64);
+        myw = s / ((float)sum + gt.eps) * gt.scaling;
+    } else {
+        const float myval = lane < K ? sv[mysel] : 0.f;
+        myw = softmax_selected_wave(myval, K, lane);
+    }
+    if (gt.expert_scale && lane < K) myw = myw * gt.expert_scale[mysel];
 }
 
 }  // namespace mimoe

@@ -19,7 +19,7 @@ DECODE_CHAIN, DECODE_FUSED_COOPERATIVE, DECODE_FUSED_EXCLUSIVE = 0, 1, 2
 TYPE_F32, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K, TYPE_I32 = 0, 1, 12, 14, 26
 ACT_SILU, ACT_GELU_ERF_GP1, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2, 3
 NORM_NONE, NORM_RMS, NORM_LAYER = 0, 1, 2
-GATING_SOFTMAX_TOPK = 0
+GATING_SOFTMAX_TOPK, GATING_SIGMOID_BIAS = 0, 1
 QK_K = 256
 BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210}
 STATUS = {0: "ok", -1: "null", -2: "shape", -3: "type", -4: "capacity", -5: "hip",
@@ -49,7 +49,8 @@ class Tensor(C.Structure):
 class Layer(C.Structure):
     _fields_ = [("n_embd", i32), ("n_expert", i32), ("n_expert_used", i32), ("n_ff", i32),
                 ("router_w", P), ("router_b", P), ("gate", Tensor), ("up", Tensor),
-                ("down", Tensor), ("fused_gate_up", i32), ("act", i32), ("gating", i32)]
+                ("down", Tensor), ("fused_gate_up", i32), ("act", i32), ("gating", i32),
+                ("sel_bias", P), ("expert_scale", P), ("routed_scaling", C.c_float), ("gate_eps", C.c_float)]
 
 
 class Norm(C.Structure):

@@ -214,3 +214,38 @@ def test_forward_routing_shapes(D, E, K):
         assert np.allclose(gw, O.softmax_selected(ref_l, ref_s), rtol=1e-6, atol=1e-7), f"weights T={T}"
     log(f"routing D={D} E={E} K={K}: T 1..600 bit-exact")
     ctx.close()
+
+
+@pytest.mark.parametrize("kind", [M.GATING_SOFTMAX_TOPK, M.GATING_SIGMOID_BIAS])
+def test_gating_variants(kind):
+    """Router gating variants in the forward (the top-k kernel; the fused
+    single-token kernel declines them, so T = 1 runs the chain) against the
+    oracle on the forward's own logits: ids bit-exact, weights within 1e-6.
+    kind 0 with a per-expert scale (diffusiongemma's renorm x scale), kind 1
+    with a selection bias, routed scaling 2.5 and an eps (nemotronomni)."""
+    spec = W.CONFIGS[1]["spec"]
+    ctx = M.Context(0)
+    ctx.reserve(300, spec.D, spec.I, spec.E, spec.K)
+    g = W.GpuLayer(ctx, spec)
+    rng = np.random.default_rng(77 + kind)
+    bias = (rng.standard_normal(spec.E) * 0.05).astype(np.float32)
+    scale = (0.5 + rng.random(spec.E)).astype(np.float32)
+    bd, sd = M.to_device(bias), M.to_device(scale)
+    L = g.layer
+    L.gating = kind
+    L.expert_scale = sd.addr
+    if kind == M.GATING_SIGMOID_BIAS:
+        L.sel_bias, L.routed_scaling, L.gate_eps = bd.addr, 2.5, 1e-3
+    for T in [1, 17, 300]:
+        xd = M.to_device(cpu_x(spec, T))
+        out = M.DeviceBuffer(4 * T * spec.D)
+        bufs, r = _routing_buffers(T, spec.E, spec.K)
+        M.check("forward", ctx.forward(L, xd, T, None, out, r))
+        lg = bufs["logits"].download(np.float32, (T, spec.E))
+        sel, w = O.route_gated(lg, spec.K, kind, sel_bias=bias if kind else None, expert_scale=scale,
+                               scaling=2.5 if kind else 1.0, eps=1e-3 if kind else 0.0)
+        assert np.array_equal(bufs["sel"].download(np.int32, (T, spec.K)), sel), f"ids T={T}"
+        assert np.allclose(bufs["weights"].download(np.float32, (T, spec.K)), w, rtol=1e-6, atol=1e-7), f"w T={T}"
+        assert np.isfinite(out.download(np.float32, (T, spec.D))).all()
+    log(f"gating kind {kind}: T 1, 17, 300 ids bit-exact, weights within 1e-6")
+    ctx.close()

@@ -197,3 +197,44 @@ def test_layer_matches_fp64_composition():
     # measured 1.9e-7 (fp32 vs fp64 summation); one Q8_K rounding flip of an
     # activation would already cost ~1e-4, a wrong term far more
     assert rel < 1e-5, rel
+
+
+# ------------------------------------------------------------------ gating variants
+def test_route_gated_hand_case():
+    """nemotronomni gating (sigmoid, selection bias, renorm x scaling) and the
+    per-expert scale on a case worked by hand."""
+    l = np.array([[0.0, 1.0, -1.0, 2.0]], np.float32)
+    sel, w = O.route_gated(l, 2, 1, sel_bias=np.array([0, 0, 5, 0], np.float32), scaling=2.5)
+    assert sel.tolist() == [[2, 3]]   # sig(-1) + 5 first, then sig(2) = 0.881 over sig(1) = 0.731
+    s = 1 / (1 + np.exp(-np.array([-1.0, 2.0])))
+    assert np.allclose(w[0], s / s.sum() * 2.5, rtol=1e-6)
+    sel, w = O.route_gated(l, 2, 0, expert_scale=np.array([1, 2, 3, 4], np.float32))
+    assert sel.tolist() == [[3, 1]]
+    p = np.exp([2.0, 1.0]) / np.exp([2.0, 1.0]).sum()
+    assert np.allclose(w[0], p * [4, 2], rtol=1e-6)
+
+
+def test_route_gated_properties():
+    rng = np.random.default_rng(3)
+    T, E, K = 200, 64, 8
+    l = (rng.standard_normal((T, E)) * 2).astype(np.float32)
+    b = (rng.standard_normal(E) * 0.5).astype(np.float32)
+    sc = (1 + rng.random(E)).astype(np.float32)
+    # kind 1: the ranking is that of fp64 sigmoid + bias (distinct values here)
+    sel, w = O.route_gated(l, K, 1, sel_bias=b, scaling=2.5, eps=0.0)
+    score = (1 / (1 + np.exp(-l.astype(np.float64)))).astype(np.float32) + b
+    ref = np.argsort(-score.astype(np.float64), axis=1, kind="stable")[:, :K]
+    assert np.array_equal(sel, ref)
+    assert np.allclose(w.astype(np.float64).sum(axis=1), 2.5, rtol=2e-6)
+    # kind 1 without a bias selects the top-k logits (sigmoid is monotonic)
+    sel0, _ = O.route_gated(l, K, 1)
+    assert np.array_equal(sel0, O.top_k(l, K))
+    # eps enters the denominator once
+    _, we = O.route_gated(l, K, 1, sel_bias=b, scaling=1.0, eps=0.5)
+    s_sel = (1 / (1 + np.exp(-np.take_along_axis(l, sel, 1).astype(np.float64))))
+    assert np.allclose(we, s_sel / (s_sel.sum(axis=1, keepdims=True) + 0.5), rtol=2e-6)
+    # kind 0 with a per-expert scale: the default weights times scale[sel], exactly
+    s0, w0 = O.route_gated(l, K, 0, expert_scale=sc)
+    assert np.array_equal(s0, O.top_k(l, K))
+    wd = O.softmax_selected(l, s0)
+    assert np.array_equal(w0, (wd * sc[s0]).astype(np.float32))

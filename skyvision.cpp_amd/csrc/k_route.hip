@@ -574,23 +574,34 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
             dispatch_stage(ids + c0, m, sid, tid);
             __syncthreads();
         }
-        for (int r0 = 0; r0 < m; r0 += DISPATCH_THREADS) {
-            const int i = r0 + tid;
-            const bool hit = i < m && sid[i] == me;
-            const uint64_t mask = __ballot(hit);
-            if (lane == 0) wsum[wave] = __popcll(mask);
-            __syncthreads();
-            int before = 0, total = 0;
-#pragma unroll
-            for (int w = 0; w < DISPATCH_WAVES; ++w) {
-                const int v = wsum[w];
-                before += w < wave ? v : 0;
-                total += v;
-            }
-            if (hit) d.perm[run + before + __popcll(mask & ((1ull << lane) - 1ull))] = (int32_t)(c0 + i);
-            run += total;
-            __syncthreads();   // wsum is rewritten next round
+        // wave w takes the contiguous ids [w0, w1): counts its hits, meets the
+        // other waves once for the prefix, then writes them in order
+        const int span = ((m + DISPATCH_WAVES - 1) / DISPATCH_WAVES + 63) & ~63;
+        const int w0 = wave * span, w1 = w0 + span < m ? w0 + span : m;
+        int mine = 0;
+        for (int i0 = w0; i0 < w1; i0 += 64) {
+            const int i = i0 + lane;
+            mine += __popcll(__ballot(i < w1 && sid[i] == me));
         }
+        if (lane == 0) wsum[wave] = mine;
+        __syncthreads();
+        int before = 0, total = 0;
+#pragma unroll
+        for (int w = 0; w < DISPATCH_WAVES; ++w) {
+            const int v = wsum[w];
+            before += w < wave ? v : 0;
+            total += v;
+        }
+        int pos = run + before;
+        for (int i0 = w0; i0 < w1; i0 += 64) {
+            const int i = i0 + lane;
+            const bool hit = i < w1 && sid[i] == me;
+            const uint64_t mask = __ballot(hit);
+            if (hit) d.perm[pos + __popcll(mask & ((1ull << lane) - 1ull))] = (int32_t)(c0 + i);
+            pos += __popcll(mask);
+        }
+        run += total;
+        __syncthreads();   // wsum (and sid) are rewritten for the next chunk
     }
 }
 

@@ -515,13 +515,27 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
         psc[tid] = !balanced && cnt[tid] % BM > 0 ? 1 : 0;
     }
     __syncthreads();
-    for (int off = 1; off < E; off <<= 1) {        // four inclusive scans at once
-        int a0 = 0, a1 = 0, a2 = 0, a3 = 0;
-        if (tid < E && tid >= off) { a0 = scn[tid - off]; a1 = tsc[tid - off]; a2 = asc[tid - off]; a3 = psc[tid - off]; }
-        __syncthreads();
-        if (tid < E) { scn[tid] += a0; tsc[tid] += a1; asc[tid] += a2; psc[tid] += a3; }
-        __syncthreads();
+    if (wave == 0) {   // four inclusive scans by one wave: lane l holds entries 4 l .. 4 l + 3
+        int *arr[4] = {scn, tsc, asc, psc};
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            int v[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = 4 * lane + j < E ? arr[a][4 * lane + j] : 0;
+            v[1] += v[0]; v[2] += v[1]; v[3] += v[2];
+            int inc = v[3];
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(inc, o, 64);
+                if (lane >= o) inc += y;
+            }
+            const int ex = inc - v[3];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (4 * lane + j < E) arr[a][4 * lane + j] = v[j] + ex;
+        }
     }
+    __syncthreads();
     const int c = cnt[me];
     const int off = scn[me] - c;
     if (tid == 0) {

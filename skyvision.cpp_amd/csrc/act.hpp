@@ -61,9 +61,11 @@ __device__ inline float act_pair_fast(float a, float b) {
     } else if constexpr (ACT == 1) {
         return 0.5f * a * one_plus_erf_fast(a * SQRT_2_INV) * (b + 1.0f);
     } else if constexpr (ACT == 2) {
-        // 1 + tanh(u) = 2 - 2 / (exp(2u) + 1)
-        const float u = SQRT_2_OVER_PI * a * (1.0f + GELU_COEF_A * a * a);
-        return 0.5f * a * (2.0f - 2.0f * rcp_fast(exp_fast(2.0f * u) + 1.0f)) * b;
+        // (1 + tanh(u)) / 2 = 1 / (1 + exp(-2u)): one exp2 with the constants
+        // folded, -2 sqrt(2/pi) log2(e) * a * (1 + c a^2)
+        const float k = -2.0f * SQRT_2_OVER_PI * 1.4426950408889634f;
+        const float e = __builtin_amdgcn_exp2f(k * a * (1.0f + GELU_COEF_A * a * a));
+        return a * b * rcp_fast(1.0f + e);
     } else {
         return 0.5f * a * one_plus_erf_fast(a * SQRT_2_INV) * b;
     }

@@ -20,6 +20,9 @@ TYPE_F32, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K, TYPE_I32 = 0, 1, 12, 14, 26
 ACT_SILU, ACT_GELU_ERF_GP1, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2, 3
 NORM_NONE, NORM_RMS, NORM_LAYER = 0, 1, 2
 GATING_SOFTMAX_TOPK, GATING_SIGMOID_BIAS = 0, 1
+# mi_moe_status
+OK, ERR_NULL, ERR_SHAPE, ERR_TYPE, ERR_CAPACITY, ERR_HIP = 0, -1, -2, -3, -4, -5
+ERR_UNSUPPORTED, ERR_DEVICE, ERR_ARG, ERR_FORMAT = -6, -7, -8, -9
 QK_K = 256
 BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210}
 STATUS = {0: "ok", -1: "null", -2: "shape", -3: "type", -4: "capacity", -5: "hip",

@@ -67,3 +67,13 @@ def test_null_arguments_rejected_without_device(lib):
     # argument checks come before any HIP call
     lib.mi_moe_forward.restype = C.c_int
     assert lib.mi_moe_forward(None, None, None, C.c_int64(1), None, None, None, None) == -1
+
+
+def test_status_codes_match_header():
+    """The binding's status constants are the header's mi_moe_status values."""
+    import mimoe as M
+    text = (ROOT / "include" / "mi_moe.h").read_text()
+    codes = dict(re.findall(r"MI_MOE_(OK|ERR_[A-Z]+)\s*=\s*(-?\d+)", text))
+    assert len(codes) == 10, codes
+    for name, v in codes.items():
+        assert getattr(M, name) == int(v), name

@@ -117,6 +117,40 @@ def test_layer_small(spec, path):
         assert e_rel <= TOL_REL_L2
 
 
+def test_forward_edges():
+    """Edge cases of the forward through the C ABI: an empty batch returns OK
+    and writes nothing; the maximum batch the context reserved (256) matches
+    the oracle to the usual bars; one token more, a negative count, a null
+    input and a layer with K > E are refused with their status codes, again
+    without writing the output."""
+    spec = SMALL[1]
+    ctx, g, cpu = _gpu_layer_and_cpu(spec)
+    cap = 256
+    sentinel = np.full((cap + 1, spec.D), 7.0, np.float32)
+    out = M.DeviceBuffer(4 * (cap + 1) * spec.D).upload(sentinel)
+    x = cpu_x(spec, cap + 1)
+    xd = M.to_device(x)
+    assert ctx.forward(g.layer, xd, 0, None, out) == M.OK
+    assert ctx.forward(g.layer, xd, cap + 1, None, out) == M.ERR_CAPACITY
+    assert ctx.forward(g.layer, xd, -1, None, out) == M.ERR_SHAPE
+    assert ctx.forward(g.layer, None, 5, None, out) == M.ERR_NULL
+    g.layer.n_expert_used = spec.E + 1
+    assert ctx.forward(g.layer, xd, 5, None, out) == M.ERR_SHAPE
+    g.layer.n_expert_used = spec.K
+    assert np.array_equal(out.download(np.float32, (cap + 1, spec.D)), sentinel), "refused calls wrote output"
+    bufs, r = _routing_buffers(cap, spec.E, spec.K)
+    M.check("forward", ctx.forward(g.layer, xd, cap, None, out, r))
+    got = out.download(np.float32, (cap + 1, spec.D))
+    assert np.array_equal(got[cap], sentinel[cap]), "row past T written"
+    ref, dbg = O.moe_forward(oracle_layer_dict(cpu, spec, cpu["router_w"], cpu["router_b"]), x[:cap], None)
+    assert np.array_equal(bufs["sel"].download(np.int32, (cap, spec.K)), dbg["sel"]), "top-k ids"
+    assert np.array_equal(bufs["perm"].download(np.int32, (cap * spec.K,)), dbg["perm"]), "dispatch"
+    e_rel = rel_l2(got[:cap], ref)
+    log(f"edges {spec.name}: T=0 / cap+1 / -1 / null / K>E refused or no-op; T=cap rel-L2 {e_rel:.3e}")
+    assert e_rel <= TOL_REL_L2
+    ctx.close()
+
+
 def test_known_answer_f32_silu():
     """moe_compute.cpp:156-214: D=2, I=3, K=2, F32 SiLU -> [3.6423913, 4.1931758]."""
     ctx = M.Context(0)

@@ -225,7 +225,7 @@ def config3_sweep(copies: int) -> dict:
             f" | touched {touched}, {row['GBs']:.0f} GB/s")
         rows.append(row)
         del xs, out
-    ctx.set_gemm_threshold(16)
+    ctx.set_gemm_threshold(0)
     cross = next((r["tokens"] for r in rows if r["gemm_ms"] < r["gemv_ms"]), None)
     del layers
     ctx.close()

@@ -253,7 +253,9 @@ int  mi_gguf_load_moe_layer(const mi_gguf *gguf, int32_t block, int32_t act, mi_
 int mi_moe_ctx_set_profiling(mi_moe_ctx *ctx, int on);
 int mi_moe_ctx_stage_times(mi_moe_ctx *ctx, int max_stages, const char **names, float *ms,
                            int *n_stages);
-/* path choice for a token count: 0 = grouped GEMV (decode), 1 = grouped MFMA GEMM */
+/* Product path of a call: the grouped MFMA GEMM from min_tokens_for_gemm
+ * tokens on, the grouped GEMV below.  0 (the default) picks by shape: the
+ * GEMM when 4 * T * K >= 5 * E (1.25 dispatched rows per expert). */
 int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *ctx, int64_t min_tokens_for_gemm);
 /* Schedule of single-token calls of mi_moe_forward.  The fused modes run the
  * whole block in one kernel of one work-group per CU that synchronizes

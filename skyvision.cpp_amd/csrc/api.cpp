@@ -5,8 +5,9 @@
 // then enqueues the kernel chain on the caller's stream:
 //   router -> top-k/softmax -> dispatch -> Q8_K(x) -> gate/up (+GLU, +Q8_K)
 //   -> down -> weighted combine (+residual)
-// Decode-sized calls (fewer than gemm_threshold tokens) use the grouped
-// integer-dot GEMV kernels; larger calls use the grouped MFMA GEMM kernels.
+// Decode-sized calls use the grouped integer-dot GEMV kernels, larger calls
+// the grouped MFMA GEMM kernels (use_gemm: by default from 1.25 dispatched
+// rows per expert on average).
 // All workspace comes from mi_moe_ctx_reserve; forward calls never allocate.
 #include <hip/hip_runtime.h>
 
@@ -93,7 +94,7 @@ struct mi_moe_ctx {
     float *f1 = nullptr;      // [rows][max(2I, kmax)]  GLU / F32 scratch
     float *f2 = nullptr;      // [rows][I]
     float *z = nullptr;       // [rows][max(D, 2I)]
-    int64_t gemm_threshold = 16;
+    int64_t gemm_threshold = 0;   // 0: the shape rule of use_gemm
     // single-token fused kernel (k_decode.hip)
     int fused_decode = MI_DECODE_FUSED_COOPERATIVE;
     int dec_grid = 0;          // cooperative grid (one WG per CU), 0: unavailable
@@ -239,10 +240,19 @@ int run_decode1(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, const floa
 // How the expert path consumes x: false for fp32 expert tables, else the
 // Q8_K form it reads (GEMV: codes, scales, block sums; GEMM: fp16 d*q in the
 // gate weight's MFMA K order).
+bool use_gemm(const mi_moe_ctx *c, int64_t T, int K, int E) {
+    // Measured crossover (MI355X, Q4_K tables, 16 rotated layer copies): the
+    // grouped GEMM pays per M-tile, the GEMV per token and row, so the switch
+    // follows the rows per expert T*K/E: qwen3omni (E 128, K 8) GEMV faster up
+    // to T = 20, GEMM from 24; moondream3 (E 64, K 8) GEMV at 8, GEMM from 12.
+    if (c->gemm_threshold > 0) return T >= c->gemm_threshold;
+    return 4 * T * K >= 5 * (int64_t)E;
+}
+
 bool x_q8_spec(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T, Q8Out &qx) {
     const int D = L->n_embd, I = L->n_ff;
     if (!is_kquant(L->gate.type)) return false;
-    const bool gemm = T >= c->gemm_threshold || D > 8 * QK || I > 8 * QK;
+    const bool gemm = use_gemm(c, T, L->n_expert_used, L->n_expert) || D > 8 * QK || I > 8 * QK;
     qx = Q8Out{};
     if (!gemm) {
         qx.q8 = c->ax.q8; qx.d8 = c->ax.d8; qx.bsums = c->ax.bs;
@@ -262,7 +272,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
     const int max_active = (int)std::min<int64_t>(E, rows);
     const bool same_ids = ids_gu == ids_dn;
     const bool kq = is_kquant(L->gate.type);
-    const bool gemm = kq && (T >= c->gemm_threshold || D > 8 * QK || I > 8 * QK);
+    const bool gemm = kq && (use_gemm(c, T, K, E) || D > 8 * QK || I > 8 * QK);
     // GEMM M-tiles: balanced tiles of at most G4_BM rows for the 4-wave GEMMs
     // (Q4_K gate/up), GEMM_BM-row tiles otherwise
     const bool g4 = gemm && L->gate.type == MI_TYPE_Q4_K;
@@ -536,7 +546,7 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
 
 int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *c, int64_t t) {
     if (!c) return MI_MOE_ERR_NULL;
-    if (t < 1) return MI_MOE_ERR_ARG;
+    if (t < 0) return MI_MOE_ERR_ARG;
     c->gemm_threshold = t;
     return MI_MOE_OK;
 }
@@ -741,7 +751,7 @@ int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const 
         a.y = (float *)dst->data; a.ldy = N; a.ncols = N;
         return launch_mm_id_f32(a, bp, Kin, st);
     }
-    const bool gemm = T >= c->gemm_threshold || Kin > 8 * QK;
+    const bool gemm = use_gemm(c, T, (int)n_used, (int)E) || Kin > 8 * QK;
     if (!gemm) {
         Q8Out qx;
         qx.q8 = c->ax.q8; qx.d8 = c->ax.d8; qx.bsums = c->ax.bs;

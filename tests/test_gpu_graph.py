@@ -1,8 +1,8 @@
 """HIP graph capture of the forward.  The C ABI takes a stream, so a serving
 loop may capture mi_moe_forward once and replay it: every replay must give the
 eager forward's bits.  Covered: the prefill path (router + Q8_K of x, top-k,
-dispatch, grouped MFMA GEMMs, Q8_K of the GLU rows, combine), the T < 16 GEMV
-chain, and the single-token fused kernel in its plain-launch mode (its
+dispatch, grouped MFMA GEMMs, Q8_K of the GLU rows, combine), the small-batch
+GEMV chain, and the single-token fused kernel in its plain-launch mode (its
 epoch-tagged logits and monotonic barrier counters carry over between
 replays).  Each replay reads a new input written into the captured buffer,
 with eager forwards and synchronizations between replays, so graph nodes that
@@ -57,10 +57,10 @@ def _graph_vs_eager(ctx, layer, spec, T, res=True):
     s.destroy()
 
 
-@pytest.mark.parametrize("T", [1, 5, 300])
+@pytest.mark.parametrize("T", [1, 4, 300])
 def test_graph_small_layer(T):
-    """Small moondream-shape layer: T = 300 on the GEMM path, T = 5 on the
-    GEMV chain, T = 1 on the chain (the layer is outside the fused kernel's
+    """Small moondream-shape layer: T = 300 on the GEMM path, T = 4 on the
+    GEMV chain (4 T K < 5 E), T = 1 on the chain (the layer is outside the fused kernel's
     shapes or the fused kernel, whichever the planner picks)."""
     spec = small_spec("md_graph", D=512, E=8, K=2, I=256, fused=True, down_type=O.TYPE_Q6_K,
                       act=O.ACT_GELU_TANH, seed=0x5EED3000)

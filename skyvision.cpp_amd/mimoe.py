@@ -259,6 +259,7 @@ class Context:
         call("mi_moe_ctx_reserve", self.h, max_tokens, D, I, E, K)
 
     def set_gemm_threshold(self, t: int) -> None:
+        """GEMM from t tokens on; 0 = by shape (GEMM when 4 T K >= 5 E)."""
         call("mi_moe_ctx_set_gemm_threshold", self.h, t)
 
     def set_fused_decode(self, mode) -> None:

@@ -384,7 +384,9 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the MoE layer is sharded by replicating experts per GPU; see DESIGN.md)",
+              "(across GPUs the layer would shard by experts: each GPU holds E/N experts' "
+              "tables, tokens reach them by an all-to-all, and each GPU runs these same kernels "
+              "on its share)",
               file=sys.stderr)
         return 2
 

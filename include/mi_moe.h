@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MI_MOE_ABI_VERSION 1
+#define MI_MOE_ABI_VERSION 2
 
 /* hipStream_t without pulling in HIP headers */
 typedef struct ihipStream_t *mi_stream_t;
@@ -55,17 +55,23 @@ typedef enum {                     /* activation between the two expert products
     MI_ACT_GELU_TANH     = 2,      /* gelu_tanh(gate)*up                                            */
     MI_ACT_GELU_ERF      = 3,      /* gelu_erf(gate)*up: ggml_mul(ggml_unary(gu, act), up),
                                       moe_compute.cpp:127-129                                       */
+    MI_ACT_RELU_SQR      = 4,      /* relu(u)^2 of ONE product, non-gated experts: ggml_sqr(ggml_relu(
+                                      mul_mat_id(up_exps, x))), nemotronomni_model.cpp:366-367; the
+                                      layer's gate tensor holds ffn_up_exps ne=[D, I, E],
+                                      fused_gate_up must be 0 and up is ignored                     */
 } mi_act;
 
 typedef enum {
     MI_GATING_SOFTMAX_TOPK = 0,    /* top_k on logits, softmax over the K selected
                                       (moondream.cpp:510-516, qwen3omni_model.cpp:759-766);
-                                      times expert_scale[e] when set: diffusiongemma's
-                                      softmax -> top_k -> renorm x per-expert scale
-                                      (diffusiongemma_model.cpp:923-937) */
+                                      times expert_scale[e] when set */
     MI_GATING_SIGMOID_BIAS = 1,    /* s = sigmoid(logit); top_k on s + sel_bias[e] (selection
                                       only); w = s / (sum_K s + gate_eps) * routed_scaling
                                       [* expert_scale[e]] (nemotronomni_model.cpp:344-354) */
+    MI_GATING_SOFTMAX_ALL  = 2,    /* p = soft_max over all E logits; top_k on p; w = p / sum_K p
+                                      [* expert_scale[e]] (diffusiongemma_model.cpp:923-937): ranks
+                                      the probabilities, so logits whose probabilities round to the
+                                      same float tie (lower id first) */
 } mi_gating;
 
 /* ggml_tensor stand-in: data on the device, ne fastest-first, nb in bytes. */
@@ -97,6 +103,19 @@ typedef struct {
     const float *expert_scale;     /* F32 [E] or NULL: per-expert factor on the weights */
     float routed_scaling;          /* MI_GATING_SIGMOID_BIAS: weight scale (0 is read as 1) */
     float gate_eps;                /* MI_GATING_SIGMOID_BIAS: added to the weight sum */
+    /* Shared expert, applied to every token and added to the routed sum before
+     * the residual: out = res + (routed + sh), sh = sh_down(act(sh_gate x, sh_up x))
+     * [* sigmoid(sh_gate_inp . x)].  nemotronomni: relu^2 on ffn_up_shexp, unscaled
+     * (nemotronomni_model.cpp:371-376); qwen3omni talker: SwiGLU times the sigmoid of
+     * a scalar gate row (qwen3omni_talker.cpp:396-402).  sh_n_ff = 0: none.  Used by
+     * mi_moe_forward / mi_moe_forward_norm; mi_moe_expert_ffn ignores it (the
+     * reference's table form has none). */
+    int32_t sh_n_ff;
+    int32_t sh_act;                /* mi_act of the shared expert */
+    mi_tensor sh_gate;             /* ne=[D, sh_n_ff] (ffn_gate_shexp; MI_ACT_RELU_SQR: ffn_up_shexp) */
+    mi_tensor sh_up;               /* ne=[D, sh_n_ff]; ignored for MI_ACT_RELU_SQR */
+    mi_tensor sh_down;             /* ne=[sh_n_ff, D] */
+    const float *sh_gate_inp;      /* F32 [D] or NULL (unscaled) */
 } mi_moe_layer;
 
 /* Optional routing outputs of mi_moe_forward (device pointers, any may be
@@ -137,9 +156,18 @@ typedef struct mi_moe_ctx mi_moe_ctx;
  * only by mi_moe_ctx_reserve; forward calls never allocate. */
 int  mi_moe_ctx_create(mi_moe_ctx **out, int device);
 void mi_moe_ctx_destroy(mi_moe_ctx *ctx);
-/* size the workspace for up to max_tokens tokens of layers with these dims */
+/* size the workspace for up to max_tokens tokens of layers with these dims
+ * (a shared expert's sh_n_ff may be up to n_ff * n_expert_used) */
 int  mi_moe_ctx_reserve(mi_moe_ctx *ctx, int64_t max_tokens, int32_t n_embd, int32_t n_ff,
                         int32_t n_expert, int32_t n_expert_used);
+/* Errors the GPU found inside calls that returned MI_MOE_OK (the calls do not
+ * synchronize, so these are reported afterwards), counted since the last take
+ * and then cleared.  bad_ids: caller-supplied expert ids outside [0, E)
+ * (mi_moe_expert_ffn, mi_mul_mat_id; ggml_mul_mat_id asserts them).
+ * wait_failures: fused single-token calls whose grid wait gave up (their
+ * output is NaN; MI_DECODE_FUSED_EXCLUSIVE on a GPU shared with other work).
+ * Either pointer may be NULL.  Synchronizes the context's device. */
+int  mi_moe_ctx_take_errors(mi_moe_ctx *ctx, int64_t *bad_ids, int64_t *wait_failures);
 
 /* ---- whole MoE block ------------------------------------------------------
  * out[t] = res[t] + sum_k w[t][k] * down_{sel[t][k]}( act(gate x[t], up x[t]) )
@@ -175,9 +203,12 @@ int mi_norm(mi_moe_ctx *ctx, const mi_moe_norm *norm, const float *x, int64_t n_
  * Replaces vqa::moe::build_expert_ffn_table_res (src/core/engine/moe_compute.hpp:66-71,
  * moe_compute.cpp:93-136) and the default graph B of the expert-cache decode
  * driver (moe_decode_driver.hpp:503-514):
- *   out = res + sum_k w[k] * down_k(act(gate_k x, up_k x))
+ *   out = res + sum_k w[k] * down_{down_ids[k]}(act(gate_{gu_ids[k]} x, up_{gu_ids[k]} x))
  * gate_up_ids / down_ids: I32 [T][K] device (may be the same pointer);
- * w: F32 [T][K] device.  The layer's router fields are ignored. */
+ * w: F32 [T][K] device.  The layer's router and shared-expert fields are
+ * ignored.  Ids must lie in [0, E): a slot whose gate/up or down id lies
+ * outside contributes nothing to its token's sum (the other slots still do)
+ * and is counted for mi_moe_ctx_take_errors. */
 int mi_moe_expert_ffn(mi_moe_ctx *ctx, const mi_moe_layer *layer, const float *x, int64_t n_tokens,
                       const float *res, const int32_t *gate_up_ids, const int32_t *down_ids,
                       const float *w, float *out, mi_stream_t stream);
@@ -192,7 +223,9 @@ int mi_top_k(mi_moe_ctx *ctx, const mi_tensor *a, int32_t k, mi_tensor *dst, mi_
  * ids I32 ne=[n_used, T]) -> F32 ne=[N, n_used, T]
  * (moondream.cpp:519,537; qwen3omni_model.cpp:769-774; moe_compute.cpp:124-130).
  * dst[:, k, t] = as[:, :, ids[k,t]] . b[:, k % ne11, t].  as types: Q4_K,
- * Q6_K, F32.  k-quant products quantize b to Q8_K first, like ggml-cpu. */
+ * Q6_K, F32.  k-quant products quantize b to Q8_K first, like ggml-cpu.
+ * Ids must lie in [0, E): the dst row of an id outside is written as zeros
+ * and the id is counted for mi_moe_ctx_take_errors. */
 int mi_mul_mat_id(mi_moe_ctx *ctx, const mi_tensor *as, const mi_tensor *b, const mi_tensor *ids,
                   mi_tensor *dst, mi_stream_t stream);
 
@@ -255,7 +288,7 @@ int mi_moe_ctx_stage_times(mi_moe_ctx *ctx, int max_stages, const char **names, 
                            int *n_stages);
 /* Product path of a call: the grouped MFMA GEMM from min_tokens_for_gemm
  * tokens on, the grouped GEMV below.  0 (the default) picks by shape: the
- * GEMM when 4 * T * K >= 5 * E (1.25 dispatched rows per expert). */
+ * GEMM when 4 * T * K > 5 * E (more than 1.25 dispatched rows per expert). */
 int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *ctx, int64_t min_tokens_for_gemm);
 /* Schedule of single-token calls of mi_moe_forward.  The fused modes run the
  * whole block in one kernel of one work-group per CU that synchronizes

@@ -764,12 +764,17 @@ void orc_softmax_selected(const float *logits, const int32_t *sel,
 
 /* Router gating variants (kind 0: top-k on logits + softmax over the K;
  * kind 1: nemotronomni_model.cpp:344-354 - s = sigmoid(logit), top-k on
- * s + sel_bias, w = s / (sum s + eps) * scaling); expert_scale multiplies the
- * weights (diffusiongemma_model.cpp:932-936).  The sigmoid is evaluated in
- * double and rounded once to float (the restatement's choice, so rankings do
- * not depend on a float exp's last bit; ggml's ggml_sigmoid is float); the
- * weight sum is a double sum in slot order, rounded to float before eps is
- * added; ties rank the lower id first (strict > in the repeated selection). */
+ * s + sel_bias, w = s / (sum s + eps) * scaling; kind 2:
+ * diffusiongemma_model.cpp:923-932 - p = soft_max over all E logits, top-k
+ * on p, w = p / sum_K p); expert_scale multiplies the weights
+ * (diffusiongemma_model.cpp:932-936).  The sigmoid and the exponentials of
+ * kind 2 are evaluated in double and rounded once to float (the restatement's
+ * choice, so rankings do not depend on a float exp's last bit; ggml's
+ * ggml_sigmoid / soft_max use float exp); weight sums are double sums in slot
+ * order, rounded to float (kind 1 then adds eps); kind 2's full softmax is
+ * ggml's: max, e = fl32(exp(l - max)) with the difference in float, the sum of
+ * the e in double in expert order, p = e * fl32(1 / sum).  Ties rank the lower
+ * id first (strict > in the repeated selection). */
 static float orc_sigmoid(float x) { return (float)(1.0 / (1.0 + exp(-(double)x))); }
 
 void orc_route_gated(const float *logits, int64_t T, int E, int K, int kind, const float *sel_bias,
@@ -778,8 +783,20 @@ void orc_route_gated(const float *logits, int64_t T, int E, int K, int kind, con
         const float *l = logits + t * E;
         int32_t *s = sel + t * K;
         float score[1024];
-        for (int e = 0; e < E; e++)
-            score[e] = kind == 1 ? orc_sigmoid(l[e]) + (sel_bias ? sel_bias[e] : 0.f) : l[e];
+        if (kind == 2) {
+            float mx = -INFINITY;
+            for (int e = 0; e < E; e++) mx = MAX(mx, l[e]);
+            double sum = 0.0;
+            for (int e = 0; e < E; e++) {
+                score[e] = (float)exp((double)(l[e] - mx));
+                sum += (double)score[e];
+            }
+            const float inv = (float)(1.0 / sum);
+            for (int e = 0; e < E; e++) score[e] = score[e] * inv;
+        } else {
+            for (int e = 0; e < E; e++)
+                score[e] = kind == 1 ? orc_sigmoid(l[e]) + (sel_bias ? sel_bias[e] : 0.f) : l[e];
+        }
         for (int k = 0; k < K; k++) {
             int best = -1;
             for (int e = 0; e < E; e++) {
@@ -798,6 +815,11 @@ void orc_route_gated(const float *logits, int64_t T, int E, int K, int kind, con
                 sum += (double)sv[k];
             }
             for (int k = 0; k < K; k++) w[t * K + k] = sv[k] / ((float)sum + eps) * scaling;
+        } else if (kind == 2) {
+            double sum = 0.0;
+            for (int k = 0; k < K; k++) sum += (double)score[s[k]];
+            const float fs = (float)sum;
+            for (int k = 0; k < K; k++) w[t * K + k] = score[s[k]] / fs;
         } else {
             orc_softmax_selected(logits + t * E, s, 1, E, K, w + t * K);
         }
@@ -933,6 +955,10 @@ float orc_act_pair(int act, float a, float b) {
     case ORC_ACT_GELU_TANH:
         return 0.5f * a * (1.0f + tanhf(SQRT_2_OVER_PI * a * (1.0f + GELU_COEF_A * a * a))) * b;
     case ORC_ACT_GELU_ERF: return 0.5f * a * (1.0f + erff(a * SQRT_2_INV)) * b;
+    case ORC_ACT_RELU_SQR: {                                        /* ggml_sqr(ggml_relu(u)) */
+        const float r = a > 0.f ? a : 0.f;
+        return r * r;
+    }
     default: return 0.f;
     }
 }
@@ -944,6 +970,7 @@ static double act_pair_f64(int act, double a, double b) {
     case ORC_ACT_GELU_TANH:
         return 0.5 * a * (1.0 + tanh(0.79788456080286535588 * a * (1.0 + 0.044715 * a * a))) * b;
     case ORC_ACT_GELU_ERF: return 0.5 * a * (1.0 + erf(a * 0.70710678118654752440)) * b;
+    case ORC_ACT_RELU_SQR: return a > 0.0 ? a * a : 0.0;
     default: return 0.0;
     }
 }
@@ -951,19 +978,79 @@ static double act_pair_f64(int act, double a, double b) {
 /* ------------------------------------------------------------------------ */
 /* whole layer                                                              */
 /* ------------------------------------------------------------------------ */
+/* act rows from the gate (and up) products: gated pairs, or one product */
+static void orc_act_rows(int act, int fused, int64_t rows, int I, const float *gu, const float *up, float *out,
+                         int exact, int nthreads) {
+    const int gated = ORC_ACT_GATED(act);
+    const int64_t Ng = gated && fused ? 2 * (int64_t)I : I;
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        for (int i = 0; i < I; i++) {
+            float a, bb = 0.f;
+            if (!gated) {
+                a = gu[r * Ng + i];
+            } else if (fused) {
+                a = gu[r * Ng + i];
+                bb = gu[r * Ng + I + i];
+            } else {
+                a = gu[r * I + i];
+                bb = up[r * I + i];
+            }
+            out[r * I + i] = exact ? (float)act_pair_f64(act, a, bb) : orc_act_pair(act, a, bb);
+        }
+    }
+}
+
+/* the shared expert of every token: sh[t] = down(act(gate x, up x)) [* sigmoid
+ * (gate_inp . x)], each product a mul_mat with Q8_K activations (ggml
+ * vec_dot_type) - here mul_mat_id over one expert; the scalar gate row is a
+ * router row of one expert (the router's fixed fp64 order) whose sigmoid is
+ * evaluated in double and rounded once */
+static int orc_shared_expert(const orc_layer *L, const float *x, int64_t T, float *sh, int exact, int nthreads) {
+    const int D = L->D, I = L->sh_I;
+    const int gated = ORC_ACT_GATED(L->sh_act);
+    int32_t *z0 = (int32_t *)calloc((size_t)T, sizeof(int32_t));
+    float *g = (float *)malloc(sizeof(float) * (size_t)(T * I));
+    float *u = gated ? (float *)malloc(sizeof(float) * (size_t)(T * I)) : NULL;
+    float *a = (float *)malloc(sizeof(float) * (size_t)(T * I));
+    int rc = orc_mul_mat_id(L->sh_type, L->sh_gate, D, I, 1, x, 1, z0, 1, T, g, exact, nthreads);
+    if (!rc && gated) rc = orc_mul_mat_id(L->sh_type, L->sh_up, D, I, 1, x, 1, z0, 1, T, u, exact, nthreads);
+    if (!rc) {
+        orc_act_rows(L->sh_act, 0, T, I, g, u, a, exact, nthreads);
+        rc = orc_mul_mat_id(L->sh_down_type, L->sh_down, I, D, 1, a, 1, z0, 1, T, sh, exact, nthreads);
+    }
+    if (!rc && L->sh_gate_inp) {
+        float *lg = (float *)malloc(sizeof(float) * (size_t)T);
+        orc_router_logits(L->sh_gate_inp, NULL, x, T, D, 1, lg, nthreads);
+        for (int64_t t = 0; t < T; t++) {
+            const float s = orc_sigmoid(lg[t]);
+            for (int n = 0; n < D; n++) sh[t * D + n] = sh[t * D + n] * s;   /* ggml_mul(sd, gate_row) */
+        }
+        free(lg);
+    }
+    free(z0); free(g); free(u); free(a);
+    return rc;
+}
+
 int orc_moe_forward(const orc_layer *L, const float *x, int64_t T,
                     const float *res, float *out, orc_debug *dbg,
-                    const int32_t *sel_in, const float *w_in,
+                    const int32_t *sel_in, const int32_t *down_sel_in, const float *w_in,
                     int exact, int nthreads) {
     if (!L || !x || !out || T < 0) return -1;
     const int D = L->D, E = L->E, K = L->K, I = L->I;
+    const int gated = ORC_ACT_GATED(L->act);
     if (D <= 0 || E <= 0 || K <= 0 || K > E || I <= 0) return -1;
-    if (!L->gate || !L->down || (!L->fused_gate_up && !L->up)) return -1;
+    if (!L->gate || !L->down || (gated && !L->fused_gate_up && !L->up)) return -1;
+    if (!gated && L->fused_gate_up) return -1;
     if ((!sel_in || !w_in) && !L->router_w) return -1;
+    if (L->gating < 0 || L->gating > 2) return -1;
+    if (L->sh_I < 0 || (L->sh_I > 0 && (!L->sh_gate || !L->sh_down || (ORC_ACT_GATED(L->sh_act) && !L->sh_up))))
+        return -1;
     if (T == 0) return 0;
 
     float *logits = (float *)malloc(sizeof(float) * (size_t)(T * E));
     int32_t *sel = (int32_t *)malloc(sizeof(int32_t) * (size_t)(T * K));
+    int32_t *dsel = (int32_t *)malloc(sizeof(int32_t) * (size_t)(T * K));
     float *w = (float *)malloc(sizeof(float) * (size_t)(T * K));
     if (sel_in && w_in) {
         memcpy(sel, sel_in, sizeof(int32_t) * (size_t)(T * K));
@@ -971,42 +1058,30 @@ int orc_moe_forward(const orc_layer *L, const float *x, int64_t T,
         memset(logits, 0, sizeof(float) * (size_t)(T * E));
     } else {
         orc_router_logits(L->router_w, L->router_b, x, T, D, E, logits, nthreads);
-        orc_top_k(logits, T, E, K, sel);
-        orc_softmax_selected(logits, sel, T, E, K, w);
+        orc_route_gated(logits, T, E, K, L->gating, L->sel_bias, L->expert_scale,
+                        L->routed_scaling != 0.f ? L->routed_scaling : 1.f, L->gate_eps, sel, w);
     }
+    memcpy(dsel, down_sel_in ? down_sel_in : sel, sizeof(int32_t) * (size_t)(T * K));
 
-    const int64_t Ng = L->fused_gate_up ? 2 * (int64_t)I : I;
+    const int64_t Ng = gated && L->fused_gate_up ? 2 * (int64_t)I : I;
     float *gu = (float *)malloc(sizeof(float) * (size_t)(T * K * Ng));
-    float *up = L->fused_gate_up ? NULL : (float *)malloc(sizeof(float) * (size_t)(T * K * I));
+    float *up = gated && !L->fused_gate_up ? (float *)malloc(sizeof(float) * (size_t)(T * K * I)) : NULL;
     float *act = (float *)malloc(sizeof(float) * (size_t)(T * K * I));
     float *ff = (float *)malloc(sizeof(float) * (size_t)(T * K * D));
+    float *sh = L->sh_I > 0 ? (float *)malloc(sizeof(float) * (size_t)(T * D)) : NULL;
     int rc = 0;
 
     rc |= orc_mul_mat_id(L->gate_type, L->gate, D, Ng, E, x, 1, sel, K, T, gu, exact, nthreads);
-    if (!L->fused_gate_up)
-        rc |= orc_mul_mat_id(L->gate_type, L->up, D, I, E, x, 1, sel, K, T, up, exact, nthreads);
+    if (up) rc |= orc_mul_mat_id(L->gate_type, L->up, D, I, E, x, 1, sel, K, T, up, exact, nthreads);
     if (rc) goto done;
-
-#pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
-    for (int64_t r = 0; r < T * K; r++) {
-        for (int i = 0; i < I; i++) {
-            float a, bb;
-            if (L->fused_gate_up) {
-                a = gu[r * Ng + i];
-                bb = gu[r * Ng + I + i];
-            } else {
-                a = gu[r * I + i];
-                bb = up[r * I + i];
-            }
-            act[r * I + i] = exact ? (float)act_pair_f64(L->act, a, bb) : orc_act_pair(L->act, a, bb);
-        }
-    }
-
-    rc |= orc_mul_mat_id(L->down_type, L->down, I, D, E, act, K, sel, K, T, ff, exact, nthreads);
+    orc_act_rows(L->act, L->fused_gate_up, T * K, I, gu, up, act, exact, nthreads);
+    rc |= orc_mul_mat_id(L->down_type, L->down, I, D, E, act, K, dsel, K, T, ff, exact, nthreads);
+    if (rc) goto done;
+    if (sh) rc |= orc_shared_expert(L, x, T, sh, exact, nthreads);
     if (rc) goto done;
 
     /* ggml_mul(ff3, w) -> permute/cont -> sum_rows (fp64 accumulation, slot
-     * order) -> add res */
+     * order), + the shared expert (ggml_add(routed, sh)), -> add res */
 #pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
     for (int64_t t = 0; t < T; t++) {
         for (int n = 0; n < D; n++) {
@@ -1018,7 +1093,10 @@ int orc_moe_forward(const orc_layer *L, const float *x, int64_t T,
                     sum += (double)prod;
                 }
             }
-            const float moe = (float)sum;
+            float moe;
+            if (sh && exact) moe = (float)(sum + (double)sh[t * D + n]);
+            else if (sh) moe = (float)sum + sh[t * D + n];
+            else moe = (float)sum;
             out[t * D + n] = res ? res[t * D + n] + moe : moe;
         }
     }
@@ -1039,9 +1117,10 @@ int orc_moe_forward(const orc_layer *L, const float *x, int64_t T,
         }
         if (dbg->act) memcpy(dbg->act, act, sizeof(float) * (size_t)(T * K * I));
         if (dbg->ff) memcpy(dbg->ff, ff, sizeof(float) * (size_t)(T * K * D));
+        if (dbg->sh && sh) memcpy(dbg->sh, sh, sizeof(float) * (size_t)(T * D));
     }
 
 done:
-    free(logits); free(sel); free(w); free(gu); free(up); free(act); free(ff);
+    free(logits); free(sel); free(dsel); free(w); free(gu); free(up); free(act); free(ff); free(sh);
     return rc ? -1 : 0;
 }

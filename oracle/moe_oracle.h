@@ -79,6 +79,18 @@ enum {                    /* activation applied between the two expert products 
     ORC_ACT_GELU_ERF_GP1   = 1,  /* gelu_erf(h) * (g + 1)        (moondream3, geglu_erf_split)    */
     ORC_ACT_GELU_TANH      = 2,  /* gelu_tanh(gate) * up         (BASELINE config-0 literal)      */
     ORC_ACT_GELU_ERF       = 3,  /* gelu_erf(gate) * up                                           */
+    ORC_ACT_RELU_SQR       = 4,  /* relu(u)^2 of ONE product, non-gated (nemotronomni experts,
+                                    nemotronomni_model.cpp:366-367, 372-373): the gate table holds
+                                    ffn_up_exps, no up table                                       */
+};
+/* act uses a gate/up pair (0..3) or one product (RELU_SQR) */
+#define ORC_ACT_GATED(a) ((a) != ORC_ACT_RELU_SQR)
+
+enum {                    /* router gating */
+    ORC_GATING_SOFTMAX_TOPK = 0, /* top_k on logits, softmax over the K (moondream.cpp:510-516)   */
+    ORC_GATING_SIGMOID_BIAS = 1, /* sigmoid, top_k on s + bias, renorm (nemotronomni_model.cpp:344-354) */
+    ORC_GATING_SOFTMAX_ALL  = 2, /* softmax over all E, top_k on the probabilities, renorm over the
+                                    K (diffusiongemma_model.cpp:923-932)                          */
 };
 
 /* ---- scalar helpers ---------------------------------------------------- */
@@ -145,7 +157,8 @@ void orc_top_k(const float *logits, int64_t T, int E, int K, int32_t *sel);
 void orc_softmax_selected(const float *logits, const int32_t *sel,
                           int64_t T, int E, int K, float *w);
 /* router gating variants: kind 0 top-k on logits + softmax over the K, kind 1
- * sigmoid + selection bias + renorm with eps and scaling; expert_scale (or
+ * sigmoid + selection bias + renorm with eps and scaling, kind 2 softmax over
+ * all E + top-k on the probabilities + renorm over the K; expert_scale (or
  * NULL) multiplies the weights */
 void orc_route_gated(const float *logits, int64_t T, int E, int K, int kind, const float *sel_bias,
                      const float *expert_scale, float scaling, float eps, int32_t *sel, float *w);
@@ -180,7 +193,25 @@ typedef struct {
     int32_t fused_gate_up;
     int32_t down_type;
     const void *down;             /* ne=[I, D, E] */
-    int32_t act;
+    int32_t act;                  /* ORC_ACT_*; RELU_SQR: gate holds up_exps ne=[D, I, E] */
+    /* router gating (orc_route_gated) */
+    int32_t gating;               /* ORC_GATING_* */
+    const float *sel_bias;        /* [E] or NULL (kind 1) */
+    const float *expert_scale;    /* [E] or NULL */
+    float routed_scaling;         /* kind 1 (0 is read as 1) */
+    float gate_eps;               /* kind 1 */
+    /* shared expert, applied to every token (sh_I = 0: none):
+     *   sh[t] = sh_down(act(sh_gate x[t], sh_up x[t])) [* sigmoid(sh_gate_inp . x[t])]
+     * nemotronomni_model.cpp:371-376 (relu^2, unscaled), qwen3omni_talker.cpp:396-402
+     * (SwiGLU times the sigmoid of a scalar gate row) */
+    int32_t sh_I;
+    int32_t sh_act;
+    int32_t sh_type;              /* type of sh_gate / sh_up */
+    const void *sh_gate;          /* ne=[D, sh_I]; RELU_SQR: ffn_up_shexp */
+    const void *sh_up;            /* ne=[D, sh_I] or NULL */
+    int32_t sh_down_type;
+    const void *sh_down;          /* ne=[sh_I, D] */
+    const float *sh_gate_inp;     /* F32 [D] or NULL */
 } orc_layer;
 
 typedef struct {                  /* optional outputs; any pointer may be NULL */
@@ -192,16 +223,21 @@ typedef struct {                  /* optional outputs; any pointer may be NULL *
     int32_t *perm;                /* [T*K]    */
     float   *act;                 /* [T][K][I] */
     float   *ff;                  /* [T][K][D] down outputs before weighting */
+    float   *sh;                  /* [T][D] shared expert output (after its gate) */
 } orc_debug;
 
-/* out[t] = res[t] + sum_k w[t][k] * down_k(act(gate_k x[t], up_k x[t]))
+/* out[t] = res[t] + (sum_k w[t][k] * down_{dsel[t][k]}(act(gate_{sel[t][k]} x[t],
+ *                                                      up_{sel[t][k]} x[t]))
+ *                    + sh[t])
  * res may be NULL (then out = moe only).  exact = 0: ggml semantics;
  * exact = 1: fp64 on dequantized weights with unquantized activations.
  * sel_in / w_in non-NULL: skip the router and use the given routing (the
- * build_expert_ffn_table_res contract, moe_compute.cpp:93-136). */
+ * build_expert_ffn_table_res contract, moe_compute.cpp:93-136); down_sel_in
+ * non-NULL: the down product's ids (moe_compute.hpp:45, down_ids), else
+ * dsel = sel.  Ids outside [0, E) return -1 (ggml asserts them). */
 int orc_moe_forward(const orc_layer *L, const float *x, int64_t T,
                     const float *res, float *out, orc_debug *dbg,
-                    const int32_t *sel_in, const float *w_in,
+                    const int32_t *sel_in, const int32_t *down_sel_in, const float *w_in,
                     int exact, int nthreads);
 
 int orc_max_threads(void);

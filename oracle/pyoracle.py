@@ -80,7 +80,7 @@ def _declare(L: C.CDLL) -> None:
     L.orc_mul_mat_id.restype = C.c_int
     L.orc_act_pair.argtypes = [C.c_int, C.c_float, C.c_float]
     L.orc_act_pair.restype = C.c_float
-    L.orc_moe_forward.argtypes = [P, P, i64, P, P, P, P, P, C.c_int, C.c_int]
+    L.orc_moe_forward.argtypes = [P, P, i64, P, P, P, P, P, P, C.c_int, C.c_int]
     L.orc_moe_forward.restype = C.c_int
     L.orc_max_threads.restype = C.c_int
 
@@ -248,18 +248,30 @@ class _Layer(C.Structure):
     _fields_ = [("D", C.c_int32), ("E", C.c_int32), ("K", C.c_int32), ("I", C.c_int32),
                 ("router_w", P), ("router_b", P),
                 ("gate_type", C.c_int32), ("gate", P), ("up", P), ("fused_gate_up", C.c_int32),
-                ("down_type", C.c_int32), ("down", P), ("act", C.c_int32)]
+                ("down_type", C.c_int32), ("down", P), ("act", C.c_int32),
+                ("gating", C.c_int32), ("sel_bias", P), ("expert_scale", P),
+                ("routed_scaling", C.c_float), ("gate_eps", C.c_float),
+                ("sh_I", C.c_int32), ("sh_act", C.c_int32), ("sh_type", C.c_int32), ("sh_gate", P),
+                ("sh_up", P), ("sh_down_type", C.c_int32), ("sh_down", P), ("sh_gate_inp", P)]
 
 
 class _Debug(C.Structure):
     _fields_ = [("logits", P), ("sel", P), ("w", P), ("counts", P), ("offsets", P),
-                ("perm", P), ("act", P), ("ff", P)]
+                ("perm", P), ("act", P), ("ff", P), ("sh", P)]
+
+
+ACT_RELU_SQR = 4
+GATING_SOFTMAX_TOPK, GATING_SIGMOID_BIAS, GATING_SOFTMAX_ALL = 0, 1, 2
 
 
 def moe_forward(layer: dict, x: np.ndarray, res=None, exact: bool = False,
-                sel_in=None, w_in=None, nthreads: int = 0, debug: bool = True):
+                sel_in=None, w_in=None, nthreads: int = 0, debug: bool = True, down_sel_in=None):
     """layer: dict(D, E, K, I, router_w, router_b, gate_type, gate, up, fused,
-    down_type, down, act).  Returns (out, dbg dict)."""
+    down_type, down, act) and optionally the gating (gating, sel_bias,
+    expert_scale, routed_scaling, gate_eps) and a shared expert (sh_I, sh_act,
+    sh_type, sh_gate, sh_up, sh_down_type, sh_down, sh_gate_inp).
+    sel_in / w_in: caller routing (down_sel_in: separate down ids).
+    Returns (out, dbg dict)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     T, D = x.shape
     E, K, I = layer["E"], layer["K"], layer["I"]
@@ -283,6 +295,20 @@ def moe_forward(layer: dict, x: np.ndarray, res=None, exact: bool = False,
     L.down_type = layer["down_type"]
     L.down = _p(arr(layer["down"]))
     L.act = layer["act"]
+    L.gating = int(layer.get("gating", 0))
+    L.sel_bias = _p(arr(layer.get("sel_bias"), np.float32))
+    L.expert_scale = _p(arr(layer.get("expert_scale"), np.float32))
+    L.routed_scaling = float(layer.get("routed_scaling", 0.0))
+    L.gate_eps = float(layer.get("gate_eps", 0.0))
+    L.sh_I = int(layer.get("sh_I", 0))
+    if L.sh_I:
+        L.sh_act = layer["sh_act"]
+        L.sh_type = layer["sh_type"]
+        L.sh_gate = _p(arr(layer["sh_gate"]))
+        L.sh_up = _p(arr(layer.get("sh_up")))
+        L.sh_down_type = layer["sh_down_type"]
+        L.sh_down = _p(arr(layer["sh_down"]))
+        L.sh_gate_inp = _p(arr(layer.get("sh_gate_inp"), np.float32))
     out = np.zeros((T, D), dtype=np.float32)
     dbg = None
     d = {}
@@ -290,14 +316,16 @@ def moe_forward(layer: dict, x: np.ndarray, res=None, exact: bool = False,
         d = dict(logits=np.zeros((T, E), np.float32), sel=np.zeros((T, K), np.int32),
                  w=np.zeros((T, K), np.float32), counts=np.zeros(E, np.int32),
                  offsets=np.zeros(E + 1, np.int32), perm=np.zeros(T * K, np.int32),
-                 act=np.zeros((T, K, I), np.float32), ff=np.zeros((T, K, D), np.float32))
+                 act=np.zeros((T, K, I), np.float32), ff=np.zeros((T, K, D), np.float32),
+                 sh=np.zeros((T, D), np.float32))
         dbg = _Debug(*[_p(d[f]) for f, _ in _Debug._fields_])
     rres = arr(res, np.float32)
     s_in = arr(sel_in, np.int32)
     w_in_ = arr(w_in, np.float32)
+    ds_in = arr(down_sel_in, np.int32)
     rc = lib().orc_moe_forward(C.byref(L), _p(x), T, _p(rres), _p(out),
                                C.byref(dbg) if dbg is not None else None,
-                               _p(s_in), _p(w_in_), int(exact), nthreads)
+                               _p(s_in), _p(ds_in), _p(w_in_), int(exact), nthreads)
     if rc != 0:
         raise ValueError("orc_moe_forward: bad arguments")
     return out, d

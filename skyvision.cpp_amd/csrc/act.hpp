@@ -4,11 +4,19 @@
 //   GELU_ERF_GP1  gelu_erf(h) * (g + 1)          moondream.cpp:534-535
 //   GELU_TANH     gelu_tanh(a) * b
 //   GELU_ERF      gelu_erf(a) * b                moe_compute.cpp:127-129
+//   RELU_SQR      relu(a)^2 (b unused)           nemotronomni_model.cpp:366-367
 #pragma once
 
 #include <hip/hip_runtime.h>
 
 namespace mimoe {
+
+constexpr int ACT_RELU_SQR = 4;   // mi_act: non-gated experts, one product
+// ggml_sqr(ggml_relu(u)): relu keeps u > 0, else 0
+__device__ inline float relu_sqr(float a) {
+    const float r = a > 0.f ? a : 0.f;
+    return r * r;
+}
 
 // libm-accurate forms (GEMV path: a few values per token)
 __device__ inline float act_pair(int act, float a, float b) {
@@ -23,6 +31,7 @@ __device__ inline float act_pair(int act, float a, float b) {
     }
     case 2: return 0.5f * a * (1.0f + tanhf(SQRT_2_OVER_PI * a * (1.0f + GELU_COEF_A * a * a))) * b;
     case 3: return 0.5f * a * (1.0f + erff(a * SQRT_2_INV)) * b;
+    case 4: return relu_sqr(a);
     default: return 0.f;
     }
 }
@@ -66,8 +75,10 @@ __device__ inline float act_pair_fast(float a, float b) {
         const float k = -2.0f * SQRT_2_OVER_PI * 1.4426950408889634f;
         const float e = __builtin_amdgcn_exp2f(k * a * (1.0f + GELU_COEF_A * a * a));
         return a * b * rcp_fast(1.0f + e);
-    } else {
+    } else if constexpr (ACT == 3) {
         return 0.5f * a * one_plus_erf_fast(a * SQRT_2_INV) * b;
+    } else {
+        return relu_sqr(a);
     }
 }
 

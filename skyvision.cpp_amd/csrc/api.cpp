@@ -66,10 +66,12 @@ struct ActBuf {                // one Q8_K activation set
 
 struct DispBuf {
     int32_t *counts, *offsets, *perm, *tile_e, *tile_r0, *n_tiles, *active_e, *n_active, *bad;
+    int32_t *bad_total;   // the context's running count (mi_moe_ctx_take_errors)
     Dispatch view() const {
         Dispatch d;
         d.counts = counts; d.offsets = offsets; d.perm = perm; d.tile_e = tile_e; d.tile_r0 = tile_r0;
         d.n_tiles = n_tiles; d.active_e = active_e; d.n_active = n_active; d.bad_ids = bad;
+        d.bad_total = bad_total; d.zero_rows = nullptr; d.zero_ld = 0; d.zero_n = 0;
         return d;
     }
 };
@@ -94,6 +96,10 @@ struct mi_moe_ctx {
     float *f1 = nullptr;      // [rows][max(2I, kmax)]  GLU / F32 scratch
     float *f2 = nullptr;      // [rows][I]
     float *z = nullptr;       // [rows][max(D, 2I)]
+    // shared expert: its output [cap_T][D], routing (all tokens -> expert 0) and gate row
+    float *sh_out = nullptr, *sh_w = nullptr, *sh_logit = nullptr;
+    int32_t *sh_ids = nullptr;
+    int32_t *bad_total = nullptr;   // caller ids outside [0, E) since the last take
     int64_t gemm_threshold = 0;   // 0: the shape rule of use_gemm
     // single-token fused kernel (k_decode.hip)
     int fused_decode = MI_DECODE_FUSED_COOPERATIVE;
@@ -164,25 +170,39 @@ ExpertMat as_mat(const mi_tensor &t) {
     return m;
 }
 
-int validate_layer(const mi_moe_ctx *c, const mi_moe_layer *L, bool need_router) {
+bool act_gated(int act) { return act != MI_ACT_RELU_SQR; }
+
+// the expert tables of a layer (routed, or the shared expert as E = 1)
+int check_experts(const mi_tensor &gate, const mi_tensor &up, const mi_tensor &down, int fused, int act, int64_t D,
+                  int64_t I, int64_t E) {
+    if (act < MI_ACT_SILU || act > MI_ACT_RELU_SQR) return MI_MOE_ERR_ARG;
+    const bool gated = act_gated(act);
+    if (!gated && fused) return MI_MOE_ERR_ARG;   // one product: gate holds ffn_up_exps
+    const int64_t Ng = gated && fused ? 2 * I : I;
+    TRY(check_table(gate, D, Ng, E));
+    if (gated && !fused) {
+        TRY(check_table(up, D, I, E));
+        if (up.type != gate.type) return MI_MOE_ERR_TYPE;   // gate/up interchangeable (moe_compute.cpp:114-116)
+    }
+    TRY(check_table(down, I, D, E));
+    if (is_kquant(gate.type) != is_kquant(down.type)) return MI_MOE_ERR_UNSUPPORTED;   // mixed F32 / k-quant
+    return MI_MOE_OK;
+}
+
+// shared: validate the shared-expert fields too (the forward; the table form ignores them)
+int validate_layer(const mi_moe_ctx *c, const mi_moe_layer *L, bool need_router, bool shared) {
     if (!L) return MI_MOE_ERR_NULL;
     const int64_t D = L->n_embd, E = L->n_expert, K = L->n_expert_used, I = L->n_ff;
     if (D <= 0 || E <= 0 || K <= 0 || I <= 0 || K > E) return MI_MOE_ERR_SHAPE;
     if (E > 256 || K > 64) return MI_MOE_ERR_UNSUPPORTED;
-    if (L->act < MI_ACT_SILU || L->act > MI_ACT_GELU_ERF) return MI_MOE_ERR_ARG;
-    if (L->gating != MI_GATING_SOFTMAX_TOPK && L->gating != MI_GATING_SIGMOID_BIAS) return MI_MOE_ERR_ARG;
+    if (L->gating < MI_GATING_SOFTMAX_TOPK || L->gating > MI_GATING_SOFTMAX_ALL) return MI_MOE_ERR_ARG;
     if (need_router && !L->router_w) return MI_MOE_ERR_NULL;
-    const int64_t Ng = L->fused_gate_up ? 2 * I : I;
-    TRY(check_table(L->gate, D, Ng, E));
-    if (!L->fused_gate_up) {
-        TRY(check_table(L->up, D, I, E));
-        if (L->up.type != L->gate.type) return MI_MOE_ERR_TYPE;   // gate/up interchangeable (moe_compute.cpp:114-116)
-    }
-    TRY(check_table(L->down, I, D, E));
-    const bool kq = is_kquant(L->gate.type);
-    if (kq != is_kquant(L->down.type)) return MI_MOE_ERR_UNSUPPORTED;   // mixed F32 / k-quant layers
+    TRY(check_experts(L->gate, L->up, L->down, L->fused_gate_up, L->act, D, I, E));
+    if (shared && L->sh_n_ff < 0) return MI_MOE_ERR_SHAPE;
+    if (shared && L->sh_n_ff > 0) TRY(check_experts(L->sh_gate, L->sh_up, L->sh_down, 0, L->sh_act, D, L->sh_n_ff, 1));
     if (!c->reserved) return MI_MOE_ERR_CAPACITY;
     if (D > c->cap_D || I > c->cap_I || E > c->cap_E || K > c->cap_K) return MI_MOE_ERR_CAPACITY;
+    if (shared && (int64_t)L->sh_n_ff > (int64_t)c->cap_I * c->cap_K) return MI_MOE_ERR_CAPACITY;
     return MI_MOE_OK;
 }
 
@@ -192,8 +212,10 @@ bool plan_decode1(const mi_moe_ctx *c, const mi_moe_layer *L, const float *x, in
     const int64_t D = L->n_embd, E = L->n_expert, K = L->n_expert_used, I = L->n_ff;
     const int G = c->dec_grid;
     if (!c->fused_decode || G <= 0) return false;
-    // the fused kernel ranks and weights with the default gating only
+    // the fused kernel ranks and weights with the default gating only, runs
+    // gated experts and no shared expert
     if (L->gating != MI_GATING_SOFTMAX_TOPK || L->expert_scale) return false;
+    if (!act_gated(L->act) || L->sh_n_ff > 0) return false;
     if (L->gate.type != MI_TYPE_Q4_K || (!L->fused_gate_up && L->up.type != MI_TYPE_Q4_K)) return false;
     if (L->down.type != MI_TYPE_Q4_K && L->down.type != MI_TYPE_Q6_K) return false;
     if (D % QK || I % QK || K > 8 || E > 256) return false;
@@ -245,37 +267,48 @@ bool use_gemm(const mi_moe_ctx *c, int64_t T, int K, int E) {
     // grouped GEMM pays per M-tile, the GEMV per token and row, so the switch
     // follows the rows per expert T*K/E: qwen3omni (E 128, K 8) GEMV faster up
     // to T = 20, GEMM from 24; moondream3 (E 64, K 8) GEMV at 8, GEMM from 12.
+    // The rule takes the GEMM above 1.25 rows per expert: qwen3omni from
+    // T = 21, moondream3 from T = 11.
     if (c->gemm_threshold > 0) return T >= c->gemm_threshold;
-    return 4 * T * K >= 5 * (int64_t)E;
+    return 4 * T * K > 5 * (int64_t)E;
 }
 
+// the grouped MFMA GEMMs (else the grouped GEMV) for a k-quant layer
+bool gemm_path(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T) {
+    return use_gemm(c, T, L->n_expert_used, L->n_expert) || L->n_embd > 8 * QK || L->n_ff > 8 * QK;
+}
+// the 4-wave 32x32x16 GEMMs (Q4_K gate/up GLU, and every one-product layer);
+// else the 16x16x32 GEMM with its fused GLU + Q8_K epilogue (Q6_K gate/up)
+bool g4_path(const mi_moe_layer *L) { return L->gate.type == MI_TYPE_Q4_K || !act_gated(L->act); }
+
 bool x_q8_spec(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T, Q8Out &qx) {
-    const int D = L->n_embd, I = L->n_ff;
     if (!is_kquant(L->gate.type)) return false;
-    const bool gemm = use_gemm(c, T, L->n_expert_used, L->n_expert) || D > 8 * QK || I > 8 * QK;
     qx = Q8Out{};
-    if (!gemm) {
+    if (!gemm_path(c, L, T)) {
         qx.q8 = c->ax.q8; qx.d8 = c->ax.d8; qx.bsums = c->ax.bs;
     } else {
-        qx.xh = c->ax.h; qx.wtype = L->gate.type; qx.order = L->gate.type == MI_TYPE_Q4_K;
+        qx.xh = c->ax.h; qx.wtype = L->gate.type; qx.order = g4_path(L) ? 1 : 0;
     }
     return true;
 }
 
-// routed FFN body: needs c->sel-like ids (device [T][K]) and weights w [T][K];
-// x_done: x is already in the x_q8_spec form
+// routed FFN body: ids (device [T][K]; gate/up and down may differ) and
+// weights w [T][K]; x_done: x is already in the x_q8_spec form; check_ids:
+// the ids come from the caller (dead slots are left out of the combine);
+// add: [T][D] added to the routed sum before the residual (or null)
 int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const int32_t *ids_gu,
                 const int32_t *ids_dn, const float *w, const float *res, float *out, hipStream_t st,
-                bool x_done = false) {
+                bool x_done = false, bool check_ids = false, const float *add = nullptr) {
     const int D = L->n_embd, E = L->n_expert, K = L->n_expert_used, I = L->n_ff;
     const int64_t rows = T * K;
     const int max_active = (int)std::min<int64_t>(E, rows);
     const bool same_ids = ids_gu == ids_dn;
     const bool kq = is_kquant(L->gate.type);
-    const bool gemm = kq && (use_gemm(c, T, K, E) || D > 8 * QK || I > 8 * QK);
-    // GEMM M-tiles: balanced tiles of at most G4_BM rows for the 4-wave GEMMs
-    // (Q4_K gate/up), GEMM_BM-row tiles otherwise
-    const bool g4 = gemm && L->gate.type == MI_TYPE_Q4_K;
+    const bool gated = act_gated(L->act);
+    const bool gemm = kq && gemm_path(c, L, T);
+    // GEMM M-tiles: balanced tiles of at most G4_BM rows for the 4-wave GEMMs,
+    // GEMM_BM-row tiles otherwise
+    const bool g4 = gemm && g4_path(L);
     const int bm = g4 ? G4_BM : GEMM_BM;
     const int max_tiles = (int)((rows + bm - 1) / bm + max_active);
 
@@ -292,26 +325,26 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
 
     const ExpertMat gate = as_mat(L->gate), down = as_mat(L->down);
     ExpertMat up = {};
-    if (!L->fused_gate_up) up = as_mat(L->up);
+    if (gated && !L->fused_gate_up) up = as_mat(L->up);
 
     if (!kq) {
         // fp32 expert tables: reference semantics without activation quantization
-        const int64_t Ng = L->fused_gate_up ? 2LL * I : I;
+        const int64_t Ng = gated && L->fused_gate_up ? 2LL * I : I;
         GemvArgs a = {};
         a.a = gate; a.ne11 = 1; a.K = K;
         a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.active_e = dg.active_e;
         a.n_active = dg.n_active; a.max_active = max_active;
         a.y = c->f1; a.ldy = Ng; a.ncols = Ng;
         TRY(launch_mm_id_f32(a, x, D, st));
-        const float *hbuf = c->f1, *gbuf = c->f1 + I;
+        const float *hbuf = c->f1, *gbuf = gated && L->fused_gate_up ? c->f1 + I : c->f1;
         int64_t ldh = Ng, ldg = Ng;
-        if (!L->fused_gate_up) {
+        if (gated && !L->fused_gate_up) {
             a.a = up; a.y = c->f2; a.ldy = I; a.ncols = I;
             TRY(launch_mm_id_f32(a, x, D, st));
             gbuf = c->f2;
             ldg = I;
         }
-        // act into z scratch rows [rows][I]
+        // act into z scratch rows [rows][I] (RELU_SQR reads only the first operand)
         float *act = c->z;
         TRY(launch_glu_rows(hbuf, ldh, gbuf, ldg, act, I, rows, I, L->act, st));
         stage_end(c, "gate_up", st);
@@ -322,22 +355,26 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         d.y = c->f1; d.ldy = D; d.ncols = D;
         TRY(launch_mm_id_f32(d, act, I, st));
         stage_end(c, "down", st);
-        TRY(launch_combine(c->f1, w, res, out, T, K, D, st));
+        CombineIds ci;
+        if (check_ids) { ci.a = ids_gu; ci.b = ids_dn; ci.E = E; }
+        TRY(launch_combine(c->f1, w, res, out, T, K, D, st, ci, add));
         stage_end(c, "combine", st);
         return MI_MOE_OK;
     }
 
     if (!gemm) {
         GemvArgs a = {};
-        a.a = gate; a.b = up; a.epi = EPI_GLU; a.act = L->act; a.I = I; a.fused = L->fused_gate_up;
+        a.a = gate; a.b = up; a.epi = gated ? EPI_GLU : EPI_STORE; a.act = L->act; a.I = I;
+        a.fused = L->fused_gate_up;
         a.q8 = c->ax.q8; a.d8 = c->ax.d8; a.bsums = c->ax.bs; a.ne11 = 1; a.K = K;
         a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.active_e = dg.active_e;
         a.n_active = dg.n_active; a.max_active = max_active;
         a.y = c->f1; a.ldy = I; a.ncols = I;
         TRY(launch_gemv(a, st));
         stage_end(c, "gate_up", st);
+        // Q8_K of the activation rows (one product: of relu(u)^2)
         Q8Out qa;
-        qa.q8 = c->aact.q8; qa.d8 = c->aact.d8; qa.bsums = c->aact.bs;
+        qa.q8 = c->aact.q8; qa.d8 = c->aact.d8; qa.bsums = c->aact.bs; qa.pre_act = gated ? 0 : MI_ACT_RELU_SQR;
         TRY(launch_q8k_rows(c->f1, I, rows, I, qa, st));
         stage_end(c, "q8k_act", st);
         GemvArgs d = {};
@@ -348,20 +385,21 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         d.y = c->z; d.ldy = D; d.ncols = D;
         TRY(launch_gemv(d, st));
         stage_end(c, "down", st);
-    } else if (gate.type == MI_TYPE_Q4_K) {
+    } else if (g4) {
         // 4-wave GEMMs on 32x32x16 MFMA: fp16 dequantized weights x fp16
-        // d*q of the Q8_K activations, then Q8_K of the GLU rows for the down GEMM
+        // d*q of the Q8_K activations; gated: the GLU fused into the gate/up
+        // GEMM, one product: the plain GEMM; then Q8_K of the activation rows
+        // (ggml: the down mul_mat_id quantizes its F32 input) for the down GEMM
         G2Args a = {};
-        a.a = gate; a.b = up; a.glu = 1; a.fused = L->fused_gate_up; a.act = L->act; a.I = I;
+        a.a = gate; a.b = up; a.glu = gated ? 1 : 0; a.fused = L->fused_gate_up; a.act = L->act; a.I = I;
         a.xh = c->ax.h; a.ne11 = 1; a.K = K;
         a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.tile_e = dg.tile_e;
         a.tile_r0 = dg.tile_r0; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
         a.y = c->f1; a.ldy = I; a.ncols = I; a.xrows = T;
         TRY(launch_gemm4(a, st));
         stage_end(c, "gate_up", st);
-        // Q8_K of the GLU rows (ggml: the down mul_mat_id quantizes its F32 input)
         Q8Out qa;
-        qa.xh = c->aact.h; qa.wtype = down.type; qa.order = 1;
+        qa.xh = c->aact.h; qa.wtype = down.type; qa.order = 1; qa.pre_act = gated ? 0 : MI_ACT_RELU_SQR;
         TRY(launch_q8k_rows(c->f1, I, rows, I, qa, st));
         stage_end(c, "q8k_act", st);
         G2Args d = {};
@@ -389,8 +427,35 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         TRY(launch_gemm(d, st));
         stage_end(c, "down", st);
     }
-    TRY(launch_combine(c->z, w, res, out, T, K, D, st));
+    CombineIds ci;
+    if (check_ids) { ci.a = ids_gu; ci.b = ids_dn; ci.E = E; }
+    TRY(launch_combine(c->z, w, res, out, T, K, D, st, ci, add));
     stage_end(c, "combine", st);
+    return MI_MOE_OK;
+}
+
+// The shared expert of every token into c->sh_out: a one-expert layer whose
+// tokens all select expert 0 with weight 1 or the sigmoid of the scalar gate
+// row (a one-expert router in the router's fixed fp64 order).
+int run_shared(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, hipStream_t st) {
+    mi_moe_layer S = {};
+    S.n_embd = L->n_embd;
+    S.n_expert = 1;
+    S.n_expert_used = 1;
+    S.n_ff = L->sh_n_ff;
+    S.gate = L->sh_gate;
+    S.up = L->sh_up;
+    S.down = L->sh_down;
+    S.fused_gate_up = 0;
+    S.act = L->sh_act;
+    const float *lg = nullptr;
+    if (L->sh_gate_inp) {
+        TRY(launch_router(L->sh_gate_inp, nullptr, x, L->n_embd, T, L->n_embd, 1, c->sh_logit, st));
+        lg = c->sh_logit;
+    }
+    TRY(launch_shared_gate(lg, T, c->sh_ids, c->sh_w, st));
+    TRY(run_experts(c, &S, x, T, c->sh_ids, c->sh_ids, c->sh_w, nullptr, c->sh_out, st));
+    stage_end(c, "shared_expert", st);
     return MI_MOE_OK;
 }
 
@@ -488,6 +553,8 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
     need += carve_size<float>(rows * wide) + carve_size<float>(rows * I) + carve_size<float>(rows * wide);
     need += carve_size<uint64_t>(DEC_TW_WORDS) + carve_size<uint32_t>(DEC_MAX_GRID) +
             carve_size<unsigned long long>(DEC_SYNC_WORDS) + carve_size<unsigned>(1);
+    need += carve_size<float>(max_tokens * D) + 2 * carve_size<float>(max_tokens) + carve_size<int32_t>(max_tokens) +
+            carve_size<int32_t>(1);
 
     if (c->ws) {
         (void)hipFree(c->ws);
@@ -515,6 +582,8 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
         d.n_active = carve<int32_t>(q, 1);
         d.bad = carve<int32_t>(q, 1);
     }
+    c->bad_total = carve<int32_t>(q, 1);
+    c->disp[0].bad_total = c->disp[1].bad_total = c->bad_total;
     c->ax.q8 = carve<int8_t>(q, rows * kmax_q);
     c->ax.d8 = carve<float>(q, rows * kmax_q / QK);
     c->ax.bs = carve<int16_t>(q, rows * kmax_q / 16);
@@ -531,6 +600,10 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
     c->dec_epoch = carve<uint32_t>(q, DEC_MAX_GRID);
     c->dec_sync = carve<unsigned long long>(q, DEC_SYNC_WORDS);
     c->dec_err = carve<unsigned>(q, 1);
+    c->sh_out = carve<float>(q, max_tokens * D);
+    c->sh_w = carve<float>(q, max_tokens);
+    c->sh_logit = carve<float>(q, max_tokens);
+    c->sh_ids = carve<int32_t>(q, max_tokens);
     HIP_TRY(hipMemset(p, 0, need));
     c->cap_T = max_tokens;
     c->cap_D = D;
@@ -541,6 +614,25 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
     c->cap_kmax = kmax_q;
     c->cap_tiles = tiles;
     c->reserved = true;
+    return MI_MOE_OK;
+}
+
+int mi_moe_ctx_take_errors(mi_moe_ctx *c, int64_t *bad_ids, int64_t *wait_failures) {
+    if (!c) return MI_MOE_ERR_NULL;
+    if (bad_ids) *bad_ids = 0;
+    if (wait_failures) *wait_failures = 0;
+    if (!c->reserved) return MI_MOE_OK;
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(hipDeviceSynchronize());
+    int32_t b = 0;
+    unsigned f = 0;
+    HIP_TRY(hipMemcpy(&b, c->bad_total, sizeof(b), hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(&f, c->dec_err, sizeof(f), hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemset(c->bad_total, 0, sizeof(b)));
+    HIP_TRY(hipMemset(c->dec_err, 0, sizeof(f)));
+    HIP_TRY(hipDeviceSynchronize());
+    if (bad_ids) *bad_ids = b;
+    if (wait_failures) *wait_failures = f;
     return MI_MOE_OK;
 }
 
@@ -592,7 +684,7 @@ int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T
                  const mi_moe_routing *routing, const NormParams &np, hipStream_t st) {
     if (!c) return MI_MOE_ERR_NULL;
     if (T < 0) return MI_MOE_ERR_SHAPE;
-    TRY(validate_layer(c, L, true));
+    TRY(validate_layer(c, L, true, true));
     if (T == 0) return MI_MOE_OK;
     if (!x || !out) return MI_MOE_ERR_NULL;
     if (T > c->cap_T) return MI_MOE_ERR_CAPACITY;
@@ -604,6 +696,12 @@ int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T
         TRY(launch_norm(np, x, T, D, c->xn, st));
         stage_end(c, "norm", st);
         x = c->xn;
+    }
+    // the shared expert first (its own Q8_K of x; the routed block's follows)
+    const float *add = nullptr;
+    if (L->sh_n_ff > 0) {
+        TRY(run_shared(c, L, x, T, st));
+        add = c->sh_out;
     }
     int P = 0, C = 0;
     if (T == 1 && plan_decode1(c, L, x, P, C)) {
@@ -617,14 +715,14 @@ int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T
         else TRY(rc);
         stage_end(c, "router", st);
         Gating gt;
-        gt.kind = L->gating == MI_GATING_SIGMOID_BIAS ? 1 : 0;
+        gt.kind = L->gating;
         gt.sel_bias = L->sel_bias;
         gt.expert_scale = L->expert_scale;
         gt.scaling = L->routed_scaling != 0.f ? L->routed_scaling : 1.f;
         gt.eps = L->gate_eps;
         TRY(launch_topk_softmax(c->logits, E, T, E, K, c->sel, K, c->w, st, gt));
         stage_end(c, "topk_softmax", st);
-        TRY(run_experts(c, L, x, T, c->sel, c->sel, c->w, res, out, st, xq && rc == 0));
+        TRY(run_experts(c, L, x, T, c->sel, c->sel, c->w, res, out, st, xq && rc == 0, false, add));
     }
     if (routing) {
         const DispBuf &d = c->disp[0];
@@ -687,14 +785,14 @@ int mi_moe_expert_ffn(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int6
                       mi_stream_t stream) {
     if (!c) return MI_MOE_ERR_NULL;
     if (T < 0) return MI_MOE_ERR_SHAPE;
-    TRY(validate_layer(c, L, false));
+    TRY(validate_layer(c, L, false, false));
     if (T == 0) return MI_MOE_OK;
     if (!x || !out || !gate_up_ids || !down_ids || !w) return MI_MOE_ERR_NULL;
     if (T > c->cap_T) return MI_MOE_ERR_CAPACITY;
     HIP_TRY(hipSetDevice(c->device));
     hipStream_t st = (hipStream_t)stream;
     stage_begin(c, st);
-    return run_experts(c, L, x, T, gate_up_ids, down_ids, w, res, out, st);
+    return run_experts(c, L, x, T, gate_up_ids, down_ids, w, res, out, st, false, true);
 }
 
 int mi_top_k(mi_moe_ctx *c, const mi_tensor *a, int32_t k, mi_tensor *dst, mi_stream_t stream) {
@@ -740,7 +838,11 @@ int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const 
     const int max_active = (int)std::min<int64_t>(E, rows);
     const int max_tiles = (int)((rows + G4_BM - 1) / G4_BM + max_active);
     const DispBuf &dsp = c->disp[0];
-    TRY(launch_dispatch((const int32_t *)ids->data, T, (int)n_used, (int)E, G4_BM, 1, dsp.view(), st));
+    Dispatch dv = dsp.view();
+    dv.zero_rows = (float *)dst->data;   // the rows of ids outside [0, E): zeros
+    dv.zero_ld = N;
+    dv.zero_n = N;
+    TRY(launch_dispatch((const int32_t *)ids->data, T, (int)n_used, (int)E, G4_BM, 1, dv, st));
     const ExpertMat M = as_mat(*as);
     const float *bp = (const float *)b->data;
     if (as->type == MI_TYPE_F32) {

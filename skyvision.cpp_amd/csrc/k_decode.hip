@@ -30,13 +30,15 @@
 // code.  Routing is exact: the rank form below selects the same experts in
 // the same order as the stable descending argsort of ggml_top_k.
 //
-// Synchronization.  Values one WG hands to another are written through to
-// memory (relaxed agent-scope atomic stores: sc1) and read with ordinary
-// loads: a kernel launch leaves no stale L2 line behind, and within the
-// launch an XCD's first read of such a line comes after its writer's store
-// landed, so the one L2 copy the XCD's WGs share is fresh (uncached reads
-// would send ~10^6 small requests per launch to the few memory channels
-// holding these buffers).  Two hand-offs:
+// Synchronization.  Values one WG hands to another are written with relaxed
+// agent-scope atomic stores (global_store ... sc1) and read with loads that
+// carry the same agent-coherent cache policy as agent-scope atomic loads
+// (buffer_load ... sc1: the instruction a relaxed agent-scope atomic load
+// compiles to), issued only after the poll that saw the producer's completion
+// word: every hand-off read is a coherent read at agent scope, whatever an
+// XCD's L2 held before.  (Agent-scope acquire / release fences would add a
+// whole-L2 invalidate / write-back per work-group and hand-off.)  Two
+// hand-offs:
 //   logits -> every WG: each logit is a 64-bit word tagged with the launch
 //     epoch; a WG polls the E words (one coalesced wave load per try) instead
 //     of meeting a barrier.  The router WGs that also quantize x store their
@@ -150,6 +152,19 @@ __device__ inline void dec_wait(unsigned long long *sync, unsigned long long old
     __syncthreads();
 }
 
+// Hand-off reads: 16 / 4 bytes at byte offset off of a buffer of nbytes,
+// loaded with the agent-coherent cache policy (sc1) of agent-scope atomic loads
+constexpr int CPOL_SC1 = 16;
+__device__ inline __amdgpu_buffer_rsrc_t co_rsrc(const void *p, uint32_t nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)nbytes, 0x00020000);
+}
+__device__ inline u32x4 co_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, CPOL_SC1);
+}
+__device__ inline uint32_t co_ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, CPOL_SC1);
+}
+
 // reinterpret a 32-bit value (passed by value: this toolchain's
 // __builtin_bit_cast of an ext-vector element reads element 0)
 __device__ inline float as_float(uint32_t u) { return __builtin_bit_cast(float, u); }
@@ -236,15 +251,21 @@ struct Q4X {
     int bsa, bsb;    // their 16-value block sums
     float dx;
 };
-__device__ inline Q4X dec_q4x_load(const int8_t *xq, const int16_t *xbs, const float *xd, int b, int sl) {
+// (written by other WGs: coherent loads; D values, D / 16 block sums, D / 256 scales)
+__device__ inline Q4X dec_q4x_load(const int8_t *xq, const int16_t *xbs, const float *xd, int D, int b, int sl) {
     const int c = sl >> 1, l0 = 16 * (sl & 1);
+    const auto rq = co_rsrc(xq, (uint32_t)D), rb = co_rsrc(xbs, (uint32_t)(D / 8)), rd = co_rsrc(xd, (uint32_t)(D / 64));
     Q4X x;
-    const int8_t *blk = xq + b * QK;
-    x.xa = *(const u32x4 *)(blk + 64 * c + l0);
-    x.xb = *(const u32x4 *)(blk + 64 * c + 32 + l0);
-    x.bsa = xbs[b * 16 + 4 * c + (sl & 1)];
-    x.bsb = xbs[b * 16 + 4 * c + 2 + (sl & 1)];
-    x.dx = xd[b];
+    const uint32_t blk = (uint32_t)(b * QK);
+    x.xa = co_ld16(rq, blk + 64 * c + l0);
+    x.xb = co_ld16(rq, blk + 64 * c + 32 + l0);
+    // block sums 4c + (sl & 1) and 4c + 2 + (sl & 1): the low or high half of two dwords
+    const uint32_t wa = co_ld4(rb, 2u * (uint32_t)(b * 16 + 4 * c));
+    const uint32_t wb = co_ld4(rb, 2u * (uint32_t)(b * 16 + 4 * c + 2));
+    const uint32_t sh = 16u * (uint32_t)(sl & 1);
+    x.bsa = (int)(int16_t)(uint16_t)(wa >> sh);
+    x.bsb = (int)(int16_t)(uint16_t)(wb >> sh);
+    x.dx = __builtin_bit_cast(float, co_ld4(rd, 4u * (uint32_t)b));
     return x;
 }
 __device__ inline float dec_q4_piece(const uint8_t *blk, int sl, const Q4X &x) {
@@ -471,7 +492,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
     // piece sl (every logit is in, so the Q8_K of x is too)
     const int LPR = 8 * NB, RPS = 64 / LPR;
     const int rr = lane / LPR, bq = (lane % LPR) >> 3, sl = lane & 7;
-    const Q4X xg = dec_q4x_load(g.xq, g.xbs, g.xd, bq, sl);
+    const Q4X xg = dec_q4x_load(g.xq, g.xbs, g.xd, D, bq, sl);
     {
         // rank of expert e = #{i : l_i > l_e} + #{i < e : l_i == l_e}; the K
         // lowest ranks in rank order are ggml_top_k's stable descending pick.
@@ -625,18 +646,20 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
         int8_t *aq = (int8_t *)s_dn[k];
         float *ad = (float *)(s_dn[k] + 2048);
         int16_t *abs_ = (int16_t *)(s_dn[k] + 2048 + 64);
-        // 16 lanes per block, four blocks per pass
+        // 16 lanes per block, four blocks per pass (activations of other WGs:
+        // coherent loads)
+        const auto ra = co_rsrc(g.actf, (uint32_t)(4 * K * I));
         for (int b0 = 0; b0 < NBI; b0 += 4) {
             const int b = b0 + (lane >> 4), seg = lane & 15;
             float v[16];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                float4_t a4 = {0.f, 0.f, 0.f, 0.f};
-                if (b < NBI) a4 = *(const float4_t *)(g.actf + k * I + b * QK + 16 * seg + 4 * i);
-                v[4 * i] = a4.x;
-                v[4 * i + 1] = a4.y;
-                v[4 * i + 2] = a4.z;
-                v[4 * i + 3] = a4.w;
+                u32x4 a4 = {0u, 0u, 0u, 0u};
+                if (b < NBI) a4 = co_ld16(ra, 4u * (uint32_t)(k * I + b * QK + 16 * seg + 4 * i));
+                v[4 * i] = as_float(a4[0]);
+                v[4 * i + 1] = as_float(a4[1]);
+                v[4 * i + 2] = as_float(a4[2]);
+                v[4 * i + 3] = as_float(a4[3]);
             }
             int q[16], bsum;
             const float d = q8k_wave4x16(v, lane, q, bsum);
@@ -708,7 +731,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
         g.out[n0 + tid] = v;
     }
     if (tid == 0) {
-        if (failed) __hip_atomic_store(g.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (failed) __hip_atomic_fetch_add(g.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(g.epoch + wg, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }

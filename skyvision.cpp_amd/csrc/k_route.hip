@@ -10,6 +10,7 @@
 //   combine   mul(ff3, w) -> permute/cont -> sum_rows (-> add) moondream.cpp:540-543
 // Q8_K is ggml's vec_dot_type for Q4_K / Q6_K: ggml-cpu quantizes the F32
 // activation rows to it before the integer dot.
+#include "act.hpp"
 #include "common.hpp"
 #include "wave_ops.hpp"
 #include "launch.hpp"
@@ -32,7 +33,7 @@ enum { XO_ANY = 0, XO_Q4 = 1, XO_Q6 = 2 };
 // the lane's 16 values of row group (row, grp) (zeros past the row's blocks)
 template <bool VEC>
 __device__ __forceinline__ void q8k_load(const float *__restrict__ src, int64_t ld, int64_t row, int grp, int nb,
-                                         int lane, float (&v)[16]) {
+                                         int lane, float (&v)[16], int pre_act = 0) {
     const int bl = lane >> 4, l16 = lane & 15;
     const int b = 4 * grp + bl;
     if (b < nb) {
@@ -50,6 +51,10 @@ __device__ __forceinline__ void q8k_load(const float *__restrict__ src, int64_t 
     } else {
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = 0.f;
+    }
+    if (pre_act == ACT_RELU_SQR) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = relu_sqr(v[i]);
     }
 }
 
@@ -171,7 +176,7 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ src,
     for (int u = 0; u < Q8_ITEMS; ++u) {
         const int64_t item = item0 + u < n_items ? item0 + u : item0;
         const int64_t row = item / ngrp;
-        q8k_load<VEC>(src, ld, row, (int)(item - row * ngrp), nb, lane, v[u]);
+        q8k_load<VEC>(src, ld, row, (int)(item - row * ngrp), nb, lane, v[u], o.pre_act);
     }
 #pragma unroll
     for (int u = 0; u < Q8_ITEMS; ++u) {
@@ -440,7 +445,7 @@ int launch_topk_softmax(const float *logits, int64_t ld_logits, int64_t T, int E
                         int64_t ld_sel, float *w, hipStream_t st, const Gating &gt) {
     if (T <= 0) return 0;
     if (E > 64 * TOPK_MAX_PER_LANE || K > 64 || K > E || K <= 0) return -6;
-    if (gt.kind != 0 && gt.kind != 1) return -6;
+    if (gt.kind < 0 || gt.kind > 2) return -6;
     hipLaunchKernelGGL(k_topk_softmax, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, logits, ld_logits, T, E,
                        K, sel, ld_sel, w, gt);
     return hip_check_launch();
@@ -547,6 +552,17 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
             *d.n_tiles = tsc[E - 1] + psc[E - 1];
             *d.n_active = asc[E - 1];
             *d.bad_ids = bad;
+            if (bad > 0 && d.bad_total) atomicAdd(d.bad_total, bad);
+        }
+    }
+    if (me == 0 && bad > 0 && d.zero_rows) {
+        // no product writes the rows of ids outside [0, E): zeros, one row per thread
+        for (int64_t i = tid; i < n; i += DISPATCH_THREADS) {
+            const int e = ids[i];
+            if (e < 0 || e >= E) {
+                float *row = d.zero_rows + i * d.zero_ld;
+                for (int64_t c2 = 0; c2 < d.zero_n; ++c2) row[c2] = 0.f;
+            }
         }
     }
     if (balanced) {
@@ -628,10 +644,18 @@ int launch_dispatch(const int32_t *ids, int64_t T, int K, int E, int BM, int bal
 }
 
 // ---------------------------------------------------------------- combine
-// moe[t][n] = (float)( sum_k (double)(z[t*K+k][n] * w[t][k]) ), slot order;
-// out = res + moe.
+// moe[t][n] = (float)( sum_k (double)(z[t*K+k][n] * w[t][k]) ) over the live
+// slots in slot order (+ add[t][n] in fp32); out = res + moe.  A slot is dead
+// when a caller-supplied id of it lies outside [0, E): nothing wrote its z row.
+__device__ __forceinline__ bool combine_live(const CombineIds &ci, int64_t i) {
+    if (!ci.a) return true;
+    const int a = ci.a[i], b = ci.b[i];
+    return ((unsigned)a < (unsigned)ci.E) & ((unsigned)b < (unsigned)ci.E);
+}
+
 __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ z, const float *__restrict__ w,
-                                                 const float *res, float *out, int64_t T, int K, int D) {
+                                                 const float *res, float *out, int64_t T, int K, int D,
+                                                 CombineIds ci, const float *__restrict__ add) {
     const int64_t total = T * (int64_t)D;
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (int64_t)gridDim.x * blockDim.x) {
@@ -639,10 +663,12 @@ __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ z, co
         const int n = (int)(idx - t * D);
         double s = 0.0;
         for (int k = 0; k < K; ++k) {
+            if (!combine_live(ci, t * K + k)) continue;
             const float prod = z[(t * K + k) * D + n] * w[t * K + k];
             s = s + (double)prod;
         }
-        const float moe = (float)s;
+        float moe = (float)s;
+        if (add) moe = moe + add[idx];
         out[idx] = res ? res[idx] + moe : moe;
     }
 }
@@ -652,7 +678,7 @@ __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ z, co
 template <int KMAX>
 __global__ void __launch_bounds__(256) k_combine4(const float *__restrict__ z, const float *__restrict__ w,
                                                   const float *__restrict__ res, float *__restrict__ out, int K,
-                                                  int D) {
+                                                  int D, CombineIds ci, const float *__restrict__ add) {
     const int64_t t = blockIdx.y;
     const int n = 4 * ((int)blockIdx.x * 256 + (int)threadIdx.x);
     if (n >= D) return;
@@ -663,7 +689,7 @@ __global__ void __launch_bounds__(256) k_combine4(const float *__restrict__ z, c
     double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
 #pragma unroll
     for (int k = 0; k < KMAX; ++k) {
-        if (k < K) {
+        if (k < K && combine_live(ci, t * K + k)) {
             const float wk = w[t * K + k];
             s0 = s0 + (double)(zv[k].x * wk);
             s1 = s1 + (double)(zv[k].y * wk);
@@ -672,6 +698,10 @@ __global__ void __launch_bounds__(256) k_combine4(const float *__restrict__ z, c
         }
     }
     float4 o = make_float4((float)s0, (float)s1, (float)s2, (float)s3);
+    if (add) {
+        const float4 a = *(const float4 *)(add + t * D + n);
+        o.x = o.x + a.x; o.y = o.y + a.y; o.z = o.z + a.z; o.w = o.w + a.w;
+    }
     if (res) {
         const float4 r = *(const float4 *)(res + t * D + n);
         o.x = r.x + o.x; o.y = r.y + o.y; o.z = r.z + o.z; o.w = r.w + o.w;
@@ -680,19 +710,37 @@ __global__ void __launch_bounds__(256) k_combine4(const float *__restrict__ z, c
 }
 
 int launch_combine(const float *z, const float *w, const float *res, float *out, int64_t T, int K, int D,
-                   hipStream_t st) {
+                   hipStream_t st, const CombineIds &ci, const float *add) {
     if (T <= 0) return 0;
     const bool vec = D % 4 == 0 && (uintptr_t)z % 16 == 0 && (uintptr_t)out % 16 == 0 &&
-                     (!res || (uintptr_t)res % 16 == 0) && T <= 65535;
+                     (!res || (uintptr_t)res % 16 == 0) && (!add || (uintptr_t)add % 16 == 0) && T <= 65535;
     if (vec && K <= 16) {
         const dim3 grid((unsigned)((D / 4 + 255) / 256), (unsigned)T);
-        if (K <= 8) hipLaunchKernelGGL(k_combine4<8>, grid, dim3(256), 0, st, z, w, res, out, K, D);
-        else hipLaunchKernelGGL(k_combine4<16>, grid, dim3(256), 0, st, z, w, res, out, K, D);
+        if (K <= 8) hipLaunchKernelGGL(k_combine4<8>, grid, dim3(256), 0, st, z, w, res, out, K, D, ci, add);
+        else hipLaunchKernelGGL(k_combine4<16>, grid, dim3(256), 0, st, z, w, res, out, K, D, ci, add);
         return hip_check_launch();
     }
     const int64_t total = T * (int64_t)D;
     const int64_t blocks = (total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192;
-    hipLaunchKernelGGL(k_combine, dim3((unsigned)blocks), dim3(256), 0, st, z, w, res, out, T, K, D);
+    hipLaunchKernelGGL(k_combine, dim3((unsigned)blocks), dim3(256), 0, st, z, w, res, out, T, K, D, ci, add);
+    return hip_check_launch();
+}
+
+// ---------------------------------------------------------------- shared expert
+// The shared expert runs as a one-expert layer whose every token selects
+// expert 0 with weight 1, or with the sigmoid of its scalar gate row
+// (qwen3omni_talker.cpp:399-401), evaluated in fp64 and rounded once.
+__global__ void __launch_bounds__(256) k_shared_gate(const float *__restrict__ logit, int64_t T,
+                                                     int32_t *__restrict__ ids, float *__restrict__ w) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= T) return;
+    ids[t] = 0;
+    w[t] = logit ? gating_sigmoid(logit[t]) : 1.f;
+}
+
+int launch_shared_gate(const float *logit, int64_t T, int32_t *ids, float *w, hipStream_t st) {
+    if (T <= 0) return 0;
+    hipLaunchKernelGGL(k_shared_gate, dim3((unsigned)((T + 255) / 256)), dim3(256), 0, st, logit, T, ids, w);
     return hip_check_launch();
 }
 

@@ -34,6 +34,7 @@ struct Q8Out {
     int order = 0;               // 0: 16x16x32 K order, 1: 32x32x16 K order
     int exact = 0;               // 1: xh holds the codes q (exact), d8 and xbs the scales / block sums
     _Float16 *xbs = nullptr;     // [rows][K/16] block sums of 16 codes, as fp16 (exact)
+    int pre_act = 0;             // 4 (ACT_RELU_SQR): quantize relu(v)^2 instead of v
 };
 // quantize rows of src (row r at src + r*ld floats) to Q8_K
 int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, const Q8Out &o, hipStream_t st);
@@ -60,6 +61,9 @@ struct Dispatch {
     int32_t *active_e;   // [E] experts with count > 0, ascending
     int32_t *n_active;   // [1]
     int32_t *bad_ids;    // [1] number of ids outside [0, E) (skipped)
+    int32_t *bad_total;  // [1] or null: running count of such ids (never reset by the kernel)
+    float *zero_rows;    // or null: row p (p = flat id index) of zero_n floats at zero_rows + p * zero_ld
+    int64_t zero_ld, zero_n;   // is zeroed for every id outside [0, E)
 };
 // balanced = 0: per expert floor(cnt / BM) full tiles, then one partial tile
 // per expert with cnt % BM rows (largest first); balanced = 1: per expert
@@ -68,9 +72,17 @@ struct Dispatch {
 int launch_dispatch(const int32_t *ids, int64_t T, int K, int E, int BM, int balanced, const Dispatch &d,
                     hipStream_t st);
 
-// out[t][n] = res[t][n] + sum_k (double)(z[t*K+k][n] * w[t][k])   (res may be NULL)
+// out[t][n] = res[t][n] + (sum_k (double)(z[t*K+k][n] * w[t][k]) + add[t][n])   (res, add may be NULL)
+// ids_a / ids_b (or null): slot k of token t is live only if both ids lie in
+// [0, E); dead slots add nothing
+struct CombineIds {
+    const int32_t *a = nullptr, *b = nullptr;
+    int E = 0;
+};
 int launch_combine(const float *z, const float *w, const float *res, float *out, int64_t T, int K, int D,
-                   hipStream_t st);
+                   hipStream_t st, const CombineIds &ids = CombineIds{}, const float *add = nullptr);
+// shared expert's routing: ids[t] = 0, w[t] = logit ? fl32(1 / (1 + exp(-logit[t]))) (fp64) : 1
+int launch_shared_gate(const float *logit, int64_t T, int32_t *ids, float *w, hipStream_t st);
 
 // ---- expert products
 struct ExpertMat {

@@ -229,8 +229,11 @@ __device__ inline void wave_lds_sync() {
 // and takes the softmax over the K selected; kind 1 ranks s + sel_bias[e]
 // with s = fl32(1 / (1 + exp(-logit))) evaluated in fp64 (one rounding, so
 // every implementation ranks the same values) and weights s / (fl32(sum_K
-// s in fp64, slot order) + eps) * scaling; expert_scale[e] multiplies the
-// weights of either kind.
+// s in fp64, slot order) + eps) * scaling; kind 2 ranks the probabilities of
+// the softmax over all E (ggml_soft_max: max, e = fl32(exp(fl32(l - max)))
+// with the exp in fp64, the e summed in fp64 in expert order, p = e *
+// fl32(1 / sum)) and weights p / fl32(sum_K p in fp64, slot order);
+// expert_scale[e] multiplies the weights of every kind.
 struct Gating {
     int kind = 0;
     const float *sel_bias = nullptr;
@@ -254,6 +257,32 @@ __device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane,
         } else {
             v[i] = -INFINITY;
         }
+    }
+    if (gt.kind == 2) {
+        float mx = v[0];
+#pragma unroll
+        for (int i = 1; i < TOPK_MAX_PER_LANE; ++i) mx = fmaxf(mx, v[i]);
+        mx = wave_max(mx);
+        float ex[TOPK_MAX_PER_LANE];
+#pragma unroll
+        for (int i = 0; i < TOPK_MAX_PER_LANE; ++i)
+            ex[i] = lane + 64 * i < E ? (float)exp((double)(v[i] - mx)) : 0.f;
+        // the sum in expert order e = 64 i + lane: uniform lane reads
+        double sum = 0.0;
+#pragma unroll
+        for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
+            if (i >= nper) break;
+            const int eb = __builtin_bit_cast(int, ex[i]);
+            for (int j = 0; j < 64; ++j) sum = sum + (double)__builtin_bit_cast(float, __builtin_amdgcn_readlane(eb, j));
+        }
+        const float inv = (float)(1.0 / sum);
+#pragma unroll
+        for (int i = 0; i < TOPK_MAX_PER_LANE; ++i)
+            if (lane + 64 * i < E) v[i] = ex[i] * inv;
+    }
+#pragma unroll
+    for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
+        const int e = lane + 64 * i;
         if (e < E4) sv[e] = v[i];
     }
     wave_lds_sync();
@@ -285,6 +314,11 @@ __device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane,
         double sum = 0.0;
         for (int k = 0; k < K; ++k) sum = sum + (double)__shfl(s, k, 64);
         myw = s / ((float)sum + gt.eps) * gt.scaling;
+    } else if (gt.kind == 2) {
+        const float p = lane < K ? sv[mysel] : 0.f;
+        double sum = 0.0;
+        for (int k = 0; k < K; ++k) sum = sum + (double)__shfl(p, k, 64);
+        myw = p / (float)sum;
     } else {
         const float myval = lane < K ? sv[mysel] : 0.f;
         myw = softmax_selected_wave(myval, K, lane);

@@ -244,8 +244,65 @@ Tensor *build_expert_ffn(Session &s, Tensor *x, const std::vector<Tensor *> &gat
 // 4.1931758] (hand-computed there); a w with the wrong row count gives
 // nullptr.  Added: the same answer through the slot-table form, the residual
 // split (res != x), and the table form's argument checks.
+//
+// `vqa_moe_selftest --table DIR` instead runs build_expert_ffn_table_res on
+// tables read from DIR (meta.txt: T D I E K gate_type down_type act same_ids
+// gemm_threshold; x.bin res.bin gate.bin up.bin down.bin ids_gu.bin
+// [ids_dn.bin] w.bin, raw little-endian) and writes out.bin: a caller's
+// check of the table form on any table type and id pattern.
 #include <cmath>
 #include <cstdio>
+#include <string>
+
+static bool load_into(vqa::moe::Session &s, vqa::moe::Tensor *t, const std::string &path, size_t bytes) {
+    if (!t) return false;
+    std::FILE *f = std::fopen(path.c_str(), "rb");
+    if (!f) return false;
+    std::vector<char> buf(bytes);
+    const size_t got = std::fread(buf.data(), 1, bytes, f);
+    std::fclose(f);
+    return got == bytes && s.set(t, buf.data(), bytes) == 0;
+}
+
+static int table_mode(const std::string &dir) {
+    long T, D, I, E, K, gt, dt, act, same, thr;
+    std::FILE *m = std::fopen((dir + "/meta.txt").c_str(), "r");
+    if (!m) return 2;
+    const int n = std::fscanf(m, "%ld %ld %ld %ld %ld %ld %ld %ld %ld %ld", &T, &D, &I, &E, &K, &gt, &dt, &act, &same, &thr);
+    std::fclose(m);
+    if (n != 10) return 2;
+    vqa::moe::Session s(0);
+    if (s.status()) return 3;
+    using vqa::moe::Tensor;
+    Tensor *x = s.new_tensor(MI_TYPE_F32, D, T), *res = s.new_tensor(MI_TYPE_F32, D, T);
+    Tensor *g = s.new_tensor((int)gt, D, I, E), *u = s.new_tensor((int)gt, D, I, E), *d = s.new_tensor((int)dt, I, D, E);
+    Tensor *ig = s.new_tensor(MI_TYPE_I32, K, T);
+    Tensor *id = same ? ig : s.new_tensor(MI_TYPE_I32, K, T);
+    Tensor *w = s.new_tensor(MI_TYPE_F32, K, T);
+    bool ok = x && res && g && u && d && ig && id && w;
+    ok = ok && load_into(s, x, dir + "/x.bin", x->nb[3]) && load_into(s, res, dir + "/res.bin", res->nb[3]);
+    ok = ok && load_into(s, g, dir + "/gate.bin", g->nb[3]) && load_into(s, u, dir + "/up.bin", u->nb[3]);
+    ok = ok && load_into(s, d, dir + "/down.bin", d->nb[3]) && load_into(s, ig, dir + "/ids_gu.bin", ig->nb[3]);
+    ok = ok && (same || load_into(s, id, dir + "/ids_dn.bin", id->nb[3])) && load_into(s, w, dir + "/w.bin", w->nb[3]);
+    if (!ok) return 4;
+    if (mi_moe_ctx_set_gemm_threshold(s.ctx(), thr)) return 5;
+    const vqa::moe::UnaryOp op = act == 0 ? vqa::moe::UnaryOp::SILU
+                                 : act == 1 ? vqa::moe::UnaryOp::GELU : vqa::moe::UnaryOp::GELU_ERF;
+    Tensor *out = vqa::moe::build_expert_ffn_table_res(s, x, res, g, u, d, ig, id, w, op);
+    if (!out || s.compute()) {
+        std::fprintf(stderr, "table build failed: status %d\n", s.status());
+        return 6;
+    }
+    std::vector<char> o(out->nb[3]);
+    if (s.get(out, o.data(), o.size())) return 7;
+    std::FILE *f = std::fopen((dir + "/out.bin").c_str(), "wb");
+    if (!f) return 8;
+    const size_t wr = std::fwrite(o.data(), 1, o.size(), f);
+    std::fclose(f);
+    std::fprintf(stderr, "table mode: T=%ld D=%ld I=%ld E=%ld K=%ld types %ld/%ld, %s ids: wrote out.bin\n", T, D, I,
+                 E, K, gt, dt, same ? "one" : "two");
+    return wr == o.size() ? 0 : 9;
+}
 
 static int g_fail = 0;
 #define CHECK(cond, msg)                                               \
@@ -258,7 +315,8 @@ static int g_fail = 0;
 
 using vqa::moe::Tensor;
 
-int main(void) {
+int main(int argc, char **argv) {
+    if (argc == 3 && std::string(argv[1]) == "--table") return table_mode(argv[2]);
     vqa::moe::Session s(0);
     CHECK(s.status() == 0, "session");
     if (s.status()) return 1;

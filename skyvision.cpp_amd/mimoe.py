@@ -17,9 +17,10 @@ LIB_PATH = HERE / "libmimoe.so"
 DECODE_CHAIN, DECODE_FUSED_COOPERATIVE, DECODE_FUSED_EXCLUSIVE = 0, 1, 2
 
 TYPE_F32, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K, TYPE_I32 = 0, 1, 12, 14, 26
-ACT_SILU, ACT_GELU_ERF_GP1, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2, 3
+ACT_SILU, ACT_GELU_ERF_GP1, ACT_GELU_TANH, ACT_GELU_ERF, ACT_RELU_SQR = 0, 1, 2, 3, 4
 NORM_NONE, NORM_RMS, NORM_LAYER = 0, 1, 2
-GATING_SOFTMAX_TOPK, GATING_SIGMOID_BIAS = 0, 1
+GATING_SOFTMAX_TOPK, GATING_SIGMOID_BIAS, GATING_SOFTMAX_ALL = 0, 1, 2
+ABI_VERSION = 2
 # mi_moe_status
 OK, ERR_NULL, ERR_SHAPE, ERR_TYPE, ERR_CAPACITY, ERR_HIP = 0, -1, -2, -3, -4, -5
 ERR_UNSUPPORTED, ERR_DEVICE, ERR_ARG, ERR_FORMAT = -6, -7, -8, -9
@@ -53,7 +54,9 @@ class Layer(C.Structure):
     _fields_ = [("n_embd", i32), ("n_expert", i32), ("n_expert_used", i32), ("n_ff", i32),
                 ("router_w", P), ("router_b", P), ("gate", Tensor), ("up", Tensor),
                 ("down", Tensor), ("fused_gate_up", i32), ("act", i32), ("gating", i32),
-                ("sel_bias", P), ("expert_scale", P), ("routed_scaling", C.c_float), ("gate_eps", C.c_float)]
+                ("sel_bias", P), ("expert_scale", P), ("routed_scaling", C.c_float), ("gate_eps", C.c_float),
+                ("sh_n_ff", i32), ("sh_act", i32), ("sh_gate", Tensor), ("sh_up", Tensor), ("sh_down", Tensor),
+                ("sh_gate_inp", P)]
 
 
 class Norm(C.Structure):
@@ -81,6 +84,7 @@ SYMBOLS = {
     "mi_moe_ctx_create": ([C.POINTER(P), C.c_int], C.c_int),
     "mi_moe_ctx_destroy": ([P], None),
     "mi_moe_ctx_reserve": ([P, i64, i32, i32, i32, i32], C.c_int),
+    "mi_moe_ctx_take_errors": ([P, C.POINTER(i64), C.POINTER(i64)], C.c_int),
     "mi_moe_forward": ([P, C.POINTER(Layer), P, i64, P, P, C.POINTER(Routing), P], C.c_int),
     "mi_moe_expert_ffn": ([P, C.POINTER(Layer), P, i64, P, P, P, P, P, P], C.c_int),
     "mi_top_k": ([P, C.POINTER(Tensor), i32, C.POINTER(Tensor), P], C.c_int),
@@ -145,6 +149,8 @@ def load(path: str | None = None) -> C.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = res
+        if lib.mi_moe_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{p}: ABI {lib.mi_moe_abi_version()}, binding expects {ABI_VERSION}: rebuild")
         _lib = lib
     return _lib
 
@@ -266,6 +272,12 @@ class Context:
         """False / DECODE_CHAIN, True / DECODE_FUSED_COOPERATIVE, DECODE_FUSED_EXCLUSIVE"""
         m = DECODE_FUSED_COOPERATIVE if mode is True else DECODE_CHAIN if mode is False else int(mode)
         call("mi_moe_ctx_set_fused_decode", self.h, m)
+
+    def take_errors(self):
+        """(bad ids, fused-decode wait failures) since the last take; syncs the device."""
+        b, f = i64(), i64()
+        call("mi_moe_ctx_take_errors", self.h, C.byref(b), C.byref(f))
+        return b.value, f.value
 
     def set_profiling(self, on: bool) -> None:
         call("mi_moe_ctx_set_profiling", self.h, int(on))

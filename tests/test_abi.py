@@ -77,3 +77,25 @@ def test_status_codes_match_header():
     assert len(codes) == 10, codes
     for name, v in codes.items():
         assert getattr(M, name) == int(v), name
+
+
+def test_layer_struct_layout_matches_header(tmp_path):
+    """The binding's mi_moe_layer / mi_tensor mirrors have the C layout: a
+    program compiled against include/mi_moe.h prints sizeof and every field's
+    offset (gcc, host only)."""
+    import ctypes as Cty
+    import subprocess
+
+    import mimoe as M
+    fields = [f for f, _ in M.Layer._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "mi_moe.h"\nint main(void) {\n'
+                   '  printf("%zu %zu\\n", sizeof(mi_moe_layer), sizeof(mi_tensor));\n' +
+                   "".join(f'  printf("%zu\\n", offsetof(mi_moe_layer, {f}));\n' for f in fields) +
+                   "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    assert int(out[0]) == Cty.sizeof(M.Layer) and int(out[1]) == Cty.sizeof(M.Tensor)
+    for f, off in zip(fields, out[2:]):
+        assert getattr(M.Layer, f).offset == int(off), f

@@ -7,7 +7,9 @@ fused [h | g] ffn_up_exps Q4_K, ffn_down_exps Q6_K; convert_hf_to_gguf.py:
 173-183, moondream.cpp:149-172, 241-251) and qwen3omni (blk.N.ffn_router F32,
 ffn_gate_exps / ffn_up_exps / ffn_down_exps; convert_qwen3omni.py:188-219).
 CPU: parsing, metadata, tensor infos and every malformed-file error (no
-device).  GPU: a loaded layer's forward is bit-identical to the forward of
+device).  GPU: a loaded layer's forward matches the CPU oracle run on the
+tables the test wrote (the F16 router promoted to F32 by numpy): routing
+bit-exact, output rel-L2 <= 1e-2; and it is bit-identical to the forward of
 the same tables uploaded directly.
 """
 import pathlib
@@ -18,6 +20,7 @@ import pytest
 
 import mimoe as M
 import pyoracle as O
+from _util import max_abs, rel_l2
 
 GV_U32, GV_F32, GV_STR, GV_ARR = 4, 6, 8, 9
 
@@ -164,10 +167,23 @@ def test_gguf_layer_forward(tmp_path, style):
     x = np.random.default_rng(5).standard_normal((T, D)).astype(np.float32)
     xd = M.to_device(x)
     o1, o2 = M.DeviceBuffer(4 * T * D), M.DeviceBuffer(4 * T * D)
-    M.check("forward gguf", ctx.forward(L, xd, T, xd, o1))
+    sel = M.DeviceBuffer(4 * T * K)
+    r = M.Routing()
+    r.sel = sel.addr
+    M.check("forward gguf", ctx.forward(L, xd, T, xd, o1, r))
     M.check("forward direct", ctx.forward(Ld, xd, T, xd, o2))
     a, b = o1.download(np.float32, (T, D)), o2.download(np.float32, (T, D))
     assert np.isfinite(a).all() and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # the oracle on the written tables; router = the file's F16 values promoted by numpy
+    OL = dict(D=D, E=E, K=K, I=I, router_w=router, router_b=bias, gate_type=O.TYPE_Q4_K,
+              gate=np.frombuffer(t["up"] if fused else t["gate"], np.uint8),
+              up=None if fused else np.frombuffer(t["up"], np.uint8), fused=fused,
+              down_type=O.TYPE_Q6_K if fused else O.TYPE_Q4_K, down=np.frombuffer(t["down"], np.uint8), act=act)
+    ref, dbg = O.moe_forward(OL, x, x)
+    assert np.array_equal(sel.download(np.int32, (T, K)), dbg["sel"]), "routing of the loaded layer"
+    e = rel_l2(a - x, ref - x)
+    print(f"gguf {style}: loaded layer vs oracle rel-L2 {e:.3e} max-abs {max_abs(a, ref):.3e}", flush=True)
+    assert e <= 1e-2
     M.check("free", M.load().mi_dev_free(buf))
     g.close()
     ctx.close()

@@ -182,6 +182,25 @@ int mi_moe_forward(mi_moe_ctx *ctx, const mi_moe_layer *layer, const float *x, i
                    const float *res, float *out, const mi_moe_routing *routing,
                    mi_stream_t stream);
 
+/* ---- the block with no context and no allocation --------------------------
+ * No counterpart in the reference: mi_moe_forward for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It calls no hipMalloc / hipFree or any
+ * allocating routine: its workspace is one file-scope device array of the
+ * library per GPU, 16,678,656 bytes, held until the process ends, sized for
+ * calls of at most MI_NOALLOC_MAX_TOKENS tokens of layers with n_embd <= 2048,
+ * n_ff <= 1024, n_expert <= 128, n_expert_used <= 8 (a shared expert's
+ * sh_n_ff <= 8192); larger calls return MI_MOE_ERR_CAPACITY and enqueue
+ * nothing.  Single-token calls run the kernel chain (MI_DECODE_CHAIN) and the
+ * product path follows the default shape rule, so the results are bit for bit
+ * those of mi_moe_forward on a context in MI_DECODE_CHAIN mode.  Every call on
+ * a GPU uses that GPU's one array: calls that overlap on one GPU (other streams
+ * or host threads) race.  Each call writes every part of the array it reads,
+ * so nothing there has to start at zero. */
+#define MI_NOALLOC_MAX_TOKENS 64
+int mi_moe_forward_noalloc(const mi_moe_layer *layer, const float *x, int64_t n_tokens, const float *res,
+                           float *out, const mi_moe_routing *routing, mi_stream_t stream);
+
 /* ---- norm + MoE block in one call ----------------------------------------
  * out[t] = res[t] + MoE(norm(h[t])): the reference's ffn_norm followed by its
  * MoE block (moondream.cpp:405-407 + 509-547; qwen3omni_model.cpp:756-780),

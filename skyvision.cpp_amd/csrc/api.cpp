@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/mi_moe.h"
@@ -467,8 +468,97 @@ T *carve(char *&p, size_t n) {
     return r;
 }
 template <typename T>
-size_t carve_size(size_t n) {
+constexpr size_t carve_size(size_t n) {
     return (sizeof(T) * n + 255) & ~(size_t)255;
+}
+
+// Workspace of a context sized for max_tokens tokens of layers up to these
+// dims: every piece 256-byte aligned, in the order carve_workspace lays them out.
+constexpr size_t ws_bytes(int64_t max_tokens, int64_t D, int64_t I, int64_t E, int64_t K) {
+    const int64_t rows = max_tokens * K;
+    const int64_t kmax = D > I ? D : I;
+    const int64_t kmax_q = (kmax + QK - 1) / QK * QK;
+    const int64_t wide = (D > 2 * I ? D : 2 * I) > kmax ? (D > 2 * I ? D : 2 * I) : kmax;
+    const int64_t tiles = (rows + GEMM_BM - 1) / GEMM_BM + (E < rows ? E : rows);
+    const int64_t iq = (I + QK - 1) / QK * QK;
+    size_t need = 0;
+    need += carve_size<float>(max_tokens * E) + carve_size<int32_t>(rows) + carve_size<float>(rows);
+    need += carve_size<float>(max_tokens * D);
+    for (int s = 0; s < 2; ++s)
+        need += carve_size<int32_t>(E) + carve_size<int32_t>(E + 1) + carve_size<int32_t>(rows) +
+                2 * carve_size<int32_t>(tiles) + carve_size<int32_t>(1) + carve_size<int32_t>(E) +
+                2 * carve_size<int32_t>(1);
+    need += carve_size<int32_t>(1);
+    // activation sets: x/b rows (rows x kmax) and act rows (rows x I)
+    need += carve_size<int8_t>(rows * kmax_q) + carve_size<float>(rows * kmax_q / QK) +
+            carve_size<int16_t>(rows * kmax_q / 16) + carve_size<_Float16>(rows * kmax_q) +
+            carve_size<_Float16>(rows * kmax_q / 16);
+    need += carve_size<int8_t>(rows * iq) + carve_size<float>(rows * iq / QK) +
+            carve_size<int16_t>(rows * iq / 16) + carve_size<_Float16>(rows * iq);
+    need += carve_size<float>(rows * wide) + carve_size<float>(rows * I) + carve_size<float>(rows * wide);
+    need += carve_size<uint64_t>(DEC_TW_WORDS) + carve_size<uint32_t>(DEC_MAX_GRID) +
+            carve_size<unsigned long long>(DEC_SYNC_WORDS) + carve_size<unsigned>(1);
+    need += carve_size<float>(max_tokens * D) + 2 * carve_size<float>(max_tokens) + carve_size<int32_t>(max_tokens);
+    return need;
+}
+
+// Lays the workspace of ws_bytes(...) bytes at base out into c's pointers and
+// records the capacities; false if the layout and ws_bytes disagree.
+bool carve_workspace(mi_moe_ctx *c, char *base, int64_t max_tokens, int32_t D, int32_t I, int32_t E, int32_t K) {
+    const int64_t rows = max_tokens * K;
+    const int64_t kmax = std::max<int64_t>(D, I);
+    const int64_t kmax_q = (kmax + QK - 1) / QK * QK;
+    const int64_t wide = std::max<int64_t>(std::max<int64_t>(D, 2LL * I), kmax);
+    const int64_t tiles = (rows + GEMM_BM - 1) / GEMM_BM + std::min<int64_t>(E, rows);
+    const int64_t iq = (I + QK - 1) / QK * QK;
+    char *q = base;
+    c->logits = carve<float>(q, max_tokens * E);
+    c->sel = carve<int32_t>(q, rows);
+    c->w = carve<float>(q, rows);
+    c->xn = carve<float>(q, max_tokens * D);
+    for (int s = 0; s < 2; ++s) {
+        DispBuf &d = c->disp[s];
+        d.counts = carve<int32_t>(q, E);
+        d.offsets = carve<int32_t>(q, E + 1);
+        d.perm = carve<int32_t>(q, rows);
+        d.tile_e = carve<int32_t>(q, tiles);
+        d.tile_r0 = carve<int32_t>(q, tiles);
+        d.n_tiles = carve<int32_t>(q, 1);
+        d.active_e = carve<int32_t>(q, E);
+        d.n_active = carve<int32_t>(q, 1);
+        d.bad = carve<int32_t>(q, 1);
+    }
+    c->bad_total = carve<int32_t>(q, 1);
+    c->disp[0].bad_total = c->disp[1].bad_total = c->bad_total;
+    c->ax.q8 = carve<int8_t>(q, rows * kmax_q);
+    c->ax.d8 = carve<float>(q, rows * kmax_q / QK);
+    c->ax.bs = carve<int16_t>(q, rows * kmax_q / 16);
+    c->ax.h = carve<_Float16>(q, rows * kmax_q);
+    c->ax.bsh = carve<_Float16>(q, rows * kmax_q / 16);
+    c->aact.q8 = carve<int8_t>(q, rows * iq);
+    c->aact.d8 = carve<float>(q, rows * iq / QK);
+    c->aact.bs = carve<int16_t>(q, rows * iq / 16);
+    c->aact.h = carve<_Float16>(q, rows * iq);
+    c->f1 = carve<float>(q, rows * wide);
+    c->f2 = carve<float>(q, rows * I);
+    c->z = carve<float>(q, rows * wide);
+    c->dec_tw = carve<uint64_t>(q, DEC_TW_WORDS);
+    c->dec_epoch = carve<uint32_t>(q, DEC_MAX_GRID);
+    c->dec_sync = carve<unsigned long long>(q, DEC_SYNC_WORDS);
+    c->dec_err = carve<unsigned>(q, 1);
+    c->sh_out = carve<float>(q, max_tokens * D);
+    c->sh_w = carve<float>(q, max_tokens);
+    c->sh_logit = carve<float>(q, max_tokens);
+    c->sh_ids = carve<int32_t>(q, max_tokens);
+    c->cap_T = max_tokens;
+    c->cap_D = D;
+    c->cap_I = I;
+    c->cap_E = E;
+    c->cap_K = K;
+    c->cap_rows = rows;
+    c->cap_kmax = kmax_q;
+    c->cap_tiles = tiles;
+    return (size_t)(q - base) == ws_bytes(max_tokens, D, I, E, K);
 }
 
 }  // namespace
@@ -531,31 +621,7 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
     if (max_tokens <= 0 || D <= 0 || I <= 0 || E <= 0 || K <= 0 || K > E) return MI_MOE_ERR_SHAPE;
     if (E > 256 || K > 64) return MI_MOE_ERR_UNSUPPORTED;
     HIP_TRY(hipSetDevice(c->device));
-    const int64_t rows = max_tokens * K;
-    const int64_t kmax = std::max<int64_t>(D, I);
-    const int64_t kmax_q = (kmax + QK - 1) / QK * QK;
-    const int64_t wide = std::max<int64_t>(std::max<int64_t>(D, 2LL * I), kmax);
-    const int64_t tiles = (rows + GEMM_BM - 1) / GEMM_BM + std::min<int64_t>(E, rows);
-    size_t need = 0;
-    need += carve_size<float>(max_tokens * E) + carve_size<int32_t>(rows) + carve_size<float>(rows);
-    need += carve_size<float>(max_tokens * D);
-    for (int s = 0; s < 2; ++s)
-        need += carve_size<int32_t>(E) + carve_size<int32_t>(E + 1) + carve_size<int32_t>(rows) +
-                2 * carve_size<int32_t>(tiles) + carve_size<int32_t>(1) + carve_size<int32_t>(E) +
-                2 * carve_size<int32_t>(1);
-    // activation sets: x/b rows (rows x kmax) and act rows (rows x I)
-    need += carve_size<int8_t>(rows * kmax_q) + carve_size<float>(rows * kmax_q / QK) +
-            carve_size<int16_t>(rows * kmax_q / 16) + carve_size<_Float16>(rows * kmax_q) +
-            carve_size<_Float16>(rows * kmax_q / 16);
-    const int64_t iq = (I + QK - 1) / QK * QK;
-    need += carve_size<int8_t>(rows * iq) + carve_size<float>(rows * iq / QK) +
-            carve_size<int16_t>(rows * iq / 16) + carve_size<_Float16>(rows * iq);
-    need += carve_size<float>(rows * wide) + carve_size<float>(rows * I) + carve_size<float>(rows * wide);
-    need += carve_size<uint64_t>(DEC_TW_WORDS) + carve_size<uint32_t>(DEC_MAX_GRID) +
-            carve_size<unsigned long long>(DEC_SYNC_WORDS) + carve_size<unsigned>(1);
-    need += carve_size<float>(max_tokens * D) + 2 * carve_size<float>(max_tokens) + carve_size<int32_t>(max_tokens) +
-            carve_size<int32_t>(1);
-
+    const size_t need = ws_bytes(max_tokens, D, I, E, K);
     if (c->ws) {
         (void)hipFree(c->ws);
         c->ws = nullptr;
@@ -565,54 +631,8 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
     HIP_TRY(hipMalloc(&p, need));
     c->ws = p;
     c->ws_bytes = need;
-    char *q = (char *)p;
-    c->logits = carve<float>(q, max_tokens * E);
-    c->sel = carve<int32_t>(q, rows);
-    c->w = carve<float>(q, rows);
-    c->xn = carve<float>(q, max_tokens * D);
-    for (int s = 0; s < 2; ++s) {
-        DispBuf &d = c->disp[s];
-        d.counts = carve<int32_t>(q, E);
-        d.offsets = carve<int32_t>(q, E + 1);
-        d.perm = carve<int32_t>(q, rows);
-        d.tile_e = carve<int32_t>(q, tiles);
-        d.tile_r0 = carve<int32_t>(q, tiles);
-        d.n_tiles = carve<int32_t>(q, 1);
-        d.active_e = carve<int32_t>(q, E);
-        d.n_active = carve<int32_t>(q, 1);
-        d.bad = carve<int32_t>(q, 1);
-    }
-    c->bad_total = carve<int32_t>(q, 1);
-    c->disp[0].bad_total = c->disp[1].bad_total = c->bad_total;
-    c->ax.q8 = carve<int8_t>(q, rows * kmax_q);
-    c->ax.d8 = carve<float>(q, rows * kmax_q / QK);
-    c->ax.bs = carve<int16_t>(q, rows * kmax_q / 16);
-    c->ax.h = carve<_Float16>(q, rows * kmax_q);
-    c->ax.bsh = carve<_Float16>(q, rows * kmax_q / 16);
-    c->aact.q8 = carve<int8_t>(q, rows * iq);
-    c->aact.d8 = carve<float>(q, rows * iq / QK);
-    c->aact.bs = carve<int16_t>(q, rows * iq / 16);
-    c->aact.h = carve<_Float16>(q, rows * iq);
-    c->f1 = carve<float>(q, rows * wide);
-    c->f2 = carve<float>(q, rows * I);
-    c->z = carve<float>(q, rows * wide);
-    c->dec_tw = carve<uint64_t>(q, DEC_TW_WORDS);
-    c->dec_epoch = carve<uint32_t>(q, DEC_MAX_GRID);
-    c->dec_sync = carve<unsigned long long>(q, DEC_SYNC_WORDS);
-    c->dec_err = carve<unsigned>(q, 1);
-    c->sh_out = carve<float>(q, max_tokens * D);
-    c->sh_w = carve<float>(q, max_tokens);
-    c->sh_logit = carve<float>(q, max_tokens);
-    c->sh_ids = carve<int32_t>(q, max_tokens);
+    if (!carve_workspace(c, (char *)p, max_tokens, D, I, E, K)) return MI_MOE_ERR_UNSUPPORTED;
     HIP_TRY(hipMemset(p, 0, need));
-    c->cap_T = max_tokens;
-    c->cap_D = D;
-    c->cap_I = I;
-    c->cap_E = E;
-    c->cap_K = K;
-    c->cap_rows = rows;
-    c->cap_kmax = kmax_q;
-    c->cap_tiles = tiles;
     c->reserved = true;
     return MI_MOE_OK;
 }
@@ -670,6 +690,8 @@ int mi_moe_ctx_stage_times(mi_moe_ctx *c, int max_stages, const char **names, fl
     *n_stages = n;
     return MI_MOE_OK;
 }
+
+}  // extern "C"
 
 namespace {
 
@@ -756,8 +778,77 @@ int norm_params(const mi_moe_norm *norm, NormParams &np) {
 
 }  // namespace
 
+extern "C" {
+
 int mi_moe_forward(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const float *res,
                    float *out, const mi_moe_routing *routing, mi_stream_t stream) {
+    return forward_impl(c, L, x, T, res, out, routing, NormParams{}, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------- no allocation
+// mi_moe_forward_noalloc: the workspace of a context reserved for the limits
+// below lives in one file-scope device array per GPU (scratch).  In host code
+// `scratch` names a host-side stand-in, not device memory: the array's device
+// address comes from hipGetSymbolAddress, once per device with that device
+// current (the first call on it), and only that address is used.  Single
+// tokens run the kernel chain (no grid-wide waits, no cooperative launch), and
+// every buffer a call reads it writes first in the same call, so nothing in
+// the array has to start at zero.
+}  // extern "C"
+
+namespace {
+constexpr int64_t NA_T = MI_NOALLOC_MAX_TOKENS;
+constexpr int32_t NA_D = 2048, NA_I = 1024, NA_E = 128, NA_K = 8;
+constexpr size_t NA_BYTES = ws_bytes(NA_T, NA_D, NA_I, NA_E, NA_K);
+constexpr int NA_MAX_DEVICES = 64;
+
+struct NoallocDevice {
+    std::once_flag once;
+    int status = MI_MOE_OK;
+    mi_moe_ctx ctx;   // workspace pointers into this device's scratch; never destroyed
+};
+NoallocDevice g_noalloc[NA_MAX_DEVICES];
+}  // namespace
+
+static __device__ __attribute__((aligned(256))) char scratch[NA_BYTES];
+
+namespace {
+int noalloc_ctx(mi_moe_ctx **out) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= NA_MAX_DEVICES) return MI_MOE_ERR_DEVICE;
+    NoallocDevice &d = g_noalloc[dev];
+    std::call_once(d.once, [&d, dev] {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            d.status = e != hipSuccess ? record_hip_error(e) : MI_MOE_ERR_HIP;
+            return;
+        }
+        mi_moe_ctx &c = d.ctx;
+        c.device = dev;
+        c.fused_decode = MI_DECODE_CHAIN;
+        c.ws = nullptr;   // not owned
+        c.ws_bytes = NA_BYTES;
+        if (!carve_workspace(&c, (char *)ptr, NA_T, NA_D, NA_I, NA_E, NA_K)) {
+            d.status = MI_MOE_ERR_UNSUPPORTED;
+            return;
+        }
+        c.reserved = true;
+    });
+    if (d.status) return d.status;
+    *out = &d.ctx;
+    return MI_MOE_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int mi_moe_forward_noalloc(const mi_moe_layer *L, const float *x, int64_t T, const float *res, float *out,
+                           const mi_moe_routing *routing, mi_stream_t stream) {
+    if (!L) return MI_MOE_ERR_NULL;
+    mi_moe_ctx *c = nullptr;
+    TRY(noalloc_ctx(&c));
     return forward_impl(c, L, x, T, res, out, routing, NormParams{}, (hipStream_t)stream);
 }
 

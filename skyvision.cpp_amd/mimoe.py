@@ -86,6 +86,7 @@ SYMBOLS = {
     "mi_moe_ctx_reserve": ([P, i64, i32, i32, i32, i32], C.c_int),
     "mi_moe_ctx_take_errors": ([P, C.POINTER(i64), C.POINTER(i64)], C.c_int),
     "mi_moe_forward": ([P, C.POINTER(Layer), P, i64, P, P, C.POINTER(Routing), P], C.c_int),
+    "mi_moe_forward_noalloc": ([C.POINTER(Layer), P, i64, P, P, C.POINTER(Routing), P], C.c_int),
     "mi_moe_expert_ffn": ([P, C.POINTER(Layer), P, i64, P, P, P, P, P, P], C.c_int),
     "mi_top_k": ([P, C.POINTER(Tensor), i32, C.POINTER(Tensor), P], C.c_int),
     "mi_mul_mat_id": ([P, C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor),
@@ -338,6 +339,16 @@ class Context:
             self.close()
         except Exception:
             pass
+
+
+NOALLOC_MAX_TOKENS = 64
+
+
+def forward_noalloc(layer: Layer, x, T: int, res, out, routing: Routing | None = None, stream=None) -> int:
+    """mi_moe_forward_noalloc: the forward with the library's per-GPU static
+    workspace (no context, no allocation)."""
+    return load().mi_moe_forward_noalloc(C.byref(layer), _addr(x), T, _addr(res), _addr(out),
+                                         C.byref(routing) if routing is not None else None, _addr(stream))
 
 
 def _addr(x):

@@ -66,11 +66,12 @@ struct ActBuf {                // one Q8_K activation set
 };
 
 struct DispBuf {
-    int32_t *counts, *offsets, *perm, *tile_e, *tile_r0, *n_tiles, *active_e, *n_active, *bad;
+    int32_t *counts, *offsets, *perm, *tile_e, *tile_r0, *tile_start, *tile_rows, *n_tiles, *active_e, *n_active, *bad;
     int32_t *bad_total;   // the context's running count (mi_moe_ctx_take_errors)
     Dispatch view() const {
         Dispatch d;
         d.counts = counts; d.offsets = offsets; d.perm = perm; d.tile_e = tile_e; d.tile_r0 = tile_r0;
+        d.tile_start = tile_start; d.tile_rows = tile_rows;
         d.n_tiles = n_tiles; d.active_e = active_e; d.n_active = n_active; d.bad_ids = bad;
         d.bad_total = bad_total; d.zero_rows = nullptr; d.zero_ld = 0; d.zero_n = 0;
         return d;
@@ -395,7 +396,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         a.a = gate; a.b = up; a.glu = gated ? 1 : 0; a.fused = L->fused_gate_up; a.act = L->act; a.I = I;
         a.xh = c->ax.h; a.ne11 = 1; a.K = K;
         a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.tile_e = dg.tile_e;
-        a.tile_r0 = dg.tile_r0; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
+        a.tile_r0 = dg.tile_r0; a.tile_start = dg.tile_start; a.tile_rows = dg.tile_rows; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
         a.y = c->f1; a.ldy = I; a.ncols = I; a.xrows = T;
         TRY(launch_gemm4(a, st));
         stage_end(c, "gate_up", st);
@@ -406,7 +407,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         G2Args d = {};
         d.a = down; d.glu = 0; d.xh = c->aact.h; d.ne11 = K; d.K = K;
         d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
-        d.tile_r0 = dd.tile_r0; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles; d.xrows = (int64_t)T * K;
+        d.tile_r0 = dd.tile_r0; d.tile_start = dd.tile_start; d.tile_rows = dd.tile_rows; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles; d.xrows = (int64_t)T * K;
         d.y = c->z; d.ldy = D; d.ncols = D;
         TRY(launch_gemm4(d, st));
         stage_end(c, "down", st);
@@ -486,7 +487,7 @@ constexpr size_t ws_bytes(int64_t max_tokens, int64_t D, int64_t I, int64_t E, i
     need += carve_size<float>(max_tokens * D);
     for (int s = 0; s < 2; ++s)
         need += carve_size<int32_t>(E) + carve_size<int32_t>(E + 1) + carve_size<int32_t>(rows) +
-                2 * carve_size<int32_t>(tiles) + carve_size<int32_t>(1) + carve_size<int32_t>(E) +
+                4 * carve_size<int32_t>(tiles) + carve_size<int32_t>(1) + carve_size<int32_t>(E) +
                 2 * carve_size<int32_t>(1);
     need += carve_size<int32_t>(1);
     // activation sets: x/b rows (rows x kmax) and act rows (rows x I)
@@ -523,6 +524,8 @@ bool carve_workspace(mi_moe_ctx *c, char *base, int64_t max_tokens, int32_t D, i
         d.perm = carve<int32_t>(q, rows);
         d.tile_e = carve<int32_t>(q, tiles);
         d.tile_r0 = carve<int32_t>(q, tiles);
+        d.tile_start = carve<int32_t>(q, tiles);
+        d.tile_rows = carve<int32_t>(q, tiles);
         d.n_tiles = carve<int32_t>(q, 1);
         d.active_e = carve<int32_t>(q, E);
         d.n_active = carve<int32_t>(q, 1);
@@ -963,7 +966,7 @@ int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const 
     G2Args a = {};
     a.a = M; a.glu = 0; a.xh = c->ax.h; a.ne11 = (int)ne11; a.K = (int)n_used;
     a.counts = dsp.counts; a.offsets = dsp.offsets; a.perm = dsp.perm; a.tile_e = dsp.tile_e;
-    a.tile_r0 = dsp.tile_r0; a.n_tiles = dsp.n_tiles; a.max_tiles = max_tiles; a.xrows = T * ne11;
+    a.tile_r0 = dsp.tile_r0; a.tile_start = dsp.tile_start; a.tile_rows = dsp.tile_rows; a.n_tiles = dsp.n_tiles; a.max_tiles = max_tiles; a.xrows = T * ne11;
     a.y = (float *)dst->data; a.ldy = N; a.ncols = N;
     return launch_gemm4(a, st);
 }

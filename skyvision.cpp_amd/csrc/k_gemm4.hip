@@ -74,36 +74,39 @@ __device__ inline rsrc_t g4_rsrc(const void *p, int64_t nbytes) {
 }
 
 // ------------------------------------------------------------------ tiles
+// Prologue order (each step one memory round trip): the tile's descriptor
+// (expert, first row in perm, rows) and n_tiles together; then the rows'
+// slot indices (perm) with the block-0 weight loads issued right behind
+// them (they need only the expert); then the block-0 activation loads.
 struct G4Tile {
-    int e, mrows, nrt;
+    int e, start, mrows, nrt;
+    bool live;   // tile < n_tiles (the grid is rounded up to whole XCD rounds)
 };
 
-// rows of expert e's tile starting at r0: the expert's cnt rows are split in
-// nt = ceil(cnt / G4_BM) tiles, the first cnt % nt of them one row longer
-__device__ __forceinline__ int g4_tile_rows(int cnt, int r0) {
-    const int nt = (cnt + G4_BM - 1) / G4_BM;
-    const int base = cnt / nt, extra = cnt - base * nt;
-    const int j = r0 < extra * (base + 1) ? r0 / (base + 1) : extra + (r0 - extra * (base + 1)) / base;
-    return base + (j < extra ? 1 : 0);
+__device__ __forceinline__ G4Tile g4_desc(const G2Args &g, int tile) {
+    const int tt = tile < g.max_tiles ? tile : g.max_tiles - 1;   // padding tiles read a valid entry
+    G4Tile t;
+    int nt = *g.n_tiles;
+    t.e = g.tile_e[tt];
+    t.start = g.tile_start[tt];
+    t.mrows = g.tile_rows[tt];
+    // all four values before the n_tiles test: one round trip, not two (the
+    // compiler would not hoist the tile loads above the exit)
+    asm volatile("" : "+s"(t.e), "+s"(t.start), "+s"(t.mrows), "+s"(nt));
+    t.nrt = (t.mrows + 31) >> 5;
+    t.live = tile < nt;
+    return t;
 }
 
-// rows of the tile: thread m < G4_BM gets row m's flat slot index p (t*K + k,
-// or -1 past the tile) and writes its activation row to s_arow
-__device__ __forceinline__ G4Tile g4_tile(const G2Args &g, int tile, int *s_arow, int &p) {
-    G4Tile t;
-    t.e = g.tile_e[tile];
-    const int r0 = g.tile_r0[tile];
-    const int cnt = g.counts[t.e], off = g.offsets[t.e];
-    t.mrows = g4_tile_rows(cnt, r0);
-    t.nrt = (t.mrows + 31) >> 5;
-    const int tid = threadIdx.x;
-    p = -1;
-    if (tid < G4_BM) {
-        p = tid < t.mrows ? g.perm[off + r0 + tid] : -1;
-        s_arow[tid] = p < 0 ? 0 : (g.ne11 == 1 ? p / g.K : p);
-    }
+// thread m < mrows: row m's flat slot index p (t*K + k), else -1
+__device__ __forceinline__ int g4_rows_load(const G2Args &g, const G4Tile &t) {
+    return (int)threadIdx.x < t.mrows ? g.perm[t.start + threadIdx.x] : -1;
+}
+
+// the rows' activation row indices to s_arow (row 0 past the tile)
+__device__ __forceinline__ void g4_rows_publish(const G2Args &g, int p, int *s_arow) {
+    if (threadIdx.x < G4_BM) s_arow[threadIdx.x] = p < 0 ? 0 : (g.ne11 == 1 ? p / g.K : p);
     __syncthreads();
-    return t;
 }
 
 // after the K loop (every load of this wave landed): the rows' slot indices
@@ -193,6 +196,11 @@ __device__ __forceinline__ G4WDma<WT> g4_wdma(rsrc_t r0, rsrc_t r1, const int64_
     return dm;
 }
 
+// block 0's weight loads (issued before the K loop, right after the tile's
+// descriptor is known)
+template <int WT>
+__device__ __forceinline__ void g4_issue_w0(const G4WDma<WT> &dm, uint8_t *W);
+
 // load j (0 .. 2 NLD - 1: column tile j / NLD) of block b into the region W
 template <int WT>
 __device__ __forceinline__ void g4_issue_w(const G4WDma<WT> &dm, uint8_t *W, int j, int b) {
@@ -207,6 +215,12 @@ __device__ __forceinline__ void g4_issue_w(const G4WDma<WT> &dm, uint8_t *W, int
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)dst, 16, (int)((x & ~3u) + dm.kk[jj & 1]), 0, 0,
                                                  0);
     }
+}
+
+template <int WT>
+__device__ __forceinline__ void g4_issue_w0(const G4WDma<WT> &dm, uint8_t *W) {
+#pragma unroll
+    for (int j = 0; j < 2 * G4Fmt<WT>::NLD; ++j) g4_issue_w<WT>(dm, W, j, 0);
 }
 
 // the lane's operand bytes of the whole block from the region
@@ -415,7 +429,9 @@ __device__ __forceinline__ void g4_stage(const _Float16 *st, uint32_t abase, con
 // The sync before (b, 1) waits only for the activations (issued before the
 // weight loads, which stay in flight); the one before (b + 1, 0) for all.
 // The last block's loads for a next one repeat it (valid addresses, unused
-// data; the epilogue waits for them).
+// data; the epilogue waits for them): measured faster than skipping them
+// behind a uniform test per block, which costs the stage code more than the
+// loads cost.
 template <int WT, int NRT>
 __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_t arowbytes, const G4WDma<WT> &dm,
                                            const uint32_t (&wsh)[2], uint8_t *W, int nb, int wave, int lane,
@@ -434,10 +450,9 @@ __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_
             for (int i = 0; i < 16; ++i) acc[rt][ct][i] = 0.f;
     G4W<WT> w;
     G4Sc<WT> s0, s1;
+    // (block 0's weight loads are out already: g4_issue_w0)
 #pragma unroll
     for (int j = 0; j < 2 * NRT; ++j) g4_issue_a<NRT>(rx, aoff, wave, j, As0, 0, 0);
-#pragma unroll
-    for (int j = 0; j < NW; ++j) g4_issue_w<WT>(dm, W, j, 0);
     // extra work of stage 0 spread over its 16 NRT slots: the activation
     // loads at slots 4 i (i < 2 NRT), then, all after the last of them (the
     // sync before stage 1 counts on that order) and after the copy has
@@ -485,13 +500,12 @@ __device__ __forceinline__ void g4_kloop(rsrc_t rx, const int *s_arow, uint32_t 
     }
 }
 
-// work-group -> (tile, column tile); false for padding work-groups
-__device__ __forceinline__ bool g4_coords(int nct, const int *n_tiles, int &tile, int &ctile) {
+// work-group -> (tile, column tile)
+__device__ __forceinline__ void g4_coords(int nct, int &tile, int &ctile) {
     const int lin = blockIdx.x, q = lin >> 3, x = lin & 7;
     const int kk = q / nct;
     ctile = q - kk * nct;
     tile = 8 * kk + x;
-    return tile < *n_tiles;
 }
 
 // ------------------------------------------------------------------ GLU
@@ -520,13 +534,11 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     __shared__ __attribute__((aligned(1024))) _Float16 As1[G4_AST];
     __shared__ __attribute__((aligned(1024))) uint8_t Ws[G4_WAVES][g4_wregion<12>()];
     int tile, ctile;
-    if (!g4_coords((int)(g.I / 128), g.n_tiles, tile, ctile)) return;
+    g4_coords((int)(g.I / 128), tile, ctile);
+    const G4Tile t = g4_desc(g, tile);
+    if (!t.live) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    // the activation rows live in the second activation buffer until the K
-    // loop has computed its load offsets (its first write comes later)
-    int *s_arow = (int *)As1;
-    int my_p;
-    const G4Tile t = g4_tile(g, tile, s_arow, my_p);
+    const int my_p = g4_rows_load(g, t);
     const int nrt = __builtin_amdgcn_readfirstlane(t.nrt);
     const uint32_t Kin = (uint32_t)g.a.K;
     const rsrc_t rx = g4_rsrc(g.xh, g.xrows * (int64_t)Kin * 2);
@@ -537,6 +549,11 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     const rsrc_t rg = g.fused ? ra : g4_rsrc(g.b.data + (int64_t)t.e * g.b.mat_bytes, g.b.mat_bytes);
     const int64_t rowbase[2] = {n0, g.fused ? g.I + n0 : n0};
     const G4WDma<12> dm = g4_wdma<12>(ra, rg, rowbase, (uint32_t)g.a.row_bytes, 0u, lane);
+    g4_issue_w0<12>(dm, Ws[wave]);
+    // the activation rows live in the second activation buffer until the K
+    // loop has computed its load offsets (its first write comes later)
+    int *s_arow = (int *)As1;
+    g4_rows_publish(g, my_p, s_arow);
     const uint32_t wsh[2] = {0u, 0u};
     f32x16 acc[G4_BM / 32][2];
     g4_kloop<12>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc);
@@ -560,12 +577,12 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     __shared__ __attribute__((aligned(1024))) _Float16 As1[G4_AST];
     __shared__ __attribute__((aligned(1024))) uint8_t Ws[G4_WAVES][g4_wregion<WT>()];
     int tile, ctile;
-    if (!g4_coords((int)((g.ncols + G4_NWG - 1) / G4_NWG), g.n_tiles, tile, ctile)) return;
+    g4_coords((int)((g.ncols + G4_NWG - 1) / G4_NWG), tile, ctile);
+    const G4Tile t = g4_desc(g, tile);
+    if (!t.live) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int l32 = lane & 31, g2 = lane >> 5;
-    int *s_arow = (int *)As1;   // as in k_g4_glu
-    int my_p;
-    const G4Tile t = g4_tile(g, tile, s_arow, my_p);
+    const int my_p = g4_rows_load(g, t);
     const int nrt = __builtin_amdgcn_readfirstlane(t.nrt);
     const uint32_t Kin = (uint32_t)g.a.K;
     const rsrc_t rx = g4_rsrc(g.xh, g.xrows * (int64_t)Kin * 2);
@@ -576,6 +593,9 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     const int n0 = ctile * G4_NWG + 64 * wave;
     const int64_t rowbase[2] = {n0, n0 + 32};
     const G4WDma<WT> dm = g4_wdma<WT>(r, r, rowbase, rb, mis, lane);
+    g4_issue_w0<WT>(dm, Ws[wave]);
+    int *s_arow = (int *)As1;   // as in k_g4_glu
+    g4_rows_publish(g, my_p, s_arow);
     // byte offset of the lane's own rows (Q6_K block alignment)
     const uint32_t wsh[2] = {mis + (uint32_t)(n0 + l32) * rb, mis + (uint32_t)(n0 + 32 + l32) * rb};
     f32x16 acc[G4_BM / 32][2];

@@ -569,8 +569,11 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
         const int nt = (c + BM - 1) / BM, tb = tsc[me] - nt;
         const int base = nt ? c / nt : 0, extra = c - base * nt;
         for (int j = tid; j < nt; j += DISPATCH_THREADS) {
+            const int r0 = j * base + (j < extra ? j : extra);
             d.tile_e[tb + j] = me;
-            d.tile_r0[tb + j] = j * base + (j < extra ? j : extra);
+            d.tile_r0[tb + j] = r0;
+            d.tile_start[tb + j] = off + r0;
+            d.tile_rows[tb + j] = base + (j < extra ? 1 : 0);
         }
     } else {
         const int nf = c / BM, rem = c - nf * BM;
@@ -578,6 +581,8 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
         for (int j = tid; j < nf; j += DISPATCH_THREADS) {
             d.tile_e[tb + j] = me;
             d.tile_r0[tb + j] = j * BM;
+            d.tile_start[tb + j] = off + j * BM;
+            d.tile_rows[tb + j] = BM;
         }
         if (rem > 0) {
             // rank among the partial tiles: one expert per thread, summed in LDS
@@ -591,6 +596,8 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
             if (tid == 0) {
                 d.tile_e[tsc[E - 1] + prank] = me;
                 d.tile_r0[tsc[E - 1] + prank] = nf * BM;
+                d.tile_start[tsc[E - 1] + prank] = off + nf * BM;
+                d.tile_rows[tsc[E - 1] + prank] = rem;
             }
         }
     }

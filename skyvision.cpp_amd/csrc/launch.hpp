@@ -56,7 +56,9 @@ struct Dispatch {
     int32_t *offsets;    // [E+1]
     int32_t *perm;       // [T*K] value t*K+k, per expert token-ascending
     int32_t *tile_e;     // [max_tiles] expert of each GEMM M-tile
-    int32_t *tile_r0;    // [max_tiles] first list row of each tile
+    int32_t *tile_r0;    // [max_tiles] first list row of each tile (within its expert's list)
+    int32_t *tile_start; // [max_tiles] its first row in perm (offsets[e] + tile_r0)
+    int32_t *tile_rows;  // [max_tiles] its row count
     int32_t *n_tiles;    // [1]
     int32_t *active_e;   // [E] experts with count > 0, ascending
     int32_t *n_active;   // [1]
@@ -160,6 +162,7 @@ struct G2Args {
     const _Float16 *xbs;
     int ne11, K;
     const int32_t *counts, *offsets, *perm, *tile_e, *tile_r0, *n_tiles;
+    const int32_t *tile_start, *tile_rows;   // the tiles' perm starts and row counts
     int max_tiles;
     int64_t xrows;        // rows of xh (glu = 1: tokens)
     float *y;

@@ -45,7 +45,8 @@ import numpy as np  # noqa: E402
 import mimoe as M  # noqa: E402
 import workloads as W  # noqa: E402
 
-PEAK_MFMA_TFLOPS = 2500.0      # MI355X dense fp16 / bf16 MFMA
+PEAK_MFMA_TFLOPS = 2500.0      # MI355X dense fp16 / bf16 MFMA (published, 2.4 GHz)
+CUS, FLOPS_PER_CU_CYCLE = 256, 4096
 ACT_NAMES = {0: "silu(gate)*up", 1: "gelu_erf(h)*(g+1)", 2: "gelu_tanh(gate)*up", 3: "gelu_erf(gate)*up"}
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 
@@ -56,21 +57,27 @@ def log(msg: str) -> None:
 
 def time_layer(ctx, layers, xs, T, out, steps, warmup, profile=False):
     """Run `steps` forwards rotating over layer copies; returns (ms/step,
-    per-stage mean ms or None)."""
+    {"wall_ms_per_step"}), or with profile=True (the shader clock in GHz under
+    each grouped GEMM, per-stage mean ms)."""
     n = len(layers)
     for i in range(warmup):
         M.check("forward", ctx.forward(layers[i % n].layer, xs[i % n], T, None, out))
     M.synchronize()
     if profile:
         ctx.set_profiling(True)
-        acc = {}
+        acc, clk = {}, {}
         for i in range(steps):
             M.check("forward", ctx.forward(layers[i % n].layer, xs[i % n], T, None, out))
             for name, ms in ctx.stage_times():
                 acc.setdefault(name, []).append(ms)
+            for name in ("gate_up", "down"):
+                r = ctx.stage_clock(name)
+                if r is not None:
+                    clk.setdefault(name, []).append(r[0])
         ctx.set_profiling(False)
         M.synchronize()
-        return None, {k: float(np.mean(v)) for k, v in acc.items()}
+        return ({k: float(np.mean(v)) for k, v in clk.items()},
+                {k: float(np.mean(v)) for k, v in acc.items()})
     e0, e1 = M.Event(), M.Event()
     M.synchronize()
     t0 = time.perf_counter()
@@ -361,6 +368,105 @@ def config4_stack(n_layers: int = 24, T_prefill: int = 2048, n_decode: int = 256
     return res
 
 
+def mfma_counters(kernel: str):
+    """MFMA utilisation of `kernel` from the committed counter summary
+    (profiles/mfma_counters.json: rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES and
+    SQ_INSTS_VALU_MFMA_MOPS_F16 per dispatch, and the shader clock measured
+    under the kernel); None when not measured."""
+    p = ROOT / "profiles" / "mfma_counters.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(kernel)
+    except (ValueError, AttributeError):
+        return None
+
+
+def prefill_line(config: int, args, primary: bool) -> dict:
+    """One prefill configuration (1 or 2): the K forwards replayed as a HIP
+    graph (stream-issued timing beside it), the per-stage times, the roofline
+    of the gate/up grouped GEMM and the routing's load balance."""
+    cfg = W.CONFIGS[config]
+    spec = cfg["spec"]
+    T = cfg["tokens"][0]
+    ctx = M.Context(0)
+    ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
+    t0 = time.perf_counter()
+    layers = [W.GpuLayer(ctx, spec, copy=c) for c in range(args.copies)]
+    xs = [W.gen_x(ctx, spec, T, copy=c) for c in range(args.copies)]
+    out = M.DeviceBuffer(4 * T * spec.D)
+    M.synchronize()
+    log(f"built {args.copies} layer copies of {spec.name} in {time.perf_counter() - t0:.1f}s "
+        f"({sum(l.expert_bytes() * spec.E for l in layers) / 1e9:.2f} GB of expert tables)")
+    if args.calib_copy and primary:
+        nbytes = 512 << 20
+        src, dst = M.DeviceBuffer(nbytes), M.DeviceBuffer(nbytes)
+        M.check("memcpy", M.load().mi_memcpy_d2d(dst.ptr, src.ptr, nbytes))
+        M.synchronize()
+        log(f"calibration copy: {nbytes} bytes device to device")
+        del src, dst
+    ms, extra = time_layer(ctx, layers, xs, T, out, args.steps, args.warmup)
+    log(f"config {config}: {ms:.4f} ms/step, wall {extra['wall_ms_per_step']:.4f} ms/step (stream)")
+    schedule = "stream: one host launch per kernel"
+    gr = None if args.no_graph else time_layer_graph(ctx, layers, xs, T, out, args.steps)
+    if gr is not None:
+        log(f"config {config}: {gr[0]:.4f} ms/step, wall {gr[1]:.4f} ms/step (HIP graph replay)")
+        extra = {"stream_ms_per_step": ms, "stream_wall_ms_per_step": extra["wall_ms_per_step"],
+                 "wall_ms_per_step": gr[1]}
+        ms = gr[0]
+        schedule = "HIP graph of the K forwards (captured once, replayed; every kernel runs each step)"
+    clocks, stages = time_layer(ctx, layers, xs, T, out, min(args.steps, 20), 2, profile=True)
+    log(f"config {config} stages (ms): {json.dumps({k: round(v, 4) for k, v in stages.items()})}; "
+        f"shader clock under the GEMMs (GHz): {json.dumps({k: round(v, 3) for k, v in clocks.items()})}")
+    gu_ms = stages.get("gate_up", float("nan"))
+    gu_flops = 2.0 * T * spec.K * spec.D * (2 * spec.I)
+    achieved = gu_flops / (gu_ms * 1e-3) / 1e12
+    touched, counts = touched_experts(ctx, layers[0], xs[0], T)
+    srt = np.sort(counts)[::-1]
+    roof = {"bound": "mfma", "kernel": "k_g4_glu (gate/up grouped GEMM + GLU)",
+            "achieved": achieved, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
+            "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": measured_traffic("k_g4_glu"),
+            "kernel_ms": gu_ms, "flops_per_launch": gu_flops}
+    clk = clocks.get("gate_up")
+    if clk:
+        # the dense fp16 peak at the shader clock measured under this kernel:
+        # 256 CUs x 4 SIMDs x 1024 flops per SIMD-cycle (one 32x32x16 MFMA,
+        # 32768 flops, per 32 cycles) x clock
+        peak_clk = CUS * FLOPS_PER_CU_CYCLE * clk * 1e9 / 1e12
+        roof["measured_clock_ghz"] = clk
+        roof["peak_at_measured_clock"] = peak_clk
+        roof["frac_of_peak_at_measured_clock"] = achieved / peak_clk
+    mc = mfma_counters("k_g4_glu")
+    if mc:
+        # MFMA busy share of the SIMD cycles under the kernel (committed profile)
+        roof["mfma_busy_frac_profiled"] = mc.get("mfma_busy_frac")
+    line = {
+        "workload": f"config {config}: moondream3 MoE layer prefill" +
+                    (", Zipf(1.2) router bias (load-imbalanced)" if spec.router_bias == "zipf" else ""),
+        "tokens_per_s": T / (ms * 1e-3),
+        "ms_per_step": ms,
+        "config": {"workload": f"config {config}: moondream3 MoE layer prefill", "schedule": schedule,
+                   "tokens": T, "n_embd": spec.D, "n_expert": spec.E, "n_expert_used": spec.K,
+                   "n_ff": spec.I, "gate_up": "Q4_K",
+                   "down": "Q6_K" if spec.down_type == M.TYPE_Q6_K else "Q4_K",
+                   "act": ACT_NAMES[spec.act], "layer_copies": args.copies,
+                   "touched_experts": touched, "layer_flops": W.flops(spec, T)},
+        "roofline": roof,
+        "stages_ms": stages,
+        "gemm_clock_ghz": clocks,
+        "load_balance": {"empty_experts": int((counts == 0).sum()),
+                         "top4_share": float(srt[:4].sum() / counts.sum()),
+                         "hot_expert_rows": [int(v) for v in srt[:4]],
+                         "tiles_per_hot_expert": [int((v + 191) // 192) for v in srt[:4]],
+                         "rows_per_expert_min_max": [int(counts[counts > 0].min()), int(counts.max())]},
+        "extra": extra,
+        "layer0": layers[0],
+    }
+    del layers, xs, out
+    ctx.close()
+    return line
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -393,67 +499,29 @@ def main() -> int:
     M.load()
     info = M.device_info(0)
     log(f"device: {info}")
-    cfg = W.CONFIGS[args.config]
-    spec = cfg["spec"]
-    T = cfg["tokens"][0]
-    ctx = M.Context(0)
-    ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
-    t0 = time.perf_counter()
-    layers = [W.GpuLayer(ctx, spec, copy=c) for c in range(args.copies)]
-    xs = [W.gen_x(ctx, spec, T, copy=c) for c in range(args.copies)]
-    out = M.DeviceBuffer(4 * T * spec.D)
-    M.synchronize()
-    log(f"built {args.copies} layer copies of {spec.name} in {time.perf_counter() - t0:.1f}s "
-        f"({sum(l.expert_bytes() * spec.E for l in layers) / 1e9:.2f} GB of expert tables)")
-
-    if args.calib_copy:
-        nbytes = 512 << 20
-        src, dst = M.DeviceBuffer(nbytes), M.DeviceBuffer(nbytes)
-        M.check("memcpy", M.load().mi_memcpy_d2d(dst.ptr, src.ptr, nbytes))
-        M.synchronize()
-        log(f"calibration copy: {nbytes} bytes device to device")
-        del src, dst
-    ms, extra = time_layer(ctx, layers, xs, T, out, args.steps, args.warmup)
-    log(f"config {args.config}: {ms:.4f} ms/step, wall {extra['wall_ms_per_step']:.4f} ms/step (stream)")
-    schedule = "stream: one host launch per kernel"
-    gr = None if args.no_graph else time_layer_graph(ctx, layers, xs, T, out, args.steps)
-    if gr is not None:
-        log(f"config {args.config}: {gr[0]:.4f} ms/step, wall {gr[1]:.4f} ms/step (HIP graph replay)")
-        extra = {"stream_ms_per_step": ms, "stream_wall_ms_per_step": extra["wall_ms_per_step"],
-                 "wall_ms_per_step": gr[1]}
-        ms = gr[0]
-        schedule = "HIP graph of the K forwards (captured once, replayed; every kernel runs each step)"
-    _, stages = time_layer(ctx, layers, xs, T, out, min(args.steps, 20), 2, profile=True)
-    log(f"stages (ms): {json.dumps({k: round(v, 4) for k, v in stages.items()})}")
-    gu_ms = stages.get("gate_up", float("nan"))
-    gu_flops = 2.0 * T * spec.K * spec.D * (2 * spec.I)
-    achieved = gu_flops / (gu_ms * 1e-3) / 1e12
-    touched, _ = touched_experts(ctx, layers[0], xs[0], T)
-
+    line = prefill_line(args.config, args, primary=True)
     result = {
         "metric": "MoE layer tokens/s + % HBM roofline (decode) / % MFMA peak (prefill), 1 GPU",
-        "value": T / (ms * 1e-3),
+        "value": line["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms,
+        "ms_per_step": line["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic",
-        "config": {"workload": f"config {args.config}: moondream3 MoE layer prefill", "schedule": schedule,
-                   "tokens": T, "n_embd": spec.D, "n_expert": spec.E, "n_expert_used": spec.K,
-                   "n_ff": spec.I, "gate_up": "Q4_K", "down": "Q6_K" if spec.down_type == M.TYPE_Q6_K else "Q4_K",
-                   "act": ACT_NAMES[spec.act], "layer_copies": args.copies,
-                   "touched_experts": touched, "layer_flops": W.flops(spec, T)},
-        "roofline": {"bound": "mfma", "kernel": "k_g4_glu (gate/up grouped GEMM + GLU)",
-                     "achieved": achieved, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": measured_traffic("k_g4_glu"),
-                     "kernel_ms": gu_ms, "flops_per_launch": gu_flops},
-        "stages_ms": stages,
+        "config": line["config"],
+        "roofline": line["roofline"],
+        "stages_ms": line["stages_ms"],
     }
+    extra = line["extra"]
+    layers0 = line["layer0"]
+    if args.config == 1 and not args.no_sweeps:
+        c2 = prefill_line(2, args, primary=False)
+        result["config2"] = {k: v for k, v in c2.items() if k not in ("extra", "layer0")}
 
     if not args.no_decode:
         dspec = W.CONFIGS[0]["spec"]
@@ -505,12 +573,11 @@ def main() -> int:
         dctx.close()
 
     if not args.no_cpu:
-        cb = cpu_baseline(spec, layers[0], args.cpu_tokens)
+        cb = cpu_baseline(layers0.spec, layers0, args.cpu_tokens)
         result["cpu_baseline"] = cb
+    del layers0, line
 
     if not args.no_sweeps:
-        del layers, xs
-        ctx.close()
         result["config3"] = config3_sweep(args.copies)
         result["config4"] = config4_stack()
     result.update({k: v for k, v in extra.items() if k.startswith("stream")})

@@ -166,8 +166,14 @@ int  mi_moe_ctx_reserve(mi_moe_ctx *ctx, int64_t max_tokens, int32_t n_embd, int
  * (mi_moe_expert_ffn, mi_mul_mat_id; ggml_mul_mat_id asserts them).
  * wait_failures: fused single-token calls whose grid wait gave up (their
  * output is NaN; MI_DECODE_FUSED_EXCLUSIVE on a GPU shared with other work).
- * Either pointer may be NULL.  Synchronizes the context's device. */
-int  mi_moe_ctx_take_errors(mi_moe_ctx *ctx, int64_t *bad_ids, int64_t *wait_failures);
+ * fp16_saturated: 256-value Q8_K blocks of the grouped-GEMM path (input rows
+ * or activation rows) whose largest |value| exceeds 65504, the fp16 range of
+ * the MFMA operands: their operands were clamped to +-65504, so the products
+ * of those rows are inexact (ggml's own fp16 GPU paths overflow there; the
+ * integer GEMV path has no such limit).
+ * Any pointer may be NULL.  Synchronizes the context's device. */
+int  mi_moe_ctx_take_errors(mi_moe_ctx *ctx, int64_t *bad_ids, int64_t *wait_failures,
+                            int64_t *fp16_saturated);
 
 /* ---- whole MoE block ------------------------------------------------------
  * out[t] = res[t] + sum_k w[t][k] * down_{sel[t][k]}( act(gate x[t], up x[t]) )
@@ -187,7 +193,7 @@ int mi_moe_forward(mi_moe_ctx *ctx, const mi_moe_layer *layer, const float *x, i
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  It calls no hipMalloc / hipFree or any
  * allocating routine: its workspace is one file-scope device array of the
- * library per GPU, 16,678,656 bytes, held until the process ends, sized for
+ * library per GPU, 16,678,912 bytes, held until the process ends, sized for
  * calls of at most MI_NOALLOC_MAX_TOKENS tokens of layers with n_embd <= 2048,
  * n_ff <= 1024, n_expert <= 128, n_expert_used <= 8 (a shared expert's
  * sh_n_ff <= 8192); larger calls return MI_MOE_ERR_CAPACITY and enqueue
@@ -305,6 +311,13 @@ int  mi_gguf_load_moe_layer(const mi_gguf *gguf, int32_t block, int32_t act, mi_
 int mi_moe_ctx_set_profiling(mi_moe_ctx *ctx, int on);
 int mi_moe_ctx_stage_times(mi_moe_ctx *ctx, int max_stages, const char **names, float *ms,
                            int *n_stages);
+/* The shader clock (GHz) the CUs ran at under one grouped GEMM of the last
+ * forward when profiling is on: stage "gate_up" or "down" of the 4-wave MFMA
+ * GEMM path, from each work-group's shader-clock and wall-clock counters at
+ * its start and end (summed cycles / summed wall time).  n_wg (may be NULL)
+ * receives the work-groups measured.  MI_MOE_ERR_ARG when that stage did not
+ * run on the GEMM path.  Synchronizes with the call's stream. */
+int mi_moe_ctx_stage_clock(mi_moe_ctx *ctx, const char *stage, double *ghz, int *n_wg);
 /* Product path of a call: the grouped MFMA GEMM from min_tokens_for_gemm
  * tokens on, the grouped GEMV below.  0 (the default) picks by shape: the
  * GEMM when 4 * T * K > 5 * E (more than 1.25 dispatched rows per expert). */

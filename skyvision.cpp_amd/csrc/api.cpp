@@ -16,6 +16,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/mi_moe.h"
 #include "../../include/mi_moe_util.h"
@@ -56,6 +57,7 @@ using namespace mimoe;
 namespace {
 
 constexpr int kMaxStages = 16;
+constexpr int kClkWGs = 16384;   // clock records per GEMM launch (profiling)
 
 struct ActBuf {                // one Q8_K activation set
     int8_t *q8 = nullptr;
@@ -102,6 +104,7 @@ struct mi_moe_ctx {
     float *sh_out = nullptr, *sh_w = nullptr, *sh_logit = nullptr;
     int32_t *sh_ids = nullptr;
     int32_t *bad_total = nullptr;   // caller ids outside [0, E) since the last take
+    int32_t *range_total = nullptr; // GEMM-path Q8_K blocks saturated at the fp16 range
     int64_t gemm_threshold = 0;   // 0: the shape rule of use_gemm
     // single-token fused kernel (k_decode.hip)
     int fused_decode = MI_DECODE_FUSED_COOPERATIVE;
@@ -116,6 +119,10 @@ struct mi_moe_ctx {
     const char *stage_name[kMaxStages] = {};
     int n_stages = 0;
     hipStream_t prof_stream = nullptr;
+    // profiling: per-work-group clock records of the two grouped GEMMs
+    // (gate_up, down) of the last forward on the 4-wave GEMM path
+    uint64_t *clk = nullptr;        // [2][kClkWGs][4]
+    int clk_grid[2] = {0, 0};       // work-groups the last launch recorded, 0: none
 };
 
 namespace {
@@ -123,6 +130,7 @@ namespace {
 void stage_begin(mi_moe_ctx *c, hipStream_t st) {
     if (!c->profiling) return;
     c->n_stages = 0;
+    c->clk_grid[0] = c->clk_grid[1] = 0;
     c->prof_stream = st;
     (void)hipEventRecord(c->ev[0], st);
 }
@@ -131,6 +139,14 @@ void stage_end(mi_moe_ctx *c, const char *name, hipStream_t st) {
     c->stage_name[c->n_stages] = name;
     c->n_stages++;
     (void)hipEventRecord(c->ev[c->n_stages], st);
+}
+
+// profiling: point the GEMM's clock records at the context's buffer k
+void prof_clock(mi_moe_ctx *c, G2Args &g, int k) {
+    if (!c->profiling || !c->clk) return;
+    g.clk = c->clk + (size_t)k * 4 * kClkWGs;
+    g.clk_n = kClkWGs;
+    c->clk_grid[k] = gemm4_grid(g);
 }
 
 bool is_kquant(int t) { return t == MI_TYPE_Q4_K || t == MI_TYPE_Q6_K; }
@@ -290,6 +306,7 @@ bool x_q8_spec(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T, Q8Out &qx)
         qx.q8 = c->ax.q8; qx.d8 = c->ax.d8; qx.bsums = c->ax.bs;
     } else {
         qx.xh = c->ax.h; qx.wtype = L->gate.type; qx.order = g4_path(L) ? 1 : 0;
+        qx.range_total = c->range_total;
     }
     return true;
 }
@@ -398,10 +415,12 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.tile_e = dg.tile_e;
         a.tile_r0 = dg.tile_r0; a.tile_start = dg.tile_start; a.tile_rows = dg.tile_rows; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
         a.y = c->f1; a.ldy = I; a.ncols = I; a.xrows = T;
+        prof_clock(c, a, 0);
         TRY(launch_gemm4(a, st));
         stage_end(c, "gate_up", st);
         Q8Out qa;
         qa.xh = c->aact.h; qa.wtype = down.type; qa.order = 1; qa.pre_act = gated ? 0 : MI_ACT_RELU_SQR;
+        qa.range_total = c->range_total;
         TRY(launch_q8k_rows(c->f1, I, rows, I, qa, st));
         stage_end(c, "q8k_act", st);
         G2Args d = {};
@@ -409,6 +428,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
         d.tile_r0 = dd.tile_r0; d.tile_start = dd.tile_start; d.tile_rows = dd.tile_rows; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles; d.xrows = (int64_t)T * K;
         d.y = c->z; d.ldy = D; d.ncols = D;
+        prof_clock(c, d, 1);
         TRY(launch_gemm4(d, st));
         stage_end(c, "down", st);
     } else {
@@ -418,7 +438,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         a.xh = c->ax.h; a.ne11 = 1; a.K = K;
         a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.tile_e = dg.tile_e;
         a.tile_r0 = dg.tile_r0; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
-        a.acth = c->aact.h; a.next_type = down.type; a.ncols = I;
+        a.acth = c->aact.h; a.next_type = down.type; a.ncols = I; a.range_total = c->range_total;
         TRY(launch_gemm(a, st));
         stage_end(c, "gate_up", st);
         GemmArgs d = {};
@@ -489,7 +509,7 @@ constexpr size_t ws_bytes(int64_t max_tokens, int64_t D, int64_t I, int64_t E, i
         need += carve_size<int32_t>(E) + carve_size<int32_t>(E + 1) + carve_size<int32_t>(rows) +
                 4 * carve_size<int32_t>(tiles) + carve_size<int32_t>(1) + carve_size<int32_t>(E) +
                 2 * carve_size<int32_t>(1);
-    need += carve_size<int32_t>(1);
+    need += 2 * carve_size<int32_t>(1);   // bad_total, range_total
     // activation sets: x/b rows (rows x kmax) and act rows (rows x I)
     need += carve_size<int8_t>(rows * kmax_q) + carve_size<float>(rows * kmax_q / QK) +
             carve_size<int16_t>(rows * kmax_q / 16) + carve_size<_Float16>(rows * kmax_q) +
@@ -533,6 +553,7 @@ bool carve_workspace(mi_moe_ctx *c, char *base, int64_t max_tokens, int32_t D, i
     }
     c->bad_total = carve<int32_t>(q, 1);
     c->disp[0].bad_total = c->disp[1].bad_total = c->bad_total;
+    c->range_total = carve<int32_t>(q, 1);
     c->ax.q8 = carve<int8_t>(q, rows * kmax_q);
     c->ax.d8 = carve<float>(q, rows * kmax_q / QK);
     c->ax.bs = carve<int16_t>(q, rows * kmax_q / 16);
@@ -614,6 +635,7 @@ void mi_moe_ctx_destroy(mi_moe_ctx *c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     if (c->ws) (void)hipFree(c->ws);
+    if (c->clk) (void)hipFree(c->clk);
     for (int i = 0; i <= kMaxStages; ++i)
         if (c->ev[i]) (void)hipEventDestroy(c->ev[i]);
     delete c;
@@ -640,22 +662,26 @@ int mi_moe_ctx_reserve(mi_moe_ctx *c, int64_t max_tokens, int32_t D, int32_t I, 
     return MI_MOE_OK;
 }
 
-int mi_moe_ctx_take_errors(mi_moe_ctx *c, int64_t *bad_ids, int64_t *wait_failures) {
+int mi_moe_ctx_take_errors(mi_moe_ctx *c, int64_t *bad_ids, int64_t *wait_failures, int64_t *fp16_saturated) {
     if (!c) return MI_MOE_ERR_NULL;
     if (bad_ids) *bad_ids = 0;
     if (wait_failures) *wait_failures = 0;
+    if (fp16_saturated) *fp16_saturated = 0;
     if (!c->reserved) return MI_MOE_OK;
     HIP_TRY(hipSetDevice(c->device));
     HIP_TRY(hipDeviceSynchronize());
-    int32_t b = 0;
+    int32_t b = 0, r = 0;
     unsigned f = 0;
     HIP_TRY(hipMemcpy(&b, c->bad_total, sizeof(b), hipMemcpyDeviceToHost));
     HIP_TRY(hipMemcpy(&f, c->dec_err, sizeof(f), hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(&r, c->range_total, sizeof(r), hipMemcpyDeviceToHost));
     HIP_TRY(hipMemset(c->bad_total, 0, sizeof(b)));
     HIP_TRY(hipMemset(c->dec_err, 0, sizeof(f)));
+    HIP_TRY(hipMemset(c->range_total, 0, sizeof(r)));
     HIP_TRY(hipDeviceSynchronize());
     if (bad_ids) *bad_ids = b;
     if (wait_failures) *wait_failures = f;
+    if (fp16_saturated) *fp16_saturated = r;
     return MI_MOE_OK;
 }
 
@@ -675,8 +701,45 @@ int mi_moe_ctx_set_fused_decode(mi_moe_ctx *c, int on) {
 
 int mi_moe_ctx_set_profiling(mi_moe_ctx *c, int on) {
     if (!c) return MI_MOE_ERR_NULL;
+    if (on && !c->clk) {
+        HIP_TRY(hipSetDevice(c->device));
+        HIP_TRY(hipMalloc(&c->clk, sizeof(uint64_t) * 2 * 4 * kClkWGs));
+    }
     c->profiling = on != 0;
     c->n_stages = 0;
+    c->clk_grid[0] = c->clk_grid[1] = 0;
+    return MI_MOE_OK;
+}
+
+int mi_moe_ctx_stage_clock(mi_moe_ctx *c, const char *stage, double *ghz, int *n_wg) {
+    if (!c || !stage || !ghz) return MI_MOE_ERR_NULL;
+    *ghz = 0.0;
+    if (n_wg) *n_wg = 0;
+    const int k = std::strcmp(stage, "gate_up") == 0 ? 0 : std::strcmp(stage, "down") == 0 ? 1 : -1;
+    if (k < 0) return MI_MOE_ERR_ARG;
+    if (!c->profiling || c->clk_grid[k] == 0 || c->n_stages == 0) return MI_MOE_ERR_ARG;
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(hipEventSynchronize(c->ev[c->n_stages]));
+    int wall_khz = 0;
+    HIP_TRY(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, c->device));
+    if (wall_khz <= 0) return MI_MOE_ERR_ARG;
+    const int n = std::min(c->clk_grid[k], kClkWGs);
+    std::vector<uint64_t> h((size_t)4 * n);
+    HIP_TRY(hipMemcpy(h.data(), c->clk + (size_t)k * 4 * kClkWGs, h.size() * sizeof(uint64_t),
+                      hipMemcpyDeviceToHost));
+    // the clock over the work-groups' summed lifetimes: shader cycles / wall ticks
+    double cyc = 0.0, ticks = 0.0;
+    int live = 0;
+    for (int i = 0; i < n; ++i) {
+        const uint64_t *r = &h[(size_t)4 * i];
+        if (r[1] == 0 || r[3] <= r[1] || r[2] <= r[0]) continue;
+        cyc += (double)(r[2] - r[0]);
+        ticks += (double)(r[3] - r[1]);
+        ++live;
+    }
+    if (live == 0 || ticks <= 0.0) return MI_MOE_ERR_ARG;
+    *ghz = cyc / ticks * (double)wall_khz * 1e-6;
+    if (n_wg) *n_wg = live;
     return MI_MOE_OK;
 }
 
@@ -961,7 +1024,7 @@ int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const 
         return launch_gemv(a, st);
     }
     Q8Out qx;
-    qx.xh = c->ax.h; qx.wtype = as->type; qx.order = 1;
+    qx.xh = c->ax.h; qx.wtype = as->type; qx.order = 1; qx.range_total = c->range_total;
     TRY(launch_q8k_rows(bp, Kin, T * ne11, Kin, qx, st));
     G2Args a = {};
     a.a = M; a.glu = 0; a.xh = c->ax.h; a.ne11 = (int)ne11; a.K = (int)n_used;

@@ -115,6 +115,20 @@ __device__ inline void scale_min_k4_reg(int j, uint32_t w0, uint32_t w1, uint32_
     m = lo ? m_lo : m_hi;
 }
 
+// fp16 operand d*q of the GEMM path, saturated at the largest finite fp16:
+// a Q8_K block whose scale puts 127 d beyond it (|x| > 65504) is counted by
+// its producer (range_total) instead of turning into inf.
+constexpr float kF16Max = 65504.f;
+__device__ inline _Float16 f16_sat(float v) { return (_Float16)fminf(fmaxf(v, -kF16Max), kF16Max); }
+__device__ inline bool f16_over(float d) { return fabsf(d) * 127.f > kF16Max; }
+
+// Offset of a Q4_K sub-block dequantized from centred codes: with s = d*sc,
+// w = s q - dmin m = s (q - 8) + (8 s - dmin m).  Both products are exact in
+// fp32 (11-bit d times a 6-bit integer), so the offset is rounded once.
+__device__ inline float q4k_center(float d, int sc, float dmin, int m) {
+    return 8.0f * (d * (float)sc) - dmin * (float)m;
+}
+
 // ---------------------------------------------------------------- MFMA K order
 // The prefill GEMM feeds v_mfma_f32_16x16x32_f16 with 8 fp16 values per lane.
 // Inside a 256-value super-block, MFMA step s (0..7), lane group g (lane/16,

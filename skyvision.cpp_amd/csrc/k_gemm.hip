@@ -50,17 +50,20 @@ __device__ inline uint4 load16_a2(const uint8_t *p) {
 
 // Q4_K: dword v holds nibbles n0..n7 = (a0,b0,a1,b1,a2,b2,a3,b3), a = sub-block
 // 2g (elements 64g+4s+i), b = sub-block 2g+1 (64g+32+4s+i).  Output operand
-// order (a0,a2,b0,b2,a1,a3,b1,b3).  Codes become exact fp16 integers through
-// the 1024 (bits 0-3) and 64 (bits 4-7) exponent tricks; one packed fma per
-// pair applies d*sc and -dmin*m.
+// order (a0,a2,b0,b2,a1,a3,b1,b3).  Codes become exact fp16 integers q - 8
+// through the 1024 (bits 0-3) and 64 (bits 4-7) exponent tricks; one packed
+// fma per pair applies s = d*sc and c = 8 d*sc - dmin*m (q4k_center):
+// w = (q - 8) s + c.  Centring the codes halves the weight of s's rounding
+// and leaves c small, so w lands close to the fp16 rounding of the exact
+// d*sc*q - dmin*m.
 __device__ inline half8_t dq_q4k(uint32_t v, half2_t sA, half2_t nmA, half2_t sB, half2_t nmB) {
-    const half2_t c1024 = {(_Float16)1024.f, (_Float16)1024.f};
-    const half2_t c64 = {(_Float16)64.f, (_Float16)64.f};
+    const half2_t c1032 = {(_Float16)1032.f, (_Float16)1032.f};
+    const half2_t c72 = {(_Float16)72.f, (_Float16)72.f};
     const uint32_t v8 = v >> 8;
-    const half2_t t0 = u2h2((v & 0x000F000Fu) | 0x64006400u) - c1024;
-    const half2_t t1 = u2h2((v & 0x00F000F0u) | 0x54005400u) - c64;
-    const half2_t t2 = u2h2((v8 & 0x000F000Fu) | 0x64006400u) - c1024;
-    const half2_t t3 = u2h2((v8 & 0x00F000F0u) | 0x54005400u) - c64;
+    const half2_t t0 = u2h2((v & 0x000F000Fu) | 0x64006400u) - c1032;
+    const half2_t t1 = u2h2((v & 0x00F000F0u) | 0x54005400u) - c72;
+    const half2_t t2 = u2h2((v8 & 0x000F000Fu) | 0x64006400u) - c1032;
+    const half2_t t3 = u2h2((v8 & 0x00F000F0u) | 0x54005400u) - c72;
     const half2_t w0 = __builtin_elementwise_fma(t0, sA, nmA);
     const half2_t w1 = __builtin_elementwise_fma(t1, sB, nmB);
     const half2_t w2 = __builtin_elementwise_fma(t2, sA, nmA);
@@ -197,9 +200,9 @@ __global__ void __launch_bounds__(GM_THREADS) k_gemm(GemmArgs g) {
                 scale_min_k4_reg(2 * g4, h.y, h.z, h.w, scA, mA);
                 scale_min_k4_reg(2 * g4 + 1, h.y, h.z, h.w, scB, mB);
                 w4[nt].sA = splat(d * (float)scA);
-                w4[nt].nmA = splat(-(dmin * (float)mA));
+                w4[nt].nmA = splat(q4k_center(d, scA, dmin, mA));
                 w4[nt].sB = splat(d * (float)scB);
-                w4[nt].nmB = splat(-(dmin * (float)mB));
+                w4[nt].nmB = splat(q4k_center(d, scB, dmin, mB));
             } else {
                 const uint8_t *blk = rowp[nt] + (int64_t)b * Q6K_BYTES;
                 const int h = g4 >> 1, lo16 = 16 * (g4 & 1);
@@ -284,6 +287,7 @@ __global__ void __launch_bounds__(GM_THREADS) k_gemm(GemmArgs g) {
                 const float iscale = -127.f / a.val;
                 s_is[tid] = iscale;
                 s_d[tid] = 1 / iscale;
+                if (g.range_total && tid < mrows && f16_over(1 / iscale)) atomicAdd(g.range_total, 1);
             } else {
                 s_is[tid] = 0.f;
                 s_d[tid] = 0.f;
@@ -297,7 +301,7 @@ __global__ void __launch_bounds__(GM_THREADS) k_gemm(GemmArgs g) {
                 for (int j = 0; j < 2; ++j) {
                     const int c = 32 * wave + 16 * j + l16;
                     const int q = d != 0.f ? imin(127, nearest_int(is * v[mt][j][i])) : 0;
-                    As[m * GM_LDA + mfma_pos(NEXT, c)] = (_Float16)(d * (float)q);
+                    As[m * GM_LDA + mfma_pos(NEXT, c)] = f16_sat(d * (float)q);
                 }
             }
         __syncthreads();

@@ -264,7 +264,7 @@ __device__ __forceinline__ void g4_copy_w(const uint8_t *W, int l32, int g2, uin
 }
 
 // ------------------------------------------------------------------ scales
-// Per column tile and stage h: Q4_K s = d*sc and nm = -dmin*m of the lane's
+// Per column tile and stage h: Q4_K s = d*sc and nm = 8 d*sc - dmin*m of the lane's
 // sub-blocks 4 h + 2 g2 (low nibbles) and + 1 (high); Q6_K d*scale of the
 // scales 8 h + g2 + {0, 2, 4, 6} of the lane's quarter-rows (steps with w = 0
 // use the first two, w = 1 the last two).
@@ -284,10 +284,10 @@ __device__ __forceinline__ void g4_scales(const G4W<WT> &w, int ct, int g2, int 
         int sc, m;
         scale_min_k4_reg(4 * h + 2 * g2, hv.y, hv.z, hv.w, sc, m);
         s.s_lo[ct] = g4_splat(d * (float)sc);
-        s.nm_lo[ct] = g4_splat(-(dmin * (float)m));
+        s.nm_lo[ct] = g4_splat(q4k_center(d, sc, dmin, m));
         scale_min_k4_reg(4 * h + 2 * g2 + 1, hv.y, hv.z, hv.w, sc, m);
         s.s_hi[ct] = g4_splat(d * (float)sc);
-        s.nm_hi[ct] = g4_splat(-(dmin * (float)m));
+        s.nm_hi[ct] = g4_splat(q4k_center(d, sc, dmin, m));
     } else {
         const uint32_t dw = __builtin_amdgcn_alignbyte(w.sc[ct][4], w.sc[ct][4], sh);   // bytes 16 + sh .. : d
         const float d = h2f((uint16_t)(dw & 0xffffu));
@@ -308,13 +308,14 @@ template <int WT>
 __device__ __forceinline__ uint32_t g4_piece(const G4W<WT> &w, const G4Sc<WT> &s, uint32_t sh, int h, int sp, int ct,
                                              int p) {
     if constexpr (WT == 12) {
-        const half2_t c1024 = {(_Float16)1024.f, (_Float16)1024.f};
-        const half2_t c64 = {(_Float16)64.f, (_Float16)64.f};
+        // centred codes q - 8 (see dq_q4k): 1024 + q - 1032, 64 + q - 72
+        const half2_t c1032 = {(_Float16)1032.f, (_Float16)1032.f};
+        const half2_t c72 = {(_Float16)72.f, (_Float16)72.f};
         const uint32_t v = w.q[ct][h][sp >> 2][sp & 3];
         const uint32_t x = p < 2 ? v : v >> 8;
         half2_t t;
-        if (p & 1) t = g4_u2h2(g4_and_or(x, 0x00F000F0u, 0x54005400u)) - c64;
-        else t = g4_u2h2(g4_and_or(x, 0x000F000Fu, 0x64006400u)) - c1024;
+        if (p & 1) t = g4_u2h2(g4_and_or(x, 0x00F000F0u, 0x54005400u)) - c72;
+        else t = g4_u2h2(g4_and_or(x, 0x000F000Fu, 0x64006400u)) - c1032;
         return g4_h22u((p & 1) ? __builtin_elementwise_fma(t, s.s_hi[ct], s.nm_hi[ct])
                                : __builtin_elementwise_fma(t, s.s_lo[ct], s.nm_lo[ct]));
     } else {
@@ -529,6 +530,18 @@ __device__ __forceinline__ void g4_glu_store(const G2Args &g, const f32x16 (&acc
     }
 }
 
+// Profiling only: the work-group's shader-clock and wall-clock counters
+// (s_memtime, s_memrealtime) at its start (slot 0) and end (slot 1), from
+// which the host measures the clock the CUs ran at under this kernel; a
+// work-group with no tile writes zeros.
+__device__ __forceinline__ void g4_clock(const G2Args &g, int slot, bool live) {
+    if (g.clk != nullptr && threadIdx.x == 0 && blockIdx.x < (unsigned)g.clk_n) {
+        uint64_t *p = g.clk + 4 * (size_t)blockIdx.x + 2 * slot;
+        p[0] = live ? (uint64_t)clock64() : 0ull;
+        p[1] = live ? (uint64_t)wall_clock64() : 0ull;
+    }
+}
+
 __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) k_g4_glu(G2Args g) {
     __shared__ __attribute__((aligned(1024))) _Float16 As0[G4_AST];
     __shared__ __attribute__((aligned(1024))) _Float16 As1[G4_AST];
@@ -536,7 +549,11 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     int tile, ctile;
     g4_coords((int)(g.I / 128), tile, ctile);
     const G4Tile t = g4_desc(g, tile);
-    if (!t.live) return;
+    g4_clock(g, 0, t.live);
+    if (!t.live) {
+        g4_clock(g, 1, false);
+        return;
+    }
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int my_p = g4_rows_load(g, t);
     const int nrt = __builtin_amdgcn_readfirstlane(t.nrt);
@@ -565,6 +582,7 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     case 2: g4_glu_store<2>(g, acc, t, ctile, wave, lane, s_p); break;
     default: g4_glu_store<3>(g, acc, t, ctile, wave, lane, s_p); break;
     }
+    g4_clock(g, 1, true);
 }
 
 // ------------------------------------------------------------------ STORE
@@ -579,7 +597,11 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     int tile, ctile;
     g4_coords((int)((g.ncols + G4_NWG - 1) / G4_NWG), tile, ctile);
     const G4Tile t = g4_desc(g, tile);
-    if (!t.live) return;
+    g4_clock(g, 0, t.live);
+    if (!t.live) {
+        g4_clock(g, 1, false);
+        return;
+    }
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int l32 = lane & 31, g2 = lane >> 5;
     const int my_p = g4_rows_load(g, t);
@@ -617,9 +639,16 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
             }
         }
     }
+    g4_clock(g, 1, true);
 }
 
 // ------------------------------------------------------------------ launch
+int gemm4_grid(const G2Args &g) {
+    const int ntile8 = (g.max_tiles + 7) / 8;
+    const int nct = g.glu ? (int)(g.I / 128) : (int)((g.ncols + G4_NWG - 1) / G4_NWG);
+    return 8 * nct * ntile8;
+}
+
 int launch_gemm4(const G2Args &g, hipStream_t st) {
     if (g.max_tiles <= 0) return 0;
     if (g.a.K % QK) return -6;

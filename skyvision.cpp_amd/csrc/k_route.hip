@@ -92,6 +92,7 @@ __device__ __forceinline__ void q8k_quant(const float (&v)[16], int64_t row, int
         *(uint4 *)&sq[bl * QK + 16 * l16] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         if (l16 == 0) sd[bl] = d;
         wave_lds_sync();
+        if (bok && l16 == 0 && !exact && o.range_total && f16_over(d)) atomicAdd(o.range_total, 1);
         if (bok && XO != XO_ANY) {
             const float db = sd[bl];
             const int s = l16;
@@ -115,8 +116,8 @@ __device__ __forceinline__ void q8k_quant(const float (&v)[16], int64_t row, int
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     half2_t hh;
-                    hh[0] = (_Float16)(db * (float)q[2 * k]);
-                    hh[1] = (_Float16)(db * (float)q[2 * k + 1]);
+                    hh[0] = f16_sat(db * (float)q[2 * k]);
+                    hh[1] = f16_sat(db * (float)q[2 * k + 1]);
                     h[4 * g + k] = __builtin_bit_cast(uint32_t, hh);
                 }
             }
@@ -137,8 +138,8 @@ __device__ __forceinline__ void q8k_quant(const float (&v)[16], int64_t row, int
                     qv[j] = exact ? qf : db * qf;
                 }
                 half2_t hh;
-                hh[0] = (_Float16)qv[0];
-                hh[1] = (_Float16)qv[1];
+                hh[0] = f16_sat(qv[0]);
+                hh[1] = f16_sat(qv[1]);
                 h[i] = __builtin_bit_cast(uint32_t, hh);
             }
             uint4 *dst = (uint4 *)(xh + row * K + (int64_t)b * QK + 16 * l16);

@@ -35,6 +35,7 @@ struct Q8Out {
     int exact = 0;               // 1: xh holds the codes q (exact), d8 and xbs the scales / block sums
     _Float16 *xbs = nullptr;     // [rows][K/16] block sums of 16 codes, as fp16 (exact)
     int pre_act = 0;             // 4 (ACT_RELU_SQR): quantize relu(v)^2 instead of v
+    int32_t *range_total = nullptr;   // [1] or null: blocks whose xh saturated at the fp16 range
 };
 // quantize rows of src (row r at src + r*ld floats) to Q8_K
 int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, const Q8Out &o, hipStream_t st);
@@ -142,6 +143,7 @@ struct GemmArgs {
     _Float16 *acth;
     int next_type;
     int64_t ncols;
+    int32_t *range_total;   // [1] or null: activation blocks saturated at the fp16 range
 };
 constexpr int GEMM_BM = 64;
 int launch_gemm(const GemmArgs &g, hipStream_t st);
@@ -170,9 +172,14 @@ struct G2Args {
     _Float16 *acth;
     int next_type;
     int64_t ncols;
+    // profiling only (else NULL): per work-group {shader clock, wall clock} at
+    // its start and end, 4 words per work-group of the grid (dead ones write 0)
+    uint64_t *clk;
+    int clk_n;            // work-groups clk holds
 };
 constexpr int G4_BM = 192;
 int launch_gemm4(const G2Args &g, hipStream_t st);
+int gemm4_grid(const G2Args &g);   // work-groups launch_gemm4 launches
 
 // Single-token MoE block in one cooperative kernel (k_decode.hip).
 struct DecArgs {

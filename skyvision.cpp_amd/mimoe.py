@@ -84,7 +84,7 @@ SYMBOLS = {
     "mi_moe_ctx_create": ([C.POINTER(P), C.c_int], C.c_int),
     "mi_moe_ctx_destroy": ([P], None),
     "mi_moe_ctx_reserve": ([P, i64, i32, i32, i32, i32], C.c_int),
-    "mi_moe_ctx_take_errors": ([P, C.POINTER(i64), C.POINTER(i64)], C.c_int),
+    "mi_moe_ctx_take_errors": ([P, C.POINTER(i64), C.POINTER(i64), C.POINTER(i64)], C.c_int),
     "mi_moe_forward": ([P, C.POINTER(Layer), P, i64, P, P, C.POINTER(Routing), P], C.c_int),
     "mi_moe_forward_noalloc": ([C.POINTER(Layer), P, i64, P, P, C.POINTER(Routing), P], C.c_int),
     "mi_moe_expert_ffn": ([P, C.POINTER(Layer), P, i64, P, P, P, P, P, P], C.c_int),
@@ -98,6 +98,7 @@ SYMBOLS = {
     "mi_moe_forward_norm": ([P, C.POINTER(Layer), C.POINTER(Norm), P, i64, P, P, C.POINTER(Routing), P],
                             C.c_int),
     "mi_moe_ctx_set_profiling": ([P, C.c_int], C.c_int),
+    "mi_moe_ctx_stage_clock": ([P, C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_int)], C.c_int),
     "mi_moe_ctx_stage_times": ([P, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_float),
                                 C.POINTER(C.c_int)], C.c_int),
     "mi_moe_ctx_set_gemm_threshold": ([P, i64], C.c_int),
@@ -275,10 +276,16 @@ class Context:
         call("mi_moe_ctx_set_fused_decode", self.h, m)
 
     def take_errors(self):
-        """(bad ids, fused-decode wait failures) since the last take; syncs the device."""
-        b, f = i64(), i64()
-        call("mi_moe_ctx_take_errors", self.h, C.byref(b), C.byref(f))
-        return b.value, f.value
+        """(bad ids, fused-decode wait failures) since the last take; syncs the
+        device.  The fp16-saturated block count is take_all_errors()[2]."""
+        return self.take_all_errors()[:2]
+
+    def take_all_errors(self):
+        """(bad ids, fused-decode wait failures, GEMM-path Q8_K blocks clamped
+        at the fp16 range) since the last take; syncs the device."""
+        b, f, r = i64(), i64(), i64()
+        call("mi_moe_ctx_take_errors", self.h, C.byref(b), C.byref(f), C.byref(r))
+        return b.value, f.value, r.value
 
     def set_profiling(self, on: bool) -> None:
         call("mi_moe_ctx_set_profiling", self.h, int(on))
@@ -289,6 +296,17 @@ class Context:
         n = C.c_int()
         call("mi_moe_ctx_stage_times", self.h, 16, names, ms, C.byref(n))
         return [(names[i].decode(), ms[i]) for i in range(n.value)]
+
+    def stage_clock(self, stage: str):
+        """(GHz, work-groups measured) of the shader clock under the last
+        profiled forward's `stage` GEMM ("gate_up" / "down"), or None when that
+        stage did not run on the 4-wave GEMM path."""
+        ghz, n = C.c_double(), C.c_int()
+        rc = load().mi_moe_ctx_stage_clock(self.h, stage.encode(), C.byref(ghz), C.byref(n))
+        if rc == ERR_ARG:
+            return None
+        check("mi_moe_ctx_stage_clock", rc)
+        return ghz.value, n.value
 
     def forward(self, layer: Layer, x, T: int, res, out, routing: Routing | None = None,
                 stream=None) -> int:

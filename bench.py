@@ -483,7 +483,8 @@ def main() -> int:
     ap.add_argument("--no-coop", action="store_true",
                     help="skip timing the cooperative-launch decode schedule (rocprofv3 cannot "
                          "write its results after a cooperative launch on this image)")
-    ap.add_argument("--cpu-tokens", type=int, default=64)
+    ap.add_argument("--cpu-tokens", type=int, default=1024,
+                    help="tokens of the CPU baseline sample (default: the whole config-1 batch)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 512 MiB device-to-device copy (the known-size kernel "
                          "that scales FETCH_SIZE / WRITE_SIZE counters to bytes)")

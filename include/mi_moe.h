@@ -164,8 +164,8 @@ int  mi_moe_ctx_reserve(mi_moe_ctx *ctx, int64_t max_tokens, int32_t n_embd, int
  * synchronize, so these are reported afterwards), counted since the last take
  * and then cleared.  bad_ids: caller-supplied expert ids outside [0, E)
  * (mi_moe_expert_ffn, mi_mul_mat_id; ggml_mul_mat_id asserts them).
- * wait_failures: fused single-token calls whose grid wait gave up (their
- * output is NaN; MI_DECODE_FUSED_EXCLUSIVE on a GPU shared with other work).
+ * wait_failures: fused single-token calls whose waits gave up (their output
+ * is NaN; not expected: a work-group computes what it waited too long for).
  * fp16_saturated: 256-value Q8_K blocks of the grouped-GEMM path (input rows
  * or activation rows) whose largest |value| exceeds 65504, the fp16 range of
  * the MFMA operands: their operands were clamped to +-65504, so the products
@@ -193,7 +193,7 @@ int mi_moe_forward(mi_moe_ctx *ctx, const mi_moe_layer *layer, const float *x, i
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  It calls no hipMalloc / hipFree or any
  * allocating routine: its workspace is one file-scope device array of the
- * library per GPU, 16,678,912 bytes, held until the process ends, sized for
+ * library per GPU, 16,706,816 bytes, held until the process ends, sized for
  * calls of at most MI_NOALLOC_MAX_TOKENS tokens of layers with n_embd <= 2048,
  * n_ff <= 1024, n_expert <= 128, n_expert_used <= 8 (a shared expert's
  * sh_n_ff <= 8192); larger calls return MI_MOE_ERR_CAPACITY and enqueue
@@ -323,25 +323,33 @@ int mi_moe_ctx_stage_clock(mi_moe_ctx *ctx, const char *stage, double *ghz, int 
  * GEMM when 4 * T * K > 5 * E (more than 1.25 dispatched rows per expert). */
 int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *ctx, int64_t min_tokens_for_gemm);
 /* Schedule of single-token calls of mi_moe_forward.  The fused modes run the
- * whole block in one kernel of one work-group per CU that synchronizes
- * through grid barriers, when the layer fits it (Q4_K gate/up, Q4_K or Q6_K
- * down, top-k <= 8, 16-byte aligned tables); other layers use the chain.
+ * whole block in one kernel of one work-group per CU, when the layer fits it
+ * (Q4_K gate/up, Q4_K or Q6_K down, top-k <= 8, 16-byte aligned tables);
+ * other layers use the chain.  Inside the kernel, work-groups hand each other
+ * the router logits and the gate/up activations through completion words;
+ * a work-group that does not see a result after a bounded number of polls
+ * computes it itself (the same bits), so the kernel needs no co-residency
+ * guarantee and cannot deadlock on a GPU shared with other work.
  *   MI_DECODE_CHAIN              separate kernels
- *   MI_DECODE_FUSED_COOPERATIVE  fused, cooperative launch: the runtime
- *                                guarantees all work-groups are resident (default)
- *   MI_DECODE_FUSED_EXCLUSIVE    fused, plain launch: ~18 us less per call on
- *                                MI355X, for a GPU that runs nothing else
- *                                concurrently (two such kernels sharing the GPU
- *                                could each wait for the other's CUs; the
- *                                waits are bounded and then return NaN)
+ *   MI_DECODE_FUSED_COOPERATIVE  fused, cooperative launch (~18 us more per
+ *                                call on MI355X: the runtime's cooperative
+ *                                queue)
+ *   MI_DECODE_FUSED              fused, plain launch (default)
+ * MI_DECODE_FUSED_EXCLUSIVE is the former name of MI_DECODE_FUSED.
  * Same results in every mode; the reference has one graph per step
  * (moe_decode_driver.hpp:493-514), this only picks the GPU schedule. */
 enum {
     MI_DECODE_CHAIN = 0,
     MI_DECODE_FUSED_COOPERATIVE = 1,
+    MI_DECODE_FUSED = 2,
     MI_DECODE_FUSED_EXCLUSIVE = 2
 };
 int mi_moe_ctx_set_fused_decode(mi_moe_ctx *ctx, int mode);
+/* Polls a fused single-token work-group makes for another work-group's
+ * result before computing that result itself (default 64, about 50 us; the
+ * normal waits take under 10 polls).  0 computes every result not ready at
+ * the first look (the fallback path, for testing). */
+int mi_moe_ctx_set_decode_rescue(mi_moe_ctx *ctx, int polls);
 size_t      mi_row_size(int32_t type, int64_t n_per_row);
 const char *mi_moe_status_string(int status);
 int         mi_moe_abi_version(void);

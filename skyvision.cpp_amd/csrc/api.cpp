@@ -107,11 +107,11 @@ struct mi_moe_ctx {
     int32_t *range_total = nullptr; // GEMM-path Q8_K blocks saturated at the fp16 range
     int64_t gemm_threshold = 0;   // 0: the shape rule of use_gemm
     // single-token fused kernel (k_decode.hip)
-    int fused_decode = MI_DECODE_FUSED_COOPERATIVE;
+    int fused_decode = MI_DECODE_FUSED;
     int dec_grid = 0;          // cooperative grid (one WG per CU), 0: unavailable
     uint64_t *dec_tw = nullptr;
     uint32_t *dec_epoch = nullptr;
-    unsigned long long *dec_sync = nullptr;
+    unsigned dec_rescue_polls = DEC_RESCUE_POLLS;
     unsigned *dec_err = nullptr;
 
     bool profiling = false;
@@ -271,7 +271,7 @@ int run_decode1(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, const floa
     g.counts = c->disp[0].counts; g.offsets = c->disp[0].offsets; g.perm = c->disp[0].perm;
     g.xq = c->ax.q8; g.xd = c->ax.d8; g.xbs = c->ax.bs;
     g.actf = c->f1;
-    g.tw = c->dec_tw; g.epoch = c->dec_epoch; g.sync = c->dec_sync; g.err = c->dec_err;
+    g.tw = c->dec_tw; g.epoch = c->dec_epoch; g.err = c->dec_err; g.rescue_polls = c->dec_rescue_polls;
     TRY(launch_decode1(g, c->dec_grid, c->fused_decode == MI_DECODE_FUSED_COOPERATIVE, st));
     stage_end(c, "decode1", st);
     return MI_MOE_OK;
@@ -517,8 +517,7 @@ constexpr size_t ws_bytes(int64_t max_tokens, int64_t D, int64_t I, int64_t E, i
     need += carve_size<int8_t>(rows * iq) + carve_size<float>(rows * iq / QK) +
             carve_size<int16_t>(rows * iq / 16) + carve_size<_Float16>(rows * iq);
     need += carve_size<float>(rows * wide) + carve_size<float>(rows * I) + carve_size<float>(rows * wide);
-    need += carve_size<uint64_t>(DEC_TW_WORDS) + carve_size<uint32_t>(DEC_MAX_GRID) +
-            carve_size<unsigned long long>(DEC_SYNC_WORDS) + carve_size<unsigned>(1);
+    need += carve_size<uint64_t>(DEC_TW_WORDS) + carve_size<uint32_t>(DEC_MAX_GRID) + carve_size<unsigned>(1);
     need += carve_size<float>(max_tokens * D) + 2 * carve_size<float>(max_tokens) + carve_size<int32_t>(max_tokens);
     return need;
 }
@@ -568,7 +567,6 @@ bool carve_workspace(mi_moe_ctx *c, char *base, int64_t max_tokens, int32_t D, i
     c->z = carve<float>(q, rows * wide);
     c->dec_tw = carve<uint64_t>(q, DEC_TW_WORDS);
     c->dec_epoch = carve<uint32_t>(q, DEC_MAX_GRID);
-    c->dec_sync = carve<unsigned long long>(q, DEC_SYNC_WORDS);
     c->dec_err = carve<unsigned>(q, 1);
     c->sh_out = carve<float>(q, max_tokens * D);
     c->sh_w = carve<float>(q, max_tokens);
@@ -694,8 +692,15 @@ int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *c, int64_t t) {
 
 int mi_moe_ctx_set_fused_decode(mi_moe_ctx *c, int on) {
     if (!c) return MI_MOE_ERR_NULL;
-    if (on < MI_DECODE_CHAIN || on > MI_DECODE_FUSED_EXCLUSIVE) return MI_MOE_ERR_ARG;
+    if (on < MI_DECODE_CHAIN || on > MI_DECODE_FUSED) return MI_MOE_ERR_ARG;
     c->fused_decode = on;
+    return MI_MOE_OK;
+}
+
+int mi_moe_ctx_set_decode_rescue(mi_moe_ctx *c, int polls) {
+    if (!c) return MI_MOE_ERR_NULL;
+    if (polls < 0) return MI_MOE_ERR_ARG;
+    c->dec_rescue_polls = (unsigned)polls;
     return MI_MOE_OK;
 }
 
@@ -866,6 +871,7 @@ namespace {
 constexpr int64_t NA_T = MI_NOALLOC_MAX_TOKENS;
 constexpr int32_t NA_D = 2048, NA_I = 1024, NA_E = 128, NA_K = 8;
 constexpr size_t NA_BYTES = ws_bytes(NA_T, NA_D, NA_I, NA_E, NA_K);
+static_assert(NA_BYTES == 16706816, "mi_moe.h states the no-allocation workspace size");
 constexpr int NA_MAX_DEVICES = 64;
 
 struct NoallocDevice {

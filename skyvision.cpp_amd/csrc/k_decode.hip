@@ -1,4 +1,4 @@
-// k_decode.hip - the whole MoE block for one token in one cooperative kernel.
+// k_decode.hip - the whole MoE block for one token in one kernel.
 //
 // Reference block (one decode step): router mul_mat(+bias) -> top_k ->
 // get_rows -> soft_max -> mul_mat_id gate/up -> GLU -> mul_mat_id down ->
@@ -10,19 +10,21 @@
 // arithmetic, so its time is the HBM stream plus whatever serial latency
 // sits in front of it.  The separate-kernel chain pays a launch gap per
 // stage; here every stage lives in one grid of one work-group per CU, and
-// the stages meet at two grid barriers:
+// the stages meet at two hand-offs:
 //
-//   A  router rows (one wave per expert, fp64 fixed order) and Q8_K of x
-//   -- barrier --
-//   B  every WG ranks the E logits itself (no extra barrier for top-k), then
-//      DMAs its share of the selected experts' gate/up rows into LDS
-//      (buffer_load ... lds, 1 KB per wave instruction) and loads its share
-//      of their down rows into registers, so the down stream overlaps the
-//      gate/up arithmetic.
-//      Integer Q4_K x Q8_K dots, GLU, fp32 activations to HBM; the last WG
-//      to finish a 256-column block quantizes it to Q8_K.
-//   -- barrier --
-//   C  down dots from the LDS-resident rows, weighted combine in slot order
+//   A  units a < E: router row a (one wave, fp64 fixed order) and, for
+//      a < D/256, Q8_K of x block a.  WG a runs unit a.
+//   -- logits --
+//   B  every WG ranks the E logits itself (no extra barrier for top-k).
+//      Units u < K I / P: P (h, g) row pairs of the selected experts' gate/up
+//      rows, DMA'd into LDS (buffer_load ... lds, 1 KB per wave instruction);
+//      integer Q4_K x Q8_K dots, GLU, fp32 activations written through.  WG
+//      u runs unit u, then DMAs its share of the down rows (they stream
+//      while the activations are handed over) and unpacks them into a
+//      dot-ready form.
+//   -- activations --
+//   C  per WG: Q8_K of each slot's activations, down dots from the
+//      LDS-resident rows of its columns, weighted combine in slot order
 //      (fp64, ggml's sum_rows of the weighted rows) and residual add.
 //
 // Numerics are the GEMV path's: exact integer dots per 32-value piece,
@@ -37,21 +39,21 @@
 // compiles to), issued only after the poll that saw the producer's completion
 // word: every hand-off read is a coherent read at agent scope, whatever an
 // XCD's L2 held before.  (Agent-scope acquire / release fences would add a
-// whole-L2 invalidate / write-back per work-group and hand-off.)  Two
-// hand-offs:
-//   logits -> every WG: each logit is a 64-bit word tagged with the launch
-//     epoch; a WG polls the E words (one coalesced wave load per try) instead
-//     of meeting a barrier.  The router WGs that also quantize x store their
-//     logit only after their Q8_K of x is out, so ready logits imply ready x.
-//     The epoch is per WG (read at start, stored +1 at the end), so all
-//     epochs agree at every launch, with no atomics and no reset.
-//   activations -> every WG: a grid barrier of two levels of monotonic
-//     counters (16-WG groups, then groups) and a release word holding the
-//     round; nothing is reset between launches.
-// Both keep a captured graph replaying correctly.  Producers and consumers
-// must be resident together: the launch is cooperative, or plain on a GPU
-// that runs nothing else.  Waits are bounded; a WG whose wait gives up
-// writes NaN and sets an error word instead of hanging the GPU.
+// whole-L2 invalidate / write-back per work-group and hand-off.)  Each unit
+// publishes a 64-bit completion word tagged with the launch epoch (the
+// logit itself for an A unit; a B unit's word follows its activation
+// stores); consumers poll the words (one coalesced wave load per try).  An
+// A unit's logit is stored only after its Q8_K of x is out, so ready logits
+// imply ready x.  The epoch is per WG (read at start, stored +1 at the end),
+// so all epochs agree at every launch, with no atomics and no reset, and a
+// captured graph replays correctly.
+//
+// No co-residency is assumed: a WG that has not seen a unit complete after
+// DecArgs::rescue_polls tries computes the unit itself and publishes it
+// again (the same bits).  So a WG only ever waits on a running WG, and the
+// kernel cannot deadlock when other work holds some CUs: the plain launch is
+// safe anywhere, the cooperative launch is optional.  Waits are bounded all
+// the same; a WG whose waits give up writes NaN and sets an error word.
 #include "act.hpp"
 #include "common.hpp"
 #include "launch.hpp"
@@ -70,7 +72,7 @@ constexpr int DEC_KMAX = 8;         // slots: one wave each in the down phase
 constexpr int DEC_PMAX = 64;        // (h, g) row pairs per WG
 constexpr int DEC_CMAX = 64;        // down columns per WG
 constexpr unsigned DEC_SPIN_LIMIT = 1u << 20;
-constexpr int DEC_SYNC_GROUPS = DEC_MAX_GRID / 16;
+constexpr int DEC_GROUP = 16;       // gate/up units per completion group
 
 // ---------------------------------------------------------------- tagged words
 __device__ inline void tw_store(uint64_t *p, uint32_t tag, uint32_t v) {
@@ -79,77 +81,88 @@ __device__ inline void tw_store(uint64_t *p, uint32_t tag, uint32_t v) {
 __device__ inline uint64_t tw_load(const uint64_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// the data of N words once all carry `tag` (loads issued together, only the
-// stale ones re-read); ok is cleared if the poll gives up
-template <int N>
-__device__ inline void tw_poll(const uint64_t *const (&p)[N], uint32_t tag, uint32_t (&out)[N], bool &ok) {
-    uint64_t w[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i) w[i] = tw_load(p[i]);
-    unsigned n = 0;
-    for (;;) {
-        bool all = true;
-#pragma unroll
-        for (int i = 0; i < N; ++i) all = all && (uint32_t)(w[i] >> 32) == tag;
-        if (all) break;
-        if (++n > DEC_SPIN_LIMIT) {
-            ok = false;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-        for (int i = 0; i < N; ++i)
-            if ((uint32_t)(w[i] >> 32) != tag) w[i] = tw_load(p[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < N; ++i) out[i] = (uint32_t)w[i];
-}
 __device__ inline void st_dev4(void *base, uint32_t off, uint32_t v) {
     __hip_atomic_store((uint32_t *)((uint8_t *)base + off), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Grid barrier in two halves so a WG can work between arriving and waiting.
-// Counters 256 bytes apart: group g at sync[32 g], the top counter at
-// sync[32 * DEC_SYNC_GROUPS], the release word after it.  Every thread of the
-// WG calls both halves; the WG's write-through stores must come from wave 0
-// and be issued before dec_arrive.
-constexpr int DEC_GROUP = 16;
-__device__ inline unsigned long long dec_arrive(unsigned long long *sync) {
-    // the WG's hand-off stores come from wave 0 only (the caller's contract):
-    // once they are done, thread 0 arrives; the other waves go on at once
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-    unsigned long long old = 0;
-    if (threadIdx.x == 0) {
-        const unsigned G = gridDim.x;
-        const unsigned S = (G % DEC_GROUP == 0) ? DEC_GROUP : G;
-        const unsigned ngroups = G / S;
-        old = __hip_atomic_fetch_add(sync + 32 * (blockIdx.x / S), 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old % S == S - 1) {   // last of its group: arrive at the top level
-            unsigned long long *top = sync + 32 * DEC_SYNC_GROUPS;
-            const unsigned long long o2 = __hip_atomic_fetch_add(top, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (o2 % ngroups == ngroups - 1)
-                __hip_atomic_store(top + 32, old / S + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+// One tagged word: true once it carries `tag` (value in v), false after
+// `limit` further tries.
+__device__ inline bool tw_wait1(const uint64_t *p, uint32_t tag, unsigned limit, uint32_t &v) {
+    uint64_t w = tw_load(p);
+    unsigned n = 0;
+    while ((uint32_t)(w >> 32) != tag) {
+        if (n++ >= limit) return false;
+        __builtin_amdgcn_s_sleep(1);
+        w = tw_load(p);
     }
-    return old;
+    v = (uint32_t)w;
+    return true;
 }
-// ok is cleared if the wait gives up
-__device__ inline void dec_wait(unsigned long long *sync, unsigned long long old, bool &ok) {
-    if (threadIdx.x == 0) {
-        const unsigned G = gridDim.x;
-        const unsigned S = (G % DEC_GROUP == 0) ? DEC_GROUP : G;
-        const unsigned long long *rel = sync + 32 * DEC_SYNC_GROUPS + 32;
-        const unsigned long long round = old / S + 1;
-        unsigned n = 0;
-        while (__hip_atomic_load(rel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < round) {
-            if (++n > DEC_SPIN_LIMIT) {
-                ok = false;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
+
+// workgroup barrier that does not wait for outstanding global loads / DMA
+__device__ inline void dec_lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+}
+
+// Completion counters of the gate/up units, in two levels so that no word
+// takes more than 16 atomic adds: unit u's owner adds 1 to group u / 16 once
+// the unit is out, the add that completes a group adds 1 to the top counter,
+// and the add that completes the top stores the release word (tagged with the
+// launch epoch), the one word every WG polls.  Each launch
+// uses the set of its epoch's parity; the launch's WG 0 clears the other set,
+// which the next launch uses (it starts only after this one has ended).
+// Rescued units are not counted (their owners count them when they run):
+// past the rescue the per-unit completion words decide.
+__device__ inline unsigned long long *dec_cnt(uint64_t *tw, uint32_t tag, int word) {
+    return (unsigned long long *)(tw + DEC_TW_CNT + (int)(tag & 1u) * DEC_CNT_SET + 32 * word);
+}
+__device__ inline void dec_cnt_unit(uint64_t *tw, uint32_t tag, int u, int UB) {
+    const int grp = u / DEC_GROUP, gsz = imin(DEC_GROUP, UB - DEC_GROUP * grp);
+    const unsigned long long ngrp = (unsigned long long)((UB + DEC_GROUP - 1) / DEC_GROUP);
+    const unsigned long long old =
+        __hip_atomic_fetch_add(dec_cnt(tw, tag, 1 + grp), 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == (unsigned long long)(gsz - 1)) {
+        const unsigned long long o2 =
+            __hip_atomic_fetch_add(dec_cnt(tw, tag, 0), 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (o2 == ngrp - 1) tw_store(tw + DEC_TW_REL, tag, 1u);
     }
-    __syncthreads();
+}
+// thread 0 polls the release word (at most `limit` more tries); the answer is
+// broadcast through *s_flag
+__device__ inline bool dec_cnt_all(uint64_t *tw, uint32_t tag, unsigned limit, int *s_flag) {
+    if (threadIdx.x == 0) {
+        uint32_t v;
+        *s_flag = tw_wait1(tw + DEC_TW_REL, tag, limit, v) ? 1 : 0;
+    }
+    dec_lds_barrier();
+    return __builtin_amdgcn_readfirstlane(*s_flag) != 0;
+}
+
+// True when no thread of the WG saw a unit missing: one ballot per wave, one
+// LDS word per wave, one barrier.  (A caller that goes on polling calls
+// dec_missing first, whose barriers separate the rounds.)
+__device__ inline bool dec_none_missing(int *s_wmiss, bool miss) {
+    const bool any = __ballot(miss) != 0;
+    if ((threadIdx.x & 63) == 0) s_wmiss[threadIdx.x >> 6] = any;
+    dec_lds_barrier();
+    int m = 0;
+#pragma unroll
+    for (int w = 0; w < DEC_WAVES; ++w) m |= s_wmiss[w];
+    return m == 0;
+}
+
+// Units still missing after a WG's poll: each polling thread appends the (up
+// to two) units it did not see complete to an LDS list; returns the list's
+// length (uniform).  Three LDS-only barriers.
+__device__ inline int dec_missing(int *s_n, int *s_list, int u0, int u1, bool miss0, bool miss1) {
+    dec_lds_barrier();   // earlier readers of the list are done
+    if (threadIdx.x == 0) *s_n = 0;
+    dec_lds_barrier();
+    if (miss0) s_list[atomicAdd(s_n, 1)] = u0;
+    if (miss1) s_list[atomicAdd(s_n, 1)] = u1;
+    dec_lds_barrier();
+    return __builtin_amdgcn_readfirstlane(*s_n);
 }
 
 // Hand-off reads: 16 / 4 bytes at byte offset off of a buffer of nbytes,
@@ -168,12 +181,6 @@ __device__ inline uint32_t co_ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 // reinterpret a 32-bit value (passed by value: this toolchain's
 // __builtin_bit_cast of an ext-vector element reads element 0)
 __device__ inline float as_float(uint32_t u) { return __builtin_bit_cast(float, u); }
-
-// workgroup barrier that does not wait for outstanding global loads / DMA
-__device__ inline void dec_lds_barrier() {
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-    asm volatile("s_barrier" ::: "memory");
-}
 
 // ---------------------------------------------------------------- phase A
 // logit of expert e: the router's fixed fp64 order (64-wide chunk c: sum over
@@ -454,7 +461,8 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
     __shared__ float s_val[DEC_KMAX], s_w[DEC_KMAX];
     __shared__ float s_hg[2 * DEC_PMAX];
     __shared__ float s_z[DEC_KMAX * DEC_CMAX];
-    __shared__ int s_fail;
+    __shared__ int s_list[DEC_MAX_GRID];   // units still missing after a poll
+    __shared__ int s_fail, s_nmiss, s_flag, s_wmiss[DEC_WAVES];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -478,14 +486,37 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     dec_lds_barrier();
     if (wave == 0 && lane == 0 && wg < E) tw_store(g.tw + DEC_TW_LOGIT + wg, tag, __builtin_bit_cast(uint32_t, logit));
+    if (wg == 0 && tid <= DEC_MAX_GRID / DEC_GROUP)
+        __hip_atomic_store(dec_cnt(g.tw, tag + 1u, tid), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // ---- every logit (and so every Q8_K block of x); an A unit still missing
+    // after g.rescue_polls tries is computed here and stored again (same bits):
+    // no WG waits on a WG that is not running
+    unsigned spins = 0;
+    for (;;) {
+        bool have = true;
+        if (tid < E) {
+            uint32_t v;
+            have = tw_wait1(g.tw + DEC_TW_LOGIT + tid, tag, g.rescue_polls, v);
+            if (have) s_logit[tid] = as_float(v);
+        }
+        if (dec_none_missing(s_wmiss, !have)) break;
+        const int nmiss = dec_missing(&s_nmiss, s_list, tid, -1, !have, false);
+        spins += g.rescue_polls + 1;
+        if (spins > DEC_SPIN_LIMIT) {
+            ok = false;
+            break;
+        }
+        for (int m = wave; m < nmiss; m += DEC_WAVES) {
+            const int a = __builtin_amdgcn_readfirstlane(s_list[m]);
+            if (a < NB) dec_q8k_x(g, a, lane);
+            const float lv = dec_router_row(g, a, lane);
+            __builtin_amdgcn_s_waitcnt(0x0F70);   // the x block is out before the logit
+            if (lane == 0) tw_store(g.tw + DEC_TW_LOGIT + a, tag, __builtin_bit_cast(uint32_t, lv));
+        }
+    }
 
     // ---- B: routing (every WG), DMA of its gate/up and down rows
-    if (tid < E) {
-        const uint64_t *const p[1] = {g.tw + DEC_TW_LOGIT + tid};
-        uint32_t v[1];
-        tw_poll<1>(p, tag, v, ok);
-        s_logit[tid] = as_float(v[0]);
-    }
     if (tid < DEC_KMAX) s_sel[tid] = tid < K ? tid : 0;
     dec_lds_barrier();
     // this lane's activation piece: row group of LPR = 8*NB lanes, block bq,
@@ -522,22 +553,78 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
 
     const int64_t pairs = (int64_t)K * I;
     const int P = g.P, R = P / 4;
+    const int UB = (int)(pairs / P);          // gate/up units of P (h, g) row pairs
     const int64_t q0 = (int64_t)wg * P;
     const bool do_b = q0 < pairs;
-    const int kB = do_b ? (int)(q0 / I) : 0;
-    const int i0 = do_b ? (int)(q0 % I) : 0;
-    {
-        int eb = __builtin_amdgcn_readfirstlane(s_sel[kB]);
+    uint32_t dn_shift = 0;
+    // DMA of unit u's gate/up rows into s_gu (wave v: rows v % 4 of the h
+    // (v < 4) or g half)
+    auto b_issue = [&](int u, bool on) {
+        const int64_t q = (int64_t)u * P;
+        const int kb = on ? (int)(q / I) : 0, ib = on ? (int)(q % I) : 0;
+        int eb = __builtin_amdgcn_readfirstlane(s_sel[kb]);
         eb = eb < 0 ? 0 : (eb >= E ? E - 1 : eb);
         const bool hpart = wave < 4;
         const ExpertMat &m = (hpart || g.fused) ? g.gate : g.up;
-        const int64_t row0 = (int64_t)i0 + (wave & 3) * R + ((!hpart && g.fused) ? I : 0);
-        const DecChunk c = dec_chunk(m, eb, row0, R, do_b);
+        const int64_t row0 = (int64_t)ib + (wave & 3) * R + ((!hpart && g.fused) ? I : 0);
+        const DecChunk c = dec_chunk(m, eb, row0, R, on);
         dec_dma<DEC_GU_SEG>(c.base16, c.span, s_gu[wave], lane);
-    }
+    };
+    // gate/up dots of the unit in s_gu: wave v owns R consecutive rows (h for
+    // v < 4, g for v >= 4); every row's piece first, then the lane-group sums
+    // of all rows together (independent exchanges overlap instead of queueing
+    // one row at a time)
+    auto b_dots = [&]() {
+        const int64_t rb = (int64_t)NB * Q4K_BYTES;   // Q4_K tables are 16-byte aligned: no shift
+        float acc[DEC_RSTEPS];
+#pragma unroll
+        for (int j = 0; j < DEC_RSTEPS; ++j) {
+            acc[j] = 0.f;
+            const int r = j * RPS + rr;
+            if (j * RPS < R && r < R) acc[j] = dec_q4_piece(s_gu[wave] + r * rb + bq * Q4K_BYTES, sl, xg);
+        }
+#pragma unroll
+        for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += dpp_f<0xB1>(acc[j]);
+#pragma unroll
+        for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += dpp_f<0x4E>(acc[j]);
+#pragma unroll
+        for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += dpp_f<0x141>(acc[j]);
+        if (LPR >= 16) {
+#pragma unroll
+            for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += dpp_f<0x140>(acc[j]);
+        }
+        if (LPR >= 32) {
+#pragma unroll
+            for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += __shfl_xor(acc[j], 16, 64);
+        }
+        if (LPR >= 64) {
+#pragma unroll
+            for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += __shfl_xor(acc[j], 32, 64);
+        }
+#pragma unroll
+        for (int j = 0; j < DEC_RSTEPS; ++j) {
+            const int r = j * RPS + rr;
+            if (j * RPS < R && r < R && (lane % LPR) == 0) s_hg[(wave >> 2) * P + (wave & 3) * R + r] = acc[j];
+        }
+    };
+    // GLU of the unit (after an LDS barrier), activations written through,
+    // then the unit's completion word once wave 0's stores are out (P <= 64:
+    // every store comes from wave 0)
+    auto b_publish = [&](int u, bool owner) {
+        const int64_t q = (int64_t)u * P;
+        if (tid < P)
+            st_dev4(g.actf, 4u * (uint32_t)(q + tid), __builtin_bit_cast(uint32_t, act_pair(g.act, s_hg[tid], s_hg[P + tid])));
+        if (wave == 0) {
+            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+            if (lane == 0) {
+                tw_store(g.tw + DEC_TW_BDONE + u, tag, 1u);
+                if (owner) dec_cnt_unit(g.tw, tag, u, UB);
+            }
+        }
+    };
+    b_issue(wg, do_b);
     // down rows of slot k = wave: prefetched into registers now (the stream
     // overlaps the gate/up arithmetic), parked in LDS after it
-    uint32_t dn_shift;
     u32x4 dnv[DEC_DN_SEG];
     {
         const int k = wave < K ? wave : 0;
@@ -579,63 +666,74 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
         if (tid == 0) g.offsets[E] = K;
     }
 
-    // gate/up dots: wave v owns R consecutive rows (h for v < 4, g for v >= 4);
-    // every row's piece first, then the lane-group sums of all rows together
-    // (independent exchanges overlap instead of queueing one row at a time)
-    if (do_b) {
-        const int64_t rb = (int64_t)NB * Q4K_BYTES;   // Q4_K tables are 16-byte aligned: no shift
-        float acc[DEC_RSTEPS];
-#pragma unroll
-        for (int j = 0; j < DEC_RSTEPS; ++j) {
-            acc[j] = 0.f;
-            const int r = j * RPS + rr;
-            if (j * RPS < R && r < R) acc[j] = dec_q4_piece(s_gu[wave] + r * rb + bq * Q4K_BYTES, sl, xg);
-        }
-#pragma unroll
-        for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += dpp_f<0xB1>(acc[j]);
-#pragma unroll
-        for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += dpp_f<0x4E>(acc[j]);
-#pragma unroll
-        for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += dpp_f<0x141>(acc[j]);
-        if (LPR >= 16) {
-#pragma unroll
-            for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += dpp_f<0x140>(acc[j]);
-        }
-        if (LPR >= 32) {
-#pragma unroll
-            for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += __shfl_xor(acc[j], 16, 64);
-        }
-        if (LPR >= 64) {
-#pragma unroll
-            for (int j = 0; j < DEC_RSTEPS; ++j) acc[j] += __shfl_xor(acc[j], 32, 64);
-        }
-#pragma unroll
-        for (int j = 0; j < DEC_RSTEPS; ++j) {
-            const int r = j * RPS + rr;
-            if (j * RPS < R && r < R && (lane % LPR) == 0) s_hg[(wave >> 2) * P + (wave & 3) * R + r] = acc[j];
-        }
-    }
+    if (do_b) b_dots();
 #pragma unroll
     for (int s = 0; s < DEC_DN_SEG; ++s) *(u32x4 *)(s_dn[wave] + 1024 * s + 16 * lane) = dnv[s];
     dec_lds_barrier();
-    if (do_b && tid < P) {
-        const float a = act_pair(g.act, s_hg[tid], s_hg[P + tid]);
-        st_dev4(g.actf, 4u * (uint32_t)(kB * I + i0 + tid), __builtin_bit_cast(uint32_t, a));
-    }
-    const unsigned long long arrival = dec_arrive(g.sync);
+    if (do_b) b_publish(wg, true);
 
     // while the other WGs finish: turn this wave's slot of down rows into the
     // dot-ready form (raw rows in s_dn[wave], result in s_gu[wave])
     const DnLayout UL = dn_layout(C, I);
+    auto unpack = [&]() {
+        if (do_c && wave < K) {
+            const uint32_t rbd = (uint32_t)g.down.row_bytes;
+            for (int u = lane; u < C * NBI * 2; u += 64) {
+                const int c = u / (2 * NBI), rem = u % (2 * NBI), b = rem >> 1, h = rem & 1;
+                if constexpr (DT == 12) dn_unpack_q4(s_dn[wave] + dn_shift, s_gu[wave], UL, I, NBI, rbd, c, b, h);
+                else dn_unpack_q6(s_dn[wave], s_gu[wave], UL, I, NBI, dn_shift + c * rbd + b * Q6K_BYTES, c, b, h);
+            }
+        }
+    };
+
+    unpack();
+    // ---- every gate/up unit: every owner counted, or else each unit's
+    // completion word; a unit still missing after g.rescue_polls tries is
+    // computed here (its rows pass through s_gu, so this WG's down rows are
+    // unpacked again afterwards)
+    const bool all_b = dec_cnt_all(g.tw, tag, g.rescue_polls, &s_flag);
+    for (; !all_b;) {
+        const int u0 = tid, u1 = tid + DEC_THREADS;
+        uint32_t v;
+        const bool miss0 = u0 < UB && !tw_wait1(g.tw + DEC_TW_BDONE + u0, tag, g.rescue_polls, v);
+        const bool miss1 = u1 < UB && !tw_wait1(g.tw + DEC_TW_BDONE + u1, tag, g.rescue_polls, v);
+        if (dec_none_missing(s_wmiss, miss0 || miss1)) break;
+        const int nmiss = dec_missing(&s_nmiss, s_list, u0, u1, miss0, miss1);
+        spins += g.rescue_polls + 1;
+        if (spins > DEC_SPIN_LIMIT) {
+            ok = false;
+            break;
+        }
+        for (int m = 0; m < nmiss; ++m) {
+            const int u = __builtin_amdgcn_readfirstlane(s_list[m]);
+            dec_lds_barrier();   // s_gu / s_hg readers of the previous unit are done
+            b_issue(u, true);
+            b_dots();
+            dec_lds_barrier();
+            b_publish(u, false);
+        }
+        dec_lds_barrier();
+        unpack();
+    }
+    // the activations of slot k = wave (written by other WGs: coherent
+    // loads), 16 lanes per 256-block, four blocks per pass
+    constexpr int NPASS = (NBI + 3) / 4;
+    float av[NPASS][16];
     if (do_c && wave < K) {
-        const uint32_t rbd = (uint32_t)g.down.row_bytes;
-        for (int u = lane; u < C * NBI * 2; u += 64) {
-            const int c = u / (2 * NBI), rem = u % (2 * NBI), b = rem >> 1, h = rem & 1;
-            if constexpr (DT == 12) dn_unpack_q4(s_dn[wave] + dn_shift, s_gu[wave], UL, I, NBI, rbd, c, b, h);
-            else dn_unpack_q6(s_dn[wave], s_gu[wave], UL, I, NBI, dn_shift + c * rbd + b * Q6K_BYTES, c, b, h);
+        const auto ra = co_rsrc(g.actf, (uint32_t)(4 * K * I));
+        const int seg = lane & 15;
+#pragma unroll
+        for (int pp = 0; pp < NPASS; ++pp) {
+            const int b = 4 * pp + (lane >> 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                u32x4 a4 = {0u, 0u, 0u, 0u};
+                if (b < NBI) a4 = co_ld16(ra, 4u * (uint32_t)(wave * I + b * QK + 16 * seg + 4 * i));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) av[pp][4 * i + e] = as_float(a4[e]);
+            }
         }
     }
-    dec_wait(g.sync, arrival, ok);
 
     // ---- C: Q8_K of slot k = wave's activations, down rows, weighted combine
     if (do_c && wave < K) {
@@ -646,23 +744,12 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
         int8_t *aq = (int8_t *)s_dn[k];
         float *ad = (float *)(s_dn[k] + 2048);
         int16_t *abs_ = (int16_t *)(s_dn[k] + 2048 + 64);
-        // 16 lanes per block, four blocks per pass (activations of other WGs:
-        // coherent loads)
-        const auto ra = co_rsrc(g.actf, (uint32_t)(4 * K * I));
-        for (int b0 = 0; b0 < NBI; b0 += 4) {
-            const int b = b0 + (lane >> 4), seg = lane & 15;
-            float v[16];
+        // 16 lanes per block, four blocks per pass, from the polled values
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                u32x4 a4 = {0u, 0u, 0u, 0u};
-                if (b < NBI) a4 = co_ld16(ra, 4u * (uint32_t)(k * I + b * QK + 16 * seg + 4 * i));
-                v[4 * i] = as_float(a4[0]);
-                v[4 * i + 1] = as_float(a4[1]);
-                v[4 * i + 2] = as_float(a4[2]);
-                v[4 * i + 3] = as_float(a4[3]);
-            }
+        for (int pp = 0; pp < NPASS; ++pp) {
+            const int b = 4 * pp + (lane >> 4), seg = lane & 15;
             int q[16], bsum;
-            const float d = q8k_wave4x16(v, lane, q, bsum);
+            const float d = q8k_wave4x16(av[pp], lane, q, bsum);
             if (b < NBI) {
                 u32x4 pk;
 #pragma unroll

@@ -199,19 +199,23 @@ struct DecArgs {
     float *xd;
     int16_t *xbs;
     float *actf;                  // GLU output fp32 [K][I]
-    uint64_t *tw;                 // epoch-tagged logits [E]
+    uint64_t *tw;                 // epoch-tagged logits [E] and gate/up unit completions, launch counters
     uint32_t *epoch;              // [grid] per-WG launch epochs
-    unsigned long long *sync;     // grid barrier counters (only grow), DEC_SYNC_WORDS
     unsigned *err;                // set when a wait gave up (output is NaN)
+    unsigned rescue_polls;        // polls for another WG's unit before computing it here
 };
-constexpr int DEC_TW_LOGIT = 0, DEC_TW_WORDS = 256;
 constexpr int DEC_MAX_GRID = 1024;
-constexpr int DEC_SYNC_WORDS = 32 * (DEC_MAX_GRID / 16 + 2);   // 256 B per counter
+constexpr int DEC_TW_LOGIT = 0, DEC_TW_BDONE = 256, DEC_TW_REL = 256 + DEC_MAX_GRID;
+constexpr int DEC_TW_CNT = DEC_TW_REL + 32;   // the release word on a line of its own
+// two sets of completion counters (top + one per 16 units), 256 bytes apart
+constexpr int DEC_CNT_SET = 32 * (1 + DEC_MAX_GRID / 16);
+constexpr int DEC_TW_WORDS = DEC_TW_CNT + 2 * DEC_CNT_SET;
+constexpr unsigned DEC_RESCUE_POLLS = 64;
 constexpr int DEC_LIMIT_GU_BYTES = 9 * 1024;   // LDS per wave of gate/up rows
 constexpr int DEC_LIMIT_DN_BYTES = 7 * 1024;   // LDS per slot of down rows
 constexpr int DEC_LIMIT_UNPACKED_BYTES = 10 * 1024;   // LDS per slot of dot-ready down rows
-// cooperative: hipLaunchCooperativeKernel (residency guaranteed by the runtime);
-// otherwise a plain launch that relies on the GPU running nothing else
+// cooperative: hipLaunchCooperativeKernel; otherwise a plain launch (the
+// kernel needs no co-residency: a WG computes any unit it waited too long for)
 int launch_decode1(const DecArgs &g, int grid, bool cooperative, hipStream_t st);
 // work-groups of the cooperative grid (one per CU), 0 if it cannot be resident
 int decode1_max_grid(int device, int *grid);

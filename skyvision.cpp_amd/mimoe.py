@@ -14,7 +14,8 @@ import numpy as np
 HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "libmimoe.so"
 
-DECODE_CHAIN, DECODE_FUSED_COOPERATIVE, DECODE_FUSED_EXCLUSIVE = 0, 1, 2
+DECODE_CHAIN, DECODE_FUSED_COOPERATIVE, DECODE_FUSED = 0, 1, 2
+DECODE_FUSED_EXCLUSIVE = DECODE_FUSED   # former name
 
 TYPE_F32, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K, TYPE_I32 = 0, 1, 12, 14, 26
 ACT_SILU, ACT_GELU_ERF_GP1, ACT_GELU_TANH, ACT_GELU_ERF, ACT_RELU_SQR = 0, 1, 2, 3, 4
@@ -103,6 +104,7 @@ SYMBOLS = {
                                 C.POINTER(C.c_int)], C.c_int),
     "mi_moe_ctx_set_gemm_threshold": ([P, i64], C.c_int),
     "mi_moe_ctx_set_fused_decode": ([P, C.c_int], C.c_int),
+    "mi_moe_ctx_set_decode_rescue": ([P, C.c_int], C.c_int),
     "mi_row_size": ([i32, i64], C.c_size_t),
     "mi_moe_status_string": ([C.c_int], C.c_char_p),
     "mi_moe_abi_version": ([], C.c_int),
@@ -271,9 +273,13 @@ class Context:
         call("mi_moe_ctx_set_gemm_threshold", self.h, t)
 
     def set_fused_decode(self, mode) -> None:
-        """False / DECODE_CHAIN, True / DECODE_FUSED_COOPERATIVE, DECODE_FUSED_EXCLUSIVE"""
-        m = DECODE_FUSED_COOPERATIVE if mode is True else DECODE_CHAIN if mode is False else int(mode)
+        """False / DECODE_CHAIN, True / DECODE_FUSED, DECODE_FUSED_COOPERATIVE"""
+        m = DECODE_FUSED if mode is True else DECODE_CHAIN if mode is False else int(mode)
         call("mi_moe_ctx_set_fused_decode", self.h, m)
+
+    def set_decode_rescue(self, polls: int) -> None:
+        """Polls before a fused-decode work-group computes a result it waits for."""
+        call("mi_moe_ctx_set_decode_rescue", self.h, int(polls))
 
     def take_errors(self):
         """(bad ids, fused-decode wait failures) since the last take; syncs the

@@ -113,7 +113,7 @@ def test_decode_fused_parity(name):
     for t in range(n_tok):
         got_f, rt_f, st_f = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED_COOPERATIVE)
         assert "decode1" in st_f, f"fused kernel not taken: {st_f}"
-        got_x, rt_x, st_x = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED_EXCLUSIVE)
+        got_x, rt_x, st_x = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED)
         assert "decode1" in st_x
         got_c, rt_c, st_c = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_CHAIN)
         assert "decode1" not in st_c
@@ -152,7 +152,7 @@ def test_decode_fused_ties(pattern):
     ref, dbg = O.moe_forward(L, x, res)
     assert np.array_equal(dbg["sel"][0], np.argsort(-bias, kind="stable")[:spec.K])
     for t in range(2):
-        got, rt, st = _run_token(ctx, layer, spec, x[t], res[t], M.DECODE_FUSED_EXCLUSIVE)
+        got, rt, st = _run_token(ctx, layer, spec, x[t], res[t], M.DECODE_FUSED)
         assert "decode1" in st
         e = _check_token(f"ties_{pattern}", t, spec, got, rt, ref[t], res[t], dbg, True)
         log(f"ties {pattern} t={t}: sel {rt['sel'].tolist()} rel-L2 {e:.3e}")
@@ -175,7 +175,37 @@ def test_decode_fused_shape_changes():
         layers.append((spec, g, x, res, ref, dbg))
     for t in range(3):
         for spec, g, x, res, ref, dbg in layers:
-            got, rt, st = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED_EXCLUSIVE if t % 2 else M.DECODE_FUSED_COOPERATIVE)
+            got, rt, st = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED if t % 2 else M.DECODE_FUSED_COOPERATIVE)
             assert "decode1" in st
             _check_token(f"mixed_{spec.name}", t, spec, got, rt, ref[t], res[t], dbg, True)
+    ctx.close()
+
+
+@pytest.mark.parametrize("polls", [0, 1])
+def test_decode_fused_rescue(polls):
+    """The fallback that makes the plain launch safe on a shared GPU: a
+    work-group that does not see another's router logit or gate/up unit
+    within `polls` tries computes it itself.  With 0 polls nearly every
+    work-group recomputes every unit not ready at its first look; the
+    results must be the default schedule's, bit for bit."""
+    spec = CASES["md_d1024_q6"]
+    n_tok = 3
+    ctx = M.Context(0)
+    ctx.reserve(n_tok, spec.D, spec.I, spec.E, spec.K)
+    g = W.GpuLayer(ctx, spec)
+    L = oracle_layer_dict(g.download_tables(), spec, g.download_router(), g.bias_host)
+    x = cpu_x(spec, n_tok)
+    res = cpu_x(spec, n_tok, stream=W.S_RES)
+    ref, dbg = O.moe_forward(L, x, res)
+    for t in range(n_tok):
+        ctx.set_decode_rescue(64)
+        base, _, st = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED)
+        assert "decode1" in st
+        ctx.set_decode_rescue(polls)
+        got, rt, st = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED)
+        assert "decode1" in st
+        _check_token(f"rescue_{polls}", t, spec, got, rt, ref[t], res[t], dbg, True)
+        assert np.array_equal(got.view(np.uint32), base.view(np.uint32)), "rescued units changed the bits"
+    assert ctx.take_errors() == (0, 0)
+    log(f"rescue after {polls} polls: {n_tok} tokens bit-identical to the default schedule")
     ctx.close()

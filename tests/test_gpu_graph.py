@@ -79,7 +79,7 @@ def test_graph_config_layer(T):
     spec = W.CONFIGS[1]["spec"]
     ctx = M.Context(0)
     ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
-    ctx.set_fused_decode(M.DECODE_FUSED_EXCLUSIVE)
+    ctx.set_fused_decode(M.DECODE_FUSED)
     g = W.GpuLayer(ctx, spec)
     _graph_vs_eager(ctx, g.layer, spec, T, res=False)
     log(f"graph md_cfg1 T={T}: {REPLAYS} replays bit-identical to eager")

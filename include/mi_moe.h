@@ -166,11 +166,12 @@ int  mi_moe_ctx_reserve(mi_moe_ctx *ctx, int64_t max_tokens, int32_t n_embd, int
  * (mi_moe_expert_ffn, mi_mul_mat_id; ggml_mul_mat_id asserts them).
  * wait_failures: fused single-token calls whose waits gave up (their output
  * is NaN; not expected: a work-group computes what it waited too long for).
- * fp16_saturated: 256-value Q8_K blocks of the grouped-GEMM path (input rows
- * or activation rows) whose largest |value| exceeds 65504, the fp16 range of
- * the MFMA operands: their operands were clamped to +-65504, so the products
- * of those rows are inexact (ggml's own fp16 GPU paths overflow there; the
- * integer GEMV path has no such limit).
+ * fp16_saturated: fp16 values of the grouped-GEMM path clamped to +-65504:
+ * 256-value Q8_K blocks (input rows or activation rows) whose largest |value|
+ * exceeds it, counted per block, and down-product outputs (the per-slot rows
+ * the weighted sum reads, kept as fp16) beyond it, counted per wave of 64
+ * values that held one.  The products of those rows are inexact (ggml's own
+ * fp16 GPU paths overflow there; the integer GEMV path has no such limit).
  * Any pointer may be NULL.  Synchronizes the context's device. */
 int  mi_moe_ctx_take_errors(mi_moe_ctx *ctx, int64_t *bad_ids, int64_t *wait_failures,
                             int64_t *fp16_saturated);

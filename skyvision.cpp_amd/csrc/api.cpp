@@ -381,6 +381,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         return MI_MOE_OK;
     }
 
+    _Float16 *zh = nullptr;   // fp16 slot rows (4-wave GEMM path), else fp32 in c->z
     if (!gemm) {
         GemvArgs a = {};
         a.a = gate; a.b = up; a.epi = gated ? EPI_GLU : EPI_STORE; a.act = L->act; a.I = I;
@@ -427,7 +428,9 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         d.a = down; d.glu = 0; d.xh = c->aact.h; d.ne11 = K; d.K = K;
         d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
         d.tile_r0 = dd.tile_r0; d.tile_start = dd.tile_start; d.tile_rows = dd.tile_rows; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles; d.xrows = (int64_t)T * K;
-        d.y = c->z; d.ldy = D; d.ncols = D;
+        // the slot rows as fp16 (half the bytes of the round trip to the
+        // combine; saturation at the fp16 range is counted)
+        d.y = c->z; d.yh = zh = (_Float16 *)c->z; d.range_total = c->range_total; d.ldy = D; d.ncols = D;
         prof_clock(c, d, 1);
         TRY(launch_gemm4(d, st));
         stage_end(c, "down", st);
@@ -451,7 +454,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
     }
     CombineIds ci;
     if (check_ids) { ci.a = ids_gu; ci.b = ids_dn; ci.E = E; }
-    TRY(launch_combine(c->z, w, res, out, T, K, D, st, ci, add));
+    TRY(launch_combine(zh ? nullptr : c->z, w, res, out, T, K, D, st, ci, add, zh));
     stage_end(c, "combine", st);
     return MI_MOE_OK;
 }

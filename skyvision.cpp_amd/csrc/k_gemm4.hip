@@ -516,17 +516,27 @@ __device__ __forceinline__ void g4_coords(int nct, int &tile, int &ctile) {
 // 256-column blocks, which span two work-groups).
 template <int ACT>
 __device__ __forceinline__ void g4_glu_store(const G2Args &g, const f32x16 (&acc)[G4_BM / 32][2], const G4Tile &t,
-                                             int ctile, int wave, int lane, const int *s_p) {
+                                             int ctile, int wave, int lane, const int *s_p, _Float16 *As0,
+                                             _Float16 *As1) {
+    // through LDS: the wave's 32 GLU columns of every row into the activation
+    // buffers (rows 0-95 in As0, 96-191 in As1, 512 bytes per row), then
+    // whole 512-byte rows out in 16-byte pieces
     const int l32 = lane & 31, g2 = lane >> 5;
-    const int64_t col = (int64_t)ctile * 128 + 32 * wave + l32;
 #pragma unroll
     for (int rt = 0; rt < G4_BM / 32; ++rt) {
         if (rt >= t.nrt) break;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
-            if (m < t.mrows) g.y[(int64_t)s_p[m] * g.ldy + col] = act_pair_fast<ACT>(acc[rt][0][i], acc[rt][1][i]);
+            float *row = (float *)(m < G4_BM / 2 ? As0 + m * 256 : As1 + (m - G4_BM / 2) * 256);
+            row[32 * wave + l32] = act_pair_fast<ACT>(acc[rt][0][i], acc[rt][1][i]);
         }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < t.mrows * 32; idx += G4_THREADS) {
+        const int r = idx >> 5, c = idx & 31;
+        const float *row = (const float *)(r < G4_BM / 2 ? As0 + r * 256 : As1 + (r - G4_BM / 2) * 256);
+        *(float4 *)(g.y + (int64_t)s_p[r] * g.ldy + (int64_t)ctile * 128 + 4 * c) = *(const float4 *)(row + 4 * c);
     }
 }
 
@@ -575,12 +585,12 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     f32x16 acc[G4_BM / 32][2];
     g4_kloop<12>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc);
     __builtin_amdgcn_s_waitcnt(0);   // no load may land in LDS after the work-group ends
-    const int *s_p = g4_publish_rows(As0, my_p);
+    const int *s_p = g4_publish_rows((_Float16 *)&Ws[0][0], my_p);   // the row table in the weight region
     switch (g.act) {
-    case 0: g4_glu_store<0>(g, acc, t, ctile, wave, lane, s_p); break;
-    case 1: g4_glu_store<1>(g, acc, t, ctile, wave, lane, s_p); break;
-    case 2: g4_glu_store<2>(g, acc, t, ctile, wave, lane, s_p); break;
-    default: g4_glu_store<3>(g, acc, t, ctile, wave, lane, s_p); break;
+    case 0: g4_glu_store<0>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
+    case 1: g4_glu_store<1>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
+    case 2: g4_glu_store<2>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
+    default: g4_glu_store<3>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
     }
     g4_clock(g, 1, true);
 }
@@ -623,19 +633,50 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     f32x16 acc[G4_BM / 32][2];
     g4_kloop<WT>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc);
     __builtin_amdgcn_s_waitcnt(0);   // no load may land in LDS after the work-group ends
-    const int *s_p = g4_publish_rows(As0, my_p);
     // rows 32 rt + 8 (i / 4) + 4 g2 + i % 4, columns n0 + 32 ct + l32
+    if (g.yh) {
+        // fp16 out through LDS: the wave's columns of every row into the
+        // activation buffers (rows 0-95 in As0, 96-191 in As1, 512 bytes per
+        // row), then whole 512-byte rows out in 16-byte pieces (full lines
+        // instead of 64-byte runs); the row table lives in the weight region
+        const int *s_p = g4_publish_rows((_Float16 *)&Ws[0][0], my_p);
+        bool over = false;
 #pragma unroll
-    for (int rt = 0; rt < G4_BM / 32; ++rt) {
-        if (rt >= nrt) break;
+        for (int rt = 0; rt < G4_BM / 32; ++rt) {
+            if (rt >= nrt) break;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
-            if (m < t.mrows) {
-                float *yr = g.y + (int64_t)s_p[m] * g.ldy + n0 + l32;
+            for (int i = 0; i < 16; ++i) {
+                const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
+                _Float16 *row = m < G4_BM / 2 ? As0 + m * G4_NWG : As1 + (m - G4_BM / 2) * G4_NWG;
 #pragma unroll
-                for (int ct = 0; ct < 2; ++ct)
-                    if (n0 + 32 * ct + l32 < g.ncols) yr[32 * ct] = acc[rt][ct][i];
+                for (int ct = 0; ct < 2; ++ct) {
+                    const float v = acc[rt][ct][i];
+                    over = over || fabsf(v) > kF16Max;
+                    row[64 * wave + 32 * ct + l32] = f16_sat(v);
+                }
+            }
+        }
+        if (__ballot(over) != 0 && lane == 0 && g.range_total) atomicAdd(g.range_total, 1);
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < t.mrows * (G4_NWG / 8); idx += G4_THREADS) {
+            const int r = idx / (G4_NWG / 8), c = idx % (G4_NWG / 8);
+            const _Float16 *row = r < G4_BM / 2 ? As0 + r * G4_NWG : As1 + (r - G4_BM / 2) * G4_NWG;
+            *(uint4 *)(g.yh + (int64_t)s_p[r] * g.ldy + (int64_t)ctile * G4_NWG + 8 * c) = *(const uint4 *)(row + 8 * c);
+        }
+    } else {
+        const int *s_p = g4_publish_rows(As0, my_p);
+#pragma unroll
+        for (int rt = 0; rt < G4_BM / 32; ++rt) {
+            if (rt >= nrt) break;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
+                if (m < t.mrows) {
+                    float *yr = g.y + (int64_t)s_p[m] * g.ldy + n0 + l32;
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct)
+                        if (n0 + 32 * ct + l32 < g.ncols) yr[32 * ct] = acc[rt][ct][i];
+                }
             }
         }
     }
@@ -658,7 +699,7 @@ int launch_gemm4(const G2Args &g, hipStream_t st) {
     const int ntile8 = (g.max_tiles + 7) / 8;
     if (g.glu) {
         // fp32 GLU values out (y, ldy); the work-group covers 128 act columns
-        if (g.a.type != 12 || (g.I % 128)) return -6;
+        if (g.a.type != 12 || (g.I % 128) || g.ldy % 4 || (uintptr_t)g.y % 16) return -6;
         if (!g.fused && (g.b.mat_bytes > lim || g.b.type != 12 || g.b.row_bytes != g.a.row_bytes)) return -6;
         if ((uintptr_t)g.a.data % 4 || g.a.mat_bytes % 4 || g.a.row_bytes % 4) return -6;
         if (!g.fused && ((uintptr_t)g.b.data % 4 || g.b.mat_bytes % 4)) return -6;
@@ -667,6 +708,7 @@ int launch_gemm4(const G2Args &g, hipStream_t st) {
     } else {
         const int nct = (int)((g.ncols + G4_NWG - 1) / G4_NWG);
         const dim3 grid((unsigned)(8 * nct * ntile8));
+        if (g.yh && (g.ncols % G4_NWG || g.ldy % 8 || (uintptr_t)g.yh % 16)) return -6;
         if (g.a.type == 12) {
             if ((uintptr_t)g.a.data % 4 || g.a.mat_bytes % 4 || g.a.row_bytes % 4) return -6;
             hipLaunchKernelGGL(k_g4_store<12>, grid, dim3(G4_THREADS), 0, st, g);

@@ -661,7 +661,8 @@ __device__ __forceinline__ bool combine_live(const CombineIds &ci, int64_t i) {
     return ((unsigned)a < (unsigned)ci.E) & ((unsigned)b < (unsigned)ci.E);
 }
 
-__global__ void __launch_bounds__(256) k_combine(const float *__restrict__ z, const float *__restrict__ w,
+template <typename ZT>
+__global__ void __launch_bounds__(256) k_combine(const ZT *__restrict__ z, const float *__restrict__ w,
                                                  const float *res, float *out, int64_t T, int K, int D,
                                                  CombineIds ci, const float *__restrict__ add) {
     const int64_t total = T * (int64_t)D;
@@ -672,7 +673,7 @@ __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ z, co
         double s = 0.0;
         for (int k = 0; k < K; ++k) {
             if (!combine_live(ci, t * K + k)) continue;
-            const float prod = z[(t * K + k) * D + n] * w[t * K + k];
+            const float prod = (float)z[(t * K + k) * D + n] * w[t * K + k];
             s = s + (double)prod;
         }
         float moe = (float)s;
@@ -683,8 +684,14 @@ __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ z, co
 
 // Vector form: work-group (column chunk, token), 4 consecutive columns per
 // thread; the K slot rows' loads are issued before the (slot-order) sums.
-template <int KMAX>
-__global__ void __launch_bounds__(256) k_combine4(const float *__restrict__ z, const float *__restrict__ w,
+__device__ __forceinline__ float4 load4(const float *p) { return *(const float4 *)p; }
+__device__ __forceinline__ float4 load4(const _Float16 *p) {
+    const uint2 u = *(const uint2 *)p;
+    const half2_t a = __builtin_bit_cast(half2_t, u.x), b = __builtin_bit_cast(half2_t, u.y);
+    return make_float4((float)a[0], (float)a[1], (float)b[0], (float)b[1]);
+}
+template <int KMAX, typename ZT>
+__global__ void __launch_bounds__(256) k_combine4(const ZT *__restrict__ z, const float *__restrict__ w,
                                                   const float *__restrict__ res, float *__restrict__ out, int K,
                                                   int D, CombineIds ci, const float *__restrict__ add) {
     const int64_t t = blockIdx.y;
@@ -693,7 +700,7 @@ __global__ void __launch_bounds__(256) k_combine4(const float *__restrict__ z, c
     float4 zv[KMAX];
 #pragma unroll
     for (int k = 0; k < KMAX; ++k)
-        if (k < K) zv[k] = *(const float4 *)(z + (t * K + k) * (int64_t)D + n);
+        if (k < K) zv[k] = load4(z + (t * K + k) * (int64_t)D + n);
     double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
 #pragma unroll
     for (int k = 0; k < KMAX; ++k) {
@@ -717,21 +724,27 @@ __global__ void __launch_bounds__(256) k_combine4(const float *__restrict__ z, c
     *(float4 *)(out + t * D + n) = o;
 }
 
-int launch_combine(const float *z, const float *w, const float *res, float *out, int64_t T, int K, int D,
-                   hipStream_t st, const CombineIds &ci, const float *add) {
-    if (T <= 0) return 0;
-    const bool vec = D % 4 == 0 && (uintptr_t)z % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+template <typename ZT>
+static int combine_t(const ZT *z, const float *w, const float *res, float *out, int64_t T, int K, int D,
+                     hipStream_t st, const CombineIds &ci, const float *add) {
+    const bool vec = D % 4 == 0 && (uintptr_t)z % (4 * sizeof(ZT)) == 0 && (uintptr_t)out % 16 == 0 &&
                      (!res || (uintptr_t)res % 16 == 0) && (!add || (uintptr_t)add % 16 == 0) && T <= 65535;
     if (vec && K <= 16) {
         const dim3 grid((unsigned)((D / 4 + 255) / 256), (unsigned)T);
-        if (K <= 8) hipLaunchKernelGGL(k_combine4<8>, grid, dim3(256), 0, st, z, w, res, out, K, D, ci, add);
-        else hipLaunchKernelGGL(k_combine4<16>, grid, dim3(256), 0, st, z, w, res, out, K, D, ci, add);
+        if (K <= 8) hipLaunchKernelGGL((k_combine4<8, ZT>), grid, dim3(256), 0, st, z, w, res, out, K, D, ci, add);
+        else hipLaunchKernelGGL((k_combine4<16, ZT>), grid, dim3(256), 0, st, z, w, res, out, K, D, ci, add);
         return hip_check_launch();
     }
     const int64_t total = T * (int64_t)D;
     const int64_t blocks = (total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192;
-    hipLaunchKernelGGL(k_combine, dim3((unsigned)blocks), dim3(256), 0, st, z, w, res, out, T, K, D, ci, add);
+    hipLaunchKernelGGL(k_combine<ZT>, dim3((unsigned)blocks), dim3(256), 0, st, z, w, res, out, T, K, D, ci, add);
     return hip_check_launch();
+}
+
+int launch_combine(const float *z, const float *w, const float *res, float *out, int64_t T, int K, int D,
+                   hipStream_t st, const CombineIds &ci, const float *add, const _Float16 *zh) {
+    if (T <= 0) return 0;
+    return z ? combine_t(z, w, res, out, T, K, D, st, ci, add) : combine_t(zh, w, res, out, T, K, D, st, ci, add);
 }
 
 // ---------------------------------------------------------------- shared expert

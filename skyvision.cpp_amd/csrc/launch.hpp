@@ -82,8 +82,10 @@ struct CombineIds {
     const int32_t *a = nullptr, *b = nullptr;
     int E = 0;
 };
+// z: fp32 slot rows, or (z == NULL) fp16 slot rows zh
 int launch_combine(const float *z, const float *w, const float *res, float *out, int64_t T, int K, int D,
-                   hipStream_t st, const CombineIds &ids = CombineIds{}, const float *add = nullptr);
+                   hipStream_t st, const CombineIds &ids = CombineIds{}, const float *add = nullptr,
+                   const _Float16 *zh = nullptr);
 // shared expert's routing: ids[t] = 0, w[t] = logit ? fl32(1 / (1 + exp(-logit[t]))) (fp64) : 1
 int launch_shared_gate(const float *logit, int64_t T, int32_t *ids, float *w, hipStream_t st);
 
@@ -172,6 +174,11 @@ struct G2Args {
     _Float16 *acth;
     int next_type;
     int64_t ncols;
+    // store GEMM only (else NULL): y written as fp16 here instead, saturated
+    // at the fp16 range (waves that saturate are counted in range_total);
+    // needs ncols % 256 == 0, ldy % 8 == 0 and a 16-byte aligned yh
+    _Float16 *yh;
+    int32_t *range_total;
     // profiling only (else NULL): per work-group {shader clock, wall clock} at
     // its start and end, 4 words per work-group of the grid (dead ones write 0)
     uint64_t *clk;

@@ -724,9 +724,61 @@ __global__ void __launch_bounds__(256) k_combine4(const ZT *__restrict__ z, cons
     *(float4 *)(out + t * D + n) = o;
 }
 
+// fp16 slot rows: 8 consecutive columns per thread (16-byte loads of each
+// slot row, two float4 stores)
+template <int KMAX>
+__global__ void __launch_bounds__(256) k_combine8h(const _Float16 *__restrict__ z, const float *__restrict__ w,
+                                                   const float *__restrict__ res, float *__restrict__ out, int K,
+                                                   int D, CombineIds ci, const float *__restrict__ add) {
+    const int64_t t = blockIdx.y;
+    const int n = 8 * ((int)blockIdx.x * 256 + (int)threadIdx.x);
+    if (n >= D) return;
+    uint4 zv[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k)
+        if (k < K) zv[k] = *(const uint4 *)(z + (t * K + k) * (int64_t)D + n);
+    double s[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+        if (k < K && combine_live(ci, t * K + k)) {
+            const float wk = w[t * K + k];
+            const uint32_t u[4] = {zv[k].x, zv[k].y, zv[k].z, zv[k].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const half2_t h = __builtin_bit_cast(half2_t, u[j]);
+                s[2 * j] = s[2 * j] + (double)((float)h[0] * wk);
+                s[2 * j + 1] = s[2 * j + 1] + (double)((float)h[1] * wk);
+            }
+        }
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        float4 o = make_float4((float)s[4 * hh], (float)s[4 * hh + 1], (float)s[4 * hh + 2], (float)s[4 * hh + 3]);
+        if (add) {
+            const float4 a = *(const float4 *)(add + t * D + n + 4 * hh);
+            o.x = o.x + a.x; o.y = o.y + a.y; o.z = o.z + a.z; o.w = o.w + a.w;
+        }
+        if (res) {
+            const float4 r = *(const float4 *)(res + t * D + n + 4 * hh);
+            o.x = r.x + o.x; o.y = r.y + o.y; o.z = r.z + o.z; o.w = r.w + o.w;
+        }
+        *(float4 *)(out + t * D + n + 4 * hh) = o;
+    }
+}
+
 template <typename ZT>
 static int combine_t(const ZT *z, const float *w, const float *res, float *out, int64_t T, int K, int D,
                      hipStream_t st, const CombineIds &ci, const float *add) {
+    if constexpr (sizeof(ZT) == 2) {
+        const bool vec8 = D % 8 == 0 && (uintptr_t)z % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+                          (!res || (uintptr_t)res % 16 == 0) && (!add || (uintptr_t)add % 16 == 0) && T <= 65535;
+        if (vec8 && K <= 16) {
+            const dim3 grid((unsigned)((D / 8 + 255) / 256), (unsigned)T);
+            if (K <= 8) hipLaunchKernelGGL((k_combine8h<8>), grid, dim3(256), 0, st, z, w, res, out, K, D, ci, add);
+            else hipLaunchKernelGGL((k_combine8h<16>), grid, dim3(256), 0, st, z, w, res, out, K, D, ci, add);
+            return hip_check_launch();
+        }
+    }
     const bool vec = D % 4 == 0 && (uintptr_t)z % (4 * sizeof(ZT)) == 0 && (uintptr_t)out % 16 == 0 &&
                      (!res || (uintptr_t)res % 16 == 0) && (!add || (uintptr_t)add % 16 == 0) && T <= 65535;
     if (vec && K <= 16) {

@@ -168,9 +168,10 @@ int  mi_moe_ctx_reserve(mi_moe_ctx *ctx, int64_t max_tokens, int32_t n_embd, int
  * is NaN; not expected: a work-group computes what it waited too long for).
  * fp16_saturated: fp16 values of the grouped-GEMM path clamped to +-65504:
  * 256-value Q8_K blocks (input rows or activation rows) whose largest |value|
- * exceeds it, counted per block, and down-product outputs (the per-slot rows
- * the weighted sum reads, kept as fp16) beyond it, counted per wave of 64
- * values that held one.  The products of those rows are inexact (ggml's own
+ * exceeds it, counted per block, and GLU values (the gate/up product's rows,
+ * kept as fp16 for the activations' Q8_K) and down-product outputs (the
+ * per-slot rows the weighted sum reads, kept as fp16) beyond it, counted per
+ * wave of 64 values that held one.  The products of those rows are inexact (ggml's own
  * fp16 GPU paths overflow there; the integer GEMV path has no such limit).
  * Any pointer may be NULL.  Synchronizes the context's device. */
 int  mi_moe_ctx_take_errors(mi_moe_ctx *ctx, int64_t *bad_ids, int64_t *wait_failures,

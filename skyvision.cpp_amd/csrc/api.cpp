@@ -416,13 +416,17 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.tile_e = dg.tile_e;
         a.tile_r0 = dg.tile_r0; a.tile_start = dg.tile_start; a.tile_rows = dg.tile_rows; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
         a.y = c->f1; a.ldy = I; a.ncols = I; a.xrows = T;
+        // gated: the GLU rows as fp16 (half the bytes of their round trip to
+        // the Q8_K pass; saturation at the fp16 range is counted)
+        if (gated) { a.yh = (_Float16 *)c->f1; a.range_total = c->range_total; }
         prof_clock(c, a, 0);
         TRY(launch_gemm4(a, st));
         stage_end(c, "gate_up", st);
         Q8Out qa;
         qa.xh = c->aact.h; qa.wtype = down.type; qa.order = 1; qa.pre_act = gated ? 0 : MI_ACT_RELU_SQR;
         qa.range_total = c->range_total;
-        TRY(launch_q8k_rows(c->f1, I, rows, I, qa, st));
+        if (gated) TRY(launch_q8k_rows((const _Float16 *)c->f1, I, rows, I, qa, st));
+        else TRY(launch_q8k_rows(c->f1, I, rows, I, qa, st));
         stage_end(c, "q8k_act", st);
         G2Args d = {};
         d.a = down; d.glu = 0; d.xh = c->aact.h; d.ne11 = K; d.K = K;

@@ -512,16 +512,39 @@ __device__ __forceinline__ void g4_coords(int nct, int &tile, int &ctile) {
 // ------------------------------------------------------------------ GLU
 // Wave w owns act columns 32 w .. 32 w + 31 of the work-group's 128: column
 // tile 0 holds their h (gate) rows, column tile 1 their g (up) rows; the GLU
-// values go out as fp32 rows (their Q8_K for the down product needs whole
-// 256-column blocks, which span two work-groups).
+// values go out as rows (fp32 to y, or fp16 to yh), whose Q8_K for the down
+// product needs whole 256-column blocks, which span two work-groups.
 template <int ACT>
 __device__ __forceinline__ void g4_glu_store(const G2Args &g, const f32x16 (&acc)[G4_BM / 32][2], const G4Tile &t,
                                              int ctile, int wave, int lane, const int *s_p, _Float16 *As0,
                                              _Float16 *As1) {
     // through LDS: the wave's 32 GLU columns of every row into the activation
     // buffers (rows 0-95 in As0, 96-191 in As1, 512 bytes per row), then
-    // whole 512-byte rows out in 16-byte pieces
+    // whole rows (512 bytes fp32, 256 bytes fp16) out in 16-byte pieces
     const int l32 = lane & 31, g2 = lane >> 5;
+    if (g.yh) {
+        bool over = false;
+#pragma unroll
+        for (int rt = 0; rt < G4_BM / 32; ++rt) {
+            if (rt >= t.nrt) break;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
+                _Float16 *row = m < G4_BM / 2 ? As0 + m * 256 : As1 + (m - G4_BM / 2) * 256;
+                const float v = act_pair_fast<ACT>(acc[rt][0][i], acc[rt][1][i]);
+                over = over || !(fabsf(v) <= kF16Max);
+                row[32 * wave + l32] = f16_sat(v);
+            }
+        }
+        if (__ballot(over) != 0 && lane == 0 && g.range_total) atomicAdd(g.range_total, 1);
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < t.mrows * 16; idx += G4_THREADS) {
+            const int r = idx >> 4, c = idx & 15;
+            const _Float16 *row = r < G4_BM / 2 ? As0 + r * 256 : As1 + (r - G4_BM / 2) * 256;
+            *(uint4 *)(g.yh + (int64_t)s_p[r] * g.ldy + (int64_t)ctile * 128 + 8 * c) = *(const uint4 *)(row + 8 * c);
+        }
+        return;
+    }
 #pragma unroll
     for (int rt = 0; rt < G4_BM / 32; ++rt) {
         if (rt >= t.nrt) break;
@@ -698,8 +721,10 @@ int launch_gemm4(const G2Args &g, hipStream_t st) {
     if (g.xrows <= 0 || g.xrows * g.a.K * 2 > lim || g.a.mat_bytes + 4 > lim) return -6;
     const int ntile8 = (g.max_tiles + 7) / 8;
     if (g.glu) {
-        // fp32 GLU values out (y, ldy); the work-group covers 128 act columns
-        if (g.a.type != 12 || (g.I % 128) || g.ldy % 4 || (uintptr_t)g.y % 16) return -6;
+        // GLU values out (fp32 to y or fp16 to yh, ldy); the work-group covers
+        // 128 act columns
+        if (g.a.type != 12 || (g.I % 128)) return -6;
+        if (g.yh ? (g.ldy % 8 || (uintptr_t)g.yh % 16) : (g.ldy % 4 || (uintptr_t)g.y % 16)) return -6;
         if (!g.fused && (g.b.mat_bytes > lim || g.b.type != 12 || g.b.row_bytes != g.a.row_bytes)) return -6;
         if ((uintptr_t)g.a.data % 4 || g.a.mat_bytes % 4 || g.a.row_bytes % 4) return -6;
         if (!g.fused && ((uintptr_t)g.b.data % 4 || g.b.mat_bytes % 4)) return -6;

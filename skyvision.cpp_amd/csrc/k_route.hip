@@ -31,14 +31,27 @@ namespace mimoe {
 enum { XO_ANY = 0, XO_Q4 = 1, XO_Q6 = 2 };
 
 // the lane's 16 values of row group (row, grp) (zeros past the row's blocks)
-template <bool VEC>
-__device__ __forceinline__ void q8k_load(const float *__restrict__ src, int64_t ld, int64_t row, int grp, int nb,
+template <bool VEC, typename ST>
+__device__ __forceinline__ void q8k_load(const ST *__restrict__ src, int64_t ld, int64_t row, int grp, int nb,
                                          int lane, float (&v)[16], int pre_act = 0) {
     const int bl = lane >> 4, l16 = lane & 15;
     const int b = 4 * grp + bl;
     if (b < nb) {
-        const float *x = src + row * ld + (int64_t)b * QK + 16 * l16;
-        if (VEC) {
+        const ST *x = src + row * ld + (int64_t)b * QK + 16 * l16;
+        if constexpr (sizeof(ST) == 2) {
+            // fp16 rows: 32 bytes per lane
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint4 u = *(const uint4 *)(x + 8 * j);
+                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const half2_t hh = __builtin_bit_cast(half2_t, w[i]);
+                    v[8 * j + 2 * i] = (float)hh[0];
+                    v[8 * j + 2 * i + 1] = (float)hh[1];
+                }
+            }
+        } else if (VEC) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float4 f = *(const float4 *)(x + 4 * j);
@@ -162,8 +175,8 @@ __device__ __forceinline__ void q8k_row_group(const float *__restrict__ src, int
 // (two: 12.6 vs 11.1 us; the wave count halves).
 constexpr int Q8_ITEMS = 1;
 
-template <bool VEC, int XO>
-__global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ src, int64_t ld, int64_t nrows,
+template <bool VEC, int XO, typename ST>
+__global__ void __launch_bounds__(256) k_q8k_rows(const ST *__restrict__ src, int64_t ld, int64_t nrows,
                                                   int nb, Q8Out o) {
     __shared__ __attribute__((aligned(16))) int8_t sq[4][4 * QK];
     __shared__ float sd[4][4];
@@ -201,10 +214,25 @@ int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, cons
     const bool vec = (ld % 4 == 0) && ((uintptr_t)src % 16 == 0);
     const dim3 grid((unsigned)((items + 4 * Q8_ITEMS - 1) / (4 * Q8_ITEMS)));
     const int xo = q8_xo(o);
-    if (vec && xo == XO_Q4) hipLaunchKernelGGL((k_q8k_rows<true, XO_Q4>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
-    else if (vec && xo == XO_Q6) hipLaunchKernelGGL((k_q8k_rows<true, XO_Q6>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
-    else if (vec) hipLaunchKernelGGL((k_q8k_rows<true, XO_ANY>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
-    else hipLaunchKernelGGL((k_q8k_rows<false, XO_ANY>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    if (vec && xo == XO_Q4) hipLaunchKernelGGL((k_q8k_rows<true, XO_Q4, float>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    else if (vec && xo == XO_Q6) hipLaunchKernelGGL((k_q8k_rows<true, XO_Q6, float>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    else if (vec) hipLaunchKernelGGL((k_q8k_rows<true, XO_ANY, float>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    else hipLaunchKernelGGL((k_q8k_rows<false, XO_ANY, float>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    return hip_check_launch();
+}
+
+// fp16 rows (the grouped GEMM's GLU rows): whole 256-value blocks, 16-byte
+// aligned rows
+int launch_q8k_rows(const _Float16 *src, int64_t ld, int64_t nrows, int64_t K, const Q8Out &o, hipStream_t st) {
+    if (nrows <= 0) return 0;
+    if (K % QK || ld % 8 || (uintptr_t)src % 16) return -6;
+    const int nb = (int)(K / QK);
+    const int64_t items = nrows * ((nb + 3) / 4);
+    const dim3 grid((unsigned)((items + 4 * Q8_ITEMS - 1) / (4 * Q8_ITEMS)));
+    const int xo = q8_xo(o);
+    if (xo == XO_Q4) hipLaunchKernelGGL((k_q8k_rows<true, XO_Q4, _Float16>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    else if (xo == XO_Q6) hipLaunchKernelGGL((k_q8k_rows<true, XO_Q6, _Float16>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    else hipLaunchKernelGGL((k_q8k_rows<true, XO_ANY, _Float16>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
     return hip_check_launch();
 }
 

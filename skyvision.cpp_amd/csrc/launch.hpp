@@ -37,8 +37,9 @@ struct Q8Out {
     int pre_act = 0;             // 4 (ACT_RELU_SQR): quantize relu(v)^2 instead of v
     int32_t *range_total = nullptr;   // [1] or null: blocks whose xh saturated at the fp16 range
 };
-// quantize rows of src (row r at src + r*ld floats) to Q8_K
+// quantize rows of src (row r at src + r*ld values, fp32 or fp16) to Q8_K
 int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, const Q8Out &o, hipStream_t st);
+int launch_q8k_rows(const _Float16 *src, int64_t ld, int64_t nrows, int64_t K, const Q8Out &o, hipStream_t st);
 // router logits, fixed fp64 order; W: [E][D], x rows at x + t*ldx
 int launch_router(const float *W, const float *b, const float *x, int64_t ldx, int64_t T, int D, int E,
                   float *logits, hipStream_t st);
@@ -153,9 +154,10 @@ int launch_gemm(const GemmArgs &g, hipStream_t st);
 // 4-wave grouped GEMMs on 32x32x16 MFMA (k_gemm4.hip), tiles of at most
 // G4_BM rows from a balanced dispatch.  Both take fp16 activations in the
 // weight type's 32x32x16 MFMA K order (xh; xd, xbs, acth and next_type are
-// not read).  glu = 1: Q4_K gate/up (fused [h | g] or separate), writes fp32
-// GLU rows to y (ldy), whose Q8_K the caller computes (launch_q8k_rows) for
-// the down product; glu = 0: Q4_K / Q6_K product, fp32 rows to y.
+// not read).  glu = 1: Q4_K gate/up (fused [h | g] or separate), writes the
+// GLU rows (fp32 to y or fp16 to yh, ldy), whose Q8_K the caller computes
+// (launch_q8k_rows) for the down product; glu = 0: Q4_K / Q6_K product, rows
+// to y (fp32) or yh (fp16).
 struct G2Args {
     ExpertMat a;
     ExpertMat b;
@@ -174,9 +176,9 @@ struct G2Args {
     _Float16 *acth;
     int next_type;
     int64_t ncols;
-    // store GEMM only (else NULL): y written as fp16 here instead, saturated
-    // at the fp16 range (waves that saturate are counted in range_total);
-    // needs ncols % 256 == 0, ldy % 8 == 0 and a 16-byte aligned yh
+    // or NULL: y written as fp16 here instead, saturated at the fp16 range
+    // (waves that saturate are counted in range_total); needs ldy % 8 == 0, a
+    // 16-byte aligned yh and, for glu = 0, ncols % 256 == 0
     _Float16 *yh;
     int32_t *range_total;
     // profiling only (else NULL): per work-group {shader clock, wall clock} at

@@ -549,25 +549,16 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
         psc[tid] = !balanced && cnt[tid] % BM > 0 ? 1 : 0;
     }
     __syncthreads();
-    if (wave == 0) {   // four inclusive scans by one wave: lane l holds entries 4 l .. 4 l + 3
-        int *arr[4] = {scn, tsc, asc, psc};
+    if (wave < 4) {   // four inclusive scans, one per wave: lane l holds entries 4 l .. 4 l + 3
+        int *arr = wave == 0 ? scn : wave == 1 ? tsc : wave == 2 ? asc : psc;
+        int v[4];
 #pragma unroll
-        for (int a = 0; a < 4; ++a) {
-            int v[4];
+        for (int j = 0; j < 4; ++j) v[j] = 4 * lane + j < E ? arr[4 * lane + j] : 0;
+        v[1] += v[0]; v[2] += v[1]; v[3] += v[2];
+        const int ex = wave_incl_scan(v[3]) - v[3];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] = 4 * lane + j < E ? arr[a][4 * lane + j] : 0;
-            v[1] += v[0]; v[2] += v[1]; v[3] += v[2];
-            int inc = v[3];
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int y = __shfl_up(inc, o, 64);
-                if (lane >= o) inc += y;
-            }
-            const int ex = inc - v[3];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (4 * lane + j < E) arr[a][4 * lane + j] = v[j] + ex;
-        }
+        for (int j = 0; j < 4; ++j)
+            if (4 * lane + j < E) arr[4 * lane + j] = v[j] + ex;
     }
     __syncthreads();
     const int c = cnt[me];
@@ -640,14 +631,20 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
             dispatch_stage(ids + c0, m, sid, tid);
             __syncthreads();
         }
-        // wave w takes the contiguous ids [w0, w1): counts its hits, meets the
-        // other waves once for the prefix, then writes them in order
+        // wave w takes the contiguous ids [w0, w1) (at most NIT rounds of 64):
+        // its hit masks, the other waves met once for the prefix, then the
+        // hits written in order from the masks
         const int span = ((m + DISPATCH_WAVES - 1) / DISPATCH_WAVES + 63) & ~63;
         const int w0 = wave * span, w1 = w0 + span < m ? w0 + span : m;
+        constexpr int NIT = DISPATCH_IDS / DISPATCH_WAVES / 64;
+        uint64_t hm[NIT];
         int mine = 0;
-        for (int i0 = w0; i0 < w1; i0 += 64) {
-            const int i = i0 + lane;
-            mine += __popcll(__ballot(i < w1 && sid[i] == me));
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int i = w0 + 64 * it + lane;
+            const int e = i < w1 ? sid[i] : -1;
+            hm[it] = __ballot(e == me);
+            mine += __popcll(hm[it]);
         }
         if (lane == 0) wsum[wave] = mine;
         __syncthreads();
@@ -659,11 +656,11 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
             total += v;
         }
         int pos = run + before;
-        for (int i0 = w0; i0 < w1; i0 += 64) {
-            const int i = i0 + lane;
-            const bool hit = i < w1 && sid[i] == me;
-            const uint64_t mask = __ballot(hit);
-            if (hit) d.perm[pos + __popcll(mask & ((1ull << lane) - 1ull))] = (int32_t)(c0 + i);
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const uint64_t mask = hm[it];
+            if ((mask >> lane) & 1ull)
+                d.perm[pos + __popcll(mask & ((1ull << lane) - 1ull))] = (int32_t)(c0 + w0 + 64 * it + lane);
             pos += __popcll(mask);
         }
         run += total;

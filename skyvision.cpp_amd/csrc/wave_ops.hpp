@@ -25,6 +25,25 @@ __device__ inline float dpp_f(float v) {
     return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
 }
 
+// inclusive prefix sum over the 64 lanes: Hillis-Steele inside each 16-lane
+// row (row_shr 1, 2, 4, 8; lanes shifted in from outside the row add 0), then
+// row_bcast:15 adds the last lane of rows 0 / 2 to rows 1 / 3 and row_bcast:31
+// the last lane of row 1 (rows 0-1 by then) to rows 2 and 3
+__device__ inline int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+    return v;
+}
+
+// lane k's value, uniform (a scalar read: no LDS round trip)
+__device__ inline float lane_f(float v, int k) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), k));
+}
+
 // sum over aligned groups of `width` lanes (8, 16, 32 or 64), in every lane
 __device__ inline float group_sum(float v, int width) {
     v += dpp_f<0xB1>(v);
@@ -201,11 +220,11 @@ __device__ inline uint32_t pack_i8x4(const int (&q)[4]) {
 // by (float)(1.0 / sum).  Every lane of the wave must call it; lane k < K
 // gets its weight.
 __device__ inline float softmax_selected_wave(float myval, int K, int lane) {
-    float mx = lane < K ? myval : -INFINITY;
-    mx = wave_max(mx);
+    float mx = -INFINITY;
+    for (int k = 0; k < K; ++k) mx = fmaxf(mx, lane_f(myval, k));
     const float val = lane < K ? expf(myval - mx) : 0.f;
     double sum = 0.0;
-    for (int k = 0; k < K; ++k) sum = sum + (double)__shfl(val, k, 64);
+    for (int k = 0; k < K; ++k) sum = sum + (double)lane_f(val, k);
     sum = 1.0 / sum;
     const float s = (float)sum;
     return val * s;
@@ -287,6 +306,7 @@ __device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane,
     }
     wave_lds_sync();
     int r[TOPK_MAX_PER_LANE] = {0, 0, 0, 0};
+#pragma unroll 4
     for (int j = 0; j < E4; j += 4) {
         const float4 q = *(const float4 *)(sv + j);
         const float qq[4] = {q.x, q.y, q.z, q.w};
@@ -312,12 +332,12 @@ __device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane,
     if (gt.kind == 1) {
         const float s = lane < K ? gating_sigmoid(l[mysel]) : 0.f;
         double sum = 0.0;
-        for (int k = 0; k < K; ++k) sum = sum + (double)__shfl(s, k, 64);
+        for (int k = 0; k < K; ++k) sum = sum + (double)lane_f(s, k);
         myw = s / ((float)sum + gt.eps) * gt.scaling;
     } else if (gt.kind == 2) {
         const float p = lane < K ? sv[mysel] : 0.f;
         double sum = 0.0;
-        for (int k = 0; k < K; ++k) sum = sum + (double)__shfl(p, k, 64);
+        for (int k = 0; k < K; ++k) sum = sum + (double)lane_f(p, k);
         myw = p / (float)sum;
     } else {
         const float myval = lane < K ? sv[mysel] : 0.f;

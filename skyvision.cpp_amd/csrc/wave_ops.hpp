@@ -306,16 +306,26 @@ __device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane,
     }
     wave_lds_sync();
     int r[TOPK_MAX_PER_LANE] = {0, 0, 0, 0};
+    if (nper == 1) {
+        // one value per lane: the same count against the 64 lanes' values
+        // read as scalars (lanes past E hold -inf), unrolled and branch-free
+#pragma unroll
+        for (int j = 0; j < 64; ++j) {
+            const float x = lane_f(v[0], j);
+            r[0] += (x > v[0]) | ((x == v[0]) & (j < lane));
+        }
+    } else {
 #pragma unroll 4
-    for (int j = 0; j < E4; j += 4) {
-        const float4 q = *(const float4 *)(sv + j);
-        const float qq[4] = {q.x, q.y, q.z, q.w};
+        for (int j = 0; j < E4; j += 4) {
+            const float4 q = *(const float4 *)(sv + j);
+            const float qq[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-        for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
-            if (i >= nper) break;
-            const int e = lane + 64 * i;
+            for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
+                if (i >= nper) break;
+                const int e = lane + 64 * i;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) r[i] += (qq[c] > v[i]) | ((qq[c] == v[i]) & (j + c < e));
+                for (int c = 0; c < 4; ++c) r[i] += (qq[c] > v[i]) | ((qq[c] == v[i]) & (j + c < e));
+            }
         }
     }
 #pragma unroll

@@ -467,6 +467,38 @@ def prefill_line(config: int, args, primary: bool) -> dict:
     return line
 
 
+def dense_reference(reps: int = 100) -> dict:
+    """Dense fp16 x fp16 -> fp16 GEMMs (fp32 accumulation) with the FLOP counts
+    of config 1's grouped products, through torch.matmul (hipBLASLt): gate/up
+    [T*K, D] x [D, 2I], down [T*K, I] x [I, D].  A reference point for what the
+    vendor library reaches on this GPU at the same work without dequantization,
+    routing or fused epilogues; not part of the layer."""
+    import torch  # only here: the layer itself runs on the HIP library
+
+    spec = W.CONFIGS[1]["spec"]
+    rows = W.CONFIGS[1]["tokens"][0] * spec.K
+    out = {"metric": "dense_fp16_gemm_reference", "unit": "TFLOP/s", "library": "torch.matmul (hipBLASLt)",
+           "torch": torch.__version__}
+    torch.manual_seed(0)
+    for name, (m, k, n) in (("gate_up", (rows, spec.D, 2 * spec.I)), ("down", (rows, spec.I, spec.D))):
+        a = torch.randn(m, k, device="cuda", dtype=torch.float16)
+        b = torch.randn(k, n, device="cuda", dtype=torch.float16)
+        for _ in range(10):
+            c = a @ b
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            c = a @ b
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / reps
+        out[name] = {"shape": f"{m}x{k} @ {k}x{n}", "gflop": 2.0 * m * n * k / 1e9, "us": us,
+                     "tflops": 2.0 * m * n * k / us / 1e6, "frac_of_2.5PF": 2.0 * m * n * k / us / 1e6 / 2500.0}
+        del a, b, c
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -488,7 +520,14 @@ def main() -> int:
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 512 MiB device-to-device copy (the known-size kernel "
                          "that scales FETCH_SIZE / WRITE_SIZE counters to bytes)")
+    ap.add_argument("--dense-ref", action="store_true",
+                    help="only time dense fp16 GEMMs of the two grouped products' FLOP counts "
+                         "through torch (hipBLASLt) on this GPU and print them as one JSON line: "
+                         "the vendor library's rate at the same work, for reference")
     args = ap.parse_args()
+    if args.dense_ref:
+        print(json.dumps(dense_reference()), flush=True)
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(across GPUs the layer would shard by experts: each GPU holds E/N experts' "

@@ -196,11 +196,12 @@ def host_cpu() -> str:
 
 def config3_sweep(copies: int) -> dict:
     """Config 3: qwen3omni layer (E 128, I 768, SwiGLU, Q4_K), batched decode
-    at T = 1, 8, 32, 64 on both product paths (grouped GEMV, grouped MFMA
-    GEMM; at T = 1 also the fused single-token kernel), rotating layer copies.
-    Bytes per call = the touched experts' tables + the router (measured
-    touched count); the crossover is the smallest T at which the GEMM path is
-    faster."""
+    at T = 1, 8, 32, 64 on both product paths of the kernel chain (grouped
+    GEMV, grouped MFMA GEMM) and, up to 16 tokens, the fused kernel (the
+    single-token kernel at T = 1, the batched one above), rotating layer
+    copies.  Bytes per call = the touched experts' tables + the router
+    (measured touched count); the crossover is the smallest T at which the
+    chain's GEMM path is faster than its GEMV path."""
     spec = W.CONFIGS[3]["spec"]
     Ts = W.CONFIGS[3]["tokens"]
     ctx = M.Context(0)
@@ -214,14 +215,14 @@ def config3_sweep(copies: int) -> dict:
         nbytes = W.algorithmic_bytes(spec, touched)
         row = {"tokens": T, "touched_experts": touched, "layer_bytes": nbytes}
         paths = [("gemv", 1 << 30), ("gemm", 1)]
+        ctx.set_fused_decode(M.DECODE_CHAIN)
         for name, thr in paths:
             ctx.set_gemm_threshold(thr)
-            if T == 1:
-                ctx.set_fused_decode(M.DECODE_CHAIN)
             ms, _ = time_layer(ctx, layers, xs, T, out, 100, 10)
             row[f"{name}_ms"] = ms
-        if T == 1:
-            ctx.set_fused_decode(M.DECODE_FUSED)
+        ctx.set_fused_decode(M.DECODE_FUSED)
+        ctx.set_gemm_threshold(0)
+        if T <= 16:
             row["fused_ms"] = time_layer(ctx, layers, xs, T, out, 100, 10)[0]
         best = min(v for k, v in row.items() if k.endswith("_ms"))
         row["best_ms"] = best

@@ -113,6 +113,9 @@ struct mi_moe_ctx {
     uint32_t *dec_epoch = nullptr;
     unsigned dec_rescue_polls = DEC_RESCUE_POLLS;
     unsigned *dec_err = nullptr;
+    // batched fused kernel (k_decodeb): its unit words
+    uint64_t *decb_tw = nullptr;
+    int64_t decb_words = 0;
 
     bool profiling = false;
     hipEvent_t ev[kMaxStages + 1] = {};
@@ -274,6 +277,54 @@ int run_decode1(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, const floa
     g.tw = c->dec_tw; g.epoch = c->dec_epoch; g.err = c->dec_err; g.rescue_polls = c->dec_rescue_polls;
     TRY(launch_decode1(g, c->dec_grid, c->fused_decode == MI_DECODE_FUSED_COOPERATIVE, st));
     stage_end(c, "decode1", st);
+    return MI_MOE_OK;
+}
+
+// The batched fused kernel for 2..16 tokens: the same layer kinds as the
+// single-token kernel (default gating, gated Q4_K gate/up, Q4_K / Q6_K down,
+// no shared expert) with D <= 2048 and I <= 1024 in whole 256-blocks; cc: the
+// output columns per C unit (as many units as work-groups where D allows)
+bool plan_decodeb(const mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, int &cc) {
+    const int64_t D = L->n_embd, E = L->n_expert, K = L->n_expert_used, I = L->n_ff;
+    const int G = c->dec_grid;
+    if (!c->fused_decode || G <= 0 || T < 2 || T > DECB_T_MAX) return false;
+    if (decodeb_tw_words(T, D, E, K, I) > c->decb_words) return false;
+    if (L->gating != MI_GATING_SOFTMAX_TOPK || L->expert_scale) return false;
+    if (!act_gated(L->act) || L->sh_n_ff > 0) return false;
+    if (L->gate.type != MI_TYPE_Q4_K || (!L->fused_gate_up && L->up.type != MI_TYPE_Q4_K)) return false;
+    if (L->down.type != MI_TYPE_Q4_K && L->down.type != MI_TYPE_Q6_K) return false;
+    if (D % QK || I % QK || K > 8 || E > 256) return false;
+    const int64_t NB = D / QK, NBI = I / QK;
+    if (!(NB == 1 || NB == 2 || NB == 4 || NB == 8) || NBI > 4) return false;
+    auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    if (!al16(x) || !al16(L->router_w) || !al16(L->gate.data) || L->gate.nb[2] % 16) return false;
+    if (!L->fused_gate_up && (!al16(L->up.data) || L->up.nb[2] % 16)) return false;
+    if (L->down.type == MI_TYPE_Q4_K ? (!al16(L->down.data) || L->down.nb[2] % 16)
+                                     : ((uintptr_t)L->down.data % 2 || L->down.nb[2] % 2))
+        return false;
+    cc = 64;
+    while (cc > 8 && T * (D / cc) < G) cc /= 2;
+    return D % cc == 0;
+}
+
+int run_decodeb(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const float *res, float *out,
+                int cc, hipStream_t st) {
+    DecArgs g = {};
+    g.rw = L->router_w; g.rb = L->router_b; g.x = x;
+    g.D = L->n_embd; g.E = L->n_expert; g.K = L->n_expert_used; g.I = L->n_ff; g.T = (int)T;
+    g.gate = as_mat(L->gate);
+    if (!L->fused_gate_up) g.up = as_mat(L->up);
+    g.down = as_mat(L->down);
+    g.fused = L->fused_gate_up; g.act = L->act;
+    g.res = res; g.out = out; g.C = cc;
+    g.logits = c->logits; g.sel = c->sel; g.w = c->w;
+    g.counts = c->disp[0].counts; g.offsets = c->disp[0].offsets; g.perm = c->disp[0].perm;
+    g.xq = c->ax.q8; g.xd = c->ax.d8; g.xbs = c->ax.bs;
+    g.actf = c->f1;
+    g.tw = c->dec_tw; g.tw2 = c->decb_tw; g.epoch = c->dec_epoch; g.err = c->dec_err;
+    g.rescue_polls = c->dec_rescue_polls;
+    TRY(launch_decodeb(g, c->dec_grid, st));
+    stage_end(c, "decodeb", st);
     return MI_MOE_OK;
 }
 
@@ -525,6 +576,7 @@ constexpr size_t ws_bytes(int64_t max_tokens, int64_t D, int64_t I, int64_t E, i
             carve_size<int16_t>(rows * iq / 16) + carve_size<_Float16>(rows * iq);
     need += carve_size<float>(rows * wide) + carve_size<float>(rows * I) + carve_size<float>(rows * wide);
     need += carve_size<uint64_t>(DEC_TW_WORDS) + carve_size<uint32_t>(DEC_MAX_GRID) + carve_size<unsigned>(1);
+    need += carve_size<uint64_t>(decodeb_tw_words(max_tokens < DECB_T_MAX ? max_tokens : DECB_T_MAX, D, E, K, I));
     need += carve_size<float>(max_tokens * D) + 2 * carve_size<float>(max_tokens) + carve_size<int32_t>(max_tokens);
     return need;
 }
@@ -575,6 +627,8 @@ bool carve_workspace(mi_moe_ctx *c, char *base, int64_t max_tokens, int32_t D, i
     c->dec_tw = carve<uint64_t>(q, DEC_TW_WORDS);
     c->dec_epoch = carve<uint32_t>(q, DEC_MAX_GRID);
     c->dec_err = carve<unsigned>(q, 1);
+    c->decb_words = decodeb_tw_words(std::min<int64_t>(max_tokens, DECB_T_MAX), D, E, K, I);
+    c->decb_tw = carve<uint64_t>(q, c->decb_words);
     c->sh_out = carve<float>(q, max_tokens * D);
     c->sh_w = carve<float>(q, max_tokens);
     c->sh_logit = carve<float>(q, max_tokens);
@@ -804,8 +858,11 @@ int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T
         add = c->sh_out;
     }
     int P = 0, C = 0;
+    int cc = 0;
     if (T == 1 && plan_decode1(c, L, x, P, C)) {
         TRY(run_decode1(c, L, x, res, out, P, C, st));
+    } else if (plan_decodeb(c, L, x, T, cc)) {
+        TRY(run_decodeb(c, L, x, T, res, out, cc, st));
     } else {
         // router + Q8_K(x) in one launch where the shape fits
         Q8Out qx;
@@ -878,7 +935,7 @@ namespace {
 constexpr int64_t NA_T = MI_NOALLOC_MAX_TOKENS;
 constexpr int32_t NA_D = 2048, NA_I = 1024, NA_E = 128, NA_K = 8;
 constexpr size_t NA_BYTES = ws_bytes(NA_T, NA_D, NA_I, NA_E, NA_K);
-static_assert(NA_BYTES == 16706816, "mi_moe.h states the no-allocation workspace size");
+static_assert(NA_BYTES == 16986368, "mi_moe.h states the no-allocation workspace size");
 constexpr int NA_MAX_DEVICES = 64;
 
 struct NoallocDevice {

@@ -56,6 +56,7 @@
 // the same; a WG whose waits give up writes NaN and sets an error word.
 #include "act.hpp"
 #include "common.hpp"
+#include "kq_dot.hpp"
 #include "launch.hpp"
 #include "wave_ops.hpp"
 
@@ -821,6 +822,648 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
         if (failed) __hip_atomic_fetch_add(g.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(g.epoch + wg, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+// ================================================================ batched decode
+// k_decodeb: the MoE block for 2..16 tokens in one kernel (the separate-kernel
+// chain pays seven launches of latency at these sizes).  Same numerics,
+// hand-off rules (coherent stores and loads, epoch-tagged completion words)
+// and rescue-by-recomputation as k_decode1; units belong to waves (global
+// wave w of W runs units w, w + W, ...) except the C units, which belong to
+// work-groups:
+//
+//   A  units u < E T: router row u % E for token u / E (the logit travels in
+//      the completion word); units E T + t NB + b: Q8_K of x block b of token
+//      t.
+//   -- every WG: all A words; x's Q8_K staged in LDS; each token ranked by
+//      one wave (the shared top-k / softmax code); the distinct selected
+//      experts listed in first-use order of the flat (t, k) pairs --
+//   B  units (d, q): gate/up rows 4 q .. 4 q + 3 (h and g) of distinct expert
+//      d, dotted against every pair (t, k) that selected d; GLU; fp32
+//      activations of those pairs written through.  The next unit's weight
+//      bytes are loaded while the current unit computes.
+//   -- per C unit: the B words of its token's K experts --
+//   C  units (t, 64 columns), one WG each: Q8_K of the token's K activation
+//      rows (wave k), then wave w dots columns 8 w .. 8 w + 7 of every slot's
+//      down rows (the next slot's rows load during the current slot's dots)
+//      and combines the slots in fp64 slot order with the residual.
+//
+// Word layout in tw2: A words [0, E T + T NB), B words from there, QB = I / 4
+// per distinct expert.
+constexpr int DECB_WAVES = 8;
+constexpr int DECB_THREADS = DECB_WAVES * 64;
+constexpr int DECB_NB_MAX = 8;     // D <= 2048
+constexpr int DECB_NBI_MAX = 4;    // I <= 1024 (one Q8_K pass per activation row)
+constexpr int DECB_COLS = 64;      // output columns per C unit (at most)
+constexpr int DECB_PAIRS_MAX = DECB_T_MAX;   // pairs per distinct expert: a token picks an expert once
+
+__device__ inline float decb_router_row(const float *rw, const float *rb, const float *x, int D, int e, int lane) {
+    const int nch = (D + 63) >> 6;
+    double part = 0.0;
+    if (lane < nch) {
+        const float *xr = x + 64 * lane;
+        const float *wr = rw + (int64_t)e * D + 64 * lane;
+        float xv[64], wv[64];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const float4_t a = *(const float4_t *)(xr + 4 * q);
+            const float4_t b = *(const float4_t *)(wr + 4 * q);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                xv[4 * q + j] = a[j];
+                wv[4 * q + j] = b[j];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) part = fma((double)wv[16 * q + s], (double)xv[16 * q + s], part);
+    }
+    const uint64_t pb = __builtin_bit_cast(uint64_t, part);
+    const uint32_t plo = (uint32_t)pb, phi = (uint32_t)(pb >> 32);
+    double acc = 0.0;
+    for (int c = 0; c < nch; ++c) {
+        const uint64_t v = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)phi, c) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane((int)plo, c);
+        acc = acc + __builtin_bit_cast(double, v);
+    }
+    float v = (float)acc;
+    if (rb) v = v + rb[e];
+    return v;
+}
+
+// Q8_K of x block b of token t (natural order; codes, scale, block sums),
+// written through
+__device__ inline void decb_q8k_x(const DecArgs &g, int t, int b, int lane) {
+    const int D = g.D, NB = D / QK;
+    const float4_t xv = *(const float4_t *)(g.x + (int64_t)t * D + b * QK + 4 * lane);
+    const float v[4] = {xv[0], xv[1], xv[2], xv[3]};
+    int q[4];
+    const float d = q8k_wave(v, lane, q);
+    st_dev4(g.xq, (uint32_t)(t * D + b * QK + 4 * lane), pack_i8x4(q));
+    if (lane == 0) st_dev4(g.xd, 4u * (uint32_t)(t * NB + b), __builtin_bit_cast(uint32_t, d));
+    const int s = q8k_bsum16(q);
+    const int s_hi = __shfl_down(s, 4, 64);
+    if ((lane & 7) == 0)
+        st_dev4(g.xbs, 2u * (uint32_t)(t * (D / 16) + b * 16 + (lane >> 2)),
+                (uint32_t)(uint16_t)(int16_t)s | ((uint32_t)(uint16_t)(int16_t)s_hi << 16));
+}
+
+// A unit u (see above); the wave publishes it
+__device__ inline void decb_unit_a(const DecArgs &g, uint32_t tag, int u, int lane) {
+    const int E = g.E, T = g.T, NB = g.D / QK;
+    if (u < E * T) {
+        const int t = u / E, e = u - t * E;
+        const float lv = decb_router_row(g.rw, g.rb, g.x + (int64_t)t * g.D, g.D, e, lane);
+        if (lane == 0) tw_store(g.tw2 + u, tag, __builtin_bit_cast(uint32_t, lv));
+    } else {
+        const int v = u - E * T, t = v / NB, b = v - t * NB;
+        decb_q8k_x(g, t, b, lane);
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the block is out before its word
+        if (lane == 0) tw_store(g.tw2 + u, tag, 1u);
+    }
+}
+
+// one B unit's weight bytes for the lane: NB blocks x (header, 16 qs bytes)
+struct DecBW {
+    u32x4 h[DECB_NB_MAX], q[DECB_NB_MAX];
+};
+
+template <int NB>
+__device__ inline void decb_b_load(const DecArgs &g, int e, int q, int lane, DecBW &w) {
+    const int rs = lane >> 3, sl = lane & 7;
+    const int64_t row = 4 * (int64_t)q + (rs & 3);
+    const bool hpart = rs < 4;
+    const ExpertMat &m = (hpart || g.fused) ? g.gate : g.up;
+    const int64_t wrow = row + ((!hpart && g.fused) ? g.I : 0);
+    const uint8_t *rowp = m.data + (int64_t)e * m.mat_bytes + wrow * m.row_bytes;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        w.h[b] = *(const u32x4 *)(rowp + b * Q4K_BYTES);
+        w.q[b] = *(const u32x4 *)(rowp + b * Q4K_BYTES + 16 + 16 * sl);
+    }
+}
+
+// lane piece sl of a Q4_K block (header h, qs bytes qv) against x's Q8_K
+// block in LDS (codes xq, block sums xbs, scale dx): ggml_vec_dot_q4_K_q8_K
+// restricted to the lane's 32 values
+__device__ inline float decb_q4_dot(const u32x4 &h, const u32x4 &qv, int sl, const int8_t *xq, const int16_t *xbs,
+                                    float dx) {
+    const float d = h2f((uint16_t)(h[0] & 0xffff)), dmin = h2f((uint16_t)(h[0] >> 16));
+    const int c = sl >> 1, l0 = 16 * (sl & 1);
+    int scA, mA, scB, mB;
+    scale_min_k4_reg(2 * c, h[1], h[2], h[3], scA, mA);
+    scale_min_k4_reg(2 * c + 1, h[1], h[2], h[3], scB, mB);
+    const u32x4 xa = *(const u32x4 *)(xq + 64 * c + l0);
+    const u32x4 xb = *(const u32x4 *)(xq + 64 * c + 32 + l0);
+    int sa = 0, sb = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        sa = __builtin_amdgcn_sdot4((int)(qv[i] & 0x0F0F0F0Fu), (int)xa[i], sa, false);
+        sb = __builtin_amdgcn_sdot4((int)((qv[i] >> 4) & 0x0F0F0F0Fu), (int)xb[i], sb, false);
+    }
+    const int bsa = xbs[4 * c + (sl & 1)], bsb = xbs[4 * c + 2 + (sl & 1)];
+    return (d * dx) * (float)(scA * sa + scB * sb) - (dmin * dx) * (float)(mA * bsa + mB * bsb);
+}
+
+// 8-lane sum (lanes 8 r .. 8 r + 7), in every lane of the group
+__device__ inline float decb_sum8(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    return v;
+}
+
+// Q8_K of x for all T tokens, in LDS (codes [T][D], scales [T][NB], block sums [T][D/16])
+struct DecBX {
+    int8_t *q;
+    float *d;
+    int16_t *bs;
+};
+
+// B unit (d, q) from the loaded weights w: every pair of expert d
+template <int NB>
+__device__ inline void decb_b_compute(const DecArgs &g, const DecBX &x, const int *s_dcnt, const int *s_dpair, int d,
+                                      int q, int lane, const DecBW &w) {
+    const int rs = lane >> 3, sl = lane & 7, D = g.D, I = g.I;
+    const int n = s_dcnt[d];
+    for (int j = 0; j < n; ++j) {
+        const int p = s_dpair[d * DECB_PAIRS_MAX + j], t = p / g.K;
+        float acc = 0.f;
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+            acc += decb_q4_dot(w.h[b], w.q[b], sl, x.q + t * D + b * QK, x.bs + t * (D / 16) + b * 16, x.d[t * NB + b]);
+        acc = decb_sum8(acc);
+        const float other = __shfl_xor(acc, 32, 64);   // the g row of the same column
+        if (rs < 4 && sl == 0)
+            st_dev4(g.actf, 4u * (uint32_t)((int64_t)p * I + 4 * q + rs),
+                    __builtin_bit_cast(uint32_t, act_pair(g.act, acc, other)));
+    }
+}
+
+// one lane's raw down-row bytes of a C pass: NBI blocks
+template <int DT> struct DecBDn;
+template <> struct DecBDn<12> {
+    u32x4 h[DECB_NBI_MAX], q[DECB_NBI_MAX];
+};
+template <> struct DecBDn<14> {
+    uint32_t a[DECB_NBI_MAX][3], b[DECB_NBI_MAX][3], qh[DECB_NBI_MAX][3], s[DECB_NBI_MAX][3], dw[DECB_NBI_MAX];
+    uint32_t mis[DECB_NBI_MAX];
+};
+
+// the three aligned dwords holding bytes [p, p + 8) of a 2-byte-aligned address
+// (the third only when p is not dword aligned: no byte past the range is read)
+__device__ inline void decb_raw8(const uint8_t *p, uint32_t (&w)[3]) {
+    const uint32_t *a = (const uint32_t *)((uintptr_t)p & ~(uintptr_t)3);
+    w[0] = a[0];
+    w[1] = a[1];
+    w[2] = ((uintptr_t)p & 3u) ? a[2] : 0u;
+}
+__device__ inline uint2 decb_al8(const uint32_t (&w)[3], uint32_t mis) {
+    uint2 r;
+    r.x = __builtin_amdgcn_alignbyte(w[1], w[0], mis);
+    r.y = __builtin_amdgcn_alignbyte(w[2], w[1], mis);
+    return r;
+}
+
+// row `row` of expert e's down matrix, lane piece sl of each block
+template <int DT, int NBI>
+__device__ inline void decb_dn_load(const ExpertMat &m, int e, int64_t row, int sl, DecBDn<DT> &r) {
+    const uint8_t *rowp = m.data + (int64_t)e * m.mat_bytes + row * m.row_bytes;
+#pragma unroll
+    for (int b = 0; b < NBI; ++b) {
+        if constexpr (DT == 12) {
+            r.h[b] = *(const u32x4 *)(rowp + b * Q4K_BYTES);
+            r.q[b] = *(const u32x4 *)(rowp + b * Q4K_BYTES + 16 + 16 * sl);
+        } else {
+            const uint8_t *blk = rowp + b * Q6K_BYTES;
+            const int h = sl >> 2, l0 = 8 * (sl & 3);
+            r.mis[b] = (uint32_t)((uintptr_t)blk & 3u);
+            decb_raw8(blk + 64 * h + l0, r.a[b]);
+            decb_raw8(blk + 64 * h + 32 + l0, r.b[b]);
+            decb_raw8(blk + 128 + 32 * h + l0, r.qh[b]);
+            decb_raw8(blk + 192 + 8 * h, r.s[b]);
+            r.dw[b] = *(const uint16_t *)(blk + 208);   // d (2-byte aligned)
+        }
+    }
+}
+
+// the lane's share of one down row's dot with the slot's Q8_K (LDS: codes aq,
+// scales ad, block sums abs_)
+template <int DT, int NBI>
+__device__ inline float decb_dn_dot(const DecBDn<DT> &r, int sl, const int8_t *aq, const float *ad,
+                                    const int16_t *abs_) {
+    float acc = 0.f;
+#pragma unroll
+    for (int b = 0; b < NBI; ++b) {
+        if constexpr (DT == 12) {
+            acc += decb_q4_dot(r.h[b], r.q[b], sl, aq + b * QK, abs_ + b * 16, ad[b]);
+        } else {
+            const uint32_t mis = r.mis[b];
+            Q6Piece w;
+            w.qla = decb_al8(r.a[b], mis);
+            w.qlb = decb_al8(r.b[b], mis);
+            w.qh = decb_al8(r.qh[b], mis);
+            const uint2 s8 = decb_al8(r.s[b], mis);
+            const int is = (8 * (sl & 3)) >> 4;
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+                const int idx = is + 2 * qq;
+                const uint32_t word = (idx >> 2) ? s8.y : s8.x;
+                w.sc[qq] = (int)(int8_t)(word >> (8 * (idx & 3)));
+            }
+            w.d = h2f((uint16_t)r.dw[b]);
+            acc += dot_q6_piece(w, sl, aq + b * QK, ad[b]);
+        }
+    }
+    return acc;
+}
+
+
+// Top-K of one token's E logits (LDS row l, E <= 256) by one wave, as K rounds
+// of a wave argmax over the values not yet taken: largest first, the lower id
+// first among equal values (ggml_top_k's stable descending order).  Lane k < K
+// gets the k-th id and its weight (the shared softmax over the K selected).
+__device__ inline void decb_topk(const float *l, int E, int K, int lane, int &mysel, float &myw) {
+    float v[TOPK_MAX_PER_LANE];
+    bool avail[TOPK_MAX_PER_LANE];
+#pragma unroll
+    for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
+        const int e = lane + 64 * i;
+        avail[i] = e < E;
+        v[i] = avail[i] ? l[e] : -INFINITY;
+    }
+    // (bv, bi) replaced by (pv, pi) when pv is larger, or equal with a lower id
+    auto take = [](float bv, int bi, float pv, int pi) { return (pv > bv) | ((pv == bv) & (pi < bi)); };
+    mysel = 0;
+    float myval = 0.f;
+    for (int r = 0; r < K; ++r) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
+            const int e = lane + 64 * i;
+            if (avail[i] && (take(bv, bi, v[i], e) | (bi == 0x7fffffff))) {
+                bv = v[i];
+                bi = e;
+            }
+        }
+        // every lane of a 16-lane row gets the row's best, then the four rows
+        // are compared in order through scalar reads
+#define DECB_ARGMAX_STEP(CTRL)                                                  \
+        {                                                                       \
+            const float pv = dpp_f<CTRL>(bv);                                   \
+            const int pi = dpp_i<CTRL>(bi);                                     \
+            if (take(bv, bi, pv, pi) | ((bi == 0x7fffffff) & (pi != 0x7fffffff))) { bv = pv; bi = pi; } \
+        }
+        DECB_ARGMAX_STEP(0xB1)
+        DECB_ARGMAX_STEP(0x4E)
+        DECB_ARGMAX_STEP(0x141)
+        DECB_ARGMAX_STEP(0x140)
+#undef DECB_ARGMAX_STEP
+        float wv = lane_f(bv, 0);
+        int wi = __builtin_amdgcn_readlane(bi, 0);
+#pragma unroll
+        for (int row = 1; row < 4; ++row) {
+            const float pv = lane_f(bv, 16 * row);
+            const int pi = __builtin_amdgcn_readlane(bi, 16 * row);
+            if (take(wv, wi, pv, pi) | ((wi == 0x7fffffff) & (pi != 0x7fffffff))) {
+                wv = pv;
+                wi = pi;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TOPK_MAX_PER_LANE; ++i)
+            if (lane + 64 * i == wi) avail[i] = false;
+        if (lane == r) {
+            mysel = wi;
+            myval = wv;
+        }
+    }
+    myw = softmax_selected_wave(myval, K, lane);
+}
+
+constexpr int DECB_LIST = 1024;   // missing units listed per rescue round
+
+template <int DT, int NB, int NBI>
+__global__ void __launch_bounds__(DECB_THREADS) k_decodeb(DecArgs g) {
+    __shared__ __attribute__((aligned(16))) int8_t s_xq[DECB_T_MAX * DECB_NB_MAX * QK];
+    __shared__ float s_xd[DECB_T_MAX * DECB_NB_MAX];
+    __shared__ int16_t s_xbs[DECB_T_MAX * DECB_NB_MAX * 16];
+    __shared__ float s_logit[DECB_T_MAX * 256];
+    __shared__ int s_sel[DECB_T_MAX * DEC_KMAX], s_pd[DECB_T_MAX * DEC_KMAX];
+    __shared__ float s_w[DECB_T_MAX * DEC_KMAX];
+    __shared__ int s_first[256], s_dist[DECB_T_MAX * DEC_KMAX], s_dcnt[DECB_T_MAX * DEC_KMAX];
+    __shared__ int s_eidx[256];
+    __shared__ unsigned s_tmask[256];
+    __shared__ int s_dpair[DECB_T_MAX * DEC_KMAX * DECB_PAIRS_MAX];
+    __shared__ __attribute__((aligned(16))) int8_t s_aq[DEC_KMAX][DECB_NBI_MAX * QK];
+    __shared__ float s_ad[DEC_KMAX][DECB_NBI_MAX];
+    __shared__ int16_t s_abs[DEC_KMAX][DECB_NBI_MAX * 16];
+    __shared__ float s_z[DEC_KMAX][DECB_COLS];
+    __shared__ int s_list[DECB_LIST];
+    __shared__ int s_nd, s_nmiss, s_fail, s_wmiss[DECB_WAVES];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wg = blockIdx.x, G = gridDim.x;
+    const int gw = wg * DECB_WAVES + wave, NW = G * DECB_WAVES;
+    const int D = g.D, E = g.E, K = g.K, I = g.I, T = g.T;
+    const int UA = E * T + T * NB;       // A units (= words)
+    const int QB = I / 4;                // B units per distinct expert
+    const uint32_t tag = __hip_atomic_load(g.epoch + wg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    bool ok = true;
+    unsigned spins = 0;
+    if (tid == 0) s_fail = 0;
+    const DecBX X = {s_xq, s_xd, s_xbs};
+
+    // B unit ub = d QB + q, computed and published by the calling wave
+    auto unit_b = [&](int ub) {
+        const int d = ub / QB, q = ub - d * QB;
+        DecBW w;
+        decb_b_load<NB>(g, s_dist[d], q, lane, w);
+        decb_b_compute<NB>(g, X, s_dcnt, s_dpair, d, q, lane, w);
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the activations are out before the word
+        if (lane == 0) tw_store(g.tw2 + UA + ub, tag, 1u);
+    };
+
+    // Wait until the n words at tw2[word(i)], i < n, carry this launch's tag.
+    // Each thread polls its share; after g.rescue_polls tries the missing
+    // units are listed and computed by this WG's waves (rescue(u)), which
+    // publish them, and the poll repeats.  False when the spin budget ran out.
+    auto wait_words = [&](int n, auto word, auto rescue) -> bool {
+        for (;;) {
+            // one round = every word of the thread loaded at once (one
+            // latency), repeated up to g.rescue_polls times while any is missing
+            bool miss = true;
+            for (unsigned r = 0; r <= g.rescue_polls && miss; ++r) {
+                if (r) __builtin_amdgcn_s_sleep(1);
+                miss = false;
+#pragma unroll 4
+                for (int i = tid; i < n; i += DECB_THREADS)
+                    miss |= (uint32_t)(tw_load(g.tw2 + word(i)) >> 32) != tag;
+            }
+            if (dec_none_missing(s_wmiss, miss)) return true;
+            dec_lds_barrier();   // earlier readers of the list are done
+            if (tid == 0) s_nmiss = 0;
+            dec_lds_barrier();
+            for (int i = tid; i < n; i += DECB_THREADS) {
+                const uint64_t wv = tw_load(g.tw2 + word(i));
+                if ((uint32_t)(wv >> 32) != tag) {
+                    const int at = atomicAdd(&s_nmiss, 1);
+                    if (at < DECB_LIST) s_list[at] = word(i);
+                }
+            }
+            dec_lds_barrier();
+            const int nm = imin(__builtin_amdgcn_readfirstlane(s_nmiss), DECB_LIST);
+            spins += g.rescue_polls + 1;
+            if (spins > DEC_SPIN_LIMIT) return false;
+            for (int m = wave; m < nm; m += DECB_WAVES) rescue(__builtin_amdgcn_readfirstlane(s_list[m]));
+            dec_lds_barrier();
+        }
+    };
+
+    // the single-token kernel's completion counters: a launch clears the set
+    // the next launch (either kernel) would use, as k_decode1 does
+    if (wg == 0 && tid <= DEC_MAX_GRID / DEC_GROUP)
+        __hip_atomic_store(dec_cnt(g.tw, tag + 1u, tid), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // ---- A: router rows and Q8_K of x, by waves
+    for (int u = gw; u < UA; u += NW) decb_unit_a(g, tag, u, lane);
+
+    // ---- every A word (the logits travel in them); missing units computed here
+    ok = wait_words(UA, [&](int i) { return i; }, [&](int u) { decb_unit_a(g, tag, u, lane); });
+    for (int i = tid; i < E * T; i += DECB_THREADS) s_logit[i] = as_float((uint32_t)tw_load(g.tw2 + i));
+    // x's Q8_K for every token (coherent loads: other WGs wrote it) goes out
+    // now and lands in LDS after the ranking
+    constexpr int XQ_PER = DECB_T_MAX * DECB_NB_MAX * QK / 16 / DECB_THREADS;   // 16-byte pieces per thread
+    u32x4 xqv[XQ_PER];
+    const int nxq = T * D / 16;
+    {
+        const auto rq = co_rsrc(g.xq, (uint32_t)(T * D));
+#pragma unroll
+        for (int j = 0; j < XQ_PER; ++j) {
+            const int i = tid + j * DECB_THREADS;
+            if (i < nxq) xqv[j] = co_ld16(rq, 16u * (uint32_t)i);
+        }
+        const auto rd = co_rsrc(g.xd, (uint32_t)(4 * T * NB));
+        for (int i = tid; i < T * NB; i += DECB_THREADS) s_xd[i] = as_float(co_ld4(rd, 4u * (uint32_t)i));
+        const auto rb = co_rsrc(g.xbs, (uint32_t)(2 * T * (D / 16)));
+        for (int i = tid; i < T * (D / 16) / 2; i += DECB_THREADS) {
+            const uint32_t v = co_ld4(rb, 4u * (uint32_t)i);
+            s_xbs[2 * i] = (int16_t)(uint16_t)(v & 0xffffu);
+            s_xbs[2 * i + 1] = (int16_t)(uint16_t)(v >> 16);
+        }
+    }
+    for (int e = tid; e < E; e += DECB_THREADS) {
+        s_first[e] = DECB_T_MAX * DEC_KMAX;
+        s_tmask[e] = 0u;
+    }
+    dec_lds_barrier();
+    // ---- ranking: token t by wave t % 8 (the shared top-k / softmax code)
+    for (int t = wave; t < T; t += DECB_WAVES) {
+        int mysel;
+        float myw;
+        decb_topk(s_logit + t * E, E, K, lane, mysel, myw);
+        if (lane < K) {
+            s_sel[t * K + lane] = mysel;
+            s_w[t * K + lane] = myw;
+            atomicMin(&s_first[mysel], t * K + lane);
+            atomicOr(&s_tmask[mysel], 1u << t);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < XQ_PER; ++j) {
+        const int i = tid + j * DECB_THREADS;
+        if (i < nxq) *(u32x4 *)(s_xq + 16 * i) = xqv[j];
+    }
+    dec_lds_barrier();
+    // distinct experts in first-use order of the flat pairs p = t K + k, and
+    // each one's pairs in flat order (the same lists in every WG)
+    const int NP = T * K;
+    if (wave == 0) {
+        int nd = 0;
+        for (int p0 = 0; p0 < NP; p0 += 64) {
+            const int p = p0 + lane;
+            const bool first = p < NP && s_first[s_sel[p]] == p;
+            const uint64_t m = __ballot(first);
+            if (first) {
+                const int d = nd + __popcll(m & ((1ull << lane) - 1ull));
+                s_dist[d] = s_sel[p];
+                s_eidx[s_sel[p]] = d;
+            }
+            nd += __popcll(m);
+        }
+        if (lane == 0) s_nd = nd;
+    }
+    dec_lds_barrier();
+    const int ND = __builtin_amdgcn_readfirstlane(s_nd);
+    // pair p = t K + k of expert e: the j-th of e's pairs, j = the tokens
+    // before t that picked e (a token picks an expert once)
+    for (int p = tid; p < NP; p += DECB_THREADS) {
+        const int e = s_sel[p], t = p / K, d = s_eidx[e];
+        const unsigned m = s_tmask[e];
+        s_pd[p] = d;
+        s_dpair[d * DECB_PAIRS_MAX + __popc(m & ((1u << t) - 1u))] = p;
+        if ((m & ((1u << t) - 1u)) == 0u) s_dcnt[d] = __popc(m);
+    }
+    dec_lds_barrier();
+    if (wg == 0) {
+        // routing outputs: logits, ids, weights, and the dispatch of the T K
+        // ids (stable counting sort)
+        for (int i = tid; i < E * T; i += DECB_THREADS) g.logits[i] = s_logit[i];
+        for (int p = tid; p < NP; p += DECB_THREADS) {
+            g.sel[p] = s_sel[p];
+            g.w[p] = s_w[p];
+            const int e = s_sel[p];
+            int below = 0, before = 0;
+            for (int q2 = 0; q2 < NP; ++q2) {
+                below += s_sel[q2] < e;
+                before += (s_sel[q2] == e) & (q2 < p);
+            }
+            g.perm[below + before] = p;
+        }
+        for (int e = tid; e < E; e += DECB_THREADS) {
+            int cnt = 0, below = 0;
+            for (int q2 = 0; q2 < NP; ++q2) {
+                cnt += s_sel[q2] == e;
+                below += s_sel[q2] < e;
+            }
+            g.counts[e] = cnt;
+            g.offsets[e] = below;
+        }
+        if (tid == 0) g.offsets[E] = NP;
+    }
+
+    // ---- B: (distinct expert, 4 row pairs) units by waves; the next unit's
+    // weight bytes load while the current one computes
+    const int UB = ND * QB;
+    if (ok) {
+        int u = gw;
+        DecBW wc, wn;
+        if (u < UB) decb_b_load<NB>(g, s_dist[u / QB], u % QB, lane, wc);
+        for (; u < UB; u += NW) {
+            const int un = u + NW;
+            if (un < UB) decb_b_load<NB>(g, s_dist[un / QB], un % QB, lane, wn);
+            const int d = u / QB, q = u - d * QB;
+            decb_b_compute<NB>(g, X, s_dcnt, s_dpair, d, q, lane, wc);
+            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): activations (and the next loads) are in
+            if (lane == 0) tw_store(g.tw2 + UA + u, tag, 1u);
+            wc = wn;
+        }
+    }
+
+    // ---- C: (token, CC columns) units by WGs
+    const int CC = g.C;                  // columns per C unit (a multiple of 8, <= 64)
+    const int UCT = D / CC, UC = T * UCT;
+    for (int cu = wg; cu < UC; cu += G) {
+        const int t = cu / UCT, n0 = (cu - t * UCT) * CC;
+        // the B words of the token's K experts
+        if (ok)
+            ok = wait_words(K * QB, [&](int i) { return UA + s_pd[t * K + i / QB] * QB + i % QB; },
+                            [&](int w) { unit_b(w - UA); });
+        // wave k: the Q8_K of slot k's I activations (coherent loads), then
+        // its CC down rows' dots, CC / 8 rows per pass, the next pass loading
+        if (wave < K) {
+            const int k = wave, p = t * K + k;
+            const auto ra = co_rsrc(g.actf + (int64_t)p * I, (uint32_t)(4 * I));
+            const int b = lane >> 4, seg = lane & 15;
+            float av[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                u32x4 a4 = {0u, 0u, 0u, 0u};
+                if (b < NBI) a4 = co_ld16(ra, 4u * (uint32_t)(b * QK + 16 * seg + 4 * i));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) av[4 * i + e] = as_float(a4[e]);
+            }
+            int qv[16], bsum;
+            const float dq = q8k_wave4x16(av, lane, qv, bsum);
+            if (b < NBI) {
+                u32x4 pk;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int qi[4] = {qv[4 * i], qv[4 * i + 1], qv[4 * i + 2], qv[4 * i + 3]};
+                    pk[i] = pack_i8x4(qi);
+                }
+                *(u32x4 *)(s_aq[k] + b * QK + 16 * seg) = pk;
+                s_abs[k][b * 16 + seg] = (int16_t)bsum;
+                if (seg == 0) s_ad[k][b] = dq;
+            }
+            wave_lds_sync();
+            const int e = s_sel[p], rs = lane >> 3, sl = lane & 7;
+            // passes of 8 rows, the loads AH passes ahead of the dots, as deep
+            // as the registers allow without spilling (Q6_K's raw bytes of a
+            // pass take 56 registers at I = 1024)
+            constexpr int AH = DT == 12 ? (NBI <= 3 ? 2 : 1) : 0;
+            const int npass = CC / 8;
+            DecBDn<DT> rb[AH + 1];
+#pragma unroll
+            for (int a = 0; a < AH; ++a)
+                if (a < npass) decb_dn_load<DT, NBI>(g.down, e, n0 + 8 * a + rs, sl, rb[a]);
+            // a rolled loop (the buffers rotate by copies): unrolled, the
+            // scheduler would hoist every pass's loads
+#pragma unroll 1
+            for (int ps = 0; ps < npass; ++ps) {
+                if (ps + AH < npass) decb_dn_load<DT, NBI>(g.down, e, n0 + 8 * (ps + AH) + rs, sl, rb[AH]);
+                float z = decb_dn_dot<DT, NBI>(rb[0], sl, s_aq[k], s_ad[k], s_abs[k]);
+                z = decb_sum8(z);
+                if (sl == 0) s_z[k][8 * ps + rs] = z;
+#pragma unroll
+                for (int a = 0; a < AH; ++a) rb[a] = rb[a + 1];
+            }
+        }
+        if (!ok) s_fail = 1;
+        dec_lds_barrier();
+        const bool failed = s_fail != 0;
+        if (tid < CC) {
+            double s = 0.0;
+            for (int k = 0; k < K; ++k) s = s + (double)(s_z[k][tid] * s_w[t * K + k]);
+            const int64_t o = (int64_t)t * D + n0 + tid;
+            float v = g.res ? g.res[o] + (float)s : (float)s;
+            if (failed) v = __builtin_nanf("");
+            g.out[o] = v;
+        }
+        dec_lds_barrier();   // s_z / s_aq are rewritten by the next unit
+    }
+    if (!ok) s_fail = 1;
+    dec_lds_barrier();
+    if (tid == 0) {
+        if (s_fail) __hip_atomic_fetch_add(g.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(g.epoch + wg, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <int DT, int NB>
+static const void *decodeb_fn2(int nbi) {
+    switch (nbi) {
+    case 1: return (const void *)k_decodeb<DT, NB, 1>;
+    case 2: return (const void *)k_decodeb<DT, NB, 2>;
+    case 3: return (const void *)k_decodeb<DT, NB, 3>;
+    case 4: return (const void *)k_decodeb<DT, NB, 4>;
+    default: return nullptr;
+    }
+}
+template <int DT>
+static const void *decodeb_fn(int nb, int nbi) {
+    switch (nb) {
+    case 1: return decodeb_fn2<DT, 1>(nbi);
+    case 2: return decodeb_fn2<DT, 2>(nbi);
+    case 4: return decodeb_fn2<DT, 4>(nbi);
+    case 8: return decodeb_fn2<DT, 8>(nbi);
+    default: return nullptr;
+    }
+}
+
+int launch_decodeb(const DecArgs &g, int grid, hipStream_t st) {
+    if (g.T < 2 || g.T > DECB_T_MAX || g.K > DEC_KMAX || g.E > 256 || grid <= 0 || grid > DEC_MAX_GRID) return -6;
+    if (g.C <= 0 || g.C > DECB_COLS || g.C % 8 || g.D % g.C) return -6;
+    const int nb = g.D / QK, nbi = g.I / QK;
+    const void *fn = g.down.type == 12 ? decodeb_fn<12>(nb, nbi) : g.down.type == 14 ? decodeb_fn<14>(nb, nbi) : nullptr;
+    if (!fn) return -3;
+    void *args[] = {(void *)&g};
+    const hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(DECB_THREADS), args, 0, st);
+    if (e != hipSuccess) return record_hip_error(e);
+    return hip_check_launch();
 }
 
 template <int DT>

@@ -192,23 +192,25 @@ int gemm4_grid(const G2Args &g);   // work-groups launch_gemm4 launches
 
 // Single-token MoE block in one cooperative kernel (k_decode.hip).
 struct DecArgs {
-    const float *rw, *rb, *x;     // router W [E][D], bias [E] or NULL, token [D]
+    const float *rw, *rb, *x;     // router W [E][D], bias [E] or NULL, tokens [T][D]
     int D, E, K, I;
+    int T;                        // tokens (k_decode1: 1; k_decodeb: 2 .. DECB_T_MAX)
     ExpertMat gate, up, down;     // Q4_K gate (or fused [h | g]) / up; Q4_K or Q6_K down
     int fused, act;
-    const float *res;             // [D] or NULL
-    float *out;                   // [D]
-    int P, C;                     // (h, g) row pairs per WG; down columns per WG
+    const float *res;             // [T][D] or NULL
+    float *out;                   // [T][D]
+    int P, C;                     // (h, g) row pairs per WG; down columns per WG (k_decodeb: per C unit)
     // workspace / routing outputs
-    float *logits;                // [E]
-    int32_t *sel;                 // [K]
-    float *w;                     // [K]
+    float *logits;                // [T][E]
+    int32_t *sel;                 // [T][K]
+    float *w;                     // [T][K]
     int32_t *counts, *offsets, *perm;
-    int8_t *xq;                   // Q8_K of x: codes [D], scales [D/256], block sums [D/16]
+    int8_t *xq;                   // Q8_K of x: codes [T][D], scales [T][D/256], block sums [T][D/16]
     float *xd;
     int16_t *xbs;
-    float *actf;                  // GLU output fp32 [K][I]
+    float *actf;                  // GLU output fp32 [T K][I]
     uint64_t *tw;                 // epoch-tagged logits [E] and gate/up unit completions, launch counters
+    uint64_t *tw2;                // k_decodeb's epoch-tagged unit words (decodeb_tw_words)
     uint32_t *epoch;              // [grid] per-WG launch epochs
     unsigned *err;                // set when a wait gave up (output is NaN)
     unsigned rescue_polls;        // polls for another WG's unit before computing it here
@@ -223,6 +225,14 @@ constexpr unsigned DEC_RESCUE_POLLS = 64;
 constexpr int DEC_LIMIT_GU_BYTES = 9 * 1024;   // LDS per wave of gate/up rows
 constexpr int DEC_LIMIT_DN_BYTES = 7 * 1024;   // LDS per slot of down rows
 constexpr int DEC_LIMIT_UNPACKED_BYTES = 10 * 1024;   // LDS per slot of dot-ready down rows
+// k_decodeb: 2 .. DECB_T_MAX tokens in one kernel (plain launch, no
+// co-residency needed: as k_decode1)
+constexpr int DECB_T_MAX = 16;
+// words of tw2 for T tokens (A units E T + T D/256, then I/4 per distinct expert)
+constexpr int64_t decodeb_tw_words(int64_t T, int64_t D, int64_t E, int64_t K, int64_t I) {
+    return E * T + T * (D / 256) + T * K * (I / 4);
+}
+int launch_decodeb(const DecArgs &g, int grid, hipStream_t st);
 // cooperative: hipLaunchCooperativeKernel; otherwise a plain launch (the
 // kernel needs no co-residency: a WG computes any unit it waited too long for)
 int launch_decode1(const DecArgs &g, int grid, bool cooperative, hipStream_t st);

@@ -112,6 +112,8 @@ def test_config3_batched_decode(T):
         paths += [("gemv", 1 << 30), ("gemm", 1)]
     for pname, thr in paths:
         ctx.set_gemm_threshold(thr)
+        # default: the fused kernels where they apply; gemv / gemm: the chain on that path
+        ctx.set_fused_decode(M.DECODE_FUSED if pname == "default" else M.DECODE_CHAIN)
         out = M.DeviceBuffer(4 * T * spec.D)
         bufs, r = _routing_buffers(T, spec.E, spec.K)
         M.check("forward", ctx.forward(g.layer, x, T, None, out, r))

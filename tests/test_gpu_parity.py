@@ -95,6 +95,7 @@ def _routing_buffers(T, E, K):
 def test_layer_small(spec, path):
     ctx, g, cpu = _gpu_layer_and_cpu(spec)
     ctx.set_gemm_threshold(1 if path == "gemm" else 1 << 30)
+    ctx.set_fused_decode(M.DECODE_CHAIN)   # the named path at every size (the fused kernels have their own tests)
     for T in [1, 3, 17, 64, 200]:
         x = cpu_x(spec, T)
         res = cpu_x(spec, T, stream=W.S_RES)

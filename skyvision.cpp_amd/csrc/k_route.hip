@@ -201,10 +201,103 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const ST *__restrict__ src, in
     }
 }
 
+// fp16 values only (o.xh in a Q4_K / Q6_K 32x32x16 order, no codes, scales or
+// sums): each lane loads its 16 values straight in the output order — four
+// runs of 4 consecutive values at base(g, s) and base(g, s) + 32, g = 0, 1 —
+// so no code bytes are packed, staged in LDS or unpacked again.
+//
+// The value d*q does not depend on which element of largest |x| fixes the
+// scale's sign: with m = max |x| the scale is -127 / (+-m) = -+(127 / m) (a
+// correctly rounded divide is odd), the codes round half to even (odd) and
+// stay inside [-127, 127] (|127 x / m| < 127.5), so d and q change sign
+// together and their product keeps its bits.  Only the sign of a zero
+// product may differ from the element-first form, and a zero adds nothing
+// to an MFMA sum that starts at +0.
+// first of lane s's 4 values A of half g (B: the 4 at + 32); output slot p
+// = 0..7 of the half holds Q4_K A0 A2 B0 B2 A1 A3 B1 B3, Q6_K A0..A3 B0..B3
+template <int XO>
+__device__ __forceinline__ int q8h_base(int s, int g) {
+    return XO == XO_Q4 ? 64 * (2 * (s >> 3) + g) + 4 * (s & 7)
+                       : 128 * (s >> 3) + 16 * g + 4 * ((s & 7) >> 1) + 64 * (s & 1);
+}
+
+template <int XO, typename ST>
+__global__ void __launch_bounds__(256) k_q8k_rows_h(const ST *__restrict__ src, int64_t ld, int64_t nrows, int nb,
+                                                    Q8Out o) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int ngrp = (nb + 3) >> 2;
+    const int64_t item = (int64_t)blockIdx.x * 4 + wave;
+    if (item >= nrows * ngrp) return;   // whole waves; only DPP exchanges follow
+    const int64_t row = ngrp == 1 ? item : item / ngrp;
+    const int grp = (int)(item - row * ngrp);
+    const int bl = lane >> 4, s = lane & 15;
+    const int b = 4 * grp + bl;
+    const bool bok = b < nb;
+    float v[16];
+    if (bok) {
+        const ST *x = src + row * ld + (int64_t)b * QK;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {   // run r: half g = r >> 1, A (r even) or B
+            const int g = r >> 1, half = r & 1;
+            const int start = q8h_base<XO>(s, g) + 32 * half;
+            float w[4];
+            if constexpr (sizeof(ST) == 2) {
+                const uint2 u = *(const uint2 *)(x + start);
+                const half2_t h0 = __builtin_bit_cast(half2_t, u.x), h1 = __builtin_bit_cast(half2_t, u.y);
+                w[0] = (float)h0[0]; w[1] = (float)h0[1]; w[2] = (float)h1[0]; w[3] = (float)h1[1];
+            } else {
+                const float4 f = *(const float4 *)(x + start);
+                w[0] = f.x; w[1] = f.y; w[2] = f.z; w[3] = f.w;
+            }
+            // the run's 4 values to their output slots
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int p = XO == XO_Q4 ? (i & 1) * 4 + (i >> 1) + 2 * half : i + 4 * half;
+                v[8 * g + p] = w[i];
+            }
+        }
+        if (o.pre_act == ACT_RELU_SQR) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = relu_sqr(v[i]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = 0.f;
+    }
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+    m = fmaxf(m, dpp_f<0xB1>(m));
+    m = fmaxf(m, dpp_f<0x4E>(m));
+    m = fmaxf(m, dpp_f<0x141>(m));
+    m = fmaxf(m, dpp_f<0x140>(m));   // largest |x| of the lane's block
+    const bool zero = m == 0.f;
+    const float iscale = zero ? 0.f : 127.f / m;
+    const float d = zero ? 0.f : 1 / iscale;
+    if (!bok) return;
+    uint32_t h[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        half2_t hh;
+        hh[0] = f16_sat(d * __builtin_rintf(iscale * v[2 * k]));
+        hh[1] = f16_sat(d * __builtin_rintf(iscale * v[2 * k + 1]));
+        h[k] = __builtin_bit_cast(uint32_t, hh);
+    }
+    if (s == 0 && o.range_total && f16_over(d)) atomicAdd(o.range_total, 1);
+    uint4 *dst = (uint4 *)(o.xh + row * (int64_t)nb * QK + (int64_t)b * QK + 16 * s);
+    dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
+    dst[1] = make_uint4(h[4], h[5], h[6], h[7]);
+}
+
 // the compile-time fp16 order for o (XO_ANY when o has no xh)
 inline int q8_xo(const Q8Out &o) {
     if (!o.xh || !o.order || o.exact) return XO_ANY;
     return o.wtype == 12 ? XO_Q4 : o.wtype == 14 ? XO_Q6 : XO_ANY;
+}
+
+// o asks for the fp16 values alone (k_q8k_rows_h)
+inline bool q8_h_only(const Q8Out &o, int xo) {
+    return xo != XO_ANY && !o.q8 && !o.d8 && !o.bsums && !o.xbs;
 }
 
 int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, const Q8Out &o, hipStream_t st) {
@@ -214,7 +307,11 @@ int launch_q8k_rows(const float *src, int64_t ld, int64_t nrows, int64_t K, cons
     const bool vec = (ld % 4 == 0) && ((uintptr_t)src % 16 == 0);
     const dim3 grid((unsigned)((items + 4 * Q8_ITEMS - 1) / (4 * Q8_ITEMS)));
     const int xo = q8_xo(o);
-    if (vec && xo == XO_Q4) hipLaunchKernelGGL((k_q8k_rows<true, XO_Q4, float>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    // fp16 values alone: whole 256-value blocks (each lane's runs are 4 floats)
+    const bool h_only = vec && q8_h_only(o, xo) && K % QK == 0;
+    if (h_only && xo == XO_Q4) hipLaunchKernelGGL((k_q8k_rows_h<XO_Q4, float>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    else if (h_only) hipLaunchKernelGGL((k_q8k_rows_h<XO_Q6, float>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    else if (vec && xo == XO_Q4) hipLaunchKernelGGL((k_q8k_rows<true, XO_Q4, float>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
     else if (vec && xo == XO_Q6) hipLaunchKernelGGL((k_q8k_rows<true, XO_Q6, float>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
     else if (vec) hipLaunchKernelGGL((k_q8k_rows<true, XO_ANY, float>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
     else hipLaunchKernelGGL((k_q8k_rows<false, XO_ANY, float>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
@@ -230,7 +327,9 @@ int launch_q8k_rows(const _Float16 *src, int64_t ld, int64_t nrows, int64_t K, c
     const int64_t items = nrows * ((nb + 3) / 4);
     const dim3 grid((unsigned)((items + 4 * Q8_ITEMS - 1) / (4 * Q8_ITEMS)));
     const int xo = q8_xo(o);
-    if (xo == XO_Q4) hipLaunchKernelGGL((k_q8k_rows<true, XO_Q4, _Float16>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    if (q8_h_only(o, xo) && xo == XO_Q4) hipLaunchKernelGGL((k_q8k_rows_h<XO_Q4, _Float16>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    else if (q8_h_only(o, xo)) hipLaunchKernelGGL((k_q8k_rows_h<XO_Q6, _Float16>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
+    else if (xo == XO_Q4) hipLaunchKernelGGL((k_q8k_rows<true, XO_Q4, _Float16>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
     else if (xo == XO_Q6) hipLaunchKernelGGL((k_q8k_rows<true, XO_Q6, _Float16>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
     else hipLaunchKernelGGL((k_q8k_rows<true, XO_ANY, _Float16>), grid, dim3(256), 0, st, src, ld, nrows, nb, o);
     return hip_check_launch();

@@ -359,7 +359,7 @@ def config4_stack(n_layers: int = 24, T_prefill: int = 2048, n_decode: int = 256
                       "bytes_per_step": step_bytes, "GBs": step_bytes / (dec_ms * 1e-3) / 1e9,
                       "frac_hbm": step_bytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
                       "stream_ms_per_token": dec_ms_stream,
-                      "schedule": "per layer: the RMSNorm kernel, then the fused single-token kernel, plain launch"}}
+                      "schedule": "per layer: one fused single-token kernel (RMSNorm of the row inside it), plain launch"}}
     log(f"config 4: prefill {pre_ms:.2f} ms ({res['prefill']['tokens_per_s']:.0f} tok/s, "
         f"{res['prefill']['TFLOPs']:.0f} TFLOP/s), decode {dec_ms:.3f} ms/token "
         f"({res['decode']['GBs']:.0f} GB/s); issued kernel by kernel: prefill {pre_ms_stream:.2f} ms, "

@@ -213,8 +213,10 @@ int mi_moe_forward_noalloc(const mi_moe_layer *layer, const float *x, int64_t n_
  * out[t] = res[t] + MoE(norm(h[t])): the reference's ffn_norm followed by its
  * MoE block (moondream.cpp:405-407 + 509-547; qwen3omni_model.cpp:756-780),
  * in one call: the rows are normalized once into the context's workspace
- * (mi_moe_ctx_reserve sizes it), then the block runs on them.  Same results,
- * bit for bit, as mi_norm into a buffer followed by mi_moe_forward on it.  norm NULL or MI_NORM_NONE: mi_moe_forward.
+ * (mi_moe_ctx_reserve sizes it), then the block runs on them; a single token
+ * on the fused single-token kernel is normalized inside that kernel (no
+ * separate launch).  Same results, bit for bit, as mi_norm into a buffer
+ * followed by mi_moe_forward on it.  norm NULL or MI_NORM_NONE: mi_moe_forward.
  * D <= 4096 with a norm (MI_MOE_ERR_UNSUPPORTED beyond). */
 int mi_moe_forward_norm(mi_moe_ctx *ctx, const mi_moe_layer *layer, const mi_moe_norm *norm, const float *h,
                         int64_t n_tokens, const float *res, float *out, const mi_moe_routing *routing,

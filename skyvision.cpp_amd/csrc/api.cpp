@@ -261,7 +261,7 @@ bool plan_decode1(const mi_moe_ctx *c, const mi_moe_layer *L, const float *x, in
 }
 
 int run_decode1(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, const float *res, float *out, int P,
-                int C, hipStream_t st) {
+                int C, const NormParams &np, hipStream_t st) {
     DecArgs g = {};
     g.rw = L->router_w; g.rb = L->router_b; g.x = x;
     g.D = L->n_embd; g.E = L->n_expert; g.K = L->n_expert_used; g.I = L->n_ff;
@@ -275,6 +275,7 @@ int run_decode1(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, const floa
     g.xq = c->ax.q8; g.xd = c->ax.d8; g.xbs = c->ax.bs;
     g.actf = c->f1;
     g.tw = c->dec_tw; g.epoch = c->dec_epoch; g.err = c->dec_err; g.rescue_polls = c->dec_rescue_polls;
+    g.norm = np;
     TRY(launch_decode1(g, c->dec_grid, c->fused_decode == MI_DECODE_FUSED_COOPERATIVE, st));
     stage_end(c, "decode1", st);
     return MI_MOE_OK;
@@ -827,13 +828,14 @@ int mi_moe_ctx_stage_times(mi_moe_ctx *c, int max_stages, const char **names, fl
 
 namespace {
 
-// the forward with an optional norm of its input (np.kind != NORM_NONE): the
-// rows are normalized into the workspace once, then the forward runs as
-// usual.  (Applying the norm where the kernels read x was built and measured
-// slower: in the router launch each of a token slab's expert-tile
-// work-groups recomputed the rows' statistics before its chunk loop, config-4
-// prefill 9.96 vs 9.57 ms; in the single-token kernel the extra registers of
-// phase A cost more than the launch it saved, 0.675 vs 0.641 ms per step.)
+// the forward with an optional norm of its input (np.kind != NORM_NONE).  A
+// single token on the fused kernel normalizes x inside it (every work-group
+// computes the statistics in k_norm_rows' order while its router row loads
+// stream, and stages the normed row in LDS): no norm launch.  Otherwise the
+// rows are normalized into the workspace once and the forward runs as usual.
+// (Applying the norm where the prefill router reads x was built and measured
+// slower: each of a token slab's expert-tile work-groups recomputed the rows'
+// statistics before its chunk loop, config-4 prefill 9.96 vs 9.57 ms.)
 int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const float *res, float *out,
                  const mi_moe_routing *routing, const NormParams &np, hipStream_t st) {
     if (!c) return MI_MOE_ERR_NULL;
@@ -846,7 +848,9 @@ int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T
     if (np.kind != NORM_NONE && D > 4096) return MI_MOE_ERR_UNSUPPORTED;
     HIP_TRY(hipSetDevice(c->device));
     stage_begin(c, st);
-    if (np.kind != NORM_NONE) {
+    int P = 0, C = 0;
+    const bool dec1 = T == 1 && plan_decode1(c, L, x, P, C);
+    if (np.kind != NORM_NONE && !dec1) {
         TRY(launch_norm(np, x, T, D, c->xn, st));
         stage_end(c, "norm", st);
         x = c->xn;
@@ -857,10 +861,9 @@ int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T
         TRY(run_shared(c, L, x, T, st));
         add = c->sh_out;
     }
-    int P = 0, C = 0;
     int cc = 0;
-    if (T == 1 && plan_decode1(c, L, x, P, C)) {
-        TRY(run_decode1(c, L, x, res, out, P, C, st));
+    if (dec1) {
+        TRY(run_decode1(c, L, x, res, out, P, C, np, st));
     } else if (plan_decodeb(c, L, x, T, cc)) {
         TRY(run_decodeb(c, L, x, T, res, out, cc, st));
     } else {

@@ -415,7 +415,6 @@ __global__ void __launch_bounds__(256) k_quantize_q6_K(const float *__restrict__
 // fp64 over its pieces in k order, then a fixed LDS tree (128, 64, .. 1) over
 // the threads; LayerNorm's second sum reuses the held values.  y may equal x
 // (every value is in registers before the first store).
-constexpr int NORM_T = 256, NORM_PIECES = 4;   // 4096 / (4 * 256)
 
 __device__ inline double norm_block_sum(double v, double *red) {
     red[threadIdx.x] = v;

@@ -186,32 +186,37 @@ __device__ inline float as_float(uint32_t u) { return __builtin_bit_cast(float, 
 // ---------------------------------------------------------------- phase A
 // logit of expert e: the router's fixed fp64 order (64-wide chunk c: sum over
 // s = 0..15, g = 0..3 of W[64c+16g+s] * x[64c+16g+s]; chunk partials added in
-// chunk order from 0.0; fl32; + bias in fp32).  Lane c owns chunk c.
-__device__ inline float dec_router_row(const DecArgs &g, int e, int lane) {
+// chunk order from 0.0; fl32; + bias in fp32).  Lane c owns chunk c.  The
+// row's loads are issued first (dec_row_issue) so that they stream while the
+// WG normalizes x (mi_moe_forward_norm); x then comes from the staged normed
+// row sxn in LDS (chunk c's float4 q at slot ax_slot(c, q): 16 lanes reading
+// chunks c .. c + 15 hit 16 different slots), else from global memory.
+__device__ inline int ax_slot(int c, int q) { return 16 * c + ((q + c) & 15); }
+__device__ inline void dec_row_issue(const DecArgs &g, int e, int lane, float4_t (&w)[16]) {
     const int D = g.D;
-    const int nch = (D + 63) >> 6;
+    if (64 * lane + 64 <= D) {
+        const float *wr = g.rw + (int64_t)e * D + 64 * lane;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) w[q] = *(const float4_t *)(wr + 4 * q);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) w[q] = float4_t{0.f, 0.f, 0.f, 0.f};
+    }
+}
+__device__ inline float dec_row_finish(const DecArgs &g, int e, int lane, const float4_t (&w)[16],
+                                       const float4_t *sxn) {
+    const int D = g.D;
+    const int nch = D >> 6;   // D is a multiple of 256
     double part = 0.0;
     if (lane < nch) {
-        const float *xr = g.x + 64 * lane;
-        const float *wr = g.rw + (int64_t)e * D + 64 * lane;
         float xv[64], wv[64];
-        if (64 * lane + 64 <= D) {
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const float4_t a = *(const float4_t *)(xr + 4 * q);
-                const float4_t b = *(const float4_t *)(wr + 4 * q);
+        for (int q = 0; q < 16; ++q) {
+            const float4_t a = sxn ? sxn[ax_slot(lane, q)] : *(const float4_t *)(g.x + 64 * lane + 4 * q);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    xv[4 * q + j] = a[j];
-                    wv[4 * q + j] = b[j];
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 64; ++i) {
-                const bool ok = 64 * lane + i < D;
-                xv[i] = ok ? xr[i] : 0.f;
-                wv[i] = ok ? wr[i] : 0.f;
+            for (int j = 0; j < 4; ++j) {
+                xv[4 * q + j] = a[j];
+                wv[4 * q + j] = w[q][j];
             }
         }
 #pragma unroll
@@ -234,9 +239,9 @@ __device__ inline float dec_router_row(const DecArgs &g, int e, int lane) {
 }
 
 // Q8_K of x block b (natural order, ggml block_q8_K fields split), written
-// through for the other WGs
-__device__ inline void dec_q8k_x(const DecArgs &g, int b, int lane) {
-    const float4_t xv = *(const float4_t *)(g.x + b * QK + 4 * lane);
+// through for the other WGs; x from the staged normed row when there is one
+__device__ inline void dec_q8k_x(const DecArgs &g, int b, int lane, const float4_t *sxn) {
+    const float4_t xv = sxn ? sxn[ax_slot(4 * b + (lane >> 4), lane & 15)] : *(const float4_t *)(g.x + b * QK + 4 * lane);
     const float v[4] = {xv[0], xv[1], xv[2], xv[3]};
     int q[4];
     const float d = q8k_wave(v, lane, q);
@@ -248,6 +253,96 @@ __device__ inline void dec_q8k_x(const DecArgs &g, int b, int lane) {
     if ((lane & 7) == 0)
         st_dev4(g.xbs, 2u * (b * 16 + (lane >> 2)),
                 (uint32_t)(uint16_t)(int16_t)s | ((uint32_t)(uint16_t)(int16_t)s_hi << 16));
+}
+
+// Sum of the NORM_T partials held by threads T0 .. T0 + NORM_T - 1 of the WG
+// (v of the others is ignored), paired as k_norm_rows pairs them: red[t] +=
+// red[t + o] for o = NORM_T / 2 .. 1 (two levels through LDS, the rest by lane
+// shifts in one wave; fp64 addition is commutative, so the bits agree).
+// Every thread gets the sum; LDS-only barriers (loads in flight stay so).
+template <int T0>
+__device__ inline double dec_sum_norm(double v, double *red, double *s_sum) {
+    const int t = (int)threadIdx.x - T0;
+    if (t >= 0 && t < NORM_T) red[t] = v;
+    dec_lds_barrier();
+    if (t >= 0 && t < NORM_T / 2) red[t] = red[t] + red[t + NORM_T / 2];
+    dec_lds_barrier();
+    if (t >= 0 && t < NORM_T / 4) {
+        double r = red[t] + red[t + NORM_T / 4];   // one wave: lanes t < 64
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint64_t rb = __builtin_bit_cast(uint64_t, r);
+            const uint64_t nb = ((uint64_t)(uint32_t)__shfl_down((int)(rb >> 32), o, 64) << 32) |
+                                (uint32_t)__shfl_down((int)(uint32_t)rb, o, 64);
+            r = r + __builtin_bit_cast(double, nb);
+        }
+        if (t == 0) *s_sum = r;
+    }
+    dec_lds_barrier();
+    return *s_sum;
+}
+
+// The norm of x (mi_moe_forward_norm) inside the kernel: threads DEC_NORM_T0
+// .. + NORM_T - 1 load x, compute the statistics in k_norm_rows' order and
+// stage the normed row (norm_apply: the same roundings) into sxn; every
+// thread of the WG takes part in the barriers.  Bit for bit the row mi_norm
+// writes.
+constexpr int DEC_NORM_T0 = 256;   // waves 4-7: wave 0 has its router row loads in flight
+__device__ inline void dec_norm_stage(const DecArgs &g, float4_t *sxn, double *red, double *s_sum) {
+    const NormParams &p = g.norm;
+    const int D = g.D, t = (int)threadIdx.x - DEC_NORM_T0;
+    const bool on = t >= 0 && t < NORM_T;
+    float v[NORM_PIECES][4];
+#pragma unroll
+    for (int k = 0; k < NORM_PIECES; ++k) {
+        const int i = 1024 * k + 4 * t;
+        if (on && i < D) {
+            const float4_t a = *(const float4_t *)(g.x + i);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[k][j] = a[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[k][j] = 0.f;
+        }
+    }
+    float m = 0.f, sc;
+    double acc = 0.0;
+    if (p.kind == NORM_RMS) {
+#pragma unroll
+        for (int k = 0; k < NORM_PIECES; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = acc + (double)(v[k][j] * v[k][j]);
+        const float ms = (float)(dec_sum_norm<DEC_NORM_T0>(acc, red, s_sum) / (double)D);
+        sc = 1.0f / sqrtf(ms + p.eps);
+    } else {
+#pragma unroll
+        for (int k = 0; k < NORM_PIECES; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = acc + (double)v[k][j];
+        m = (float)(dec_sum_norm<DEC_NORM_T0>(acc, red, s_sum) / (double)D);
+        double acc2 = 0.0;
+#pragma unroll
+        for (int k = 0; k < NORM_PIECES; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (1024 * k + 4 * t + j < D) {
+                    const float d = v[k][j] - m;
+                    acc2 = acc2 + (double)(d * d);
+                }
+        const float var = (float)(dec_sum_norm<DEC_NORM_T0>(acc2, red, s_sum) / (double)D);
+        sc = 1.0f / sqrtf(var + p.eps);
+    }
+#pragma unroll
+    for (int k = 0; k < NORM_PIECES; ++k) {
+        const int i = 1024 * k + 4 * t;
+        if (on && i < D) {
+            float4_t o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = norm_apply(p, v[k][j], i + j, m, sc);
+            sxn[ax_slot(i >> 6, (i & 63) >> 2)] = o;
+        }
+    }
+    dec_lds_barrier();
 }
 
 // ---------------------------------------------------------------- dots
@@ -464,6 +559,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
     __shared__ float s_z[DEC_KMAX * DEC_CMAX];
     __shared__ int s_list[DEC_MAX_GRID];   // units still missing after a poll
     __shared__ int s_fail, s_nmiss, s_flag, s_wmiss[DEC_WAVES];
+    __shared__ double s_red[NORM_T], s_nsum;   // norm of x
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -480,10 +576,19 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
     const float resv = (do_c && tid < C && g.res) ? g.res[n0 + tid] : 0.f;
 
     // ---- A: router row wg (wave 0) and Q8_K of x block wg (wave 1); the
-    // logit is published only once this WG's Q8_K of x is out
+    // logit is published only once this WG's Q8_K of x is out.  With a norm of
+    // x, every WG first normalizes x into LDS (s_dn: phase B parks down rows
+    // there later) while wave 0's row loads stream.
+    float4_t wrow[16];
+    if (wave == 0 && wg < E) dec_row_issue(g, wg, lane, wrow);
+    const float4_t *sxn = nullptr;
+    if (g.norm.kind != NORM_NONE) {
+        dec_norm_stage(g, (float4_t *)&s_dn[0][0], s_red, &s_nsum);
+        sxn = (const float4_t *)&s_dn[0][0];
+    }
     float logit = 0.f;
-    if (wave == 0 && wg < E) logit = dec_router_row(g, wg, lane);
-    else if (wave == 1 && wg < NB) dec_q8k_x(g, wg, lane);
+    if (wave == 0 && wg < E) logit = dec_row_finish(g, wg, lane, wrow, sxn);
+    else if (wave == 1 && wg < NB) dec_q8k_x(g, wg, lane, sxn);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     dec_lds_barrier();
     if (wave == 0 && lane == 0 && wg < E) tw_store(g.tw + DEC_TW_LOGIT + wg, tag, __builtin_bit_cast(uint32_t, logit));
@@ -510,8 +615,10 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
         }
         for (int m = wave; m < nmiss; m += DEC_WAVES) {
             const int a = __builtin_amdgcn_readfirstlane(s_list[m]);
-            if (a < NB) dec_q8k_x(g, a, lane);
-            const float lv = dec_router_row(g, a, lane);
+            if (a < NB) dec_q8k_x(g, a, lane, sxn);
+            float4_t wr[16];
+            dec_row_issue(g, a, lane, wr);
+            const float lv = dec_row_finish(g, a, lane, wr, sxn);
             __builtin_amdgcn_s_waitcnt(0x0F70);   // the x block is out before the logit
             if (lane == 0) tw_store(g.tw + DEC_TW_LOGIT + a, tag, __builtin_bit_cast(uint32_t, lv));
         }

@@ -214,6 +214,7 @@ struct DecArgs {
     uint32_t *epoch;              // [grid] per-WG launch epochs
     unsigned *err;                // set when a wait gave up (output is NaN)
     unsigned rescue_polls;        // polls for another WG's unit before computing it here
+    NormParams norm;              // k_decode1: the norm of x applied in the kernel (kind NORM_NONE: x as given)
 };
 constexpr int DEC_MAX_GRID = 1024;
 constexpr int DEC_TW_LOGIT = 0, DEC_TW_BDONE = 256, DEC_TW_REL = 256 + DEC_MAX_GRID;

@@ -18,6 +18,12 @@ namespace mimoe {
 
 enum { NORM_NONE = 0, NORM_RMS = 1, NORM_LAYER = 2 };
 
+// k_norm_rows' fixed summation order (also run inside the fused single-token
+// kernel): thread t < NORM_T holds elements 1024 k + 4 t + j (k < NORM_PIECES,
+// j < 4), sums them in that order in fp64, and the NORM_T partials are added
+// pairwise, red[t] += red[t + o] for o = NORM_T / 2 .. 1.
+constexpr int NORM_T = 256, NORM_PIECES = 4;   // rows up to 4096
+
 struct NormParams {
     int kind = NORM_NONE;
     float eps = 0.f;

@@ -1340,13 +1340,24 @@ __global__ void __launch_bounds__(DECB_THREADS) k_decodeb(DecArgs g) {
 
     // ---- every A word (the logits travel in them); missing units computed here
     ok = wait_words(UA, [&](int i) { return i; }, [&](int u) { decb_unit_a(g, tag, u, lane); });
-    for (int i = tid; i < E * T; i += DECB_THREADS) s_logit[i] = as_float((uint32_t)tw_load(g.tw2 + i));
-    // x's Q8_K for every token (coherent loads: other WGs wrote it) goes out
-    // now and lands in LDS after the ranking
+    // the logits and x's Q8_K for every token (coherent loads: other WGs wrote
+    // them): every load goes out at once (one memory round trip, not one per
+    // array); the logits land in LDS now, the codes after the ranking
+    constexpr int LG_PER = DECB_T_MAX * 256 / DECB_THREADS;                      // logit words per thread
     constexpr int XQ_PER = DECB_T_MAX * DECB_NB_MAX * QK / 16 / DECB_THREADS;   // 16-byte pieces per thread
+    constexpr int XB_PER = (DECB_T_MAX * DECB_NB_MAX * 8 + DECB_THREADS - 1) / DECB_THREADS;   // block-sum words
+    static_assert(DECB_T_MAX * DECB_NB_MAX <= DECB_THREADS, "one scale per thread");
+    uint64_t lgv[LG_PER];
     u32x4 xqv[XQ_PER];
-    const int nxq = T * D / 16;
+    uint32_t xbv[XB_PER];
+    float xdv = 0.f;
+    const int nxq = T * D / 16, nxb = T * (D / 16) / 2;
     {
+#pragma unroll
+        for (int j = 0; j < LG_PER; ++j) {
+            const int i = tid + j * DECB_THREADS;
+            if (i < E * T) lgv[j] = tw_load(g.tw2 + i);
+        }
         const auto rq = co_rsrc(g.xq, (uint32_t)(T * D));
 #pragma unroll
         for (int j = 0; j < XQ_PER; ++j) {
@@ -1354,12 +1365,26 @@ __global__ void __launch_bounds__(DECB_THREADS) k_decodeb(DecArgs g) {
             if (i < nxq) xqv[j] = co_ld16(rq, 16u * (uint32_t)i);
         }
         const auto rd = co_rsrc(g.xd, (uint32_t)(4 * T * NB));
-        for (int i = tid; i < T * NB; i += DECB_THREADS) s_xd[i] = as_float(co_ld4(rd, 4u * (uint32_t)i));
+        if (tid < T * NB) xdv = as_float(co_ld4(rd, 4u * (uint32_t)tid));
         const auto rb = co_rsrc(g.xbs, (uint32_t)(2 * T * (D / 16)));
-        for (int i = tid; i < T * (D / 16) / 2; i += DECB_THREADS) {
-            const uint32_t v = co_ld4(rb, 4u * (uint32_t)i);
-            s_xbs[2 * i] = (int16_t)(uint16_t)(v & 0xffffu);
-            s_xbs[2 * i + 1] = (int16_t)(uint16_t)(v >> 16);
+#pragma unroll
+        for (int j = 0; j < XB_PER; ++j) {
+            const int i = tid + j * DECB_THREADS;
+            if (i < nxb) xbv[j] = co_ld4(rb, 4u * (uint32_t)i);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < LG_PER; ++j) {
+        const int i = tid + j * DECB_THREADS;
+        if (i < E * T) s_logit[i] = as_float((uint32_t)lgv[j]);
+    }
+    if (tid < T * NB) s_xd[tid] = xdv;
+#pragma unroll
+    for (int j = 0; j < XB_PER; ++j) {
+        const int i = tid + j * DECB_THREADS;
+        if (i < nxb) {
+            s_xbs[2 * i] = (int16_t)(uint16_t)(xbv[j] & 0xffffu);
+            s_xbs[2 * i + 1] = (int16_t)(uint16_t)(xbv[j] >> 16);
         }
     }
     for (int e = tid; e < E; e += DECB_THREADS) {
@@ -1465,6 +1490,21 @@ __global__ void __launch_bounds__(DECB_THREADS) k_decodeb(DecArgs g) {
     const int UCT = D / CC, UC = T * UCT;
     for (int cu = wg; cu < UC; cu += G) {
         const int t = cu / UCT, n0 = (cu - t * UCT) * CC;
+        // wave k's down rows (slot k's expert, columns n0 ..): passes of 8
+        // rows, the loads AH passes ahead of the dots, as deep as the
+        // registers allow without spilling (Q6_K's raw bytes of a pass take 56
+        // registers at I = 1024).  The expert is known since the ranking, so
+        // the first AH passes go out before the wait for the B words below.
+        constexpr int AH = DT == 12 ? (NBI <= 3 ? 2 : 1) : 0;
+        const int npass = CC / 8;
+        const int rs = lane >> 3, sl = lane & 7;
+        const int e_dn = wave < K ? s_sel[t * K + wave] : 0;
+        DecBDn<DT> rb[AH + 1];
+        if (wave < K) {
+#pragma unroll
+            for (int a = 0; a < AH; ++a)
+                if (a < npass) decb_dn_load<DT, NBI>(g.down, e_dn, n0 + 8 * a + rs, sl, rb[a]);
+        }
         // the B words of the token's K experts
         if (ok)
             ok = wait_words(K * QB, [&](int i) { return UA + s_pd[t * K + i / QB] * QB + i % QB; },
@@ -1497,21 +1537,11 @@ __global__ void __launch_bounds__(DECB_THREADS) k_decodeb(DecArgs g) {
                 if (seg == 0) s_ad[k][b] = dq;
             }
             wave_lds_sync();
-            const int e = s_sel[p], rs = lane >> 3, sl = lane & 7;
-            // passes of 8 rows, the loads AH passes ahead of the dots, as deep
-            // as the registers allow without spilling (Q6_K's raw bytes of a
-            // pass take 56 registers at I = 1024)
-            constexpr int AH = DT == 12 ? (NBI <= 3 ? 2 : 1) : 0;
-            const int npass = CC / 8;
-            DecBDn<DT> rb[AH + 1];
-#pragma unroll
-            for (int a = 0; a < AH; ++a)
-                if (a < npass) decb_dn_load<DT, NBI>(g.down, e, n0 + 8 * a + rs, sl, rb[a]);
             // a rolled loop (the buffers rotate by copies): unrolled, the
             // scheduler would hoist every pass's loads
 #pragma unroll 1
             for (int ps = 0; ps < npass; ++ps) {
-                if (ps + AH < npass) decb_dn_load<DT, NBI>(g.down, e, n0 + 8 * (ps + AH) + rs, sl, rb[AH]);
+                if (ps + AH < npass) decb_dn_load<DT, NBI>(g.down, e_dn, n0 + 8 * (ps + AH) + rs, sl, rb[AH]);
                 float z = decb_dn_dot<DT, NBI>(rb[0], sl, s_aq[k], s_ad[k], s_abs[k]);
                 z = decb_sum8(z);
                 if (sl == 0) s_z[k][8 * ps + rs] = z;

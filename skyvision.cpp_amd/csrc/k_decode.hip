@@ -1335,8 +1335,9 @@ __global__ void __launch_bounds__(DECB_THREADS) k_decodeb(DecArgs g) {
     if (wg == 0 && tid <= DEC_MAX_GRID / DEC_GROUP)
         __hip_atomic_store(dec_cnt(g.tw, tag + 1u, tid), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-    // ---- A: router rows and Q8_K of x, by waves
-    for (int u = gw; u < UA; u += NW) decb_unit_a(g, tag, u, lane);
+    // ---- A: router rows and Q8_K of x, by waves, dealt across the WGs first
+    // (unit u to wave u / G of WG u % G): every CU takes about UA / G of them
+    for (int u = wave * G + wg; u < UA; u += NW) decb_unit_a(g, tag, u, lane);
 
     // ---- every A word (the logits travel in them); missing units computed here
     ok = wait_words(UA, [&](int i) { return i; }, [&](int u) { decb_unit_a(g, tag, u, lane); });

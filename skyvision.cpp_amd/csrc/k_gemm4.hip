@@ -77,7 +77,8 @@ __device__ inline rsrc_t g4_rsrc(const void *p, int64_t nbytes) {
 // Prologue order (each step one memory round trip): the tile's descriptor
 // (expert, first row in perm, rows) and n_tiles together; then the rows'
 // slot indices (perm) with the block-0 weight loads issued right behind
-// them (they need only the expert); then the block-0 activation loads.
+// them (they need only the expert); then, once the slot indices are in, the
+// block-0 activation loads, while the weight loads are still landing.
 struct G4Tile {
     int e, start, mrows, nrt;
     bool live;   // tile < n_tiles (the grid is rounded up to whole XCD rounds)
@@ -103,10 +104,16 @@ __device__ __forceinline__ int g4_rows_load(const G2Args &g, const G4Tile &t) {
     return (int)threadIdx.x < t.mrows ? g.perm[t.start + threadIdx.x] : -1;
 }
 
-// the rows' activation row indices to s_arow (row 0 past the tile)
+// the rows' activation row indices to s_arow (row 0 past the tile), then a
+// barrier that waits only for LDS: the block-0 weight loads issued before
+// stay in flight, so the K loop's first activation loads go out while they
+// land (__syncthreads would wait for them, vmcnt(0): one more round trip
+// before the first MFMA).  The asm memory clobber keeps the compiler from
+// moving memory accesses across the barrier.
 __device__ __forceinline__ void g4_rows_publish(const G2Args &g, int p, int *s_arow) {
     if (threadIdx.x < G4_BM) s_arow[threadIdx.x] = p < 0 ? 0 : (g.ne11 == 1 ? p / g.K : p);
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
 }
 
 // after the K loop (every load of this wave landed): the rows' slot indices

@@ -82,6 +82,17 @@ __device__ __host__ inline uint32_t f32_to_fp16_bits(float f) {
 // hardware conversion for hot paths (exact for normal and subnormal fp16)
 __device__ inline float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
+// Work-group barrier for LDS hand-offs: this wave's LDS accesses complete,
+// then s_barrier.  Outstanding global loads and stores stay in flight
+// (__syncthreads also waits for them, vmcnt(0), which costs a memory round
+// trip where a kernel has just issued loads or stores it does not need yet).
+// The asm memory clobber keeps the compiler from moving memory accesses across
+// the barrier.  Not for global data that other threads of the work-group read.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+}
+
 __device__ __host__ inline int imin(int a, int b) { return a < b ? a : b; }
 __device__ __host__ inline int imax(int a, int b) { return a > b ? a : b; }
 

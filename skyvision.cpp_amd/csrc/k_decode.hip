@@ -101,10 +101,7 @@ __device__ inline bool tw_wait1(const uint64_t *p, uint32_t tag, unsigned limit,
 }
 
 // workgroup barrier that does not wait for outstanding global loads / DMA
-__device__ inline void dec_lds_barrier() {
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-    asm volatile("s_barrier" ::: "memory");
-}
+__device__ inline void dec_lds_barrier() { lds_barrier(); }
 
 // Completion counters of the gate/up units, in two levels so that no word
 // takes more than 16 atomic adds: unit u's owner adds 1 to group u / 16 once

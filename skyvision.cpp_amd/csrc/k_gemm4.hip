@@ -107,13 +107,11 @@ __device__ __forceinline__ int g4_rows_load(const G2Args &g, const G4Tile &t) {
 // the rows' activation row indices to s_arow (row 0 past the tile), then a
 // barrier that waits only for LDS: the block-0 weight loads issued before
 // stay in flight, so the K loop's first activation loads go out while they
-// land (__syncthreads would wait for them, vmcnt(0): one more round trip
-// before the first MFMA).  The asm memory clobber keeps the compiler from
-// moving memory accesses across the barrier.
+// land (__syncthreads would wait for them: one more round trip before the
+// first MFMA)
 __device__ __forceinline__ void g4_rows_publish(const G2Args &g, int p, int *s_arow) {
     if (threadIdx.x < G4_BM) s_arow[threadIdx.x] = p < 0 ? 0 : (g.ne11 == 1 ? p / g.K : p);
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-    asm volatile("s_barrier" ::: "memory");
+    lds_barrier();
 }
 
 // after the K loop (every load of this wave landed): the rows' slot indices

@@ -513,9 +513,6 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-sweeps", action="store_true",
                     help="skip the config-3 batched-decode sweep and the config-4 layer stack")
-    ap.add_argument("--no-coop", action="store_true",
-                    help="skip timing the cooperative-launch decode schedule (rocprofv3 cannot "
-                         "write its results after a cooperative launch on this image)")
     ap.add_argument("--cpu-tokens", type=int, default=1024,
                     help="tokens of the CPU baseline sample (default: the whole config-1 batch)")
     ap.add_argument("--calib-copy", action="store_true",
@@ -571,16 +568,13 @@ def main() -> int:
         dl = [W.GpuLayer(dctx, dspec, copy=c) for c in range(args.copies)]
         dx = [W.gen_x(dctx, dspec, 1, copy=c) for c in range(args.copies)]
         dout = M.DeviceBuffer(4 * dspec.D)
-        # fused single-token kernel, plain launch (the GPU runs nothing else
-        # here); the cooperative launch is timed beside it
+        # fused single-token kernel, plain launch; the kernel chain is timed
+        # beside it
         dctx.set_fused_decode(M.DECODE_FUSED)
         dms, _ = time_layer(dctx, dl, dx, 1, dout, 200, 20)
         _, dst = time_layer(dctx, dl, dx, 1, dout, 50, 5, profile=True)
         modes = {}
-        other = [("chain", M.DECODE_CHAIN)]
-        if not args.no_coop:
-            other.insert(0, ("fused_cooperative", M.DECODE_FUSED_COOPERATIVE))
-        for mname, mode in other:
+        for mname, mode in [("chain", M.DECODE_CHAIN)]:
             dctx.set_fused_decode(mode)
             modes[mname] = time_layer(dctx, dl, dx, 1, dout, 200, 20)[0]
         dctx.set_fused_decode(M.DECODE_FUSED)

@@ -327,21 +327,21 @@ int mi_moe_ctx_stage_clock(mi_moe_ctx *ctx, const char *stage, double *ghz, int 
  * GEMM when 4 * T * K > 5 * E (more than 1.25 dispatched rows per expert). */
 int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *ctx, int64_t min_tokens_for_gemm);
 /* Schedule of decode calls of mi_moe_forward (1 token, and batches of 2..16
- * tokens).  The fused modes run the whole block in one kernel of one
+ * tokens).  The fused mode runs the whole block in one kernel of one
  * work-group per CU, when the layer fits it (Q4_K gate/up, Q4_K or Q6_K down,
  * top-k <= 8, default gating, no shared expert, 16-byte aligned tables; for
  * batches also n_embd <= 2048 and n_ff <= 1024); other layers and larger
- * batches use the chain.  Batches of 2..16 tokens always take the plain
- * launch.  Inside the kernel, work-groups hand each other
+ * batches use the chain.  Inside the kernel, work-groups hand each other
  * the router logits and the gate/up activations through completion words;
  * a work-group that does not see a result after a bounded number of polls
  * computes it itself (the same bits), so the kernel needs no co-residency
  * guarantee and cannot deadlock on a GPU shared with other work.
  *   MI_DECODE_CHAIN              separate kernels
- *   MI_DECODE_FUSED_COOPERATIVE  fused, cooperative launch (~18 us more per
- *                                call on MI355X: the runtime's cooperative
- *                                queue)
  *   MI_DECODE_FUSED              fused, plain launch (default)
+ *   MI_DECODE_FUSED_COOPERATIVE  retired (MI_MOE_ERR_UNSUPPORTED): the fused
+ *                                kernel through hipLaunchCooperativeKernel,
+ *                                ~18 us slower per call on MI355X than the
+ *                                plain launch, which needs no co-residency
  * MI_DECODE_FUSED_EXCLUSIVE is the former name of MI_DECODE_FUSED.
  * Same results in every mode; the reference has one graph per step
  * (moe_decode_driver.hpp:493-514), this only picks the GPU schedule. */

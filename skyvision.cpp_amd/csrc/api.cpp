@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -108,7 +109,7 @@ struct mi_moe_ctx {
     int64_t gemm_threshold = 0;   // 0: the shape rule of use_gemm
     // single-token fused kernel (k_decode.hip)
     int fused_decode = MI_DECODE_FUSED;
-    int dec_grid = 0;          // cooperative grid (one WG per CU), 0: unavailable
+    int dec_grid = 0;          // fused decode grid (one WG per CU), 0: unavailable
     uint64_t *dec_tw = nullptr;
     uint32_t *dec_epoch = nullptr;
     unsigned dec_rescue_polls = DEC_RESCUE_POLLS;
@@ -276,7 +277,7 @@ int run_decode1(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, const floa
     g.actf = c->f1;
     g.tw = c->dec_tw; g.epoch = c->dec_epoch; g.err = c->dec_err; g.rescue_polls = c->dec_rescue_polls;
     g.norm = np;
-    TRY(launch_decode1(g, c->dec_grid, c->fused_decode == MI_DECODE_FUSED_COOPERATIVE, st));
+    TRY(launch_decode1(g, c->dec_grid, st));
     stage_end(c, "decode1", st);
     return MI_MOE_OK;
 }
@@ -755,6 +756,7 @@ int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *c, int64_t t) {
 int mi_moe_ctx_set_fused_decode(mi_moe_ctx *c, int on) {
     if (!c) return MI_MOE_ERR_NULL;
     if (on < MI_DECODE_CHAIN || on > MI_DECODE_FUSED) return MI_MOE_ERR_ARG;
+    if (on == MI_DECODE_FUSED_COOPERATIVE) return MI_MOE_ERR_UNSUPPORTED;   // retired: the plain launch is faster
     c->fused_decode = on;
     return MI_MOE_OK;
 }
@@ -850,7 +852,12 @@ int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T
     stage_begin(c, st);
     int P = 0, C = 0;
     const bool dec1 = T == 1 && plan_decode1(c, L, x, P, C);
-    if (np.kind != NORM_NONE && !dec1) {
+    // The single-token kernel normalizes x itself only when out does not
+    // overlap x: a work-group that computes a late router row or Q8_K block
+    // re-reads x, possibly after other work-groups wrote their out columns.
+    const uintptr_t xb = (uintptr_t)x, ob = (uintptr_t)out, row = sizeof(float) * (uintptr_t)D;
+    const bool fuse_norm = dec1 && np.kind != NORM_NONE && (ob + row <= xb || xb + row <= ob);
+    if (np.kind != NORM_NONE && !fuse_norm) {
         TRY(launch_norm(np, x, T, D, c->xn, st));
         stage_end(c, "norm", st);
         x = c->xn;
@@ -863,7 +870,7 @@ int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T
     }
     int cc = 0;
     if (dec1) {
-        TRY(run_decode1(c, L, x, res, out, P, C, np, st));
+        TRY(run_decode1(c, L, x, res, out, P, C, fuse_norm ? np : NormParams{}, st));
     } else if (plan_decodeb(c, L, x, T, cc)) {
         TRY(run_decodeb(c, L, x, T, res, out, cc, st));
     } else {
@@ -942,8 +949,8 @@ static_assert(NA_BYTES == 16986368, "mi_moe.h states the no-allocation workspace
 constexpr int NA_MAX_DEVICES = 64;
 
 struct NoallocDevice {
-    std::once_flag once;
-    int status = MI_MOE_OK;
+    std::mutex mu;
+    std::atomic<bool> ready{false};
     mi_moe_ctx ctx;   // workspace pointers into this device's scratch; never destroyed
 };
 NoallocDevice g_noalloc[NA_MAX_DEVICES];
@@ -957,25 +964,24 @@ int noalloc_ctx(mi_moe_ctx **out) {
     HIP_TRY(hipGetDevice(&dev));
     if (dev < 0 || dev >= NA_MAX_DEVICES) return MI_MOE_ERR_DEVICE;
     NoallocDevice &d = g_noalloc[dev];
-    std::call_once(d.once, [&d, dev] {
-        void *ptr = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || !ptr) {
-            d.status = e != hipSuccess ? record_hip_error(e) : MI_MOE_ERR_HIP;
-            return;
+    if (!d.ready.load(std::memory_order_acquire)) {
+        // set-up once per device; a failed lookup is not cached, the next call tries again
+        std::lock_guard<std::mutex> lock(d.mu);
+        if (!d.ready.load(std::memory_order_relaxed)) {
+            void *ptr = nullptr;
+            const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return record_hip_error(e);
+            if (!ptr) return MI_MOE_ERR_HIP;
+            mi_moe_ctx &c = d.ctx;
+            c.device = dev;
+            c.fused_decode = MI_DECODE_CHAIN;
+            c.ws = nullptr;   // not owned
+            c.ws_bytes = NA_BYTES;
+            if (!carve_workspace(&c, (char *)ptr, NA_T, NA_D, NA_I, NA_E, NA_K)) return MI_MOE_ERR_UNSUPPORTED;
+            c.reserved = true;
+            d.ready.store(true, std::memory_order_release);
         }
-        mi_moe_ctx &c = d.ctx;
-        c.device = dev;
-        c.fused_decode = MI_DECODE_CHAIN;
-        c.ws = nullptr;   // not owned
-        c.ws_bytes = NA_BYTES;
-        if (!carve_workspace(&c, (char *)ptr, NA_T, NA_D, NA_I, NA_E, NA_K)) {
-            d.status = MI_MOE_ERR_UNSUPPORTED;
-            return;
-        }
-        c.reserved = true;
-    });
-    if (d.status) return d.status;
+    }
     *out = &d.ctx;
     return MI_MOE_OK;
 }

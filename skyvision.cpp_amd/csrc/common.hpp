@@ -93,6 +93,14 @@ __device__ inline void lds_barrier() {
     asm volatile("s_barrier" ::: "memory");
 }
 
+// This wave's global loads and stores complete (vmcnt(0); on gfx9 the
+// counter covers stores too), as an asm statement with a memory clobber: the
+// compiler neither sinks earlier memory accesses below it nor hoists later
+// ones above it (__builtin_amdgcn_s_waitcnt alone is not a compiler barrier).
+// A completion word stored after it is seen only after the data stored
+// before it.
+__device__ inline void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 __device__ __host__ inline int imin(int a, int b) { return a < b ? a : b; }
 __device__ __host__ inline int imax(int a, int b) { return a > b ? a : b; }
 

@@ -586,7 +586,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
     float logit = 0.f;
     if (wave == 0 && wg < E) logit = dec_row_finish(g, wg, lane, wrow, sxn);
     else if (wave == 1 && wg < NB) dec_q8k_x(g, wg, lane, sxn);
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    vm_drain();
     dec_lds_barrier();
     if (wave == 0 && lane == 0 && wg < E) tw_store(g.tw + DEC_TW_LOGIT + wg, tag, __builtin_bit_cast(uint32_t, logit));
     if (wg == 0 && tid <= DEC_MAX_GRID / DEC_GROUP)
@@ -616,7 +616,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
             float4_t wr[16];
             dec_row_issue(g, a, lane, wr);
             const float lv = dec_row_finish(g, a, lane, wr, sxn);
-            __builtin_amdgcn_s_waitcnt(0x0F70);   // the x block is out before the logit
+            vm_drain();   // the x block is out before the logit
             if (lane == 0) tw_store(g.tw + DEC_TW_LOGIT + a, tag, __builtin_bit_cast(uint32_t, lv));
         }
     }
@@ -720,7 +720,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode1(DecArgs g) {
         if (tid < P)
             st_dev4(g.actf, 4u * (uint32_t)(q + tid), __builtin_bit_cast(uint32_t, act_pair(g.act, s_hg[tid], s_hg[P + tid])));
         if (wave == 0) {
-            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+            vm_drain();
             if (lane == 0) {
                 tw_store(g.tw + DEC_TW_BDONE + u, tag, 1u);
                 if (owner) dec_cnt_unit(g.tw, tag, u, UB);
@@ -1023,7 +1023,7 @@ __device__ inline void decb_unit_a(const DecArgs &g, uint32_t tag, int u, int la
     } else {
         const int v = u - E * T, t = v / NB, b = v - t * NB;
         decb_q8k_x(g, t, b, lane);
-        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the block is out before its word
+        vm_drain();   // the block is out before its word
         if (lane == 0) tw_store(g.tw2 + u, tag, 1u);
     }
 }
@@ -1287,7 +1287,7 @@ __global__ void __launch_bounds__(DECB_THREADS) k_decodeb(DecArgs g) {
         DecBW w;
         decb_b_load<NB>(g, s_dist[d], q, lane, w);
         decb_b_compute<NB>(g, X, s_dcnt, s_dpair, d, q, lane, w);
-        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the activations are out before the word
+        vm_drain();   // the activations are out before the word
         if (lane == 0) tw_store(g.tw2 + UA + ub, tag, 1u);
     };
 
@@ -1477,7 +1477,7 @@ __global__ void __launch_bounds__(DECB_THREADS) k_decodeb(DecArgs g) {
             if (un < UB) decb_b_load<NB>(g, s_dist[un / QB], un % QB, lane, wn);
             const int d = u / QB, q = u - d * QB;
             decb_b_compute<NB>(g, X, s_dcnt, s_dpair, d, q, lane, wc);
-            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): activations (and the next loads) are in
+            vm_drain();   // activations (and the next loads) are in
             if (lane == 0) tw_store(g.tw2 + UA + u, tag, 1u);
             wc = wn;
         }
@@ -1616,14 +1616,12 @@ static const void *decode1_fn(int nbi) {
     }
 }
 
-int launch_decode1(const DecArgs &g, int grid, bool cooperative, hipStream_t st) {
+int launch_decode1(const DecArgs &g, int grid, hipStream_t st) {
     const int nbi = g.I / QK;
     const void *fn = g.down.type == 12 ? decode1_fn<12>(nbi) : g.down.type == 14 ? decode1_fn<14>(nbi) : nullptr;
     if (!fn) return -3;
     void *args[] = {(void *)&g};
-    const hipError_t e = cooperative
-                             ? hipLaunchCooperativeKernel(fn, dim3(grid), dim3(DEC_THREADS), args, 0, st)
-                             : hipLaunchKernel(fn, dim3(grid), dim3(DEC_THREADS), args, 0, st);
+    const hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(DEC_THREADS), args, 0, st);
     if (e != hipSuccess) return record_hip_error(e);
     return hip_check_launch();
 }

@@ -190,7 +190,7 @@ constexpr int G4_BM = 192;
 int launch_gemm4(const G2Args &g, hipStream_t st);
 int gemm4_grid(const G2Args &g);   // work-groups launch_gemm4 launches
 
-// Single-token MoE block in one cooperative kernel (k_decode.hip).
+// Single-token MoE block in one kernel (k_decode.hip).
 struct DecArgs {
     const float *rw, *rb, *x;     // router W [E][D], bias [E] or NULL, tokens [T][D]
     int D, E, K, I;
@@ -234,10 +234,10 @@ constexpr int64_t decodeb_tw_words(int64_t T, int64_t D, int64_t E, int64_t K, i
     return E * T + T * (D / 256) + T * K * (I / 4);
 }
 int launch_decodeb(const DecArgs &g, int grid, hipStream_t st);
-// cooperative: hipLaunchCooperativeKernel; otherwise a plain launch (the
-// kernel needs no co-residency: a WG computes any unit it waited too long for)
-int launch_decode1(const DecArgs &g, int grid, bool cooperative, hipStream_t st);
-// work-groups of the cooperative grid (one per CU), 0 if it cannot be resident
+// a plain launch of one WG per CU (the kernel needs no co-residency: a WG
+// computes any unit it waited too long for)
+int launch_decode1(const DecArgs &g, int grid, hipStream_t st);
+// work-groups of the decode grid (one per CU), 0 if one per CU cannot be resident
 int decode1_max_grid(int device, int *grid);
 
 }  // namespace mimoe

@@ -273,7 +273,8 @@ class Context:
         call("mi_moe_ctx_set_gemm_threshold", self.h, t)
 
     def set_fused_decode(self, mode) -> None:
-        """False / DECODE_CHAIN, True / DECODE_FUSED, DECODE_FUSED_COOPERATIVE"""
+        """False / DECODE_CHAIN, True / DECODE_FUSED (DECODE_FUSED_COOPERATIVE is
+        retired: the library refuses it)"""
         m = DECODE_FUSED if mode is True else DECODE_CHAIN if mode is False else int(mode)
         call("mi_moe_ctx_set_fused_decode", self.h, m)
 

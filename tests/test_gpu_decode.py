@@ -1,4 +1,4 @@
-"""Single-token MoE block in one cooperative kernel (k_decode.hip) against the
+"""Single-token MoE block in one kernel (k_decode.hip) against the
 CPU oracle and against the separate-kernel chain.
 
 Bars, as for every forward path: router logits, expert ids and the
@@ -11,9 +11,9 @@ layer one such flip in 8192 codes moves the output by 1.1e-3 (measured).  The
 two schedules must agree to a few such flips (rel-L2 <= 5e-3).
 
 Consecutive launches on one context keep counting on the kernel's barrier
-counters, so every case runs several tokens back to back, in both launch
-modes (cooperative and exclusive) and interleaved with the chain, and one
-case switches layer shapes between launches.
+counters, so every case runs several tokens back to back, twice in the fused
+mode and interleaved with the chain, and one case switches layer shapes
+between launches.  The retired cooperative mode is refused.
 """
 import ctypes as C
 import sys
@@ -110,8 +110,9 @@ def test_decode_fused_parity(name):
     x = cpu_x(spec, n_tok)
     res = cpu_x(spec, n_tok, stream=W.S_RES)
     ref, dbg = O.moe_forward(L, x, res)
+    assert M.load().mi_moe_ctx_set_fused_decode(ctx.h, M.DECODE_FUSED_COOPERATIVE) == -6   # retired
     for t in range(n_tok):
-        got_f, rt_f, st_f = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED_COOPERATIVE)
+        got_f, rt_f, st_f = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED)
         assert "decode1" in st_f, f"fused kernel not taken: {st_f}"
         got_x, rt_x, st_x = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED)
         assert "decode1" in st_x
@@ -119,7 +120,7 @@ def test_decode_fused_parity(name):
         assert "decode1" not in st_c
         e_f = _check_token(name, t, spec, got_f, rt_f, ref[t], res[t], dbg, True)
         _check_token(name, t, spec, got_x, rt_x, ref[t], res[t], dbg, True)
-        # the two launch modes run the same kernel: same bits
+        # two launches of the same kernel: same bits
         assert np.array_equal(got_f.view(np.uint32), got_x.view(np.uint32))
         e_c = _check_token(name, t, spec, got_c, rt_c, ref[t], res[t], dbg, False)
         e_p = rel_l2(got_f - res[t], got_c - res[t])
@@ -175,9 +176,9 @@ def test_decode_fused_shape_changes():
         layers.append((spec, g, x, res, ref, dbg))
     for t in range(3):
         for spec, g, x, res, ref, dbg in layers:
-            got, rt, st = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED if t % 2 else M.DECODE_FUSED_COOPERATIVE)
-            assert "decode1" in st
-            _check_token(f"mixed_{spec.name}", t, spec, got, rt, ref[t], res[t], dbg, True)
+            got, rt, st = _run_token(ctx, g.layer, spec, x[t], res[t], M.DECODE_FUSED if t % 2 else M.DECODE_CHAIN)
+            assert ("decode1" in st) == bool(t % 2)
+            _check_token(f"mixed_{spec.name}", t, spec, got, rt, ref[t], res[t], dbg, bool(t % 2))
     ctx.close()
 
 

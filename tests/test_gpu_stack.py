@@ -192,3 +192,33 @@ def test_forward_norm_config(name, kind, with_w, with_b, T):
     _fused_vs_separate(ctx, g.layer, spec, T, nrm, 1000 + T)
     log(f"forward_norm {name} md_cfg1 T={T}: fused == norm + forward")
     ctx.close()
+
+
+@pytest.mark.parametrize("T", [1, 5])
+@pytest.mark.parametrize("rescue", [64, 0])
+def test_forward_norm_in_place(T, rescue):
+    """forward_norm with out == res == h (the header allows out to alias res,
+    and res is h here): bit-identical to norm(h) -> forward(n, res=h) into a
+    separate buffer.  T = 1 runs the single-token kernel, which must then
+    normalize into the workspace first (a work-group that recomputes a late
+    router row re-reads h); rescue 0 makes every work-group recompute what
+    is not ready at its first look."""
+    spec = W.CONFIGS[1]["spec"]
+    ctx = M.Context(0)
+    ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
+    ctx.set_decode_rescue(rescue)
+    g = W.GpuLayer(ctx, spec)
+    nrm = M.make_norm(M.NORM_RMS, EPS)
+    rng = np.random.default_rng(77 + T)
+    h = (rng.standard_normal((T, spec.D)) * 2.0).astype(np.float32)
+    hd, nd, ref = M.to_device(h), M.DeviceBuffer(4 * T * spec.D), M.DeviceBuffer(4 * T * spec.D)
+    M.check("norm", ctx.norm(nrm, hd, T, spec.D, nd))
+    M.check("forward", ctx.forward(g.layer, nd, T, hd, ref))
+    for rep in range(3):
+        hd2 = M.to_device(h)
+        M.check("forward_norm in place", ctx.forward_norm(g.layer, nrm, hd2, T, hd2, hd2))
+        a = hd2.download(np.float32, (T, spec.D))
+        assert np.array_equal(a.view(np.uint32), ref.download(np.float32, (T, spec.D)).view(np.uint32)), rep
+    assert ctx.take_errors() == (0, 0)
+    log(f"forward_norm in place T={T} rescue={rescue}: == norm + forward")
+    ctx.close()

@@ -190,6 +190,18 @@ int mi_moe_forward(mi_moe_ctx *ctx, const mi_moe_layer *layer, const float *x, i
                    const float *res, float *out, const mi_moe_routing *routing,
                    mi_stream_t stream);
 
+/* ---- the block with its own router input -----------------------------------
+ * mi_moe_forward whose router reads other rows than the experts: logits =
+ * W_r . x_router[t] (+ b), then the layer's gating, and the experts read x[t].
+ * diffusiongemma routes on rms_norm(res) * router_scale * scale and feeds the
+ * experts rms_norm(res) * ffn_norm2 (diffusiongemma_model.cpp:919-922 against
+ * :937).  x_router: F32 [T][D] device; NULL (or x) is mi_moe_forward.  Calls
+ * with a separate router input run the kernel chain at every token count
+ * (the fused decode kernels quantize one row set for both). */
+int mi_moe_forward_router_input(mi_moe_ctx *ctx, const mi_moe_layer *layer, const float *x,
+                                const float *x_router, int64_t n_tokens, const float *res, float *out,
+                                const mi_moe_routing *routing, mi_stream_t stream);
+
 /* ---- the block with no context and no allocation --------------------------
  * No counterpart in the reference: mi_moe_forward for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,

@@ -838,8 +838,10 @@ namespace {
 // (Applying the norm where the prefill router reads x was built and measured
 // slower: each of a token slab's expert-tile work-groups recomputed the rows'
 // statistics before its chunk loop, config-4 prefill 9.96 vs 9.57 ms.)
+// xr: the rows the router reads when they differ from the experts' input
+// (null: x; the norm, if any, applies to x only).
 int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const float *res, float *out,
-                 const mi_moe_routing *routing, const NormParams &np, hipStream_t st) {
+                 const mi_moe_routing *routing, const NormParams &np, hipStream_t st, const float *xr = nullptr) {
     if (!c) return MI_MOE_ERR_NULL;
     if (T < 0) return MI_MOE_ERR_SHAPE;
     TRY(validate_layer(c, L, true, true));
@@ -850,8 +852,10 @@ int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T
     if (np.kind != NORM_NONE && D > 4096) return MI_MOE_ERR_UNSUPPORTED;
     HIP_TRY(hipSetDevice(c->device));
     stage_begin(c, st);
+    if (xr == x) xr = nullptr;
     int P = 0, C = 0;
-    const bool dec1 = T == 1 && plan_decode1(c, L, x, P, C);
+    // the fused decode kernels route on the rows they quantize for the experts
+    const bool dec1 = T == 1 && !xr && plan_decode1(c, L, x, P, C);
     // The single-token kernel normalizes x itself only when out does not
     // overlap x: a work-group that computes a late router row or Q8_K block
     // re-reads x, possibly after other work-groups wrote their out columns.
@@ -871,14 +875,16 @@ int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T
     int cc = 0;
     if (dec1) {
         TRY(run_decode1(c, L, x, res, out, P, C, fuse_norm ? np : NormParams{}, st));
-    } else if (plan_decodeb(c, L, x, T, cc)) {
+    } else if (!xr && plan_decodeb(c, L, x, T, cc)) {
         TRY(run_decodeb(c, L, x, T, res, out, cc, st));
     } else {
-        // router + Q8_K(x) in one launch where the shape fits
+        // router + Q8_K(x) in one launch where the shape fits (the router's
+        // own rows: the router alone, the experts quantize x themselves)
         Q8Out qx;
-        const bool xq = x_q8_spec(c, L, T, qx);
-        const int rc = launch_front(L->router_w, L->router_b, x, D, T, D, E, c->logits, xq ? &qx : nullptr, st);
-        if (rc == -6) TRY(launch_router(L->router_w, L->router_b, x, D, T, D, E, c->logits, st));
+        const bool xq = !xr && x_q8_spec(c, L, T, qx);
+        const float *xrow = xr ? xr : x;
+        const int rc = launch_front(L->router_w, L->router_b, xrow, D, T, D, E, c->logits, xq ? &qx : nullptr, st);
+        if (rc == -6) TRY(launch_router(L->router_w, L->router_b, xrow, D, T, D, E, c->logits, st));
         else TRY(rc);
         stage_end(c, "router", st);
         Gating gt;
@@ -995,6 +1001,12 @@ int mi_moe_forward_noalloc(const mi_moe_layer *L, const float *x, int64_t T, con
     mi_moe_ctx *c = nullptr;
     TRY(noalloc_ctx(&c));
     return forward_impl(c, L, x, T, res, out, routing, NormParams{}, (hipStream_t)stream);
+}
+
+int mi_moe_forward_router_input(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, const float *x_router,
+                                int64_t T, const float *res, float *out, const mi_moe_routing *routing,
+                                mi_stream_t stream) {
+    return forward_impl(c, L, x, T, res, out, routing, NormParams{}, (hipStream_t)stream, x_router);
 }
 
 int mi_moe_forward_norm(mi_moe_ctx *c, const mi_moe_layer *L, const mi_moe_norm *norm, const float *h, int64_t T,

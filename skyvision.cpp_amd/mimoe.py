@@ -88,6 +88,7 @@ SYMBOLS = {
     "mi_moe_ctx_take_errors": ([P, C.POINTER(i64), C.POINTER(i64), C.POINTER(i64)], C.c_int),
     "mi_moe_forward": ([P, C.POINTER(Layer), P, i64, P, P, C.POINTER(Routing), P], C.c_int),
     "mi_moe_forward_noalloc": ([C.POINTER(Layer), P, i64, P, P, C.POINTER(Routing), P], C.c_int),
+    "mi_moe_forward_router_input": ([P, C.POINTER(Layer), P, P, i64, P, P, C.POINTER(Routing), P], C.c_int),
     "mi_moe_expert_ffn": ([P, C.POINTER(Layer), P, i64, P, P, P, P, P, P], C.c_int),
     "mi_top_k": ([P, C.POINTER(Tensor), i32, C.POINTER(Tensor), P], C.c_int),
     "mi_mul_mat_id": ([P, C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor),
@@ -320,6 +321,13 @@ class Context:
         return load().mi_moe_forward(self.h, C.byref(layer), _addr(x), T, _addr(res), _addr(out),
                                      C.byref(routing) if routing is not None else None,
                                      _addr(stream))
+
+    def forward_router_input(self, layer: Layer, x, x_router, T: int, res, out, routing: Routing | None = None,
+                             stream=None) -> int:
+        """mi_moe_forward_router_input: the router reads x_router, the experts x."""
+        return load().mi_moe_forward_router_input(self.h, C.byref(layer), _addr(x), _addr(x_router), T, _addr(res),
+                                                  _addr(out), C.byref(routing) if routing is not None else None,
+                                                  _addr(stream))
 
     def expert_ffn(self, layer: Layer, x, T: int, res, ids_gu, ids_dn, w, out, stream=None) -> int:
         return load().mi_moe_expert_ffn(self.h, C.byref(layer), _addr(x), T, _addr(res),

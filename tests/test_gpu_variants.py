@@ -178,3 +178,67 @@ def test_softmax_all_underflow_ties():
     differs = int((logit_rank != dbg["sel"]).any(axis=1).sum())
     log(f"underflow ties: {differs} of 50 tokens pick differently from the logits' own ranking")
     assert differs > 0
+
+
+def _router_input_case(v: Variant, T, paths, name, seed):
+    """diffusiongemma's layer: the router reads xr = rms_norm(res) * router_scale
+    * s (diffusiongemma_model.cpp:919-922), the experts x = rms_norm(res) *
+    ffn_norm2 (:937); softmax over all experts, top-k of the probabilities,
+    renorm, per-expert scale (:923-935).  The oracle side is the reference's
+    graph in the oracle's ops: router logits of xr, the gating, then the
+    experts on x with that routing."""
+    D, E, K = v.o["D"], v.o["E"], v.o["K"]
+    rng = np.random.default_rng(seed)
+    res = rng.standard_normal((T, D)).astype(np.float32)
+    r64 = res.astype(np.float64)
+    nrm = r64 / np.sqrt((r64 * r64).mean(axis=1, keepdims=True) + 1e-6)
+    router_scale = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    ffn_norm2 = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    xr = ((nrm.astype(np.float32) * router_scale) * np.float32(D ** -0.5)).astype(np.float32)
+    x = (nrm.astype(np.float32) * ffn_norm2).astype(np.float32)
+    logits = O.router_logits(v.o["router_w"], None, xr)
+    sel, w = O.route_gated(logits, K, O.GATING_SOFTMAX_ALL, expert_scale=v.o["expert_scale"])
+    ref, dbg = O.moe_forward(v.o, x, res, sel_in=sel, w_in=w)
+    counts, offsets, perm = O.dispatch(sel, E)
+    # the logits of x differ from those of xr, so the bit-exact logit check below tells them apart
+    assert not np.array_equal(O.router_logits(v.o["router_w"], None, x), logits)
+    ctx = M.Context(0)
+    ctx.reserve(max(T, 1), D, v.o["I"], E, K)
+    xd, xrd, rd = M.to_device(x), M.to_device(xr), M.to_device(res)
+    for pname, thr in paths:
+        ctx.set_gemm_threshold(thr)
+        out = M.DeviceBuffer(4 * T * D)
+        bufs, r = _routing_buffers(T, E, K)
+        M.check("forward_router_input", ctx.forward_router_input(v.L, xd, xrd, T, rd, out, r))
+        got = out.download(np.float32, (T, D))
+        gl = bufs["logits"].download(np.float32, (T, E))
+        assert np.array_equal(gl.view(np.uint32), logits.view(np.uint32)), f"{name}: logits"
+        assert np.array_equal(bufs["sel"].download(np.int32, (T, K)), sel), f"{name} {pname}: ids"
+        assert np.allclose(bufs["weights"].download(np.float32, (T, K)), w, rtol=1e-6, atol=1e-7), name
+        assert np.array_equal(bufs["counts"].download(np.int32, (E,)), counts), f"{name}: counts"
+        assert np.array_equal(bufs["offsets"].download(np.int32, (E + 1,)), offsets), f"{name}: offsets"
+        assert np.array_equal(bufs["perm"].download(np.int32, (T * K,)), perm), f"{name}: permutation"
+        e = rel_l2(got - res, ref - res)
+        log(f"{name} {pname} T={T}: rel-L2 {e:.3e} max-abs {max_abs(got, ref):.3e}")
+        assert e <= TOL, (name, pname, T)
+    # x_router == x is the plain forward, bit for bit
+    out1, out2 = M.DeviceBuffer(4 * T * D), M.DeviceBuffer(4 * T * D)
+    ctx.set_gemm_threshold(0)
+    M.check("forward_router_input", ctx.forward_router_input(v.L, xd, xd, T, rd, out1))
+    M.check("forward", ctx.forward(v.L, xd, T, rd, out2))
+    assert np.array_equal(out1.download(np.uint32, (T, D)), out2.download(np.uint32, (T, D)))
+    ctx.close()
+
+
+@pytest.mark.parametrize("T", [1, 12, 150])
+def test_diffusiongemma_router_input(T):
+    v = Variant(512, 128, 8, 256, M.ACT_GELU_TANH, M.GATING_SOFTMAX_ALL, seed=46)
+    _router_input_case(v, T, PATHS, "diffusiongemma router input", 100 + T)
+
+
+def test_diffusiongemma_router_input_model_dims():
+    # the model's own widths (n_embd 2816, expert n_ff 704: no 256-value k-quant
+    # row fits 704) with F32 tables, 16 of the 128 experts
+    v = Variant(2816, 16, 8, 704, M.ACT_GELU_TANH, M.GATING_SOFTMAX_ALL, qtype=O.TYPE_F32, dtype=O.TYPE_F32,
+                seed=47)
+    _router_input_case(v, 5, [("default", 0)], "diffusiongemma router input, model widths", 200)

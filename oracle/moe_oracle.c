@@ -469,6 +469,177 @@ void orc_dequantize_row_q8_K(const void *vx, float *y, int64_t k) {
         for (int j = 0; j < QK_K; ++j) *y++ = x[i].d * x[i].qs[j];
 }
 
+/* ------------------------------------------------------------------------ */
+/* 32-value block formats (ggml ggml-quants.c, the _ref quantizers and the  */
+/* dequantizers; [ggml-ext]: ggml is not in the reference tree).  Q8_0 is    */
+/* also the activation format the Q4_0 / Q5_0 / Q8_0 dots take (ggml-cpu    */
+/* vec_dot_type).  ggml's x86 SIMD quantize_row_q8_0 rounds half to even     */
+/* with id = 127 / amax; the portable _ref form restated here uses          */
+/* id = 1 / fp32(amax / 127) and roundf (half away from zero): the two can   */
+/* differ by one code on values at a rounding boundary.                      */
+/* ------------------------------------------------------------------------ */
+void orc_quantize_row_q4_0(const float *x, void *vy, int64_t k) {
+    orc_block_q4_0 *y = (orc_block_q4_0 *)vy;
+    const int64_t nb = k / ORC_QK32;
+    for (int64_t i = 0; i < nb; i++) {
+        float amax = 0.0f, max = 0.0f;
+        for (int j = 0; j < ORC_QK32; j++) {
+            const float v = x[i * ORC_QK32 + j];
+            if (amax < fabsf(v)) {
+                amax = fabsf(v);
+                max = v;
+            }
+        }
+        const float d = max / -8;
+        const float id = d ? 1.0f / d : 0.0f;
+        y[i].d = orc_fp32_to_fp16(d);
+        for (int j = 0; j < ORC_QK32 / 2; ++j) {
+            const float x0 = x[i * ORC_QK32 + j] * id;
+            const float x1 = x[i * ORC_QK32 + ORC_QK32 / 2 + j] * id;
+            const uint8_t xi0 = (uint8_t)MIN(15, (int8_t)(x0 + 8.5f));
+            const uint8_t xi1 = (uint8_t)MIN(15, (int8_t)(x1 + 8.5f));
+            y[i].qs[j] = (uint8_t)(xi0 | (xi1 << 4));
+        }
+    }
+}
+
+void orc_quantize_row_q5_0(const float *x, void *vy, int64_t k) {
+    orc_block_q5_0 *y = (orc_block_q5_0 *)vy;
+    const int64_t nb = k / ORC_QK32;
+    for (int64_t i = 0; i < nb; i++) {
+        float amax = 0.0f, max = 0.0f;
+        for (int j = 0; j < ORC_QK32; j++) {
+            const float v = x[i * ORC_QK32 + j];
+            if (amax < fabsf(v)) {
+                amax = fabsf(v);
+                max = v;
+            }
+        }
+        const float d = max / -16;
+        const float id = d ? 1.0f / d : 0.0f;
+        y[i].d = orc_fp32_to_fp16(d);
+        uint32_t qh = 0;
+        for (int j = 0; j < ORC_QK32 / 2; ++j) {
+            const float x0 = x[i * ORC_QK32 + j] * id;
+            const float x1 = x[i * ORC_QK32 + ORC_QK32 / 2 + j] * id;
+            const uint8_t xi0 = (uint8_t)MIN(31, (int8_t)(x0 + 16.5f));
+            const uint8_t xi1 = (uint8_t)MIN(31, (int8_t)(x1 + 16.5f));
+            y[i].qs[j] = (uint8_t)((xi0 & 0x0F) | ((xi1 & 0x0F) << 4));
+            qh |= ((uint32_t)(xi0 & 0x10u) >> 4) << j;
+            qh |= ((uint32_t)(xi1 & 0x10u) >> 4) << (j + ORC_QK32 / 2);
+        }
+        memcpy(y[i].qh, &qh, sizeof(qh));
+    }
+}
+
+void orc_quantize_row_q8_0(const float *x, void *vy, int64_t k) {
+    orc_block_q8_0 *y = (orc_block_q8_0 *)vy;
+    const int64_t nb = k / ORC_QK32;
+    for (int64_t i = 0; i < nb; i++) {
+        float amax = 0.0f;
+        for (int j = 0; j < ORC_QK32; j++) amax = MAX(amax, fabsf(x[i * ORC_QK32 + j]));
+        const float d = amax / ((1 << 7) - 1);
+        const float id = d ? 1.0f / d : 0.0f;
+        y[i].d = orc_fp32_to_fp16(d);
+        for (int j = 0; j < ORC_QK32; ++j) y[i].qs[j] = (int8_t)roundf(x[i * ORC_QK32 + j] * id);
+    }
+}
+
+void orc_dequantize_row_q4_0(const void *vx, float *y, int64_t k) {
+    const orc_block_q4_0 *x = (const orc_block_q4_0 *)vx;
+    for (int64_t i = 0; i < k / ORC_QK32; i++) {
+        const float d = orc_fp16_to_fp32(x[i].d);
+        for (int j = 0; j < ORC_QK32 / 2; ++j) {
+            y[i * ORC_QK32 + j] = ((x[i].qs[j] & 0x0F) - 8) * d;
+            y[i * ORC_QK32 + j + ORC_QK32 / 2] = ((x[i].qs[j] >> 4) - 8) * d;
+        }
+    }
+}
+
+void orc_dequantize_row_q5_0(const void *vx, float *y, int64_t k) {
+    const orc_block_q5_0 *x = (const orc_block_q5_0 *)vx;
+    for (int64_t i = 0; i < k / ORC_QK32; i++) {
+        const float d = orc_fp16_to_fp32(x[i].d);
+        uint32_t qh;
+        memcpy(&qh, x[i].qh, sizeof(qh));
+        for (int j = 0; j < ORC_QK32 / 2; ++j) {
+            const uint8_t xh_0 = (uint8_t)(((qh >> j) << 4) & 0x10);
+            const uint8_t xh_1 = (uint8_t)((qh >> (j + 12)) & 0x10);
+            y[i * ORC_QK32 + j] = (((x[i].qs[j] & 0x0F) | xh_0) - 16) * d;
+            y[i * ORC_QK32 + j + ORC_QK32 / 2] = (((x[i].qs[j] >> 4) | xh_1) - 16) * d;
+        }
+    }
+}
+
+void orc_dequantize_row_q8_0(const void *vx, float *y, int64_t k) {
+    const orc_block_q8_0 *x = (const orc_block_q8_0 *)vx;
+    for (int64_t i = 0; i < k / ORC_QK32; i++) {
+        const float d = orc_fp16_to_fp32(x[i].d);
+        for (int j = 0; j < ORC_QK32; ++j) y[i * ORC_QK32 + j] = x[i].qs[j] * d;
+    }
+}
+
+/* ggml_vec_dot_q4_0_q8_0 / q5_0_q8_0 / q8_0_q8_0 (generic): per block an
+ * exact integer sum, then sumf += that sum scaled by the two fp16 scales in
+ * each function's own expression order */
+float orc_vec_dot_q4_0_q8_0(int n, const void *vx, const void *vy) {
+    const orc_block_q4_0 *x = (const orc_block_q4_0 *)vx;
+    const orc_block_q8_0 *y = (const orc_block_q8_0 *)vy;
+    float sumf = 0;
+    for (int ib = 0; ib < n / ORC_QK32; ++ib) {
+        int sumi0 = 0, sumi1 = 0;
+        for (int j = 0; j < ORC_QK32 / 2; ++j) {
+            const int v0 = (x[ib].qs[j] & 0x0F) - 8;
+            const int v1 = (x[ib].qs[j] >> 4) - 8;
+            sumi0 += v0 * y[ib].qs[j];
+            sumi1 += v1 * y[ib].qs[j + ORC_QK32 / 2];
+        }
+        const int sumi = sumi0 + sumi1;
+        sumf += sumi * orc_fp16_to_fp32(x[ib].d) * orc_fp16_to_fp32(y[ib].d);
+    }
+    return sumf;
+}
+
+float orc_vec_dot_q5_0_q8_0(int n, const void *vx, const void *vy) {
+    const orc_block_q5_0 *x = (const orc_block_q5_0 *)vx;
+    const orc_block_q8_0 *y = (const orc_block_q8_0 *)vy;
+    float sumf = 0;
+    for (int ib = 0; ib < n / ORC_QK32; ++ib) {
+        uint32_t qh;
+        memcpy(&qh, x[ib].qh, sizeof(qh));
+        int sumi0 = 0, sumi1 = 0;
+        for (int j = 0; j < ORC_QK32 / 2; ++j) {
+            const uint8_t xh_0 = (uint8_t)(((qh & (1u << j)) >> j) << 4);
+            const uint8_t xh_1 = (uint8_t)((qh & (1u << (j + 16))) >> (j + 12));
+            const int32_t x0 = (int8_t)(((x[ib].qs[j] & 0x0F) | xh_0) - 16);
+            const int32_t x1 = (int8_t)(((x[ib].qs[j] >> 4) | xh_1) - 16);
+            sumi0 += x0 * y[ib].qs[j];
+            sumi1 += x1 * y[ib].qs[j + ORC_QK32 / 2];
+        }
+        const int sumi = sumi0 + sumi1;
+        sumf += (orc_fp16_to_fp32(x[ib].d) * orc_fp16_to_fp32(y[ib].d)) * sumi;
+    }
+    return sumf;
+}
+
+float orc_vec_dot_q8_0_q8_0(int n, const void *vx, const void *vy) {
+    const orc_block_q8_0 *x = (const orc_block_q8_0 *)vx;
+    const orc_block_q8_0 *y = (const orc_block_q8_0 *)vy;
+    float sumf = 0;
+    for (int ib = 0; ib < n / ORC_QK32; ++ib) {
+        int sumi = 0;
+        for (int j = 0; j < ORC_QK32; j++) sumi += x[ib].qs[j] * y[ib].qs[j];
+        sumf += sumi * (orc_fp16_to_fp32(x[ib].d) * orc_fp16_to_fp32(y[ib].d));
+    }
+    return sumf;
+}
+
+float orc_vec_dot_f16(int n, const uint16_t *x, const uint16_t *y) {
+    double sumf = 0.0;
+    for (int i = 0; i < n; ++i) sumf += (double)(orc_fp16_to_fp32(x[i]) * orc_fp16_to_fp32(y[i]));
+    return (float)sumf;
+}
+
 size_t orc_row_size(int type, int64_t k) {
     switch (type) {
     case ORC_TYPE_F32: return (size_t)k * 4;
@@ -476,6 +647,9 @@ size_t orc_row_size(int type, int64_t k) {
     case ORC_TYPE_Q4_K: return (size_t)(k / QK_K) * sizeof(orc_block_q4_K);
     case ORC_TYPE_Q6_K: return (size_t)(k / QK_K) * sizeof(orc_block_q6_K);
     case ORC_TYPE_Q8_K: return (size_t)(k / QK_K) * sizeof(orc_block_q8_K);
+    case ORC_TYPE_Q4_0: return (size_t)(k / ORC_QK32) * sizeof(orc_block_q4_0);
+    case ORC_TYPE_Q5_0: return (size_t)(k / ORC_QK32) * sizeof(orc_block_q5_0);
+    case ORC_TYPE_Q8_0: return (size_t)(k / ORC_QK32) * sizeof(orc_block_q8_0);
     default: return 0;
     }
 }
@@ -489,6 +663,13 @@ void orc_quantize_rows(int type, const float *x, void *y, int64_t nrows, int64_t
         if (type == ORC_TYPE_Q4_K) orc_quantize_row_q4_K(xr, yr, k);
         else if (type == ORC_TYPE_Q6_K) orc_quantize_row_q6_K(xr, yr, k, 0);
         else if (type == ORC_TYPE_Q8_K) orc_quantize_row_q8_K(xr, yr, k);
+        else if (type == ORC_TYPE_Q4_0) orc_quantize_row_q4_0(xr, yr, k);
+        else if (type == ORC_TYPE_Q5_0) orc_quantize_row_q5_0(xr, yr, k);
+        else if (type == ORC_TYPE_Q8_0) orc_quantize_row_q8_0(xr, yr, k);
+        else if (type == ORC_TYPE_F16) {
+            uint16_t *h = (uint16_t *)yr;
+            for (int64_t i = 0; i < k; i++) h[i] = orc_fp32_to_fp16(xr[i]);
+        }
     }
 }
 
@@ -851,6 +1032,9 @@ static void dequant_row_any(int type, const void *row, float *out, int64_t k) {
     if (type == ORC_TYPE_Q4_K) orc_dequantize_row_q4_K(row, out, k);
     else if (type == ORC_TYPE_Q6_K) orc_dequantize_row_q6_K(row, out, k);
     else if (type == ORC_TYPE_F32) memcpy(out, row, sizeof(float) * (size_t)k);
+    else if (type == ORC_TYPE_Q4_0) orc_dequantize_row_q4_0(row, out, k);
+    else if (type == ORC_TYPE_Q5_0) orc_dequantize_row_q5_0(row, out, k);
+    else if (type == ORC_TYPE_Q8_0) orc_dequantize_row_q8_0(row, out, k);
     else if (type == ORC_TYPE_F16) {
         const uint16_t *h = (const uint16_t *)row;
         for (int64_t i = 0; i < k; i++) out[i] = orc_fp16_to_fp32(h[i]);
@@ -864,8 +1048,11 @@ int orc_mul_mat_id(int type, const void *as, int64_t Kin, int64_t N, int E,
         return -1;
     if (ne11 != 1 && ne11 != n_used) return -1;
     const int kq = (type == ORC_TYPE_Q4_K || type == ORC_TYPE_Q6_K);
+    const int b32 = (type == ORC_TYPE_Q4_0 || type == ORC_TYPE_Q5_0 || type == ORC_TYPE_Q8_0);
+    const int f16 = type == ORC_TYPE_F16;
     if (kq && (Kin % QK_K)) return -1;
-    if (!kq && type != ORC_TYPE_F32 && type != ORC_TYPE_F16) return -1;
+    if (b32 && (Kin % ORC_QK32)) return -1;
+    if (!kq && !b32 && type != ORC_TYPE_F32 && !f16) return -1;
     for (int64_t i = 0; i < T * n_used; i++)
         if (ids[i] < 0 || ids[i] >= E) return -1;
     if (T == 0) return 0;
@@ -873,13 +1060,28 @@ int orc_mul_mat_id(int type, const void *as, int64_t Kin, int64_t N, int E,
     const size_t rs = orc_row_size(type, Kin);
     const int64_t nbrows = T * ne11;
 
-    /* activations: Q8_K rows (ggml vec_dot_type), or fp32/fp64 as given */
+    /* activations in the weight type's vec_dot_type: Q8_K rows (k-quants),
+     * Q8_0 rows (32-value formats), fp16 rows (F16), or fp32/fp64 as given */
     orc_block_q8_K *bq = NULL;
+    orc_block_q8_0 *bq0 = NULL;
+    uint16_t *bh = NULL;
     if (kq && !exact) {
         bq = (orc_block_q8_K *)malloc(sizeof(orc_block_q8_K) * (size_t)(Kin / QK_K) * (size_t)nbrows);
 #pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
         for (int64_t r = 0; r < nbrows; r++)
             orc_quantize_row_q8_K(b + r * Kin, bq + r * (Kin / QK_K), Kin);
+    }
+    if (b32 && !exact) {
+        bq0 = (orc_block_q8_0 *)malloc(sizeof(orc_block_q8_0) * (size_t)(Kin / ORC_QK32) * (size_t)nbrows);
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+        for (int64_t r = 0; r < nbrows; r++)
+            orc_quantize_row_q8_0(b + r * Kin, bq0 + r * (Kin / ORC_QK32), Kin);
+    }
+    if (f16 && !exact) {
+        bh = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)Kin * (size_t)nbrows);
+#pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+        for (int64_t r = 0; r < nbrows; r++)
+            for (int64_t q = 0; q < Kin; q++) bh[r * Kin + q] = orc_fp32_to_fp16(b[r * Kin + q]);
     }
 
     /* group (t, k) rows per expert, tokens outer / slots inner */
@@ -902,7 +1104,7 @@ int orc_mul_mat_id(int type, const void *as, int64_t Kin, int64_t N, int E,
                 const char *We = (const char *)as + (size_t)e * (size_t)N * rs;
                 for (int64_t n = c * RCH; n < MIN(N, (c + 1) * RCH); n++) {
                     const char *wr = We + (size_t)n * rs;
-                    if (exact || !kq) dequant_row_any(type, wr, wrow, Kin);
+                    if (exact || type == ORC_TYPE_F32) dequant_row_any(type, wr, wrow, Kin);
                     for (int32_t i = 0; i < n_rows; i++) {
                         const int32_t p = perm[offs[e] + i];
                         const int64_t t = p / n_used;
@@ -918,6 +1120,13 @@ int orc_mul_mat_id(int type, const void *as, int64_t Kin, int64_t N, int E,
                             const void *yb = bq + brow * (Kin / QK_K);
                             v = type == ORC_TYPE_Q4_K ? orc_vec_dot_q4_K_q8_K((int)Kin, wr, yb)
                                                       : orc_vec_dot_q6_K_q8_K((int)Kin, wr, yb);
+                        } else if (b32) {
+                            const void *yb = bq0 + brow * (Kin / ORC_QK32);
+                            v = type == ORC_TYPE_Q8_0   ? orc_vec_dot_q8_0_q8_0((int)Kin, wr, yb)
+                                : type == ORC_TYPE_Q5_0 ? orc_vec_dot_q5_0_q8_0((int)Kin, wr, yb)
+                                                        : orc_vec_dot_q4_0_q8_0((int)Kin, wr, yb);
+                        } else if (f16) {
+                            v = orc_vec_dot_f16((int)Kin, (const uint16_t *)wr, bh + brow * Kin);
                         } else {
                             const float *bb = b + brow * Kin;
                             float acc = 0.f;
@@ -935,6 +1144,8 @@ int orc_mul_mat_id(int type, const void *as, int64_t Kin, int64_t N, int E,
     free(offs);
     free(perm);
     free(bq);
+    free(bq0);
+    free(bh);
     return 0;
 }
 

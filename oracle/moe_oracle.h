@@ -47,6 +47,9 @@ extern "C" {
 enum {
     ORC_TYPE_F32  = 0,
     ORC_TYPE_F16  = 1,
+    ORC_TYPE_Q4_0 = 2,
+    ORC_TYPE_Q5_0 = 6,
+    ORC_TYPE_Q8_0 = 8,
     ORC_TYPE_Q4_K = 12,
     ORC_TYPE_Q6_K = 14,
     ORC_TYPE_Q8_K = 15,
@@ -73,6 +76,29 @@ typedef struct {
     int8_t   qs[256];
     int16_t  bsums[16];  /* sum of qs in groups of 16 */
 } orc_block_q8_K;        /* 292 bytes */
+
+/* 32-value blocks (ggml QK4_0 = QK5_0 = QK8_0 = 32): the expert tables the
+ * reference's converters write by default (Q8_0: convert_hf_to_gguf.py:55-57,
+ * convert_qwen3omni.py:60-61,135; Q5_0: convert_nemotronomni.py:113-114;
+ * Q4_0: convert_diffusiongemma.py:62).  Packed without padding. */
+#define ORC_QK32 32
+#pragma pack(push, 1)
+typedef struct {
+    uint16_t d;          /* fp16 scale */
+    uint8_t  qs[16];     /* value j: low nibble of qs[j], value j+16: high nibble; x = d (q - 8) */
+} orc_block_q4_0;        /* 18 bytes */
+
+typedef struct {
+    uint16_t d;          /* fp16 scale */
+    uint8_t  qh[4];      /* bit j: 5th bit of value j (j < 32), little-endian uint32 */
+    uint8_t  qs[16];     /* low 4 bits, as q4_0; x = d (q - 16) */
+} orc_block_q5_0;        /* 22 bytes */
+
+typedef struct {
+    uint16_t d;          /* fp16 scale */
+    int8_t   qs[32];     /* x = d q */
+} orc_block_q8_0;        /* 34 bytes */
+#pragma pack(pop)
 
 enum {                    /* activation applied between the two expert products */
     ORC_ACT_SILU           = 0,  /* silu(gate) * up              (qwen3omni, swiglu_split)        */
@@ -118,18 +144,34 @@ void orc_quantize_row_q4_K(const float *x, void *y, int64_t k);
 void orc_quantize_row_q4_K_port(const float *x, void *y, int64_t k, int port);
 void orc_quantize_row_q6_K(const float *x, void *y, int64_t k, int port);
 void orc_quantize_row_q8_K(const float *x, void *y, int64_t k);
+/* 32-value formats (k a multiple of 32): ggml quantize_row_q4_0_ref /
+ * q5_0_ref / q8_0_ref; Q8_0 is also the activation type their dots use */
+void orc_quantize_row_q4_0(const float *x, void *y, int64_t k);
+void orc_quantize_row_q5_0(const float *x, void *y, int64_t k);
+void orc_quantize_row_q8_0(const float *x, void *y, int64_t k);
 /* many rows, threaded: nrows rows of k floats -> nrows * (k/256) blocks */
 void orc_quantize_rows(int type, const float *x, void *y, int64_t nrows, int64_t k, int nthreads);
 
 void orc_dequantize_row_q4_K(const void *x, float *y, int64_t k);
 void orc_dequantize_row_q6_K(const void *x, float *y, int64_t k);
 void orc_dequantize_row_q8_K(const void *x, float *y, int64_t k);
+void orc_dequantize_row_q4_0(const void *x, float *y, int64_t k);
+void orc_dequantize_row_q5_0(const void *x, float *y, int64_t k);
+void orc_dequantize_row_q8_0(const void *x, float *y, int64_t k);
 
 size_t orc_row_size(int type, int64_t k);   /* bytes of one row of k values */
 
 /* ---- k-quant x Q8_K dots (ggml_vec_dot_*_q8_K, generic scalar order) --- */
 float orc_vec_dot_q4_K_q8_K(int n, const void *x, const void *y);
 float orc_vec_dot_q6_K_q8_K(int n, const void *x, const void *y);
+/* 32-value formats x Q8_0 activations (ggml_vec_dot_q{4,5,8}_0_q8_0, generic
+ * scalar order: an exact integer dot per block, then the fp32 sum over
+ * blocks), and F16 x F16 (ggml_vec_dot_f16 generic: fp32 products, exact,
+ * summed in double) */
+float orc_vec_dot_q4_0_q8_0(int n, const void *x, const void *y);
+float orc_vec_dot_q5_0_q8_0(int n, const void *x, const void *y);
+float orc_vec_dot_q8_0_q8_0(int n, const void *x, const void *y);
+float orc_vec_dot_f16(int n, const uint16_t *x, const uint16_t *y);
 
 /* ---- seeded synthetic data ----------------------------------------------
  * Counter-based: value i of (seed, stream) is independent of how the range
@@ -172,7 +214,9 @@ void orc_dispatch(const int32_t *sel, int64_t T, int K, int E,
  * b   : F32, T x ne11 rows of Kin (ne=[Kin, ne11, T]); ne11 is 1 or n_used
  * ids : I32 [T][n_used]
  * dst : F32 [T][n_used][N]
- * For k-quant types, b rows are quantized to Q8_K first (ggml vec_dot_type).
+ * b rows are first converted to the weight type's ggml vec_dot_type: Q8_K for
+ * Q4_K / Q6_K, Q8_0 for Q4_0 / Q5_0 / Q8_0, F16 (round to nearest even) for
+ * F16; F32 weights take b as given.
  * exact = 1 instead computes in fp64 on dequantized weights and unquantized b.
  * Returns 0, or -1 on bad arguments. */
 int orc_mul_mat_id(int type, const void *as, int64_t Kin, int64_t N, int E,

@@ -17,9 +17,17 @@ HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "_build" / "liboracle.so"
 
 TYPE_F32, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K, TYPE_I32 = 0, 1, 12, 14, 15, 26
+TYPE_Q4_0, TYPE_Q5_0, TYPE_Q8_0 = 2, 6, 8
 ACT_SILU, ACT_GELU_ERF_GP1, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2, 3
 QK_K = 256
-BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210, TYPE_Q8_K: 292}
+QK32 = 32
+BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210, TYPE_Q8_K: 292, TYPE_Q4_0: 18, TYPE_Q5_0: 22, TYPE_Q8_0: 34}
+B32_TYPES = (TYPE_Q4_0, TYPE_Q5_0, TYPE_Q8_0)
+
+
+def block_values(type_: int) -> int:
+    """values per block of a quantized type (1 for F32 / F16)"""
+    return QK32 if type_ in B32_TYPES else QK_K if type_ in (TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K) else 1
 
 _lib = None
 
@@ -56,8 +64,14 @@ def _declare(L: C.CDLL) -> None:
     L.orc_quantize_row_q6_K.argtypes = [P, P, i64, C.c_int]
     L.orc_quantize_row_q8_K.argtypes = [P, P, i64]
     L.orc_quantize_rows.argtypes = [C.c_int, P, P, i64, i64, C.c_int]
-    for n in ("q4_K", "q6_K", "q8_K"):
+    for n in ("q4_K", "q6_K", "q8_K", "q4_0", "q5_0", "q8_0"):
         getattr(L, f"orc_dequantize_row_{n}").argtypes = [P, P, i64]
+    for n in ("q4_0", "q5_0", "q8_0"):
+        getattr(L, f"orc_quantize_row_{n}").argtypes = [P, P, i64]
+        getattr(L, f"orc_vec_dot_{n}_q8_0").argtypes = [C.c_int, P, P]
+        getattr(L, f"orc_vec_dot_{n}_q8_0").restype = C.c_float
+    L.orc_vec_dot_f16.argtypes = [C.c_int, P, P]
+    L.orc_vec_dot_f16.restype = C.c_float
     L.orc_row_size.argtypes = [C.c_int, i64]
     L.orc_row_size.restype = C.c_size_t
     L.orc_vec_dot_q4_K_q8_K.argtypes = [C.c_int, P, P]
@@ -115,7 +129,7 @@ def quantize(type_: int, x: np.ndarray, nthreads: int = 0, requant_fp32_d: bool 
     reference Python ports' conventions (PORT_* bits), golden comparison only"""
     x = np.ascontiguousarray(x, dtype=np.float32)
     k = x.shape[-1]
-    assert k % QK_K == 0
+    assert k % block_values(type_) == 0
     rows = x.reshape(-1, k)
     rs = row_size(type_, k)
     out = np.zeros((rows.shape[0], rs), dtype=np.uint8)
@@ -137,15 +151,23 @@ def dequantize(type_: int, q: np.ndarray, k: int) -> np.ndarray:
     rs = row_size(type_, k)
     rows = q.reshape(-1, rs)
     out = np.zeros((rows.shape[0], k), dtype=np.float32)
+    if type_ == TYPE_F16:
+        return rows.view(np.float16).astype(np.float32).reshape(*q.shape[:-1], k)
     fn = {TYPE_Q4_K: lib().orc_dequantize_row_q4_K, TYPE_Q6_K: lib().orc_dequantize_row_q6_K,
-          TYPE_Q8_K: lib().orc_dequantize_row_q8_K}[type_]
+          TYPE_Q8_K: lib().orc_dequantize_row_q8_K, TYPE_Q4_0: lib().orc_dequantize_row_q4_0,
+          TYPE_Q5_0: lib().orc_dequantize_row_q5_0, TYPE_Q8_0: lib().orc_dequantize_row_q8_0}[type_]
     for r in range(rows.shape[0]):
         fn(_p(rows[r]), _p(out[r]), k)
     return out.reshape(*q.shape[:-1], k)
 
 
 def vec_dot(type_: int, wrow: np.ndarray, q8row: np.ndarray, k: int) -> float:
-    fn = lib().orc_vec_dot_q4_K_q8_K if type_ == TYPE_Q4_K else lib().orc_vec_dot_q6_K_q8_K
+    """ggml's dot of one weight row with one activation row in the type's
+    vec_dot_type (Q8_K bytes for k-quants, Q8_0 bytes for 32-value formats,
+    fp16 values for F16)"""
+    fn = {TYPE_Q4_K: lib().orc_vec_dot_q4_K_q8_K, TYPE_Q6_K: lib().orc_vec_dot_q6_K_q8_K,
+          TYPE_Q4_0: lib().orc_vec_dot_q4_0_q8_0, TYPE_Q5_0: lib().orc_vec_dot_q5_0_q8_0,
+          TYPE_Q8_0: lib().orc_vec_dot_q8_0_q8_0, TYPE_F16: lib().orc_vec_dot_f16}[type_]
     return fn(k, _p(np.ascontiguousarray(wrow)), _p(np.ascontiguousarray(q8row)))
 
 

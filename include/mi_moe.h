@@ -43,7 +43,10 @@ typedef enum {
 
 typedef enum {                     /* ggml_type ids */
     MI_TYPE_F32  = 0,
-    MI_TYPE_F16  = 1,
+    MI_TYPE_F16  = 1,              /* expert tables: fp16 activations (ggml-cpu vec_dot_type F16) */
+    MI_TYPE_Q4_0 = 2,              /*  18 B / 32 values: d f16 | qs[16];          x = d (q - 8)  */
+    MI_TYPE_Q5_0 = 6,              /*  22 B / 32 values: d f16 | qh u32 | qs[16]; x = d (q - 16) */
+    MI_TYPE_Q8_0 = 8,              /*  34 B / 32 values: d f16 | qs[32] i8;       x = d q        */
     MI_TYPE_Q4_K = 12,             /* 144 B / 256 values, convert/q4k.py:9-10  */
     MI_TYPE_Q6_K = 14,             /* 210 B / 256 values, convert/q6k.py:10-11 */
     MI_TYPE_I32  = 26,
@@ -74,7 +77,10 @@ typedef enum {
                                       same float tie (lower id first) */
 } mi_gating;
 
-/* ggml_tensor stand-in: data on the device, ne fastest-first, nb in bytes. */
+/* Expert tables of one layer come from one family: the k-quants (Q4_K, Q6_K),
+ * the 32-value formats with F16 (Q4_0, Q5_0, Q8_0, F16; rows of a multiple
+ * of 32 values, F16 tables 16-byte aligned), or F32.
+ * ggml_tensor stand-in: data on the device, ne fastest-first, nb in bytes. */
 typedef struct {
     void    *data;
     int32_t  type;                 /* mi_type */
@@ -264,7 +270,9 @@ int mi_top_k(mi_moe_ctx *ctx, const mi_tensor *a, int32_t k, mi_tensor *dst, mi_
  * ids I32 ne=[n_used, T]) -> F32 ne=[N, n_used, T]
  * (moondream.cpp:519,537; qwen3omni_model.cpp:769-774; moe_compute.cpp:124-130).
  * dst[:, k, t] = as[:, :, ids[k,t]] . b[:, k % ne11, t].  as types: Q4_K,
- * Q6_K, F32.  k-quant products quantize b to Q8_K first, like ggml-cpu.
+ * Q6_K, Q4_0, Q5_0, Q8_0, F16, F32.  b is first converted to the type's ggml
+ * vec_dot_type, like ggml-cpu: Q8_K for k-quants, Q8_0 for the 32-value
+ * formats, fp16 for F16 (F32 tables take b as given).
  * Ids must lie in [0, E): the dst row of an id outside is written as zeros
  * and the id is counted for mi_moe_ctx_take_errors. */
 int mi_mul_mat_id(mi_moe_ctx *ctx, const mi_tensor *as, const mi_tensor *b, const mi_tensor *ids,
@@ -273,9 +281,12 @@ int mi_mul_mat_id(mi_moe_ctx *ctx, const mi_tensor *as, const mi_tensor *b, cons
 /* ---- weight preparation ----------------------------------------------------
  * quantize_row_q4_K_ref / quantize_row_q6_K_ref (ggml; ported in
  * convert/q4k.py:27-127 and convert/q6k.py:103-193; called through
- * ggml_quantize_chunk in tools/moe_cpu_bench.cpp:141).  src: F32 [nrows][n_per_row]
- * device, dst: nrows * row_size bytes device.  Byte-identical to the CPU
- * restatement of ggml's reference quantizers. */
+ * ggml_quantize_chunk in tools/moe_cpu_bench.cpp:141), quantize_row_q4_0_ref /
+ * q5_0_ref / q8_0_ref and the fp16 rounding (the converters' gguf-py
+ * quantizers, convert/_lib.py:120-130).  src: F32 [nrows][n_per_row] device
+ * (n_per_row a multiple of 256 for k-quants, of 32 otherwise), dst: nrows *
+ * row_size bytes device.  Byte-identical to the CPU restatement of ggml's
+ * reference quantizers. */
 int mi_quantize(mi_moe_ctx *ctx, int32_t type, const float *src, void *dst, int64_t nrows,
                 int64_t n_per_row, mi_stream_t stream);
 
@@ -314,7 +325,9 @@ int  mi_gguf_tensor_info(const mi_gguf *gguf, const char *name, int32_t *type, i
 /* block `block`'s MoE layer uploaded to the current device in one allocation
  * (*device_buffer; free it with mi_dev_free when the layer is no longer
  * used): router (F32), bias if present, expert tables as stored (Q4_K,
- * Q6_K or F32), K from <general.architecture>.expert_used_count, fused
+ * Q6_K, Q8_0, Q5_0, Q4_0, F16 or F32: one family per layer, the k-quants,
+ * the 32-value formats with F16, or F32), K from
+ * <general.architecture>.expert_used_count, fused
  * [h | g] when the block has no ffn_gate_exps.  act: mi_act (the
  * architecture's choice: moondream3 MI_ACT_GELU_ERF_GP1, qwen3omni
  * MI_ACT_SILU). */

@@ -154,6 +154,11 @@ void prof_clock(mi_moe_ctx *c, G2Args &g, int k) {
 }
 
 bool is_kquant(int t) { return t == MI_TYPE_Q4_K || t == MI_TYPE_Q6_K; }
+// 32-value block formats and F16: the k_b32.hip kernels
+bool is_b32(int t) { return t == MI_TYPE_Q4_0 || t == MI_TYPE_Q5_0 || t == MI_TYPE_Q8_0; }
+bool is_b32f(int t) { return is_b32(t) || t == MI_TYPE_F16; }
+// the table families one layer's products may mix: 0 F32, 1 k-quants, 2 the b32 / F16 family
+int type_family(int t) { return is_kquant(t) ? 1 : is_b32f(t) ? 2 : 0; }
 
 size_t type_row_size(int32_t type, int64_t n) {
     switch (type) {
@@ -161,6 +166,9 @@ size_t type_row_size(int32_t type, int64_t n) {
     case MI_TYPE_F16: return (size_t)n * 2;
     case MI_TYPE_Q4_K: return n % QK ? 0 : (size_t)(n / QK) * Q4K_BYTES;
     case MI_TYPE_Q6_K: return n % QK ? 0 : (size_t)(n / QK) * Q6K_BYTES;
+    case MI_TYPE_Q4_0: return n % 32 ? 0 : (size_t)(n / 32) * 18;
+    case MI_TYPE_Q5_0: return n % 32 ? 0 : (size_t)(n / 32) * 22;
+    case MI_TYPE_Q8_0: return n % 32 ? 0 : (size_t)(n / 32) * 34;
     default: return 0;
     }
 }
@@ -168,7 +176,8 @@ size_t type_row_size(int32_t type, int64_t n) {
 // an expert table ne=[K, N, E] with ggml strides
 int check_table(const mi_tensor &t, int64_t K, int64_t N, int64_t E) {
     if (!t.data) return MI_MOE_ERR_NULL;
-    if (t.type != MI_TYPE_Q4_K && t.type != MI_TYPE_Q6_K && t.type != MI_TYPE_F32) return MI_MOE_ERR_TYPE;
+    if (!is_kquant(t.type) && !is_b32f(t.type) && t.type != MI_TYPE_F32) return MI_MOE_ERR_TYPE;
+    if (is_b32f(t.type) && K % 32) return MI_MOE_ERR_UNSUPPORTED;   // whole 32-value blocks (F16: the kernels' unit)
     if (t.ne[0] != K || t.ne[1] != N || t.ne[2] < E || t.ne[3] != 1) return MI_MOE_ERR_SHAPE;
     const size_t rs = type_row_size(t.type, K);
     if (rs == 0) return MI_MOE_ERR_SHAPE;
@@ -178,6 +187,9 @@ int check_table(const mi_tensor &t, int64_t K, int64_t N, int64_t E) {
     if (t.type == MI_TYPE_Q6_K && ((uintptr_t)t.data % 4 || t.nb[1] % 2 || t.nb[2] % 2))
         return MI_MOE_ERR_UNSUPPORTED;
     if (t.type == MI_TYPE_F32 && ((uintptr_t)t.data % 4 || t.nb[1] % 4)) return MI_MOE_ERR_UNSUPPORTED;
+    if (t.type == MI_TYPE_F16 && ((uintptr_t)t.data % 16 || t.nb[1] % 16 || t.nb[2] % 16))
+        return MI_MOE_ERR_UNSUPPORTED;   // F16 rows are read with 16-byte loads
+    if (is_b32(t.type) && ((uintptr_t)t.data % 2 || t.nb[1] % 2 || t.nb[2] % 2)) return MI_MOE_ERR_UNSUPPORTED;
     return MI_MOE_OK;
 }
 
@@ -207,7 +219,8 @@ int check_experts(const mi_tensor &gate, const mi_tensor &up, const mi_tensor &d
         if (up.type != gate.type) return MI_MOE_ERR_TYPE;   // gate/up interchangeable (moe_compute.cpp:114-116)
     }
     TRY(check_table(down, I, D, E));
-    if (is_kquant(gate.type) != is_kquant(down.type)) return MI_MOE_ERR_UNSUPPORTED;   // mixed F32 / k-quant
+    // one family per layer: F32, k-quants, or the 32-value formats with F16
+    if (type_family(gate.type) != type_family(down.type)) return MI_MOE_ERR_UNSUPPORTED;
     return MI_MOE_OK;
 }
 
@@ -364,6 +377,68 @@ bool x_q8_spec(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T, Q8Out &qx)
     return true;
 }
 
+// routed FFN body of a layer with Q4_0 / Q5_0 / Q8_0 / F16 tables (k_b32.hip):
+// the rows converted to each product's ggml vec_dot_type (Q8_0 or fp16), the
+// grouped GEMV below the GEMM threshold, the grouped MFMA GEMM above it, GLU
+// rows in fp32, fp32 slot rows into the combine.  Arguments as run_experts.
+int run_experts_b32(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const int32_t *ids_gu,
+                    const int32_t *ids_dn, const float *w, const float *res, float *out, hipStream_t st,
+                    bool check_ids, const float *add) {
+    const int D = L->n_embd, E = L->n_expert, K = L->n_expert_used, I = L->n_ff;
+    const int64_t rows = T * K;
+    const int max_active = (int)std::min<int64_t>(E, rows);
+    const bool same_ids = ids_gu == ids_dn;
+    const bool gated = act_gated(L->act);
+    const bool gemm = use_gemm(c, T, K, E);
+    const int max_tiles = (int)((rows + G4_BM - 1) / G4_BM + max_active);
+    TRY(launch_dispatch(ids_gu, T, K, E, G4_BM, 1, c->disp[0].view(), st));
+    if (!same_ids) TRY(launch_dispatch(ids_dn, T, K, E, G4_BM, 1, c->disp[1].view(), st));
+    const DispBuf &dg = c->disp[0];
+    const DispBuf &dd = same_ids ? c->disp[0] : c->disp[1];
+    stage_end(c, "dispatch", st);
+    // an activation set in the operand form of a consumer type on this path
+    auto prep_for = [&](int wtype, ActBuf &ab, int pre_act) {
+        B32Prep o;
+        o.pre_act = pre_act;
+        if (wtype == MI_TYPE_F16) { o.mode = B32_PREP_F16; o.xh = ab.h; }
+        else if (gemm) { o.mode = B32_PREP_DQ; o.xh = ab.h; }
+        else { o.mode = B32_PREP_CODES; o.q8 = ab.q8; o.dh = (uint16_t *)ab.bs; }
+        return o;
+    };
+    auto args_for = [&](const ExpertMat &a, const DispBuf &d, const ActBuf &ab, int ne11) {
+        B32Args g = {};
+        g.a = a; g.ne11 = ne11; g.K = K; g.act = L->act; g.I = I;
+        g.q8 = ab.q8; g.dh = (const uint16_t *)ab.bs; g.xh = ab.h;
+        g.counts = d.counts; g.offsets = d.offsets; g.perm = d.perm; g.active_e = d.active_e;
+        g.n_active = d.n_active; g.max_active = max_active;
+        g.tile_e = d.tile_e; g.tile_start = d.tile_start; g.tile_rows = d.tile_rows; g.n_tiles = d.n_tiles;
+        g.max_tiles = max_tiles;
+        return g;
+    };
+    TRY(launch_prep_b32(x, D, T, D, prep_for(L->gate.type, c->ax, 0), st));
+    stage_end(c, "q8_x", st);
+    B32Args a = args_for(as_mat(L->gate), dg, c->ax, 1);
+    if (gated && !L->fused_gate_up) a.b = as_mat(L->up);
+    a.glu = gated ? 1 : 0;
+    a.fused = L->fused_gate_up;
+    a.y = c->f1; a.ldy = I; a.ncols = I;
+    TRY(gemm ? launch_gemm_b32(a, st) : launch_gemv_b32(a, st));
+    stage_end(c, "gate_up", st);
+    // one product (relu^2 experts): its rows are squared on the way to the down operand
+    TRY(launch_prep_b32(c->f1, I, rows, I, prep_for(L->down.type, c->aact, gated ? 0 : MI_ACT_RELU_SQR), st));
+    stage_end(c, "q8_act", st);
+    B32Args d = args_for(as_mat(L->down), dd, c->aact, K);
+    d.glu = 0;
+    d.y = c->z; d.ldy = D; d.ncols = D;
+    TRY(gemm ? launch_gemm_b32(d, st) : launch_gemv_b32(d, st));
+    stage_end(c, "down", st);
+    CombineIds ci;
+    if (check_ids) { ci.a = ids_gu; ci.b = ids_dn; ci.E = E; }
+    TRY(launch_combine(c->z, w, res, out, T, K, D, st, ci, add));
+    stage_end(c, "combine", st);
+    return MI_MOE_OK;
+}
+
 // routed FFN body: ids (device [T][K]; gate/up and down may differ) and
 // weights w [T][K]; x_done: x is already in the x_q8_spec form; check_ids:
 // the ids come from the caller (dead slots are left out of the combine);
@@ -371,6 +446,7 @@ bool x_q8_spec(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T, Q8Out &qx)
 int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const int32_t *ids_gu,
                 const int32_t *ids_dn, const float *w, const float *res, float *out, hipStream_t st,
                 bool x_done = false, bool check_ids = false, const float *add = nullptr) {
+    if (is_b32f(L->gate.type)) return run_experts_b32(c, L, x, T, ids_gu, ids_dn, w, res, out, st, check_ids, add);
     const int D = L->n_embd, E = L->n_expert, K = L->n_expert_used, I = L->n_ff;
     const int64_t rows = T * K;
     const int max_active = (int)std::min<int64_t>(E, rows);
@@ -1093,6 +1169,24 @@ int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const 
     TRY(launch_dispatch((const int32_t *)ids->data, T, (int)n_used, (int)E, G4_BM, 1, dv, st));
     const ExpertMat M = as_mat(*as);
     const float *bp = (const float *)b->data;
+    if (is_b32f(as->type)) {
+        // b in the table type's vec_dot_type (Q8_0 or fp16), then the grouped GEMV or GEMM
+        const bool gemm = use_gemm(c, T, (int)n_used, (int)E);
+        B32Prep o;
+        if (as->type == MI_TYPE_F16) { o.mode = B32_PREP_F16; o.xh = c->ax.h; }
+        else if (gemm) { o.mode = B32_PREP_DQ; o.xh = c->ax.h; }
+        else { o.mode = B32_PREP_CODES; o.q8 = c->ax.q8; o.dh = (uint16_t *)c->ax.bs; }
+        TRY(launch_prep_b32(bp, Kin, T * ne11, Kin, o, st));
+        B32Args a = {};
+        a.a = M; a.glu = 0; a.ne11 = (int)ne11; a.K = (int)n_used;
+        a.q8 = c->ax.q8; a.dh = (const uint16_t *)c->ax.bs; a.xh = c->ax.h;
+        a.counts = dsp.counts; a.offsets = dsp.offsets; a.perm = dsp.perm; a.active_e = dsp.active_e;
+        a.n_active = dsp.n_active; a.max_active = max_active;
+        a.tile_e = dsp.tile_e; a.tile_start = dsp.tile_start; a.tile_rows = dsp.tile_rows; a.n_tiles = dsp.n_tiles;
+        a.max_tiles = max_tiles;
+        a.y = (float *)dst->data; a.ldy = N; a.ncols = N;
+        return gemm ? launch_gemm_b32(a, st) : launch_gemv_b32(a, st);
+    }
     if (as->type == MI_TYPE_F32) {
         GemvArgs a = {};
         a.a = M; a.ne11 = (int)ne11; a.K = (int)n_used;
@@ -1128,6 +1222,12 @@ int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const 
 int mi_quantize(mi_moe_ctx *c, int32_t type, const float *src, void *dst, int64_t nrows, int64_t n_per_row,
                 mi_stream_t stream) {
     if (!c || !src || !dst) return MI_MOE_ERR_NULL;
+    if (is_b32f(type)) {
+        if (nrows < 0 || n_per_row <= 0 || n_per_row % 32) return MI_MOE_ERR_SHAPE;
+        if ((uintptr_t)src % 4 || (type == MI_TYPE_F16 && (uintptr_t)dst % 4)) return MI_MOE_ERR_UNSUPPORTED;
+        HIP_TRY(hipSetDevice(c->device));
+        return launch_quantize_b32(type, src, dst, nrows * (n_per_row / 32), (hipStream_t)stream);
+    }
     if (type != MI_TYPE_Q4_K && type != MI_TYPE_Q6_K) return MI_MOE_ERR_TYPE;
     if (nrows < 0 || n_per_row <= 0 || n_per_row % QK) return MI_MOE_ERR_SHAPE;
     if (type == MI_TYPE_Q4_K && ((uintptr_t)dst % 4)) return MI_MOE_ERR_UNSUPPORTED;

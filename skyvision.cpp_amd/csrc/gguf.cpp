@@ -88,7 +88,7 @@ int scalar_bytes(uint32_t t) {
     }
 }
 
-// bytes of a ggml tensor of these dims (F32, F16, I32, Q4_K, Q6_K), 0 if not
+// bytes of a ggml tensor of these dims (F32, F16, I32, Q4_0, Q5_0, Q8_0, Q4_K, Q6_K), 0 if not
 // one of them; UINT64_MAX if the product overflows (dims come from the file)
 uint64_t tensor_bytes(int32_t type, const int64_t ne[4]) {
     for (int d = 0; d < 4; ++d)
@@ -298,8 +298,15 @@ int mi_gguf_load_moe_layer(const mi_gguf *g, int32_t blk, int32_t act, mi_moe_la
     if (!fused && (gate->ne[0] != D || gate->ne[1] != I || gate->ne[2] != E || gate->type != up->type))
         return MI_MOE_ERR_SHAPE;
     if (down->ne[1] != D || down->ne[2] != E) return MI_MOE_ERR_SHAPE;
+    // expert tables as the converters write them: k-quants, the 32-value block
+    // formats (Q8_0 by default, Q5_0, Q4_0), F16 or F32 (one family per layer:
+    // the forward's validation refuses a mix)
+    auto table_type = [](int32_t t) {
+        return t == MI_TYPE_Q4_K || t == MI_TYPE_Q6_K || t == MI_TYPE_Q4_0 || t == MI_TYPE_Q5_0 ||
+               t == MI_TYPE_Q8_0 || t == MI_TYPE_F16 || t == MI_TYPE_F32;
+    };
     for (const TensorInfo *t : {up, down, fused ? up : gate})
-        if (t->type != MI_TYPE_Q4_K && t->type != MI_TYPE_Q6_K && t->type != MI_TYPE_F32) return MI_MOE_ERR_TYPE;
+        if (!table_type(t->type)) return MI_MOE_ERR_TYPE;
     int64_t K = 0;
     const auto arch = g->strs.find("general.architecture");
     if (arch == g->strs.end() || mi_gguf_get_int(g, (arch->second + ".expert_used_count").c_str(), &K) ||
@@ -349,7 +356,12 @@ int mi_gguf_load_moe_layer(const mi_gguf *g, int32_t blk, int32_t act, mi_moe_la
         m.type = t->type;
         const size_t row = mi_row_size(t->type, t->ne[0]);
         for (int d = 0; d < 4; ++d) m.ne[d] = t->ne[d];
-        m.nb[0] = t->type == MI_TYPE_F32 ? 4 : row / (size_t)(t->ne[0] / 256);
+        switch (t->type) {
+        case MI_TYPE_F32: m.nb[0] = 4; break;
+        case MI_TYPE_F16: m.nb[0] = 2; break;
+        case MI_TYPE_Q4_K: case MI_TYPE_Q6_K: m.nb[0] = row / (size_t)(t->ne[0] / 256); break;
+        default: m.nb[0] = row / (size_t)(t->ne[0] / 32); break;   // 32-value blocks
+        }
         m.nb[1] = row;
         m.nb[2] = row * (size_t)t->ne[1];
         m.nb[3] = m.nb[2] * (size_t)t->ne[2];

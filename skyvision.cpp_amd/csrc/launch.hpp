@@ -190,6 +190,40 @@ constexpr int G4_BM = 192;
 int launch_gemm4(const G2Args &g, hipStream_t st);
 int gemm4_grid(const G2Args &g);   // work-groups launch_gemm4 launches
 
+// ---- 32-value block formats (Q4_0 = 2, Q5_0 = 6, Q8_0 = 8) and F16 (1)
+// expert tables (k_b32.hip)
+// weight rows of 32-value blocks (F16: 32 values per "block"), bit for bit the
+// CPU oracle's ggml _ref quantizers / fp16 rounding
+int launch_quantize_b32(int type, const float *src, void *dst, int64_t nblocks, hipStream_t st);
+// the activation operands of one consumer weight type
+enum { B32_PREP_CODES = 0, B32_PREP_DQ = 1, B32_PREP_F16 = 2 };
+struct B32Prep {
+    int mode;                  // CODES: Q8_0 codes + scales (GEMV of Q4_0/Q5_0/Q8_0); DQ: fp16(d q) rows
+                               // (their GEMM); F16: fp16(x) rows (F16 tables, both paths)
+    int8_t *q8 = nullptr;      // CODES: [rows][K]
+    uint16_t *dh = nullptr;    // CODES: [rows][K/32] fp16 scale bits
+    _Float16 *xh = nullptr;    // DQ / F16: [rows][K]
+    int pre_act = 0;           // 4 (ACT_RELU_SQR): relu(v)^2 first
+};
+int launch_prep_b32(const float *src, int64_t ld, int64_t nrows, int64_t K, const B32Prep &o, hipStream_t st);
+struct B32Args {
+    ExpertMat a, b;            // b: up table (separate gate/up GLU), else unused
+    int glu, fused, act;
+    int64_t I;
+    const int8_t *q8;          // GEMV of Q4_0/Q5_0/Q8_0: Q8_0 codes [rows][K] and
+    const uint16_t *dh;        //   fp16 scales [rows][K/32]
+    const _Float16 *xh;        // GEMM (and F16 GEMV): fp16 rows [rows][K]
+    int ne11, K;
+    const int32_t *counts, *offsets, *perm, *active_e, *n_active;   // GEMV
+    int max_active;
+    const int32_t *tile_e, *tile_start, *tile_rows, *n_tiles;       // GEMM: balanced tiles of G4_BM rows
+    int max_tiles;
+    float *y;                  // rows p (glu: act rows [p][I]), stride ldy
+    int64_t ldy, ncols;
+};
+int launch_gemv_b32(const B32Args &g, hipStream_t st);
+int launch_gemm_b32(const B32Args &g, hipStream_t st);
+
 // Single-token MoE block in one kernel (k_decode.hip).
 struct DecArgs {
     const float *rw, *rb, *x;     // router W [E][D], bias [E] or NULL, tokens [T][D]

@@ -18,6 +18,7 @@ DECODE_CHAIN, DECODE_FUSED_COOPERATIVE, DECODE_FUSED = 0, 1, 2
 DECODE_FUSED_EXCLUSIVE = DECODE_FUSED   # former name
 
 TYPE_F32, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K, TYPE_I32 = 0, 1, 12, 14, 26
+TYPE_Q4_0, TYPE_Q5_0, TYPE_Q8_0 = 2, 6, 8
 ACT_SILU, ACT_GELU_ERF_GP1, ACT_GELU_TANH, ACT_GELU_ERF, ACT_RELU_SQR = 0, 1, 2, 3, 4
 NORM_NONE, NORM_RMS, NORM_LAYER = 0, 1, 2
 GATING_SOFTMAX_TOPK, GATING_SIGMOID_BIAS, GATING_SOFTMAX_ALL = 0, 1, 2
@@ -26,7 +27,7 @@ ABI_VERSION = 2
 OK, ERR_NULL, ERR_SHAPE, ERR_TYPE, ERR_CAPACITY, ERR_HIP = 0, -1, -2, -3, -4, -5
 ERR_UNSUPPORTED, ERR_DEVICE, ERR_ARG, ERR_FORMAT = -6, -7, -8, -9
 QK_K = 256
-BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210}
+BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210, TYPE_Q4_0: 18, TYPE_Q5_0: 22, TYPE_Q8_0: 34}
 STATUS = {0: "ok", -1: "null", -2: "shape", -3: "type", -4: "capacity", -5: "hip",
           -6: "unsupported", -7: "device", -8: "arg"}
 
@@ -244,7 +245,7 @@ def tensor(buf, type_: int, ne, nb=None, offset: int = 0) -> Tensor:
     """ggml-style descriptor; default strides are ggml's contiguous ones."""
     ne = list(ne) + [1] * (4 - len(ne))
     if nb is None:
-        if type_ in (TYPE_Q4_K, TYPE_Q6_K):
+        if type_ in (TYPE_Q4_K, TYPE_Q6_K, TYPE_Q4_0, TYPE_Q5_0, TYPE_Q8_0):
             nb0 = BLOCK_BYTES[type_]
             nb1 = row_size(type_, ne[0])
         else:

@@ -125,15 +125,23 @@ def time_layer_graph(ctx, layers, xs, T, out, steps):
     return ms, wall / steps
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed counter summary
-    (profiles/traffic.json: FETCH_SIZE + WRITE_SIZE per dispatch, scaled by
-    the same counters on a copy of known size); None when not measured."""
+def profile_key(kernel: str, config: int) -> str:
+    """key of a kernel's entry in the committed counter summaries: the kernel
+    name for config 1 (and the decode kernels), name@configN for another
+    prefill config"""
+    return kernel if config == 1 else f"{kernel}@config{config}"
+
+
+def measured_traffic(kernel: str, config: int = 1):
+    """HBM bytes per launch of `kernel` under `config` from the committed
+    counter summary (profiles/traffic.json: FETCH_SIZE + WRITE_SIZE per
+    dispatch, scaled by the same counters on a copy of known size); None when
+    that config was not measured."""
     p = ROOT / "profiles" / "traffic.json"
     if not p.exists():
         return None
     try:
-        return json.loads(p.read_text()).get(kernel, {}).get("bytes_per_launch")
+        return json.loads(p.read_text()).get(profile_key(kernel, config), {}).get("bytes_per_launch")
     except (ValueError, AttributeError):
         return None
 
@@ -149,10 +157,43 @@ def touched_experts(ctx, layer, x, T):
     return int((c > 0).sum()), c
 
 
-def cpu_baseline(spec, layer0: W.GpuLayer, T_sample: int, budget_s: float = 20.0):
+def gpu_reference(ctx, layer, x, T) -> dict:
+    """One forward of `layer` on the device rows x with every routing output:
+    the GPU side of the bench line's parity columns."""
+    spec = layer.spec
+    bufs = dict(sel=M.DeviceBuffer(4 * T * spec.K), counts=M.DeviceBuffer(4 * spec.E),
+                offsets=M.DeviceBuffer(4 * (spec.E + 1)), perm=M.DeviceBuffer(4 * T * spec.K),
+                logits=M.DeviceBuffer(4 * T * spec.E))
+    r = M.Routing()
+    for k, v in bufs.items():
+        setattr(r, k, C.c_void_p(v.addr))
+    out = M.DeviceBuffer(4 * T * spec.D)
+    M.check("forward", ctx.forward(layer.layer, x, T, None, out, r))
+    M.synchronize()
+    shapes = dict(sel=(T, spec.K), counts=(spec.E,), offsets=(spec.E + 1,), perm=(T * spec.K,), logits=(T, spec.E))
+    got = {k: bufs[k].download(np.float32 if k == "logits" else np.int32, shapes[k]) for k in bufs}
+    got["out"] = out.download(np.float32, (T, spec.D))
+    got["x"] = x.download(np.float32, (T, spec.D))
+    return got
+
+
+def parity_columns(gpu: dict, ref: np.ndarray, dbg: dict) -> dict:
+    """BASELINE.md's parity columns: routing bit-exactness and the output's
+    rel-L2 / max-abs against the CPU oracle on the same tokens."""
+    exact = {k: bool(np.array_equal(gpu[k], dbg[k])) for k in ("sel", "counts", "offsets", "perm")}
+    exact["logits"] = bool(np.array_equal(gpu["logits"].view(np.uint32), dbg["logits"].view(np.uint32)))
+    d = (gpu["out"].astype(np.float64) - ref.astype(np.float64)).ravel()
+    return {"routing_bit_exact": all(exact.values()), "routing": exact,
+            "rel_l2": float(np.linalg.norm(d) / np.linalg.norm(ref.astype(np.float64).ravel())),
+            "max_abs": float(np.abs(d).max()), "tolerance_rel_l2": 1e-2,
+            "tokens": int(ref.shape[0])}
+
+
+def cpu_baseline(spec, layer0: W.GpuLayer, T_sample: int, gpu_ref: dict | None = None, budget_s: float = 20.0):
     """CPU oracle (ggml-semantics restatement) on T_sample tokens of the same
     layer; weights copied from the GPU tables (bit-identical to the oracle's
-    own quantizer output)."""
+    own quantizer output).  Its output on the layer's 1024 bench tokens also
+    gives the parity columns against the GPU forward of the same tokens."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import pyoracle as O
     cores = O.physical_cores()
@@ -164,7 +205,14 @@ def cpu_baseline(spec, layer0: W.GpuLayer, T_sample: int, budget_s: float = 20.0
     if "up" in tables:
         L["up"] = tables["up"]
     x = O.fill_normal(T_sample * spec.D, spec.seed, W.S_X, 0.0, 1.0, cores).reshape(T_sample, spec.D)
-    O.moe_forward(L, x, nthreads=cores, debug=False)          # warm
+    parity = None
+    if gpu_ref is not None:
+        ref, dbg = O.moe_forward(L, gpu_ref["x"], nthreads=cores)        # also the warm-up
+        parity = parity_columns(gpu_ref, ref, dbg)
+        log(f"parity vs the CPU oracle on {ref.shape[0]} tokens: routing bit-exact {parity['routing_bit_exact']}, "
+            f"rel-L2 {parity['rel_l2']:.3e}, max-abs {parity['max_abs']:.3e}")
+    else:
+        O.moe_forward(L, x, nthreads=cores, debug=False)          # warm
     times = []
     t_start = time.perf_counter()
     while len(times) < 10 and (time.perf_counter() - t_start) < budget_s:
@@ -172,10 +220,11 @@ def cpu_baseline(spec, layer0: W.GpuLayer, T_sample: int, budget_s: float = 20.0
         O.moe_forward(L, x, nthreads=cores, debug=False)
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
-    return {"value": T_sample / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+    res = {"value": T_sample / med, "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"{spec.name}: {T_sample} tokens x {len(times)} runs (median {med * 1e3:.1f} ms), "
                       f"ggml-semantics CPU restatement (Q8_K activations x k-quant integer dots), "
                       f"{cores} threads on {host_cpu()}"}
+    return res, parity
 
 
 def host_cpu() -> str:
@@ -369,16 +418,16 @@ def config4_stack(n_layers: int = 24, T_prefill: int = 2048, n_decode: int = 256
     return res
 
 
-def mfma_counters(kernel: str):
-    """MFMA utilisation of `kernel` from the committed counter summary
-    (profiles/mfma_counters.json: rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES and
-    SQ_INSTS_VALU_MFMA_MOPS_F16 per dispatch, and the shader clock measured
-    under the kernel); None when not measured."""
+def mfma_counters(kernel: str, config: int = 1):
+    """MFMA utilisation of `kernel` under `config` from the committed counter
+    summary (profiles/mfma_counters.json: rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES
+    and SQ_INSTS_VALU_MFMA_MOPS_F16 per dispatch, and the shader clock
+    measured under the kernel); None when that config was not measured."""
     p = ROOT / "profiles" / "mfma_counters.json"
     if not p.exists():
         return None
     try:
-        return json.loads(p.read_text()).get(kernel)
+        return json.loads(p.read_text()).get(profile_key(kernel, config))
     except (ValueError, AttributeError):
         return None
 
@@ -426,7 +475,7 @@ def prefill_line(config: int, args, primary: bool) -> dict:
     srt = np.sort(counts)[::-1]
     roof = {"bound": "mfma", "kernel": "k_g4_glu (gate/up grouped GEMM + GLU)",
             "achieved": achieved, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
-            "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": measured_traffic("k_g4_glu"),
+            "frac": achieved / PEAK_MFMA_TFLOPS, "traffic": measured_traffic("k_g4_glu", config),
             "kernel_ms": gu_ms, "flops_per_launch": gu_flops}
     clk = clocks.get("gate_up")
     if clk:
@@ -437,7 +486,7 @@ def prefill_line(config: int, args, primary: bool) -> dict:
         roof["measured_clock_ghz"] = clk
         roof["peak_at_measured_clock"] = peak_clk
         roof["frac_of_peak_at_measured_clock"] = achieved / peak_clk
-    mc = mfma_counters("k_g4_glu")
+    mc = mfma_counters("k_g4_glu", config)
     if mc:
         # MFMA busy share of the SIMD cycles under the kernel (committed profile)
         roof["mfma_busy_frac_profiled"] = mc.get("mfma_busy_frac")
@@ -462,6 +511,7 @@ def prefill_line(config: int, args, primary: bool) -> dict:
                          "rows_per_expert_min_max": [int(counts[counts > 0].min()), int(counts.max())]},
         "extra": extra,
         "layer0": layers[0],
+        "gpu_ref": gpu_reference(ctx, layers[0], xs[0], T) if primary and not args.no_cpu else None,
     }
     del layers, xs, out
     ctx.close()
@@ -559,7 +609,7 @@ def main() -> int:
     layers0 = line["layer0"]
     if args.config == 1 and not args.no_sweeps:
         c2 = prefill_line(2, args, primary=False)
-        result["config2"] = {k: v for k, v in c2.items() if k not in ("extra", "layer0")}
+        result["config2"] = {k: v for k, v in c2.items() if k not in ("extra", "layer0", "gpu_ref")}
 
     if not args.no_decode:
         dspec = W.CONFIGS[0]["spec"]
@@ -608,8 +658,10 @@ def main() -> int:
         dctx.close()
 
     if not args.no_cpu:
-        cb = cpu_baseline(layers0.spec, layers0, args.cpu_tokens)
+        cb, parity = cpu_baseline(layers0.spec, layers0, args.cpu_tokens, line["gpu_ref"])
         result["cpu_baseline"] = cb
+        if parity is not None:
+            result["parity"] = parity
     del layers0, line
 
     if not args.no_sweeps:

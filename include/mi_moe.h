@@ -351,6 +351,13 @@ int mi_moe_ctx_stage_clock(mi_moe_ctx *ctx, const char *stage, double *ghz, int 
  * tokens on, the grouped GEMV below.  0 (the default) picks by shape: the
  * GEMM when 4 * T * K > 5 * E (more than 1.25 dispatched rows per expert). */
 int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *ctx, int64_t min_tokens_for_gemm);
+/* Row tiles of the grouped GEMMs of Q4_K gate/up layers: 0 (the default) by
+ * shape, 32-row tiles when the call dispatches at most 8 rows per expert on
+ * average (qwen3omni up to 128 tokens, moondream3 up to 64: two work-groups
+ * per CU keep twice the weight stream in flight), 192-row tiles above; 1
+ * 192-row tiles, 2 32-row tiles at every size.  Same results bit for bit
+ * (the same per-row arithmetic); this only picks the kernel. */
+int mi_moe_ctx_set_gemm_tiles(mi_moe_ctx *ctx, int kind);
 /* Schedule of decode calls of mi_moe_forward (1 token, and batches of 2..16
  * tokens).  The fused mode runs the whole block in one kernel of one
  * work-group per CU, when the layer fits it (Q4_K gate/up, Q4_K or Q6_K down,

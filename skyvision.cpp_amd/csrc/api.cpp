@@ -107,6 +107,7 @@ struct mi_moe_ctx {
     int32_t *bad_total = nullptr;   // caller ids outside [0, E) since the last take
     int32_t *range_total = nullptr; // GEMM-path Q8_K blocks saturated at the fp16 range
     int64_t gemm_threshold = 0;   // 0: the shape rule of use_gemm
+    int gemm_tiles = 0;           // 4-wave GEMM row tiles: 0 by shape, 1 G4_BM, 2 G4_BM_SMALL
     // single-token fused kernel (k_decode.hip)
     int fused_decode = MI_DECODE_FUSED;
     int dec_grid = 0;          // fused decode grid (one WG per CU), 0: unavailable
@@ -365,6 +366,17 @@ bool gemm_path(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T) {
 // else the 16x16x32 GEMM with its fused GLU + Q8_K epilogue (Q6_K gate/up)
 bool g4_path(const mi_moe_layer *L) { return L->gate.type == MI_TYPE_Q4_K || !act_gated(L->act); }
 
+// Row tiles of the 4-wave GEMMs: 32-row tiles (a quarter of the LDS: two
+// work-groups per CU keep twice the weight stream in flight) when the call
+// dispatches at most G4_SMALL_ROWS rows per expert on average (qwen3omni up
+// to 128 tokens, moondream3 up to 64), where the products are bound by that
+// stream; 192-row balanced tiles above.
+constexpr int64_t G4_SMALL_ROWS = 8;
+bool g4_small_tiles(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T) {
+    if (c->gemm_tiles) return c->gemm_tiles == 2;
+    return T * L->n_expert_used <= G4_SMALL_ROWS * L->n_expert;
+}
+
 bool x_q8_spec(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T, Q8Out &qx) {
     if (!is_kquant(L->gate.type)) return false;
     qx = Q8Out{};
@@ -457,7 +469,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
     // GEMM M-tiles: balanced tiles of at most G4_BM rows for the 4-wave GEMMs,
     // GEMM_BM-row tiles otherwise
     const bool g4 = gemm && g4_path(L);
-    const int bm = g4 ? G4_BM : GEMM_BM;
+    const int bm = !g4 ? GEMM_BM : g4_small_tiles(c, L, T) ? G4_BM_SMALL : G4_BM;
     const int max_tiles = (int)((rows + bm - 1) / bm + max_active);
 
     TRY(launch_dispatch(ids_gu, T, K, E, bm, g4, c->disp[0].view(), st));
@@ -544,6 +556,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         a.xh = c->ax.h; a.ne11 = 1; a.K = K;
         a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.tile_e = dg.tile_e;
         a.tile_r0 = dg.tile_r0; a.tile_start = dg.tile_start; a.tile_rows = dg.tile_rows; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
+        a.bm = bm;
         a.y = c->f1; a.ldy = I; a.ncols = I; a.xrows = T;
         // gated: the GLU rows as fp16 (half the bytes of their round trip to
         // the Q8_K pass; saturation at the fp16 range is counted)
@@ -561,6 +574,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         d.a = down; d.glu = 0; d.xh = c->aact.h; d.ne11 = K; d.K = K;
         d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
         d.tile_r0 = dd.tile_r0; d.tile_start = dd.tile_start; d.tile_rows = dd.tile_rows; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles; d.xrows = (int64_t)T * K;
+        d.bm = bm;
         // the slot rows as fp16 (half the bytes of the round trip to the
         // combine; saturation at the fp16 range is counted)
         d.y = c->z; d.yh = zh = (_Float16 *)c->z; d.range_total = c->range_total; d.ldy = D; d.ncols = D;
@@ -636,7 +650,7 @@ constexpr size_t ws_bytes(int64_t max_tokens, int64_t D, int64_t I, int64_t E, i
     const int64_t kmax = D > I ? D : I;
     const int64_t kmax_q = (kmax + QK - 1) / QK * QK;
     const int64_t wide = (D > 2 * I ? D : 2 * I) > kmax ? (D > 2 * I ? D : 2 * I) : kmax;
-    const int64_t tiles = (rows + GEMM_BM - 1) / GEMM_BM + (E < rows ? E : rows);
+    const int64_t tiles = (rows + G4_BM_SMALL - 1) / G4_BM_SMALL + (E < rows ? E : rows);
     const int64_t iq = (I + QK - 1) / QK * QK;
     size_t need = 0;
     need += carve_size<float>(max_tokens * E) + carve_size<int32_t>(rows) + carve_size<float>(rows);
@@ -666,7 +680,7 @@ bool carve_workspace(mi_moe_ctx *c, char *base, int64_t max_tokens, int32_t D, i
     const int64_t kmax = std::max<int64_t>(D, I);
     const int64_t kmax_q = (kmax + QK - 1) / QK * QK;
     const int64_t wide = std::max<int64_t>(std::max<int64_t>(D, 2LL * I), kmax);
-    const int64_t tiles = (rows + GEMM_BM - 1) / GEMM_BM + std::min<int64_t>(E, rows);
+    const int64_t tiles = (rows + G4_BM_SMALL - 1) / G4_BM_SMALL + std::min<int64_t>(E, rows);
     const int64_t iq = (I + QK - 1) / QK * QK;
     char *q = base;
     c->logits = carve<float>(q, max_tokens * E);
@@ -826,6 +840,13 @@ int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *c, int64_t t) {
     if (!c) return MI_MOE_ERR_NULL;
     if (t < 0) return MI_MOE_ERR_ARG;
     c->gemm_threshold = t;
+    return MI_MOE_OK;
+}
+
+int mi_moe_ctx_set_gemm_tiles(mi_moe_ctx *c, int kind) {
+    if (!c) return MI_MOE_ERR_NULL;
+    if (kind < 0 || kind > 2) return MI_MOE_ERR_ARG;
+    c->gemm_tiles = kind;
     return MI_MOE_OK;
 }
 

@@ -46,7 +46,6 @@ constexpr int G4_WAVES = 4;
 constexpr int G4_THREADS = G4_WAVES * 64;
 constexpr int G4_NWG = 256;            // weight rows per work-group
 constexpr int G4_SK = 128;             // K values per stage
-constexpr int G4_AST = G4_BM * G4_SK;  // halfs per activation stage (48 KB)
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -109,17 +108,19 @@ __device__ __forceinline__ int g4_rows_load(const G2Args &g, const G4Tile &t) {
 // stay in flight, so the K loop's first activation loads go out while they
 // land (__syncthreads would wait for them: one more round trip before the
 // first MFMA)
+template <int BM>
 __device__ __forceinline__ void g4_rows_publish(const G2Args &g, int p, int *s_arow) {
-    if (threadIdx.x < G4_BM) s_arow[threadIdx.x] = p < 0 ? 0 : (g.ne11 == 1 ? p / g.K : p);
+    if (threadIdx.x < BM) s_arow[threadIdx.x] = p < 0 ? 0 : (g.ne11 == 1 ? p / g.K : p);
     lds_barrier();
 }
 
 // after the K loop (every load of this wave landed): the rows' slot indices
 // to LDS, in the first activation buffer once no wave has a load in flight
+template <int BM>
 __device__ __forceinline__ const int *g4_publish_rows(_Float16 *As0, int p) {
     int *s_p = (int *)As0;
     __syncthreads();
-    if (threadIdx.x < G4_BM) s_p[threadIdx.x] = p;
+    if (threadIdx.x < BM) s_p[threadIdx.x] = p;
     __syncthreads();
     return s_p;
 }
@@ -390,9 +391,9 @@ __device__ __forceinline__ void g4_stage_sync() {
 // weight operand, its share of the dequantization of the next operand, during
 // column tile 0 the activation operand of row tile rt for the next step, and
 // extra(slot) (loads and scales for what comes next).
-template <int WT, int NRT, typename Extra>
+template <int WT, int NRT, int NA, typename Extra>
 __device__ __forceinline__ void g4_stage(const _Float16 *st, uint32_t abase, const G4W<WT> &w, const G4Sc<WT> &sc,
-                                         uint32_t sh, int h, f32x16 (&acc)[G4_BM / 32][2], Extra &&extra) {
+                                         uint32_t sh, int h, f32x16 (&acc)[NA][2], Extra &&extra) {
     const char *stb = (const char *)st;
     half8_t A[2][NRT];
 #pragma unroll
@@ -438,10 +439,10 @@ __device__ __forceinline__ void g4_stage(const _Float16 *st, uint32_t abase, con
 // data; the epilogue waits for them): measured faster than skipping them
 // behind a uniform test per block, which costs the stage code more than the
 // loads cost.
-template <int WT, int NRT>
+template <int WT, int NRT, int NA>
 __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_t arowbytes, const G4WDma<WT> &dm,
                                            const uint32_t (&wsh)[2], uint8_t *W, int nb, int wave, int lane,
-                                           _Float16 *As0, _Float16 *As1, f32x16 (&acc)[G4_BM / 32][2]) {
+                                           _Float16 *As0, _Float16 *As1, f32x16 (&acc)[NA][2]) {
     using F = G4Fmt<WT>;
     constexpr int NW = 2 * F::NLD;
     const int l32 = lane & 31, g2 = lane >> 5;
@@ -449,7 +450,7 @@ __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_
     uint32_t aoff[2 * NRT];
     g4_aoffsets<NRT>(s_arow, wave, lane, arowbytes, aoff);
 #pragma unroll
-    for (int rt = 0; rt < G4_BM / 32; ++rt)
+    for (int rt = 0; rt < NA; ++rt)
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
@@ -491,18 +492,23 @@ __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_
     }
 }
 
-// one specialization per row-tile count (branch once per work-group)
-template <int WT>
+// one specialization per row-tile count (branch once per work-group); NA
+// row tiles of accumulators (the tile size's)
+template <int WT, int NA>
 __device__ __forceinline__ void g4_kloop(rsrc_t rx, const int *s_arow, uint32_t arowbytes, const G4WDma<WT> &dm,
                                          const uint32_t (&wsh)[2], uint8_t *W, int nb, int wave, int lane, int nrt,
-                                         _Float16 *As0, _Float16 *As1, f32x16 (&acc)[G4_BM / 32][2]) {
-    switch (nrt) {
-    case 1: g4_kloop_n<WT, 1>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
-    case 2: g4_kloop_n<WT, 2>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
-    case 3: g4_kloop_n<WT, 3>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
-    case 4: g4_kloop_n<WT, 4>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
-    case 5: g4_kloop_n<WT, 5>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
-    default: g4_kloop_n<WT, 6>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
+                                         _Float16 *As0, _Float16 *As1, f32x16 (&acc)[NA][2]) {
+    if constexpr (NA == 1) {
+        g4_kloop_n<WT, 1>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc);
+    } else {
+        switch (nrt) {
+        case 1: g4_kloop_n<WT, 1>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
+        case 2: g4_kloop_n<WT, 2>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
+        case 3: g4_kloop_n<WT, 3>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
+        case 4: g4_kloop_n<WT, 4>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
+        case 5: g4_kloop_n<WT, 5>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
+        default: g4_kloop_n<WT, 6>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
+        }
     }
 }
 
@@ -519,8 +525,8 @@ __device__ __forceinline__ void g4_coords(int nct, int &tile, int &ctile) {
 // tile 0 holds their h (gate) rows, column tile 1 their g (up) rows; the GLU
 // values go out as rows (fp32 to y, or fp16 to yh), whose Q8_K for the down
 // product needs whole 256-column blocks, which span two work-groups.
-template <int ACT>
-__device__ __forceinline__ void g4_glu_store(const G2Args &g, const f32x16 (&acc)[G4_BM / 32][2], const G4Tile &t,
+template <int ACT, int NA>
+__device__ __forceinline__ void g4_glu_store(const G2Args &g, const f32x16 (&acc)[NA][2], const G4Tile &t,
                                              int ctile, int wave, int lane, const int *s_p, _Float16 *As0,
                                              _Float16 *As1) {
     // through LDS: the wave's 32 GLU columns of every row into the activation
@@ -530,12 +536,12 @@ __device__ __forceinline__ void g4_glu_store(const G2Args &g, const f32x16 (&acc
     if (g.yh) {
         bool over = false;
 #pragma unroll
-        for (int rt = 0; rt < G4_BM / 32; ++rt) {
+        for (int rt = 0; rt < NA; ++rt) {
             if (rt >= t.nrt) break;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
-                _Float16 *row = m < G4_BM / 2 ? As0 + m * 256 : As1 + (m - G4_BM / 2) * 256;
+                _Float16 *row = m < (16 * NA) ? As0 + m * 256 : As1 + (m - (16 * NA)) * 256;
                 const float v = act_pair_fast<ACT>(acc[rt][0][i], acc[rt][1][i]);
                 over = over || !(fabsf(v) <= kF16Max);
                 row[32 * wave + l32] = f16_sat(v);
@@ -545,25 +551,25 @@ __device__ __forceinline__ void g4_glu_store(const G2Args &g, const f32x16 (&acc
         __syncthreads();
         for (int idx = threadIdx.x; idx < t.mrows * 16; idx += G4_THREADS) {
             const int r = idx >> 4, c = idx & 15;
-            const _Float16 *row = r < G4_BM / 2 ? As0 + r * 256 : As1 + (r - G4_BM / 2) * 256;
+            const _Float16 *row = r < (16 * NA) ? As0 + r * 256 : As1 + (r - (16 * NA)) * 256;
             *(uint4 *)(g.yh + (int64_t)s_p[r] * g.ldy + (int64_t)ctile * 128 + 8 * c) = *(const uint4 *)(row + 8 * c);
         }
         return;
     }
 #pragma unroll
-    for (int rt = 0; rt < G4_BM / 32; ++rt) {
+    for (int rt = 0; rt < NA; ++rt) {
         if (rt >= t.nrt) break;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
-            float *row = (float *)(m < G4_BM / 2 ? As0 + m * 256 : As1 + (m - G4_BM / 2) * 256);
+            float *row = (float *)(m < (16 * NA) ? As0 + m * 256 : As1 + (m - (16 * NA)) * 256);
             row[32 * wave + l32] = act_pair_fast<ACT>(acc[rt][0][i], acc[rt][1][i]);
         }
     }
     __syncthreads();
     for (int idx = threadIdx.x; idx < t.mrows * 32; idx += G4_THREADS) {
         const int r = idx >> 5, c = idx & 31;
-        const float *row = (const float *)(r < G4_BM / 2 ? As0 + r * 256 : As1 + (r - G4_BM / 2) * 256);
+        const float *row = (const float *)(r < (16 * NA) ? As0 + r * 256 : As1 + (r - (16 * NA)) * 256);
         *(float4 *)(g.y + (int64_t)s_p[r] * g.ldy + (int64_t)ctile * 128 + 4 * c) = *(const float4 *)(row + 4 * c);
     }
 }
@@ -580,9 +586,15 @@ __device__ __forceinline__ void g4_clock(const G2Args &g, int slot, bool live) {
     }
 }
 
-__global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) k_g4_glu(G2Args g) {
-    __shared__ __attribute__((aligned(1024))) _Float16 As0[G4_AST];
-    __shared__ __attribute__((aligned(1024))) _Float16 As1[G4_AST];
+// BM: tile rows (G4_BM; G4_BM_SMALL for few rows per expert: a quarter of
+// the LDS, so that two work-groups share a CU and keep twice the weight
+// stream in flight)
+template <int BM>
+__global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, BM == G4_BM ? 1 : 2)))
+k_g4_glu(G2Args g) {
+    constexpr int NA = BM / 32;
+    __shared__ __attribute__((aligned(1024))) _Float16 As0[BM * G4_SK];
+    __shared__ __attribute__((aligned(1024))) _Float16 As1[BM * G4_SK];
     __shared__ __attribute__((aligned(1024))) uint8_t Ws[G4_WAVES][g4_wregion<12>()];
     int tile, ctile;
     g4_coords((int)(g.I / 128), tile, ctile);
@@ -608,17 +620,17 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     // the activation rows live in the second activation buffer until the K
     // loop has computed its load offsets (its first write comes later)
     int *s_arow = (int *)As1;
-    g4_rows_publish(g, my_p, s_arow);
+    g4_rows_publish<BM>(g, my_p, s_arow);
     const uint32_t wsh[2] = {0u, 0u};
-    f32x16 acc[G4_BM / 32][2];
-    g4_kloop<12>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc);
+    f32x16 acc[NA][2];
+    g4_kloop<12, NA>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc);
     __builtin_amdgcn_s_waitcnt(0);   // no load may land in LDS after the work-group ends
-    const int *s_p = g4_publish_rows((_Float16 *)&Ws[0][0], my_p);   // the row table in the weight region
+    const int *s_p = g4_publish_rows<BM>((_Float16 *)&Ws[0][0], my_p);   // the row table in the weight region
     switch (g.act) {
-    case 0: g4_glu_store<0>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
-    case 1: g4_glu_store<1>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
-    case 2: g4_glu_store<2>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
-    default: g4_glu_store<3>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
+    case 0: g4_glu_store<0, NA>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
+    case 1: g4_glu_store<1, NA>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
+    case 2: g4_glu_store<2, NA>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
+    default: g4_glu_store<3, NA>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
     }
     g4_clock(g, 1, true);
 }
@@ -627,10 +639,12 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
 // y[p][n] = sum_k x[p][k] w[n][k] for the tile's rows p; wave w owns weight
 // rows 256 ctile + 64 w + 32 ct + l32 (rows past ncols read zeros past the
 // matrix's resource or unused bytes, and are not stored).
-template <int WT>
-__global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) k_g4_store(G2Args g) {
-    __shared__ __attribute__((aligned(1024))) _Float16 As0[G4_AST];
-    __shared__ __attribute__((aligned(1024))) _Float16 As1[G4_AST];
+template <int WT, int BM>
+__global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, BM == G4_BM ? 1 : 2)))
+k_g4_store(G2Args g) {
+    constexpr int NA = BM / 32;
+    __shared__ __attribute__((aligned(1024))) _Float16 As0[BM * G4_SK];
+    __shared__ __attribute__((aligned(1024))) _Float16 As1[BM * G4_SK];
     __shared__ __attribute__((aligned(1024))) uint8_t Ws[G4_WAVES][g4_wregion<WT>()];
     int tile, ctile;
     g4_coords((int)((g.ncols + G4_NWG - 1) / G4_NWG), tile, ctile);
@@ -655,11 +669,11 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
     const G4WDma<WT> dm = g4_wdma<WT>(r, r, rowbase, rb, mis, lane);
     g4_issue_w0<WT>(dm, Ws[wave]);
     int *s_arow = (int *)As1;   // as in k_g4_glu
-    g4_rows_publish(g, my_p, s_arow);
+    g4_rows_publish<BM>(g, my_p, s_arow);
     // byte offset of the lane's own rows (Q6_K block alignment)
     const uint32_t wsh[2] = {mis + (uint32_t)(n0 + l32) * rb, mis + (uint32_t)(n0 + 32 + l32) * rb};
-    f32x16 acc[G4_BM / 32][2];
-    g4_kloop<WT>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc);
+    f32x16 acc[NA][2];
+    g4_kloop<WT, NA>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc);
     __builtin_amdgcn_s_waitcnt(0);   // no load may land in LDS after the work-group ends
     // rows 32 rt + 8 (i / 4) + 4 g2 + i % 4, columns n0 + 32 ct + l32
     if (g.yh) {
@@ -667,15 +681,15 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
         // activation buffers (rows 0-95 in As0, 96-191 in As1, 512 bytes per
         // row), then whole 512-byte rows out in 16-byte pieces (full lines
         // instead of 64-byte runs); the row table lives in the weight region
-        const int *s_p = g4_publish_rows((_Float16 *)&Ws[0][0], my_p);
+        const int *s_p = g4_publish_rows<BM>((_Float16 *)&Ws[0][0], my_p);
         bool over = false;
 #pragma unroll
-        for (int rt = 0; rt < G4_BM / 32; ++rt) {
+        for (int rt = 0; rt < NA; ++rt) {
             if (rt >= nrt) break;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
-                _Float16 *row = m < G4_BM / 2 ? As0 + m * G4_NWG : As1 + (m - G4_BM / 2) * G4_NWG;
+                _Float16 *row = m < (BM / 2) ? As0 + m * G4_NWG : As1 + (m - (BM / 2)) * G4_NWG;
 #pragma unroll
                 for (int ct = 0; ct < 2; ++ct) {
                     const float v = acc[rt][ct][i];
@@ -688,13 +702,13 @@ __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu
         __syncthreads();
         for (int idx = threadIdx.x; idx < t.mrows * (G4_NWG / 8); idx += G4_THREADS) {
             const int r = idx / (G4_NWG / 8), c = idx % (G4_NWG / 8);
-            const _Float16 *row = r < G4_BM / 2 ? As0 + r * G4_NWG : As1 + (r - G4_BM / 2) * G4_NWG;
+            const _Float16 *row = r < (BM / 2) ? As0 + r * G4_NWG : As1 + (r - (BM / 2)) * G4_NWG;
             *(uint4 *)(g.yh + (int64_t)s_p[r] * g.ldy + (int64_t)ctile * G4_NWG + 8 * c) = *(const uint4 *)(row + 8 * c);
         }
     } else {
-        const int *s_p = g4_publish_rows(As0, my_p);
+        const int *s_p = g4_publish_rows<BM>(As0, my_p);
 #pragma unroll
-        for (int rt = 0; rt < G4_BM / 32; ++rt) {
+        for (int rt = 0; rt < NA; ++rt) {
             if (rt >= nrt) break;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
@@ -734,16 +748,21 @@ int launch_gemm4(const G2Args &g, hipStream_t st) {
         if ((uintptr_t)g.a.data % 4 || g.a.mat_bytes % 4 || g.a.row_bytes % 4) return -6;
         if (!g.fused && ((uintptr_t)g.b.data % 4 || g.b.mat_bytes % 4)) return -6;
         const int nct = (int)(g.I / 128);
-        hipLaunchKernelGGL(k_g4_glu, dim3((unsigned)(8 * nct * ntile8)), dim3(G4_THREADS), 0, st, g);
+        const dim3 grid((unsigned)(8 * nct * ntile8));
+        if (g.bm == G4_BM_SMALL) hipLaunchKernelGGL(k_g4_glu<G4_BM_SMALL>, grid, dim3(G4_THREADS), 0, st, g);
+        else hipLaunchKernelGGL(k_g4_glu<G4_BM>, grid, dim3(G4_THREADS), 0, st, g);
     } else {
         const int nct = (int)((g.ncols + G4_NWG - 1) / G4_NWG);
         const dim3 grid((unsigned)(8 * nct * ntile8));
         if (g.yh && (g.ncols % G4_NWG || g.ldy % 8 || (uintptr_t)g.yh % 16)) return -6;
+        const bool sm = g.bm == G4_BM_SMALL;
         if (g.a.type == 12) {
             if ((uintptr_t)g.a.data % 4 || g.a.mat_bytes % 4 || g.a.row_bytes % 4) return -6;
-            hipLaunchKernelGGL(k_g4_store<12>, grid, dim3(G4_THREADS), 0, st, g);
+            if (sm) hipLaunchKernelGGL((k_g4_store<12, G4_BM_SMALL>), grid, dim3(G4_THREADS), 0, st, g);
+            else hipLaunchKernelGGL((k_g4_store<12, G4_BM>), grid, dim3(G4_THREADS), 0, st, g);
         } else if (g.a.type == 14) {
-            hipLaunchKernelGGL(k_g4_store<14>, grid, dim3(G4_THREADS), 0, st, g);
+            if (sm) hipLaunchKernelGGL((k_g4_store<14, G4_BM_SMALL>), grid, dim3(G4_THREADS), 0, st, g);
+            else hipLaunchKernelGGL((k_g4_store<14, G4_BM>), grid, dim3(G4_THREADS), 0, st, g);
         } else {
             return -3;
         }

@@ -170,6 +170,7 @@ struct G2Args {
     const int32_t *counts, *offsets, *perm, *tile_e, *tile_r0, *n_tiles;
     const int32_t *tile_start, *tile_rows;   // the tiles' perm starts and row counts
     int max_tiles;
+    int bm;               // tile rows of the dispatch: G4_BM, or G4_BM_SMALL (few rows per expert)
     int64_t xrows;        // rows of xh (glu = 1: tokens)
     float *y;
     int64_t ldy;
@@ -187,6 +188,7 @@ struct G2Args {
     int clk_n;            // work-groups clk holds
 };
 constexpr int G4_BM = 192;
+constexpr int G4_BM_SMALL = 32;   // tiles of few rows per expert (G2Args::bm)
 int launch_gemm4(const G2Args &g, hipStream_t st);
 int gemm4_grid(const G2Args &g);   // work-groups launch_gemm4 launches
 

@@ -105,6 +105,7 @@ SYMBOLS = {
     "mi_moe_ctx_stage_times": ([P, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_float),
                                 C.POINTER(C.c_int)], C.c_int),
     "mi_moe_ctx_set_gemm_threshold": ([P, i64], C.c_int),
+    "mi_moe_ctx_set_gemm_tiles": ([P, C.c_int], C.c_int),
     "mi_moe_ctx_set_fused_decode": ([P, C.c_int], C.c_int),
     "mi_moe_ctx_set_decode_rescue": ([P, C.c_int], C.c_int),
     "mi_row_size": ([i32, i64], C.c_size_t),
@@ -273,6 +274,10 @@ class Context:
     def set_gemm_threshold(self, t: int) -> None:
         """GEMM from t tokens on; 0 = by shape (GEMM when 4 T K >= 5 E)."""
         call("mi_moe_ctx_set_gemm_threshold", self.h, t)
+
+    def set_gemm_tiles(self, kind: int) -> None:
+        """Q4_K-gate GEMM row tiles: 0 by shape, 1 192-row, 2 32-row"""
+        call("mi_moe_ctx_set_gemm_tiles", self.h, int(kind))
 
     def set_fused_decode(self, mode) -> None:
         """False / DECODE_CHAIN, True / DECODE_FUSED (DECODE_FUSED_COOPERATIVE is

@@ -193,3 +193,36 @@ def test_config4_stack_and_fed_back_decode():
     b_ids, waits = ctx.take_errors()
     assert (b_ids, waits) == (0, 0)
     ctx.close()
+
+
+@pytest.mark.parametrize("name,T", [("qo_cfg3", 32), ("qo_cfg3", 64), ("md_cfg1", 300), ("md_cfg1", 40)])
+def test_gemm_row_tiles(name, T):
+    """Both row-tile sizes of the 4-wave GEMMs at one size: 32-row tiles (two
+    work-groups per CU; the default up to 8 dispatched rows per expert) and
+    192-row balanced tiles give the same bits (each output's K order is the
+    same), and match the oracle."""
+    spec = W.CONFIGS[3]["spec"] if name == "qo_cfg3" else W.CONFIGS[1]["spec"]
+    log(f"case {name} T={T} row tiles 32 / 192")
+    ctx = M.Context(0)
+    ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
+    g = W.GpuLayer(ctx, spec)
+    x = W.gen_x(ctx, spec, T)
+    xh = x.download(np.float32, (T, spec.D))
+    ref, dbg = O.moe_forward(_oracle_dict(g), xh)
+    ctx.set_fused_decode(M.DECODE_CHAIN)
+    ctx.set_gemm_threshold(1)
+    outs = []
+    for kind in (1, 2):
+        ctx.set_gemm_tiles(kind)
+        out = M.DeviceBuffer(4 * T * spec.D)
+        bufs, r = _routing_buffers(T, spec.E, spec.K)
+        M.check("forward", ctx.forward(g.layer, x, T, None, out, r))
+        got = out.download(np.float32, (T, spec.D))
+        _check_routing(bufs, dbg, T, spec.E, spec.K, f"{name} T={T} tiles {kind}")
+        e = rel_l2(got, ref)
+        log(f"{name} T={T} row tiles {'192' if kind == 1 else '32'}: rel-L2 {e:.3e} max-abs {max_abs(got, ref):.3e}")
+        assert e <= TOL
+        outs.append(got)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert ctx.take_all_errors() == (0, 0, 0)
+    ctx.close()

@@ -213,7 +213,7 @@ int mi_moe_forward_router_input(mi_moe_ctx *ctx, const mi_moe_layer *layer, cons
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  It calls no hipMalloc / hipFree or any
  * allocating routine: its workspace is one file-scope device array of the
- * library per GPU, 16,986,368 bytes, held until the process ends, sized for
+ * library per GPU, 16,952,832 bytes, held until the process ends, sized for
  * calls of at most MI_NOALLOC_MAX_TOKENS tokens of layers with n_embd <= 2048,
  * n_ff <= 1024, n_expert <= 128, n_expert_used <= 8 (a shared expert's
  * sh_n_ff <= 8192); larger calls return MI_MOE_ERR_CAPACITY and enqueue

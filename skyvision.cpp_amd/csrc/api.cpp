@@ -1048,7 +1048,7 @@ namespace {
 constexpr int64_t NA_T = MI_NOALLOC_MAX_TOKENS;
 constexpr int32_t NA_D = 2048, NA_I = 1024, NA_E = 128, NA_K = 8;
 constexpr size_t NA_BYTES = ws_bytes(NA_T, NA_D, NA_I, NA_E, NA_K);
-static_assert(NA_BYTES == 16986368, "mi_moe.h states the no-allocation workspace size");
+static_assert(NA_BYTES == 16952832, "mi_moe.h states the no-allocation workspace size");
 constexpr int NA_MAX_DEVICES = 64;
 
 struct NoallocDevice {

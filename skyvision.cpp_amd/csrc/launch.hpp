@@ -253,11 +253,9 @@ struct DecArgs {
     NormParams norm;              // k_decode1: the norm of x applied in the kernel (kind NORM_NONE: x as given)
 };
 constexpr int DEC_MAX_GRID = 1024;
-constexpr int DEC_TW_LOGIT = 0, DEC_TW_BDONE = 256, DEC_TW_REL = 256 + DEC_MAX_GRID;
-constexpr int DEC_TW_CNT = DEC_TW_REL + 32;   // the release word on a line of its own
-// two sets of completion counters (top + one per 16 units), 256 bytes apart
-constexpr int DEC_CNT_SET = 32 * (1 + DEC_MAX_GRID / 16);
-constexpr int DEC_TW_WORDS = DEC_TW_CNT + 2 * DEC_CNT_SET;
+// epoch-tagged words: the E router logits, then one per gate/up unit
+constexpr int DEC_TW_LOGIT = 0, DEC_TW_BDONE = 256;
+constexpr int DEC_TW_WORDS = DEC_TW_BDONE + DEC_MAX_GRID;
 constexpr unsigned DEC_RESCUE_POLLS = 64;
 constexpr int DEC_LIMIT_GU_BYTES = 9 * 1024;   // LDS per wave of gate/up rows
 constexpr int DEC_LIMIT_DN_BYTES = 7 * 1024;   // LDS per slot of down rows

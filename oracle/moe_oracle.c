@@ -770,6 +770,152 @@ float orc_vec_dot_q6_K_q8_K(int n, const void *vx, const void *vy) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* The same two dots on AVX-512 (BW + VNNI), bit for bit the scalar forms    */
+/* above: the generic order keeps eight int32 sums aux32[l], l = position   */
+/* mod 8, each an exact integer, then one fp32 product-and-add per l and    */
+/* block.  Here a sub-block's weight codes times its scale become int16      */
+/* (|a * sc| <= 15 * 63 / 32 * 128, exact), the Q8_K codes int16, both       */
+/* permuted so that each int32 lane pairs positions k and k + 8 (the same    */
+/* class), and vpdpwssd accumulates the pairs: lane i holds class i mod 8.   */
+/* Integer sums do not depend on their order, so aux32 is the scalar one,   */
+/* and the fp32 steps are the scalar steps.  Used by the CPU baseline when  */
+/* the host has AVX-512 VNNI (orc_set_simd); the scalar forms stay the      */
+/* checker's definition.                                                    */
+/* ------------------------------------------------------------------------ */
+#if defined(__x86_64__)
+#include <immintrin.h>
+#define ORC_AVX512 __attribute__((target("avx512f,avx512bw,avx512vnni")))
+
+/* int16 order [0, 8, 1, 9, .., 7, 15, 16, 24, 17, 25, .., 23, 31] */
+ORC_AVX512 static inline __m512i orc_pair_perm(void) {
+    return _mm512_set_epi16(31, 23, 30, 22, 29, 21, 28, 20, 27, 19, 26, 18, 25, 17, 24, 16,
+                            15, 7, 14, 6, 13, 5, 12, 4, 11, 3, 10, 2, 9, 1, 8, 0);
+}
+
+/* acc += (codes x scale-vector) . (q8 codes), 32 positions, both int16-widened */
+ORC_AVX512 static inline __m512i orc_dot32(__m512i acc, __m256i a8, int is_signed_a, __m512i scv,
+                                            const int8_t *q8, __m512i perm) {
+    const __m512i a16 = is_signed_a ? _mm512_cvtepi8_epi16(a8) : _mm512_cvtepu8_epi16(a8);
+    const __m512i as = _mm512_permutexvar_epi16(perm, _mm512_mullo_epi16(a16, scv));
+    const __m512i x16 = _mm512_permutexvar_epi16(perm, _mm512_cvtepi8_epi16(_mm256_loadu_si256((const __m256i *)q8)));
+    return _mm512_dpwssd_epi32(acc, as, x16);
+}
+
+/* aux32[l] = lane l + lane l + 8 */
+ORC_AVX512 static inline void orc_fold8(__m512i acc, int32_t aux32[8]) {
+    const __m256i lo = _mm512_castsi512_si256(acc), hi = _mm512_extracti64x4_epi64(acc, 1);
+    _mm256_storeu_si256((__m256i *)aux32, _mm256_add_epi32(lo, hi));
+}
+
+ORC_AVX512 static float orc_vec_dot_q4_K_q8_K_avx512(int n, const void *vx, const void *vy) {
+    const orc_block_q4_K *x = (const orc_block_q4_K *)vx;
+    const orc_block_q8_K *y = (const orc_block_q8_K *)vy;
+    const int nb = n / QK_K;
+    const __m512i perm = orc_pair_perm();
+    const __m256i m4 = _mm256_set1_epi8(0x0F);
+    float sums[8];
+    int32_t aux32[8];
+    memset(sums, 0, sizeof(sums));
+    float sumf = 0;
+    for (int i = 0; i < nb; ++i) {
+        uint8_t scales[8], mins[8];
+        for (int j = 0; j < 8; ++j) get_scale_min_k4(j, x[i].scales, &scales[j], &mins[j]);
+        int sumi = 0;
+        for (int j = 0; j < QK_K / 16; ++j) sumi += y[i].bsums[j] * mins[j / 2];
+        __m512i acc = _mm512_setzero_si512();
+        for (int c = 0; c < QK_K / 64; ++c) {
+            /* sub-block 2c: low nibbles of qs[32c ..], 2c + 1: high nibbles */
+            const __m256i q = _mm256_loadu_si256((const __m256i *)(x[i].qs + 32 * c));
+            const __m256i lo = _mm256_and_si256(q, m4);
+            const __m256i hi = _mm256_and_si256(_mm256_srli_epi16(q, 4), m4);
+            acc = orc_dot32(acc, lo, 0, _mm512_set1_epi16((short)scales[2 * c]), y[i].qs + 64 * c, perm);
+            acc = orc_dot32(acc, hi, 0, _mm512_set1_epi16((short)scales[2 * c + 1]), y[i].qs + 64 * c + 32, perm);
+        }
+        orc_fold8(acc, aux32);
+        const float d = orc_fp16_to_fp32(x[i].d) * y[i].d;
+        for (int l = 0; l < 8; ++l) sums[l] += d * aux32[l];
+        const float dmin = orc_fp16_to_fp32(x[i].dmin) * y[i].d;
+        sumf -= dmin * sumi;
+    }
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
+ORC_AVX512 static float orc_vec_dot_q6_K_q8_K_avx512(int n, const void *vx, const void *vy) {
+    const orc_block_q6_K *x = (const orc_block_q6_K *)vx;
+    const orc_block_q8_K *y = (const orc_block_q8_K *)vy;
+    const int nb = n / QK_K;
+    const __m512i perm = orc_pair_perm();
+    const __m256i m4 = _mm256_set1_epi8(0x0F), m3 = _mm256_set1_epi8(3), c32 = _mm256_set1_epi8(32);
+    float sums[8];
+    int32_t aux32[8];
+    memset(sums, 0, sizeof(sums));
+    float sumf = 0;
+    for (int i = 0; i < nb; ++i) {
+        __m512i acc = _mm512_setzero_si512();
+        for (int h = 0; h < 2; ++h) {   /* 128 values: ql[64 h ..], qh[32 h ..] */
+            const __m256i ql0 = _mm256_loadu_si256((const __m256i *)(x[i].ql + 64 * h));
+            const __m256i ql1 = _mm256_loadu_si256((const __m256i *)(x[i].ql + 64 * h + 32));
+            const __m256i qh = _mm256_loadu_si256((const __m256i *)(x[i].qh + 32 * h));
+            __m256i a[4];
+            a[0] = _mm256_or_si256(_mm256_and_si256(ql0, m4), _mm256_slli_epi16(_mm256_and_si256(qh, m3), 4));
+            a[1] = _mm256_or_si256(_mm256_and_si256(ql1, m4),
+                                   _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(qh, 2), m3), 4));
+            a[2] = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(ql0, 4), m4),
+                                   _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(qh, 4), m3), 4));
+            a[3] = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(ql1, 4), m4),
+                                   _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(qh, 6), m3), 4));
+            for (int r = 0; r < 4; ++r) {
+                /* values 128 h + 32 r .. + 31: scales 8 h + 2 r (first 16), + 1 (last 16) */
+                const __m256i as = _mm256_sub_epi8(a[r], c32);
+                const int j = 8 * h + 2 * r;
+                const __m512i scv = _mm512_mask_blend_epi16(0xFFFF0000u, _mm512_set1_epi16(x[i].scales[j]),
+                                                            _mm512_set1_epi16(x[i].scales[j + 1]));
+                acc = orc_dot32(acc, as, 1, scv, y[i].qs + 128 * h + 32 * r, perm);
+            }
+        }
+        orc_fold8(acc, aux32);
+        const float d = orc_fp16_to_fp32(x[i].d) * y[i].d;
+        for (int l = 0; l < 8; ++l) sums[l] += d * aux32[l];
+    }
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
+static int orc_simd_on = 0;
+
+int orc_set_simd(int on) {
+    __builtin_cpu_init();
+    const int have = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+                     __builtin_cpu_supports("avx512vnni");
+    orc_simd_on = on && have;
+    return orc_simd_on;
+}
+#else
+static int orc_simd_on = 0;
+int orc_set_simd(int on) { (void)on; return 0; }
+#endif
+
+/* the dot the mul_mat_id below uses: scalar, or the AVX-512 form when on */
+static float orc_dot_kq(int type, int n, const void *x, const void *y) {
+#if defined(__x86_64__)
+    if (orc_simd_on)
+        return type == ORC_TYPE_Q4_K ? orc_vec_dot_q4_K_q8_K_avx512(n, x, y) : orc_vec_dot_q6_K_q8_K_avx512(n, x, y);
+#endif
+    return type == ORC_TYPE_Q4_K ? orc_vec_dot_q4_K_q8_K(n, x, y) : orc_vec_dot_q6_K_q8_K(n, x, y);
+}
+
+float orc_vec_dot_kq_simd(int type, int n, const void *x, const void *y) {
+#if defined(__x86_64__)
+    __builtin_cpu_init();
+    if (__builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+        __builtin_cpu_supports("avx512vnni"))
+        return type == ORC_TYPE_Q4_K ? orc_vec_dot_q4_K_q8_K_avx512(n, x, y) : orc_vec_dot_q6_K_q8_K_avx512(n, x, y);
+#endif
+    return type == ORC_TYPE_Q4_K ? orc_vec_dot_q4_K_q8_K(n, x, y) : orc_vec_dot_q6_K_q8_K(n, x, y);
+}
+
+/* ------------------------------------------------------------------------ */
 /* seeded synthetic data                                                    */
 /* ------------------------------------------------------------------------ */
 static inline uint64_t splitmix64(uint64_t z) {
@@ -1118,8 +1264,7 @@ int orc_mul_mat_id(int type, const void *as, int64_t Kin, int64_t N, int E,
                             v = (float)acc;
                         } else if (kq) {
                             const void *yb = bq + brow * (Kin / QK_K);
-                            v = type == ORC_TYPE_Q4_K ? orc_vec_dot_q4_K_q8_K((int)Kin, wr, yb)
-                                                      : orc_vec_dot_q6_K_q8_K((int)Kin, wr, yb);
+                            v = orc_dot_kq(type, (int)Kin, wr, yb);
                         } else if (b32) {
                             const void *yb = bq0 + brow * (Kin / ORC_QK32);
                             v = type == ORC_TYPE_Q8_0   ? orc_vec_dot_q8_0_q8_0((int)Kin, wr, yb)

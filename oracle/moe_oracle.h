@@ -164,6 +164,13 @@ size_t orc_row_size(int type, int64_t k);   /* bytes of one row of k values */
 /* ---- k-quant x Q8_K dots (ggml_vec_dot_*_q8_K, generic scalar order) --- */
 float orc_vec_dot_q4_K_q8_K(int n, const void *x, const void *y);
 float orc_vec_dot_q6_K_q8_K(int n, const void *x, const void *y);
+/* The same two dots on AVX-512 BW + VNNI, bit for bit the scalar forms (the
+ * scalar forms where the host lacks them); type ORC_TYPE_Q4_K or Q6_K. */
+float orc_vec_dot_kq_simd(int type, int n, const void *x, const void *y);
+/* mul_mat_id's k-quant dots (so the layer) on the AVX-512 forms: on = 1 where
+ * the host has AVX-512 F / BW / VNNI; returns whether they are in use.  Off by
+ * default: the scalar forms are the checker's definition. */
+int orc_set_simd(int on);
 /* 32-value formats x Q8_0 activations (ggml_vec_dot_q{4,5,8}_0_q8_0, generic
  * scalar order: an exact integer dot per block, then the fp32 sum over
  * blocks), and F16 x F16 (ggml_vec_dot_f16 generic: fp32 products, exact,

@@ -72,6 +72,10 @@ def _declare(L: C.CDLL) -> None:
         getattr(L, f"orc_vec_dot_{n}_q8_0").restype = C.c_float
     L.orc_vec_dot_f16.argtypes = [C.c_int, P, P]
     L.orc_vec_dot_f16.restype = C.c_float
+    L.orc_vec_dot_kq_simd.argtypes = [C.c_int, C.c_int, P, P]
+    L.orc_vec_dot_kq_simd.restype = C.c_float
+    L.orc_set_simd.argtypes = [C.c_int]
+    L.orc_set_simd.restype = C.c_int
     L.orc_row_size.argtypes = [C.c_int, i64]
     L.orc_row_size.restype = C.c_size_t
     L.orc_vec_dot_q4_K_q8_K.argtypes = [C.c_int, P, P]
@@ -169,6 +173,24 @@ def vec_dot(type_: int, wrow: np.ndarray, q8row: np.ndarray, k: int) -> float:
           TYPE_Q4_0: lib().orc_vec_dot_q4_0_q8_0, TYPE_Q5_0: lib().orc_vec_dot_q5_0_q8_0,
           TYPE_Q8_0: lib().orc_vec_dot_q8_0_q8_0, TYPE_F16: lib().orc_vec_dot_f16}[type_]
     return fn(k, _p(np.ascontiguousarray(wrow)), _p(np.ascontiguousarray(q8row)))
+
+
+def vec_dot_simd(type_: int, wrow: np.ndarray, q8row: np.ndarray, k: int) -> float:
+    """the AVX-512 VNNI form of the Q4_K / Q6_K x Q8_K dot (the scalar form
+    where the host lacks AVX-512 VNNI)"""
+    return lib().orc_vec_dot_kq_simd(type_, k, _p(np.ascontiguousarray(wrow)), _p(np.ascontiguousarray(q8row)))
+
+
+def set_simd(on: bool) -> bool:
+    """mul_mat_id's k-quant dots on the AVX-512 VNNI forms (bit for bit the
+    scalar ones); returns whether they are in use on this host"""
+    return bool(lib().orc_set_simd(int(on)))
+
+
+def host_has_avx512_vnni() -> bool:
+    on = set_simd(True)
+    set_simd(False)
+    return on
 
 
 # ----------------------------------------------------------------- data

@@ -32,6 +32,10 @@ int mi_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int mi_memcpy_d2h(void *dst, const void *src, size_t bytes);
 int mi_memcpy_d2d(void *dst, const void *src, size_t bytes);
 int mi_memset_d(void *dst, int value, size_t bytes);
+/* copies ordered on a stream (host memory may be pageable: the call then
+ * returns once the host side is staged); wait with mi_stream_synchronize */
+int mi_memcpy_h2d_async(void *dst, const void *src, size_t bytes, mi_stream_t s);
+int mi_memcpy_d2h_async(void *dst, const void *src, size_t bytes, mi_stream_t s);
 int mi_device_synchronize(void);
 
 int mi_stream_create(mi_stream_t *s);

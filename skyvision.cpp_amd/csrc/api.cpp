@@ -1311,6 +1311,14 @@ int mi_memcpy_h2d(void *dst, const void *src, size_t bytes) {
     HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
     return MI_MOE_OK;
 }
+int mi_memcpy_h2d_async(void *dst, const void *src, size_t bytes, mi_stream_t s) {
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)s));
+    return MI_MOE_OK;
+}
+int mi_memcpy_d2h_async(void *dst, const void *src, size_t bytes, mi_stream_t s) {
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)s));
+    return MI_MOE_OK;
+}
 int mi_memcpy_d2h(void *dst, const void *src, size_t bytes) {
     HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
     return MI_MOE_OK;

@@ -238,6 +238,69 @@ Tensor *build_expert_ffn(Session &s, Tensor *x, const std::vector<Tensor *> &gat
 }  // namespace moe
 }  // namespace vqa
 
+// ------------------------------------------------------------------ GraphB
+namespace vqa {
+namespace moe {
+
+GraphB::GraphB(int device, const mi_moe_layer &layer, int64_t max_tokens) : layer_(layer), cap_T_(max_tokens) {
+    const int64_t D = layer.n_embd, K = layer.n_expert_used;
+    if (max_tokens <= 0 || D <= 0 || K <= 0) {
+        fail(MI_MOE_ERR_SHAPE);
+        return;
+    }
+    if (fail(mi_moe_ctx_create(&ctx_, device))) return;
+    if (fail(mi_moe_ctx_reserve(ctx_, max_tokens, layer.n_embd, layer.n_ff, layer.n_expert, layer.n_expert_used)))
+        return;
+    if (fail(mi_stream_create(&stream_))) return;
+    const size_t rows = sizeof(float) * (size_t)(max_tokens * D), route = 4 * (size_t)(max_tokens * K);
+    if (fail(mi_dev_malloc((void **)&d_in_, rows)) || fail(mi_dev_malloc((void **)&d_xmid_, rows)) ||
+        fail(mi_dev_malloc((void **)&d_out_, rows)) || fail(mi_dev_malloc((void **)&d_w_, route)) ||
+        fail(mi_dev_malloc((void **)&d_ids_, route)))
+        return;
+}
+
+GraphB::~GraphB() {
+    if (stream_) (void)mi_stream_synchronize(stream_);
+    for (void *p : {(void *)d_in_, (void *)d_xmid_, (void *)d_out_, (void *)d_w_, (void *)d_ids_})
+        if (p) (void)mi_dev_free(p);
+    if (stream_) (void)mi_stream_destroy(stream_);
+    mi_moe_ctx_destroy(ctx_);
+}
+
+int GraphB::fail(int rc) {
+    if (rc && !status_) status_ = rc;
+    return rc;
+}
+
+int GraphB::feed(const float *moe_in, const float *xmid_in, int64_t T, const int32_t *ids, const float *w) {
+    if (status_) return status_;
+    if (!moe_in || !xmid_in || (!ids) != (!w)) return MI_MOE_ERR_NULL;
+    if (T <= 0 || T > cap_T_) return MI_MOE_ERR_CAPACITY;
+    const size_t rows = sizeof(float) * (size_t)(T * layer_.n_embd), route = 4 * (size_t)(T * layer_.n_expert_used);
+    int rc = mi_memcpy_h2d_async(d_in_, moe_in, rows, stream_);
+    if (!rc) rc = mi_memcpy_h2d_async(d_xmid_, xmid_in, rows, stream_);
+    if (!rc && ids) rc = mi_memcpy_h2d_async(d_ids_, ids, route, stream_);
+    if (!rc && w) rc = mi_memcpy_h2d_async(d_w_, w, route, stream_);
+    if (rc) return fail(rc);
+    T_ = T;
+    routed_ = ids != nullptr;
+    return MI_MOE_OK;
+}
+
+int GraphB::compute(float *hid_out) {
+    if (status_) return status_;
+    if (!hid_out) return MI_MOE_ERR_NULL;
+    if (T_ <= 0) return MI_MOE_ERR_ARG;   // nothing fed
+    int rc = routed_ ? mi_moe_expert_ffn(ctx_, &layer_, d_in_, T_, d_xmid_, d_ids_, d_ids_, d_w_, d_out_, stream_)
+                     : mi_moe_forward(ctx_, &layer_, d_in_, T_, d_xmid_, d_out_, nullptr, stream_);
+    if (!rc) rc = mi_memcpy_d2h_async(hid_out, d_out_, sizeof(float) * (size_t)(T_ * layer_.n_embd), stream_);
+    if (!rc) rc = mi_stream_synchronize(stream_);
+    return rc ? fail(rc) : MI_MOE_OK;
+}
+
+}  // namespace moe
+}  // namespace vqa
+
 #ifdef VQA_MOE_SELFTEST
 // The reference's self-test (moe_compute.cpp:154-230) on this build: D = 2,
 // I = 3, K = 2, T = 1, F32, SiLU; out = x + 0.5 f0 + 1.0 f1 = [3.6423913,
@@ -394,6 +457,82 @@ int main(int argc, char **argv) {
     CHECK(vqa::moe::build_expert_ffn_table(s, x, gT, uT, dT, ids, ids, wbad) == nullptr, "w rows -> nullptr");
     CHECK(s.compute() == 0, "session status");
     if (s.status()) std::fprintf(stderr, "session status %d (%s)\n", s.status(), mi_last_hip_error());
+
+    // GraphB, the driver's graph B: (1) with the driver's routing, on the
+    // known answer's F32 tables (experts 0, 1 = the slot tables above)
+    {
+        mi_moe_layer L{};
+        L.n_embd = 2;
+        L.n_ff = 3;
+        L.n_expert = 2;
+        L.n_expert_used = 2;
+        auto desc = [](const Tensor *t) {
+            mi_tensor m{};
+            m.data = t->data;
+            m.type = t->type;
+            for (int i = 0; i < 4; ++i) {
+                m.ne[i] = t->ne[i];
+                m.nb[i] = t->nb[i];
+            }
+            return m;
+        };
+        L.gate = desc(gT);
+        L.up = desc(uT);
+        L.down = desc(dT);
+        L.act = MI_ACT_SILU;
+        vqa::moe::GraphB gb(0, L, 4);
+        CHECK(gb.status() == 0, "graphb create");
+        float hid[2] = {0, 0};
+        CHECK(gb.feed(xv, xv, 1, idv, wv) == 0, "graphb feed");
+        CHECK(gb.compute(hid) == 0, "graphb compute");
+        CHECK(std::fabs(hid[0] - want[0]) < 1e-5f && std::fabs(hid[1] - want[1]) < 1e-5f, "graphb values");
+        std::fprintf(stderr, "graphb out = [%.7f, %.7f]\n", hid[0], hid[1]);
+        CHECK(gb.feed(xv, xv, 5, idv, wv) == MI_MOE_ERR_CAPACITY, "graphb rows beyond max_tokens");
+        CHECK(gb.feed(xv, xv, 1, idv, nullptr) == MI_MOE_ERR_NULL, "graphb ids without weights");
+    }
+    // (2) routing itself: a Q4_K layer built on the device (D 512, I 256, E 8,
+    // K 2), three rows, the same bits as mi_moe_forward
+    {
+        const int D = 512, I = 256, E = 8, K = 2, T = 3;
+        mi_moe_layer L{};
+        L.n_embd = D;
+        L.n_ff = I;
+        L.n_expert = E;
+        L.n_expert_used = K;
+        L.act = MI_ACT_GELU_ERF_GP1;
+        L.fused_gate_up = 1;
+        mi_moe_ctx *c = s.ctx();
+        float *tmp = nullptr, *rw = nullptr, *xd = nullptr, *od = nullptr;
+        void *gq = nullptr, *dq = nullptr;
+        const size_t rg = mi_row_size(MI_TYPE_Q4_K, D), rd = mi_row_size(MI_TYPE_Q4_K, I);
+        bool ok = mi_dev_malloc((void **)&tmp, sizeof(float) * E * 2 * I * D) == 0 &&
+                  mi_dev_malloc((void **)&rw, sizeof(float) * E * D) == 0 &&
+                  mi_dev_malloc((void **)&xd, sizeof(float) * T * D) == 0 &&
+                  mi_dev_malloc((void **)&od, sizeof(float) * T * D) == 0 &&
+                  mi_dev_malloc(&gq, rg * E * 2 * I) == 0 && mi_dev_malloc(&dq, rd * E * D) == 0;
+        ok = ok && mi_moe_ctx_reserve(c, T, D, I, E, K) == 0;
+        ok = ok && mi_fill_normal(c, rw, (int64_t)E * D, 7, 1, 0.f, 0.05f, s.stream()) == 0;
+        ok = ok && mi_fill_normal(c, tmp, (int64_t)E * 2 * I * D, 7, 2, 0.f, 0.02f, s.stream()) == 0;
+        ok = ok && mi_quantize(c, MI_TYPE_Q4_K, tmp, gq, (int64_t)E * 2 * I, D, s.stream()) == 0;
+        ok = ok && mi_fill_normal(c, tmp, (int64_t)E * D * I, 7, 3, 0.f, 0.02f, s.stream()) == 0;
+        ok = ok && mi_quantize(c, MI_TYPE_Q4_K, tmp, dq, (int64_t)E * D, I, s.stream()) == 0;
+        ok = ok && mi_fill_normal(c, xd, (int64_t)T * D, 7, 4, 0.f, 1.f, s.stream()) == 0;
+        L.router_w = rw;
+        L.gate = mi_tensor{gq, MI_TYPE_Q4_K, {D, 2 * I, E, 1}, {144, rg, rg * 2 * I, rg * 2 * I * E}};
+        L.down = mi_tensor{dq, MI_TYPE_Q4_K, {I, D, E, 1}, {144, rd, rd * D, rd * D * E}};
+        ok = ok && mi_moe_forward(c, &L, xd, T, xd, od, nullptr, s.stream()) == 0 && s.compute() == 0;
+        std::vector<float> x(T * D), want_o(T * D), got(T * D);
+        ok = ok && mi_memcpy_d2h(x.data(), xd, sizeof(float) * T * D) == 0 &&
+             mi_memcpy_d2h(want_o.data(), od, sizeof(float) * T * D) == 0;
+        CHECK(ok, "graphb q4_k layer setup");
+        vqa::moe::GraphB gb(0, L, 8);
+        CHECK(gb.feed(x.data(), x.data(), T) == 0 && gb.compute(got.data()) == 0, "graphb routed by the layer");
+        CHECK(std::memcmp(got.data(), want_o.data(), sizeof(float) * T * D) == 0, "graphb == mi_moe_forward");
+        std::fprintf(stderr, "graphb q4_k layer: %s mi_moe_forward\n",
+                     std::memcmp(got.data(), want_o.data(), sizeof(float) * T * D) ? "differs from" : "bit-identical to");
+        for (void *p : {(void *)tmp, (void *)rw, (void *)xd, (void *)od, gq, dq})
+            if (p) mi_dev_free(p);
+    }
     std::fprintf(stderr, "%s (%d failures)\n", g_fail ? "FAIL" : "PASS", g_fail);
     return g_fail ? 1 : 0;
 }

@@ -93,5 +93,49 @@ Tensor *build_expert_ffn_table(Session &s, Tensor *x, Tensor *gate_table, Tensor
                                Tensor *gate_up_ids, Tensor *down_ids, Tensor *w,
                                UnaryOp act = UnaryOp::SILU);
 
+// The expert-cache decode driver's graph B on the GPU: the body a
+// Hooks::build_b / feed_b pair runs (src/core/engine/moe_decode_driver.hpp:
+// 125-144, called at :493-519; the driver's default build at :503-514).  Per
+// layer and step the driver hands over the normed rows (moe_in), the residual
+// rows (xmid_in), and either its routing (the K selected experts and weights
+// of each row) or nothing (a model whose graph B routes moe_in itself,
+// moondream.cpp:509-516); graph B returns hid = xmid + sum_k w_k down_k(act(
+// gate_k moe_in, up_k moe_in)).  The layer's tables stay resident in HBM
+// whole, so the driver's cache slots are plain expert ids here.
+//   feed()     feed_b: uploads the rows (host memory) on this object's stream
+//   compute()  the graph compute and readback of hid; waits on this object's
+//              stream only (other streams of the GPU keep running)
+// Not thread-safe (one GraphB per layer and driver thread, as the driver's
+// per-layer graph state).
+class GraphB {
+public:
+    // layer: device tables of one MoE layer (mi_gguf_load_moe_layer, or built
+    // by the caller); max_tokens: rows per step
+    GraphB(int device, const mi_moe_layer &layer, int64_t max_tokens);
+    ~GraphB();
+    GraphB(const GraphB &) = delete;
+    GraphB &operator=(const GraphB &) = delete;
+    // 0, or the first negative mi_moe_status of a call
+    int status() const { return status_; }
+    // moe_in, xmid_in: host F32 [T][D]; ids (I32 [T][K], expert ids) and w
+    // (F32 [T][K]) both given, or both nullptr (the layer's router)
+    int feed(const float *moe_in, const float *xmid_in, int64_t T, const int32_t *ids = nullptr,
+             const float *w = nullptr);
+    // hid_out: host F32 [T][D] of the last feed()
+    int compute(float *hid_out);
+    mi_stream_t stream() const { return stream_; }
+
+private:
+    int fail(int rc);
+    mi_moe_layer layer_{};
+    mi_moe_ctx *ctx_ = nullptr;
+    mi_stream_t stream_ = nullptr;
+    int64_t cap_T_ = 0, T_ = 0;
+    bool routed_ = false;
+    float *d_in_ = nullptr, *d_xmid_ = nullptr, *d_out_ = nullptr, *d_w_ = nullptr;
+    int32_t *d_ids_ = nullptr;
+    int status_ = 0;
+};
+
 }  // namespace moe
 }  // namespace vqa

@@ -7,7 +7,10 @@ lists, and the self-test binary is built and linked to libmimoe.so.
 GPU: the self-test runs - the reference's own known answer (D = 2, I = 3,
 K = 2, F32 SiLU -> [3.6423913, 4.1931758], moe_compute.cpp:154-230) through
 the per-slot and slot-table forms, the residual split, and the nullptr
-returns of the argument checks."""
+returns of the argument checks; and vqa::moe::GraphB, the decode driver's
+graph B (Hooks::build_b / feed_b, moe_decode_driver.hpp:125-144): the same
+known answer with the driver's routing, and a Q4_K layer routing its own
+rows bit-identical to mi_moe_forward."""
 import pathlib
 import re
 import subprocess
@@ -54,3 +57,7 @@ def test_selftest_runs_on_gpu():
     assert m, r.stderr
     # the reference's hand-computed answer, to its 1e-5
     assert abs(float(m.group(1)) - 3.6423913) < 1e-5 and abs(float(m.group(2)) - 4.1931758) < 1e-5
+    m = re.search(r"graphb out = \[([-0-9.]+), ([-0-9.]+)\]", r.stderr)
+    assert m, r.stderr
+    assert abs(float(m.group(1)) - 3.6423913) < 1e-5 and abs(float(m.group(2)) - 4.1931758) < 1e-5
+    assert "graphb q4_k layer: bit-identical to mi_moe_forward" in r.stderr

@@ -213,7 +213,7 @@ int mi_moe_forward_router_input(mi_moe_ctx *ctx, const mi_moe_layer *layer, cons
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  It calls no hipMalloc / hipFree or any
  * allocating routine: its workspace is one file-scope device array of the
- * library per GPU, 16,952,832 bytes, held until the process ends, sized for
+ * library per GPU, 16,973,312 bytes, held until the process ends, sized for
  * calls of at most MI_NOALLOC_MAX_TOKENS tokens of layers with n_embd <= 2048,
  * n_ff <= 1024, n_expert <= 128, n_expert_used <= 8 (a shared expert's
  * sh_n_ff <= 8192); larger calls return MI_MOE_ERR_CAPACITY and enqueue
@@ -348,22 +348,30 @@ int mi_moe_ctx_stage_times(mi_moe_ctx *ctx, int max_stages, const char **names, 
  * run on the GEMM path.  Synchronizes with the call's stream. */
 int mi_moe_ctx_stage_clock(mi_moe_ctx *ctx, const char *stage, double *ghz, int *n_wg);
 /* Product path of a call: the grouped MFMA GEMM from min_tokens_for_gemm
- * tokens on, the grouped GEMV below.  0 (the default) picks by shape: the
- * GEMM when 4 * T * K > 5 * E (more than 1.25 dispatched rows per expert). */
+ * tokens on, the grouped GEMV below.  0 (the default) picks by shape: for
+ * k-quant layers the GEMM when 2 * T * K >= E (from half a dispatched row
+ * per expert); for Q4_0 / Q5_0 / Q8_0 / F16 tables and mi_moe_mul_mat_id
+ * when 4 * T * K > 5 * E (more than 1.25 rows per expert). */
 int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *ctx, int64_t min_tokens_for_gemm);
 /* Row tiles of the grouped GEMMs of Q4_K gate/up layers: 0 (the default) by
  * shape, 32-row tiles when the call dispatches at most 8 rows per expert on
  * average (qwen3omni up to 128 tokens, moondream3 up to 64: two work-groups
  * per CU keep twice the weight stream in flight), 192-row tiles above; 1
- * 192-row tiles, 2 32-row tiles at every size.  Same results bit for bit
- * (the same per-row arithmetic); this only picks the kernel. */
+ * 192-row tiles, 2 32-row tiles at every size; 3 the skinny products (16-row
+ * tiles, one work-group per CU, the weight stream held in registers several
+ * blocks ahead) on layers whose tables are all Q4_K with n_embd and n_ff <=
+ * 2048 (others take the shape rule).  Kinds 0-2 give the same bits (the same
+ * per-row arithmetic); the skinny products sum each output's products in
+ * another order (fp32; the rows agree to ~2e-4 rel-L2 after the activations'
+ * fp16 and Q8_K roundings). */
 int mi_moe_ctx_set_gemm_tiles(mi_moe_ctx *ctx, int kind);
 /* Schedule of decode calls of mi_moe_forward (1 token, and batches of 2..16
- * tokens).  The fused mode runs the whole block in one kernel of one
- * work-group per CU, when the layer fits it (Q4_K gate/up, Q4_K or Q6_K down,
- * top-k <= 8, default gating, no shared expert, 16-byte aligned tables; for
- * batches also n_embd <= 2048 and n_ff <= 1024); other layers and larger
- * batches use the chain.  Inside the kernel, work-groups hand each other
+ * tokens; for experts of more than 2 MiB, batches that dispatch at most one
+ * row per expert on average, T * K <= E).  The fused mode runs the whole block in one kernel of one work-group per
+ * CU, when the layer fits it (Q4_K gate/up, Q4_K or Q6_K down, top-k <= 8,
+ * default gating, no shared expert, 16-byte aligned tables; for batches also
+ * n_embd <= 2048 and n_ff <= 1024); other layers and larger batches use the
+ * chain.  Inside the kernel, work-groups hand each other
  * the router logits and the gate/up activations through completion words;
  * a work-group that does not see a result after a bounded number of polls
  * computes it itself (the same bits), so the kernel needs no co-residency

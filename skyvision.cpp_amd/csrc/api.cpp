@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <atomic>
 #include <cstdio>
 #include <cstring>
@@ -69,12 +70,13 @@ struct ActBuf {                // one Q8_K activation set
 };
 
 struct DispBuf {
-    int32_t *counts, *offsets, *perm, *tile_e, *tile_r0, *tile_start, *tile_rows, *n_tiles, *active_e, *n_active, *bad;
+    int32_t *counts, *offsets, *perm, *tile_e, *tile_r0, *tile_start, *tile_rows, *tile_perm, *n_tiles, *active_e,
+        *n_active, *bad;
     int32_t *bad_total;   // the context's running count (mi_moe_ctx_take_errors)
     Dispatch view() const {
         Dispatch d;
         d.counts = counts; d.offsets = offsets; d.perm = perm; d.tile_e = tile_e; d.tile_r0 = tile_r0;
-        d.tile_start = tile_start; d.tile_rows = tile_rows;
+        d.tile_start = tile_start; d.tile_rows = tile_rows; d.tile_perm = tile_perm;
         d.n_tiles = n_tiles; d.active_e = active_e; d.n_active = n_active; d.bad_ids = bad;
         d.bad_total = bad_total; d.zero_rows = nullptr; d.zero_ld = 0; d.zero_n = 0;
         return d;
@@ -107,7 +109,8 @@ struct mi_moe_ctx {
     int32_t *bad_total = nullptr;   // caller ids outside [0, E) since the last take
     int32_t *range_total = nullptr; // GEMM-path Q8_K blocks saturated at the fp16 range
     int64_t gemm_threshold = 0;   // 0: the shape rule of use_gemm
-    int gemm_tiles = 0;           // 4-wave GEMM row tiles: 0 by shape, 1 G4_BM, 2 G4_BM_SMALL
+    int gemm_tiles = 0;           // Q4_K GEMM row tiles: 0 by shape, 1 G4_BM, 2 G4_BM_SMALL, 3 GS_BM (k_gs)
+    int n_cu = 0;                 // compute units of the device
     // single-token fused kernel (k_decode.hip)
     int fused_decode = MI_DECODE_FUSED;
     int dec_grid = 0;          // fused decode grid (one WG per CU), 0: unavailable
@@ -304,6 +307,13 @@ bool plan_decodeb(const mi_moe_ctx *c, const mi_moe_layer *L, const float *x, in
     const int64_t D = L->n_embd, E = L->n_expert, K = L->n_expert_used, I = L->n_ff;
     const int G = c->dec_grid;
     if (!c->fused_decode || G <= 0 || T < 2 || T > DECB_T_MAX) return false;
+    // Experts of more than 2 MiB (the model shapes): at most one dispatched
+    // row per expert on average.  The kernel reads an expert's rows once per
+    // token routed to it, the grouped GEMMs on 32-row tiles once per call:
+    // above that they are as fast or faster (moondream3 Q6_K down, T = 12:
+    // 105.7 vs 91.8 us; qwen3omni T = 16, one row per expert: 92.2 vs 101.1).
+    const int64_t ebytes = L->gate.nb[2] + (L->fused_gate_up ? 0 : L->up.nb[2]) + L->down.nb[2];
+    if (ebytes > (2LL << 20) && T * L->n_expert_used > L->n_expert) return false;
     if (decodeb_tw_words(T, D, E, K, I) > c->decb_words) return false;
     if (L->gating != MI_GATING_SOFTMAX_TOPK || L->expert_scale) return false;
     if (!act_gated(L->act) || L->sh_n_ff > 0) return false;
@@ -348,12 +358,19 @@ int run_decodeb(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
 // Q8_K form it reads (GEMV: codes, scales, block sums; GEMM: fp16 d*q in the
 // gate weight's MFMA K order).
 bool use_gemm(const mi_moe_ctx *c, int64_t T, int K, int E) {
-    // Measured crossover (MI355X, Q4_K tables, 16 rotated layer copies): the
-    // grouped GEMM pays per M-tile, the GEMV per token and row, so the switch
-    // follows the rows per expert T*K/E: qwen3omni (E 128, K 8) GEMV faster up
-    // to T = 20, GEMM from 24; moondream3 (E 64, K 8) GEMV at 8, GEMM from 12.
-    // The rule takes the GEMM above 1.25 rows per expert: qwen3omni from
-    // T = 21, moondream3 from T = 11.
+    // Measured crossover (MI355X, Q4_K tables, 16 rotated layer copies, the
+    // GEMMs on 32-row tiles): the grouped GEMM pays per M-tile, the GEMV per
+    // token and row, so the switch follows the rows per expert T*K/E:
+    // qwen3omni (E 128, K 8) GEMV faster up to T = 6 (72.1 / 73.0 us), GEMM
+    // from 8 (79.9 / 82.8 us); moondream3 (E 64, K 8) GEMV up to 3, GEMM from
+    // 4 (63.9 / 67.8 us).  The rule takes the GEMM from half a row per expert.
+    if (c->gemm_threshold > 0) return T >= c->gemm_threshold;
+    return 2 * T * K >= (int64_t)E;
+}
+// The switch of the products still on 192-row tiles (mul_mat_id) and of
+// the Q4_0 / Q5_0 / Q8_0 / F16 tables, as measured on them: the GEMM above
+// 1.25 dispatched rows per expert.
+bool use_gemm_wide(const mi_moe_ctx *c, int64_t T, int K, int E) {
     if (c->gemm_threshold > 0) return T >= c->gemm_threshold;
     return 4 * T * K > 5 * (int64_t)E;
 }
@@ -373,8 +390,34 @@ bool g4_path(const mi_moe_layer *L) { return L->gate.type == MI_TYPE_Q4_K || !ac
 // stream; 192-row balanced tiles above.
 constexpr int64_t G4_SMALL_ROWS = 8;
 bool g4_small_tiles(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T) {
-    if (c->gemm_tiles) return c->gemm_tiles == 2;
+    if (c->gemm_tiles == 1 || c->gemm_tiles == 2) return c->gemm_tiles == 2;
     return T * L->n_expert_used <= G4_SMALL_ROWS * L->n_expert;
+}
+
+// The skinny products (k_gs.hip: 16-row tiles, one work-group per CU, each
+// wave's weight stream held several blocks ahead in registers) for Q4_K
+// layers (gate/up and down) with K <= GS_KMAX, on request only
+// (mi_moe_ctx_set_gemm_tiles kind 3): measured against the 4-wave GEMMs on
+// 32-row tiles at 16 to 128 tokens of the qwen3omni layer they were within a
+// few percent either way from box to box.
+bool gs_path(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T) {
+    (void)T;
+    if (L->gate.type != MI_TYPE_Q4_K || L->down.type != MI_TYPE_Q4_K) return false;
+    if (act_gated(L->act) && !L->fused_gate_up && L->up.type != MI_TYPE_Q4_K) return false;
+    if (L->n_embd > GS_KMAX || L->n_ff > GS_KMAX || L->n_ff % 16 || L->n_embd % 16) return false;
+    return c->gemm_tiles == 3;
+}
+
+// work-groups per tile of the skinny products: about one work-group per CU
+// (they run one per CU) for the tiles a call of `rows` rows over E experts
+// is expected to make (uniform routing: the experts hit plus one tile per
+// further GS_BM rows), at least one column group per wave (waves per
+// work-group)
+int gs_splits(const mi_moe_ctx *c, int64_t rows, int E, int64_t ncols, int waves) {
+    const double hit = E * (1.0 - std::pow(1.0 - 1.0 / E, (double)rows));
+    const double tiles = std::max(1.0, hit + std::max(0.0, (double)rows - hit * GS_BM) / GS_BM);
+    const int cap = (int)std::max<int64_t>(1, ncols / 16 / waves);
+    return std::max(1, std::min(cap, (int)std::lround(std::max(1, c->n_cu) / tiles)));
 }
 
 bool x_q8_spec(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T, Q8Out &qx) {
@@ -401,7 +444,7 @@ int run_experts_b32(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_
     const int max_active = (int)std::min<int64_t>(E, rows);
     const bool same_ids = ids_gu == ids_dn;
     const bool gated = act_gated(L->act);
-    const bool gemm = use_gemm(c, T, K, E);
+    const bool gemm = use_gemm_wide(c, T, K, E);
     const int max_tiles = (int)((rows + G4_BM - 1) / G4_BM + max_active);
     TRY(launch_dispatch(ids_gu, T, K, E, G4_BM, 1, c->disp[0].view(), st));
     if (!same_ids) TRY(launch_dispatch(ids_dn, T, K, E, G4_BM, 1, c->disp[1].view(), st));
@@ -469,7 +512,8 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
     // GEMM M-tiles: balanced tiles of at most G4_BM rows for the 4-wave GEMMs,
     // GEMM_BM-row tiles otherwise
     const bool g4 = gemm && g4_path(L);
-    const int bm = !g4 ? GEMM_BM : g4_small_tiles(c, L, T) ? G4_BM_SMALL : G4_BM;
+    const bool gs = g4 && gs_path(c, L, T);
+    const int bm = !g4 ? GEMM_BM : gs ? GS_BM : g4_small_tiles(c, L, T) ? G4_BM_SMALL : G4_BM;
     const int max_tiles = (int)((rows + bm - 1) / bm + max_active);
 
     TRY(launch_dispatch(ids_gu, T, K, E, bm, g4, c->disp[0].view(), st));
@@ -556,13 +600,14 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         a.xh = c->ax.h; a.ne11 = 1; a.K = K;
         a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.tile_e = dg.tile_e;
         a.tile_r0 = dg.tile_r0; a.tile_start = dg.tile_start; a.tile_rows = dg.tile_rows; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
+        a.tile_perm = dg.tile_perm;
         a.bm = bm;
         a.y = c->f1; a.ldy = I; a.ncols = I; a.xrows = T;
         // gated: the GLU rows as fp16 (half the bytes of their round trip to
         // the Q8_K pass; saturation at the fp16 range is counted)
         if (gated) { a.yh = (_Float16 *)c->f1; a.range_total = c->range_total; }
-        prof_clock(c, a, 0);
-        TRY(launch_gemm4(a, st));
+        if (!gs) prof_clock(c, a, 0);   // (the skinny kernels record no clocks)
+        TRY(gs ? launch_gemm_gs(a, gs_splits(c, rows, E, gated ? I : a.ncols, gated ? 8 : 16), st) : launch_gemm4(a, st));
         stage_end(c, "gate_up", st);
         Q8Out qa;
         qa.xh = c->aact.h; qa.wtype = down.type; qa.order = 1; qa.pre_act = gated ? 0 : MI_ACT_RELU_SQR;
@@ -574,12 +619,13 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         d.a = down; d.glu = 0; d.xh = c->aact.h; d.ne11 = K; d.K = K;
         d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
         d.tile_r0 = dd.tile_r0; d.tile_start = dd.tile_start; d.tile_rows = dd.tile_rows; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles; d.xrows = (int64_t)T * K;
+        d.tile_perm = dd.tile_perm;
         d.bm = bm;
         // the slot rows as fp16 (half the bytes of the round trip to the
         // combine; saturation at the fp16 range is counted)
         d.y = c->z; d.yh = zh = (_Float16 *)c->z; d.range_total = c->range_total; d.ldy = D; d.ncols = D;
-        prof_clock(c, d, 1);
-        TRY(launch_gemm4(d, st));
+        if (!gs) prof_clock(c, d, 1);
+        TRY(gs ? launch_gemm_gs(d, gs_splits(c, rows, E, D, 16), st) : launch_gemm4(d, st));
         stage_end(c, "down", st);
     } else {
         // Q6_K gate/up: fp16 dequant on 16x16x32 MFMA
@@ -650,14 +696,15 @@ constexpr size_t ws_bytes(int64_t max_tokens, int64_t D, int64_t I, int64_t E, i
     const int64_t kmax = D > I ? D : I;
     const int64_t kmax_q = (kmax + QK - 1) / QK * QK;
     const int64_t wide = (D > 2 * I ? D : 2 * I) > kmax ? (D > 2 * I ? D : 2 * I) : kmax;
-    const int64_t tiles = (rows + G4_BM_SMALL - 1) / G4_BM_SMALL + (E < rows ? E : rows);
+    const int64_t tiles = (rows + GS_BM - 1) / GS_BM + (E < rows ? E : rows);
     const int64_t iq = (I + QK - 1) / QK * QK;
     size_t need = 0;
     need += carve_size<float>(max_tokens * E) + carve_size<int32_t>(rows) + carve_size<float>(rows);
     need += carve_size<float>(max_tokens * D);
     for (int s = 0; s < 2; ++s)
         need += carve_size<int32_t>(E) + carve_size<int32_t>(E + 1) + carve_size<int32_t>(rows) +
-                4 * carve_size<int32_t>(tiles) + carve_size<int32_t>(1) + carve_size<int32_t>(E) +
+                4 * carve_size<int32_t>(tiles) + carve_size<int32_t>(tiles * GS_BM) + carve_size<int32_t>(1) +
+                carve_size<int32_t>(E) +
                 2 * carve_size<int32_t>(1);
     need += 2 * carve_size<int32_t>(1);   // bad_total, range_total
     // activation sets: x/b rows (rows x kmax) and act rows (rows x I)
@@ -680,7 +727,7 @@ bool carve_workspace(mi_moe_ctx *c, char *base, int64_t max_tokens, int32_t D, i
     const int64_t kmax = std::max<int64_t>(D, I);
     const int64_t kmax_q = (kmax + QK - 1) / QK * QK;
     const int64_t wide = std::max<int64_t>(std::max<int64_t>(D, 2LL * I), kmax);
-    const int64_t tiles = (rows + G4_BM_SMALL - 1) / G4_BM_SMALL + std::min<int64_t>(E, rows);
+    const int64_t tiles = (rows + GS_BM - 1) / GS_BM + std::min<int64_t>(E, rows);
     const int64_t iq = (I + QK - 1) / QK * QK;
     char *q = base;
     c->logits = carve<float>(q, max_tokens * E);
@@ -696,6 +743,7 @@ bool carve_workspace(mi_moe_ctx *c, char *base, int64_t max_tokens, int32_t D, i
         d.tile_r0 = carve<int32_t>(q, tiles);
         d.tile_start = carve<int32_t>(q, tiles);
         d.tile_rows = carve<int32_t>(q, tiles);
+        d.tile_perm = carve<int32_t>(q, tiles * GS_BM);
         d.n_tiles = carve<int32_t>(q, 1);
         d.active_e = carve<int32_t>(q, E);
         d.n_active = carve<int32_t>(q, 1);
@@ -770,6 +818,7 @@ int mi_moe_ctx_create(mi_moe_ctx **out, int device) {
     mi_moe_ctx *c = new mi_moe_ctx();
     c->device = device;
     if (decode1_max_grid(device, &c->dec_grid)) c->dec_grid = 0;
+    if (hipDeviceGetAttribute(&c->n_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) c->n_cu = 256;
     for (int i = 0; i <= kMaxStages; ++i) {
         const hipError_t e = hipEventCreate(&c->ev[i]);
         if (e != hipSuccess) {
@@ -845,7 +894,7 @@ int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *c, int64_t t) {
 
 int mi_moe_ctx_set_gemm_tiles(mi_moe_ctx *c, int kind) {
     if (!c) return MI_MOE_ERR_NULL;
-    if (kind < 0 || kind > 2) return MI_MOE_ERR_ARG;
+    if (kind < 0 || kind > 3) return MI_MOE_ERR_ARG;
     c->gemm_tiles = kind;
     return MI_MOE_OK;
 }
@@ -1048,7 +1097,7 @@ namespace {
 constexpr int64_t NA_T = MI_NOALLOC_MAX_TOKENS;
 constexpr int32_t NA_D = 2048, NA_I = 1024, NA_E = 128, NA_K = 8;
 constexpr size_t NA_BYTES = ws_bytes(NA_T, NA_D, NA_I, NA_E, NA_K);
-static_assert(NA_BYTES == 16952832, "mi_moe.h states the no-allocation workspace size");
+static_assert(NA_BYTES == 16973312, "mi_moe.h states the no-allocation workspace size");
 constexpr int NA_MAX_DEVICES = 64;
 
 struct NoallocDevice {
@@ -1192,7 +1241,7 @@ int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const 
     const float *bp = (const float *)b->data;
     if (is_b32f(as->type)) {
         // b in the table type's vec_dot_type (Q8_0 or fp16), then the grouped GEMV or GEMM
-        const bool gemm = use_gemm(c, T, (int)n_used, (int)E);
+        const bool gemm = use_gemm_wide(c, T, (int)n_used, (int)E);
         B32Prep o;
         if (as->type == MI_TYPE_F16) { o.mode = B32_PREP_F16; o.xh = c->ax.h; }
         else if (gemm) { o.mode = B32_PREP_DQ; o.xh = c->ax.h; }
@@ -1216,7 +1265,7 @@ int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const 
         a.y = (float *)dst->data; a.ldy = N; a.ncols = N;
         return launch_mm_id_f32(a, bp, Kin, st);
     }
-    const bool gemm = use_gemm(c, T, (int)n_used, (int)E) || Kin > 8 * QK;
+    const bool gemm = use_gemm_wide(c, T, (int)n_used, (int)E) || Kin > 8 * QK;
     if (!gemm) {
         Q8Out qx;
         qx.q8 = c->ax.q8; qx.d8 = c->ax.d8; qx.bsums = c->ax.bs;

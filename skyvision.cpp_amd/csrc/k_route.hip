@@ -549,20 +549,19 @@ int launch_router(const float *W, const float *b, const float *x, int64_t ldx, i
 }
 
 // ---------------------------------------------------------------- top-k
-// One wave per token: rank-based top-k (largest value, lowest id on ties),
-// then softmax over the K selected logits: max, expf(v - max), sum in fp64 in
-// slot order, scale by (float)(1.0 / sum) - the ggml_soft_max order.
+// One wave per token: top-k by K rounds of the wave's largest remaining
+// value (largest value, lowest id on ties; topk_softmax_wave), then softmax
+// over the K selected logits: max, expf(v - max), sum in fp64 in slot order,
+// scale by (float)(1.0 / sum) - the ggml_soft_max order.
 __global__ void __launch_bounds__(256) k_topk_softmax(const float *__restrict__ logits, int64_t ldl, int64_t T,
                                                       int E, int K, int32_t *__restrict__ sel, int64_t lds,
                                                       float *__restrict__ w, Gating gt) {
-    __shared__ __attribute__((aligned(16))) float s_v[4][64 * TOPK_MAX_PER_LANE];
-    __shared__ int s_sel[4][64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t t = (int64_t)blockIdx.x * 4 + wave;
-    if (t >= T) return;   // whole waves; the routine synchronizes only its own wave
+    if (t >= T) return;   // whole waves; the routine works inside its own wave
     int mysel;
     float myw;
-    topk_softmax_wave(logits + t * ldl, E, K, lane, s_v[wave], s_sel[wave], mysel, myw, w != nullptr, gt);
+    topk_softmax_wave(logits + t * ldl, E, K, lane, mysel, myw, w != nullptr, gt);
     if (lane < K) {
         sel[t * lds + lane] = mysel;
         if (w) w[t * K + lane] = myw;
@@ -684,9 +683,11 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
             }
         }
     }
+    // balanced tiles: nt of them, the first `extra` with base + 1 rows
+    const int nt = balanced ? (c + BM - 1) / BM : 0, tb = balanced ? tsc[me] - nt : 0;
+    const int base = nt ? c / nt : 0, extra = c - base * nt;
+    const bool tperm = balanced && d.tile_perm && BM <= GS_BM;
     if (balanced) {
-        const int nt = (c + BM - 1) / BM, tb = tsc[me] - nt;
-        const int base = nt ? c / nt : 0, extra = c - base * nt;
         for (int j = tid; j < nt; j += DISPATCH_THREADS) {
             const int r0 = j * base + (j < extra ? j : extra);
             d.tile_e[tb + j] = me;
@@ -758,8 +759,18 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int32_t *__
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
             const uint64_t mask = hm[it];
-            if ((mask >> lane) & 1ull)
-                d.perm[pos + __popcll(mask & ((1ull << lane) - 1ull))] = (int32_t)(c0 + w0 + 64 * it + lane);
+            if ((mask >> lane) & 1ull) {
+                const int at = pos + __popcll(mask & ((1ull << lane) - 1ull));
+                const int32_t val = (int32_t)(c0 + w0 + 64 * it + lane);
+                d.perm[at] = val;
+                if (tperm) {
+                    // the entry's tile j and row within it (rank r in the expert's list)
+                    const int r = at - off, r1 = extra * (base + 1);
+                    const int j = r < r1 ? r / (base + 1) : extra + (r - r1) / base;
+                    const int r0 = j * base + (j < extra ? j : extra);
+                    d.tile_perm[(int64_t)(tb + j) * GS_BM + (r - r0)] = val;
+                }
+            }
             pos += __popcll(mask);
         }
         run += total;

@@ -10,6 +10,10 @@
 
 namespace mimoe {
 
+// tile rows and longest K of the skinny grouped products (k_gs.hip)
+constexpr int GS_BM = 16;
+constexpr int GS_KMAX = 2048;
+
 // records the HIP error string for mi_last_hip_error(); returns MI_MOE_ERR_HIP (-5)
 int record_hip_error(hipError_t e);
 // check hipGetLastError() after a launch
@@ -61,6 +65,7 @@ struct Dispatch {
     int32_t *tile_r0;    // [max_tiles] first list row of each tile (within its expert's list)
     int32_t *tile_start; // [max_tiles] its first row in perm (offsets[e] + tile_r0)
     int32_t *tile_rows;  // [max_tiles] its row count
+    int32_t *tile_perm;  // or null: [max_tiles][GS_BM] the tile's perm entries (balanced tiles of at most GS_BM rows)
     int32_t *n_tiles;    // [1]
     int32_t *active_e;   // [E] experts with count > 0, ascending
     int32_t *n_active;   // [1]
@@ -169,6 +174,7 @@ struct G2Args {
     int ne11, K;
     const int32_t *counts, *offsets, *perm, *tile_e, *tile_r0, *n_tiles;
     const int32_t *tile_start, *tile_rows;   // the tiles' perm starts and row counts
+    const int32_t *tile_perm;                // skinny products: [max_tiles][GS_BM] the tiles' perm entries
     int max_tiles;
     int bm;               // tile rows of the dispatch: G4_BM, or G4_BM_SMALL (few rows per expert)
     int64_t xrows;        // rows of xh (glu = 1: tokens)
@@ -191,6 +197,13 @@ constexpr int G4_BM = 192;
 constexpr int G4_BM_SMALL = 32;   // tiles of few rows per expert (G2Args::bm)
 int launch_gemm4(const G2Args &g, hipStream_t st);
 int gemm4_grid(const G2Args &g);   // work-groups launch_gemm4 launches
+
+// Skinny grouped Q4_K products (k_gs.hip) on tiles of at most GS_BM rows
+// from a balanced dispatch (G2Args::bm = GS_BM), same arguments and outputs
+// as launch_gemm4 (glu = 1: the GLU rows; glu = 0: the plain product, whose
+// ncols must be a multiple of 16); K <= GS_KMAX.  splits: work-groups per
+// tile, each taking an equal share of the tile's 16-column groups.
+int launch_gemm_gs(const G2Args &g, int splits, hipStream_t st);
 
 // ---- 32-value block formats (Q4_0 = 2, Q5_0 = 6, Q8_0 = 8) and F16 (1)
 // expert tables (k_b32.hip)

@@ -231,13 +231,14 @@ __device__ inline float softmax_selected_wave(float myval, int K, int lane) {
 }
 
 // Top-k of one token's E logits by one wave (E <= 64 * TOPK_MAX_PER_LANE,
-// K <= 64), largest value first, lower id first on ties.  The logits go to
-// the wave's LDS row sv (padded with -inf to a multiple of 4); each lane ranks
-// its own logits against all of them (rank = logits that come first: larger,
-// or equal with a lower id) and logit e of rank r < K becomes slot r.  Lane
-// k < K gets the k-th id and, when want_w, its softmax weight over the K
-// selected logits: max, expf(v - max), sum in fp64 in slot order, scale by
-// (float)(1.0 / sum) (ggml_soft_max).
+// K <= 64), largest value first, lower id first on ties: K rounds of the
+// wave's largest remaining value (a max reduction), whose id is the lowest
+// set bit of a ballot of its holders (ids 64 i + lane, block i = 0 first);
+// the winner then leaves the race (NaN: the max skips it, == never holds).
+// The order equals ranking every value by the values that come before it
+// (larger, or equal with a lower id).  Lane k < K gets the k-th id and, when
+// want_w, its softmax weight over the K selected logits: max, expf(v - max),
+// sum in fp64 in slot order, scale by (float)(1.0 / sum) (ggml_soft_max).
 constexpr int TOPK_MAX_PER_LANE = 4;
 __device__ inline void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -263,9 +264,24 @@ struct Gating {
 
 __device__ inline float gating_sigmoid(float x) { return (float)(1.0 / (1.0 + exp(-(double)x))); }
 
-__device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane, float *sv, int *ssel, int &mysel,
-                                         float &myw, bool want_w, const Gating &gt = Gating{}) {
-    const int nper = (E + 63) >> 6, E4 = (E + 3) & ~3;
+// the wave's largest value, uniform: max within 16-lane rows (DPP), then
+// rows 0 -> 1, 2 -> 3 (row_bcast:15) and row 1 -> 2, 3 (row_bcast:31): lane
+// 63 holds the maximum of all four rows
+__device__ inline float wave_max_uniform(float m) {
+    m = fmaxf(m, dpp_f<0xB1>(m));
+    m = fmaxf(m, dpp_f<0x4E>(m));
+    m = fmaxf(m, dpp_f<0x141>(m));
+    m = fmaxf(m, dpp_f<0x140>(m));
+    const int mi = __builtin_bit_cast(int, m);
+    m = fmaxf(m, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(mi, mi, 0x142, 0xA, 0xF, false)));
+    const int mj = __builtin_bit_cast(int, m);
+    m = fmaxf(m, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(mj, mj, 0x143, 0xC, 0xF, false)));
+    return lane_f(m, 63);
+}
+
+__device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane, int &mysel, float &myw, bool want_w,
+                                         const Gating &gt = Gating{}) {
+    const int nper = (E + 63) >> 6;
     float v[TOPK_MAX_PER_LANE];
 #pragma unroll
     for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
@@ -299,59 +315,46 @@ __device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane,
         for (int i = 0; i < TOPK_MAX_PER_LANE; ++i)
             if (lane + 64 * i < E) v[i] = ex[i] * inv;
     }
+    mysel = 0;
+    float mys = 0.f;   // lane k: the k-th selected value
+    for (int r = 0; r < K; ++r) {
+        float m = v[0];
 #pragma unroll
-    for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
-        const int e = lane + 64 * i;
-        if (e < E4) sv[e] = v[i];
-    }
-    wave_lds_sync();
-    int r[TOPK_MAX_PER_LANE] = {0, 0, 0, 0};
-    if (nper == 1) {
-        // one value per lane: the same count against the 64 lanes' values
-        // read as scalars (lanes past E hold -inf), unrolled and branch-free
+        for (int i = 1; i < TOPK_MAX_PER_LANE; ++i)
+            if (i < nper) m = fmaxf(m, v[i]);
+        const float s = wave_max_uniform(m);
+        int e = -1;
 #pragma unroll
-        for (int j = 0; j < 64; ++j) {
-            const float x = lane_f(v[0], j);
-            r[0] += (x > v[0]) | ((x == v[0]) & (j < lane));
+        for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
+            if (i >= nper) break;
+            const unsigned long long b = __ballot(v[i] == s);
+            if (e < 0 && b != 0ull) e = 64 * i + (int)__builtin_ctzll(b);
         }
-    } else {
-#pragma unroll 4
-        for (int j = 0; j < E4; j += 4) {
-            const float4 q = *(const float4 *)(sv + j);
-            const float qq[4] = {q.x, q.y, q.z, q.w};
+        e = __builtin_amdgcn_readfirstlane(e);
 #pragma unroll
-            for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
-                if (i >= nper) break;
-                const int e = lane + 64 * i;
-#pragma unroll
-                for (int c = 0; c < 4; ++c) r[i] += (qq[c] > v[i]) | ((qq[c] == v[i]) & (j + c < e));
-            }
+        for (int i = 0; i < TOPK_MAX_PER_LANE; ++i)
+            if (e == 64 * i + lane) v[i] = __builtin_nanf("");
+        if (lane == r) {
+            mysel = e;
+            mys = s;
         }
     }
-#pragma unroll
-    for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
-        const int e = lane + 64 * i;
-        if (i < nper && e < E && r[i] < K) ssel[r[i]] = e;
-    }
-    wave_lds_sync();
-    mysel = lane < K ? ssel[lane] : 0;
     if (!want_w) {
         myw = 0.f;
         return;
     }
     if (gt.kind == 1) {
-        const float s = lane < K ? gating_sigmoid(l[mysel]) : 0.f;
+        const float sg = lane < K ? gating_sigmoid(l[mysel]) : 0.f;
         double sum = 0.0;
-        for (int k = 0; k < K; ++k) sum = sum + (double)lane_f(s, k);
-        myw = s / ((float)sum + gt.eps) * gt.scaling;
+        for (int k = 0; k < K; ++k) sum = sum + (double)lane_f(sg, k);
+        myw = sg / ((float)sum + gt.eps) * gt.scaling;
     } else if (gt.kind == 2) {
-        const float p = lane < K ? sv[mysel] : 0.f;
+        const float p = lane < K ? mys : 0.f;
         double sum = 0.0;
         for (int k = 0; k < K; ++k) sum = sum + (double)lane_f(p, k);
         myw = p / (float)sum;
     } else {
-        const float myval = lane < K ? sv[mysel] : 0.f;
-        myw = softmax_selected_wave(myval, K, lane);
+        myw = softmax_selected_wave(lane < K ? mys : 0.f, K, lane);
     }
     if (gt.expert_scale && lane < K) myw = myw * gt.expert_scale[mysel];
 }

@@ -272,11 +272,12 @@ class Context:
         call("mi_moe_ctx_reserve", self.h, max_tokens, D, I, E, K)
 
     def set_gemm_threshold(self, t: int) -> None:
-        """GEMM from t tokens on; 0 = by shape (GEMM when 4 T K >= 5 E)."""
+        """GEMM from t tokens on; 0 = by shape (GEMM when 2 T K >= E)."""
         call("mi_moe_ctx_set_gemm_threshold", self.h, t)
 
     def set_gemm_tiles(self, kind: int) -> None:
-        """Q4_K-gate GEMM row tiles: 0 by shape, 1 192-row, 2 32-row"""
+        """Q4_K-gate GEMM row tiles: 0 by shape, 1 192-row, 2 32-row, 3 the
+        skinny 16-row products (all-Q4_K layers)"""
         call("mi_moe_ctx_set_gemm_tiles", self.h, int(kind))
 
     def set_fused_decode(self, mode) -> None:

@@ -581,6 +581,8 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-sweeps", action="store_true",
                     help="skip the config-3 batched-decode sweep and the config-4 layer stack")
+    ap.add_argument("--no-stack", action="store_true",
+                    help="skip the config-4 layer stack (its HIP graph capture) but run the config-3 sweep")
     ap.add_argument("--cpu-tokens", type=int, default=1024,
                     help="tokens of the CPU baseline sample (default: the whole config-1 batch)")
     ap.add_argument("--calib-copy", action="store_true",
@@ -684,7 +686,8 @@ def main() -> int:
 
     if not args.no_sweeps:
         result["config3"] = config3_sweep(args.copies)
-        result["config4"] = config4_stack()
+        if not args.no_stack:
+            result["config4"] = config4_stack()
     result.update({k: v for k, v in extra.items() if k.startswith("stream")})
     print(json.dumps(result), flush=True)
     return 0

@@ -6,8 +6,9 @@
 //   router -> top-k/softmax -> dispatch -> Q8_K(x) -> gate/up (+GLU, +Q8_K)
 //   -> down -> weighted combine (+residual)
 // Decode-sized calls use the grouped integer-dot GEMV kernels, larger calls
-// the grouped MFMA GEMM kernels (use_gemm: by default from 1.25 dispatched
-// rows per expert on average).
+// the grouped MFMA GEMM kernels (use_gemm: by default from half a dispatched
+// row per expert on average for Q4_K / Q6_K tables, use_gemm_wide: from 1.25
+// for the others).
 // All workspace comes from mi_moe_ctx_reserve; forward calls never allocate.
 #include <hip/hip_runtime.h>
 

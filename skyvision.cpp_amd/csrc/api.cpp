@@ -92,6 +92,7 @@ struct mi_moe_ctx {
     int64_t cap_T = 0;
     int32_t cap_D = 0, cap_I = 0, cap_E = 0, cap_K = 0;
     int64_t cap_rows = 0, cap_kmax = 0, cap_tiles = 0;
+    int64_t cap_z = 0;   // floats of z
     void *ws = nullptr;
     size_t ws_bytes = 0;
 
@@ -390,6 +391,10 @@ bool g4_path(const mi_moe_layer *L) { return L->gate.type == MI_TYPE_Q4_K || !ac
 // to 128 tokens, moondream3 up to 64), where the products are bound by that
 // stream; 192-row balanced tiles above.
 constexpr int64_t G4_SMALL_ROWS = 8;
+// logits (T x E) up to which the router may split its chunks: beyond, the
+// partials' round trip costs more than the split saves (qwen3omni T = 128:
+// +0.8 us per layer; moondream3 T = 128, half the partials: -3.2 us)
+constexpr int64_t FRONT_SPLIT_TE_MAX = 8192;
 bool g4_small_tiles(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T) {
     if (c->gemm_tiles == 1 || c->gemm_tiles == 2) return c->gemm_tiles == 2;
     return T * L->n_expert_used <= G4_SMALL_ROWS * L->n_expert;
@@ -419,6 +424,24 @@ int gs_splits(const mi_moe_ctx *c, int64_t rows, int E, int64_t ncols, int waves
     const double tiles = std::max(1.0, hit + std::max(0.0, (double)rows - hit * GS_BM) / GS_BM);
     const int cap = (int)std::max<int64_t>(1, ncols / 16 / waves);
     return std::max(1, std::min(cap, (int)std::lround(std::max(1, c->n_cu) / tiles)));
+}
+
+// Small batches: the router's D / 64 chunks split over work-groups when the
+// (16-token, 16-expert) tiles alone would leave at least half of the CUs
+// idle (launch_front_parts); the chunk partials live in z, which is free
+// until the down product.  The chunks per work-group, or 0 for the
+// one-launch front.  Measured (layer us, same box, 16 rotated copies, the
+// default product paths): qwen3omni T = 1 / 4 / 16 / 32 / 64: 40.2 / 60.9 /
+// 100.6 / 114.2 / 118.5 -> 38.0 / 58.4 / 97.6 / 112.1 / 118.4; moondream3
+// 42.2 / 63.9 / 86.8 / 87.9 / 88.7 -> 38.1 / 60.6 / 82.2 / 85.1 / 85.9.
+int front_split_cps(const mi_moe_ctx *c, int64_t T, int D, int E) {
+    const int nch = (D + 63) / 64;
+    if (nch > 32 || T * E > FRONT_SPLIT_TE_MAX || E > 128) return 0;
+    const int64_t tiles = ((T + 15) / 16) * ((E + 15) / 16);
+    int nsp = 1;
+    while (2 * nsp <= nch && tiles * 2 * nsp <= std::max(1, c->n_cu)) nsp *= 2;
+    if (nsp < 2 || (int64_t)nch * T * E * 2 > c->cap_z) return 0;
+    return (nch + nsp - 1) / nsp;
 }
 
 bool x_q8_spec(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T, Q8Out &qx) {
@@ -782,6 +805,7 @@ bool carve_workspace(mi_moe_ctx *c, char *base, int64_t max_tokens, int32_t D, i
     c->cap_rows = rows;
     c->cap_kmax = kmax_q;
     c->cap_tiles = tiles;
+    c->cap_z = rows * wide;
     return (size_t)(q - base) == ws_bytes(max_tokens, D, I, E, K);
 }
 
@@ -1030,19 +1054,30 @@ int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T
         Q8Out qx;
         const bool xq = !xr && x_q8_spec(c, L, T, qx);
         const float *xrow = xr ? xr : x;
-        const int rc = launch_front(L->router_w, L->router_b, xrow, D, T, D, E, c->logits, xq ? &qx : nullptr, st);
-        if (rc == -6) TRY(launch_router(L->router_w, L->router_b, xrow, D, T, D, E, c->logits, st));
-        else TRY(rc);
-        stage_end(c, "router", st);
         Gating gt;
         gt.kind = L->gating;
         gt.sel_bias = L->sel_bias;
         gt.expert_scale = L->expert_scale;
         gt.scaling = L->routed_scaling != 0.f ? L->routed_scaling : 1.f;
         gt.eps = L->gate_eps;
-        TRY(launch_topk_softmax(c->logits, E, T, E, K, c->sel, K, c->w, st, gt));
+        const int cps = front_split_cps(c, T, D, E);
+        bool x_done = false;   // the Q8_K of x came with the router
+        if (cps > 0) {
+            double *parts = (double *)c->z;   // free until the down product
+            TRY(launch_front_parts(L->router_w, xrow, D, T, D, E, cps, parts, xq ? &qx : nullptr, st));
+            x_done = xq;
+            stage_end(c, "router", st);
+            TRY(launch_topk_parts(parts, D, L->router_b, c->logits, T, E, K, c->sel, K, c->w, st, gt));
+        } else {
+            const int rc = launch_front(L->router_w, L->router_b, xrow, D, T, D, E, c->logits, xq ? &qx : nullptr, st);
+            if (rc == -6) TRY(launch_router(L->router_w, L->router_b, xrow, D, T, D, E, c->logits, st));
+            else TRY(rc);
+            x_done = xq && rc == 0;
+            stage_end(c, "router", st);
+            TRY(launch_topk_softmax(c->logits, E, T, E, K, c->sel, K, c->w, st, gt));
+        }
         stage_end(c, "topk_softmax", st);
-        TRY(run_experts(c, L, x, T, c->sel, c->sel, c->w, res, out, st, xq && rc == 0, false, add));
+        TRY(run_experts(c, L, x, T, c->sel, c->sel, c->w, res, out, st, x_done, false, add));
     }
     if (routing) {
         const DispBuf &d = c->disp[0];
@@ -1127,6 +1162,7 @@ int noalloc_ctx(mi_moe_ctx **out) {
             if (!ptr) return MI_MOE_ERR_HIP;
             mi_moe_ctx &c = d.ctx;
             c.device = dev;
+            if (hipDeviceGetAttribute(&c.n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) c.n_cu = 256;
             c.fused_decode = MI_DECODE_CHAIN;
             c.ws = nullptr;   // not owned
             c.ws_bytes = NA_BYTES;

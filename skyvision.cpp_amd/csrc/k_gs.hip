@@ -11,10 +11,9 @@
 // share of the split's 16-column groups block by block.  A step is one
 // 256-value super-block of 16 weight rows (GLU: 16 gate rows and the 16
 // matching up rows).  The lane's weight bytes go straight into registers
-// (16-byte buffer loads of the block's header - d, dmin, scales - and of the
-// 32 bytes of its qs chunk), GS_RING - 1 steps ahead of the step computed,
-// across column-group boundaries: a wave keeps weights in flight from its
-// first step to its last.
+// (16-byte loads of the block's header - d, dmin, scales - and of the 32
+// bytes of its qs chunk) in groups of consecutive steps, across column-group
+// boundaries.
 //
 // MFMA: v_mfma_f32_16x16x32_f16, weights as A (16 rows), the tile's rows as
 // B (16 columns).  Lane (i = lane % 16, G = lane / 16) supplies 8 weights of
@@ -37,11 +36,12 @@
 namespace mimoe {
 
 // waves per work-group: one work-group per CU (GLU: 2 waves per SIMD; the
-// store's smaller ring: 4), so that no work-group of a CU outlasts another
-// (the older work-group's waves win the issue arbitration)
+// store, with fewer weight registers per step: 4), so that no work-group of
+// a CU outlasts another (the older work-group's waves win the issue
+// arbitration)
 template <bool GLU> constexpr int gs_waves() { return GLU ? 8 : 16; }
-constexpr int GS_RING_GLU = 5;   // steps of weights held per wave (GLU: 2 matrices per step)
-constexpr int GS_RING_ST = 8;    // (store: 1 matrix per step)
+constexpr int GS_GROUP_GLU = 3;   // weight steps per load group (GLU: 2 matrices per step)
+constexpr int GS_GROUP_ST = 6;    // (store: 1 matrix per step)
 
 typedef __attribute__((address_space(3))) void gs_lds_t;
 typedef __amdgpu_buffer_rsrc_t gs_rsrc_t;
@@ -249,7 +249,8 @@ template <bool GLU, int ACT, int KMAX>
 __global__ void __launch_bounds__(64 * gs_waves<GLU>()) __attribute__((amdgpu_waves_per_eu(gs_waves<GLU>() / 4, gs_waves<GLU>() / 4)))
 k_gs(G2Args g, int splits) {
     constexpr int NW = gs_waves<GLU>();
-    constexpr int NM = GLU ? 2 : 1, R = GLU ? GS_RING_GLU : GS_RING_ST, LPS = 3 * NM;
+    constexpr int NM = GLU ? 2 : 1, LPS = 3 * NM;
+    constexpr int D = GLU ? GS_GROUP_GLU : GS_GROUP_ST;
     constexpr int LDSB = ((GS_BM * (2 * KMAX + 16) + 1023) / 1024) * 1024;
     __shared__ __attribute__((aligned(1024))) char As[LDSB];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -275,20 +276,23 @@ k_gs(G2Args g, int splits) {
     st.nb = nb;
     st.left = nsteps - 1;
     // Prologue, in issue order: once the slot indices are in, the activation
-    // rows into LDS and the ring's first R - 1 weight steps; the K loop
-    // starts when the work-group's rows are in.  (Issuing only the first
-    // step before the barrier and the rest after it shortens the prologue
-    // but measured slower overall: the weight stream starts later.)
+    // rows into LDS and the first group of weight steps; the K loop starts
+    // when the work-group's rows are in.
     gs_wait<0>();
     asm volatile("" : "+v"(p_row));
     const int arow = g.ne11 == 1 ? p_row / g.K : p_row;
     const gs_rsrc_t rx = gs_rsrc(g.xh, g.xrows * (int64_t)Kin * 2);
     gs_stage_rows(rx, As, arow, it.mrows, Kin / 8, 2u * (uint32_t)Kin, wave, NW, lane);
-    GsW<NM> w[R];
+    // weights in groups of D steps: a group is loaded, waited for and
+    // computed (the other waves of the CU keep the memory busy meanwhile).
+    // Consecutive blocks of a row leave together, which the memory serves
+    // faster than the same loads spread one step apart: a rolling ring that
+    // kept D steps in flight measured 1-3 % slower per layer.
+    GsW<NM> w[D];
 #pragma unroll
-    for (int j = 0; j < R - 1; ++j) gs_load<NM>(st, w[j]);
-    gs_wait<(R - 1) * LPS>();   // the wave's LDS loads landed
-    lds_barrier();               // (a barrier without the memory fence: the weight steps stay in flight)
+    for (int j = 0; j < D; ++j) gs_load<NM>(st, w[j]);
+    gs_wait<D * LPS>();   // the wave's LDS loads landed
+    lds_barrier();        // (a barrier without the memory fence: the weight steps stay in flight)
     const uint32_t rs = 2u * (uint32_t)Kin + 16u;
     const char *lds_lane = As + i16 * rs + 16 * (G & 1) + 256 * (G >> 1);
     float4_t acc[NM];
@@ -297,47 +301,50 @@ k_gs(G2Args g, int splits) {
     bool over = false;
     int ckb = 0, ccg = c_lo + wave;
     const bool row_live = i16 < it.mrows;
-    // steps in groups of R (ring slot u); the exit test before every step
-    // leaves the group only forwards
-    for (int s0 = 0;; s0 += R) {
+    // one step on the weights in w[j]; at a column group's last block its
+    // 16 x 16 outputs leave
+    auto step = [&](GsW<NM> &wj) __attribute__((always_inline)) {
+        gs_pin<NM>(wj);
+        gs_step<NM>(wj, lds_lane + 512 * ckb, G, acc);
+        if (++ckb == nb) {
+            ckb = 0;
+            float v[4];
 #pragma unroll
-        for (int u = 0; u < R; ++u) {
-            if (s0 + u >= nsteps) goto done;
-            // step s0 + u + R - 1 into the slot step s0 + u - 1 used, then
-            // wait for this step's (every later step's loads may stay out)
-            gs_load<NM>(st, w[(u + R - 1) % R]);
-            gs_wait<(R - 1) * LPS>();
-            gs_pin<NM>(w[u]);
-            gs_step<NM>(w[u], lds_lane + 512 * ckb, G, acc);
-            if (++ckb == nb) {
-                ckb = 0;
-                float v[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    if constexpr (GLU) v[r] = act_pair_fast<ACT>(acc[0][r], acc[1][r]);
-                    else v[r] = acc[0][r];
-                }
-                const int64_t col = (int64_t)ccg * 16 + 4 * G;
-                if (g.yh) {
-                    // (rows past the tile's hold stale LDS bytes: not counted, not stored)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) over = over || (row_live && !(fabsf(v[r]) <= kF16Max));
-                    const uint32_t h01 = (uint32_t)__builtin_bit_cast(uint16_t, f16_sat(v[0])) |
-                                         ((uint32_t)__builtin_bit_cast(uint16_t, f16_sat(v[1])) << 16);
-                    const uint32_t h23 = (uint32_t)__builtin_bit_cast(uint16_t, f16_sat(v[2])) |
-                                         ((uint32_t)__builtin_bit_cast(uint16_t, f16_sat(v[3])) << 16);
-                    if (row_live) *(uint2 *)(g.yh + (int64_t)p_row * g.ldy + col) = make_uint2(h01, h23);
-                } else if (row_live) {
-                    *(float4 *)(g.y + (int64_t)p_row * g.ldy + col) = make_float4(v[0], v[1], v[2], v[3]);
-                }
-#pragma unroll
-                for (int m = 0; m < NM; ++m) acc[m] = float4_t{0.f, 0.f, 0.f, 0.f};
-                ccg += NW;
+            for (int r = 0; r < 4; ++r) {
+                if constexpr (GLU) v[r] = act_pair_fast<ACT>(acc[0][r], acc[1][r]);
+                else v[r] = acc[0][r];
             }
+            const int64_t col = (int64_t)ccg * 16 + 4 * G;
+            if (g.yh) {
+                // (rows past the tile's hold stale LDS bytes: not counted, not stored)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) over = over || (row_live && !(fabsf(v[r]) <= kF16Max));
+                const uint32_t h01 = (uint32_t)__builtin_bit_cast(uint16_t, f16_sat(v[0])) |
+                                     ((uint32_t)__builtin_bit_cast(uint16_t, f16_sat(v[1])) << 16);
+                const uint32_t h23 = (uint32_t)__builtin_bit_cast(uint16_t, f16_sat(v[2])) |
+                                     ((uint32_t)__builtin_bit_cast(uint16_t, f16_sat(v[3])) << 16);
+                if (row_live) *(uint2 *)(g.yh + (int64_t)p_row * g.ldy + col) = make_uint2(h01, h23);
+            } else if (row_live) {
+                *(float4 *)(g.y + (int64_t)p_row * g.ldy + col) = make_float4(v[0], v[1], v[2], v[3]);
+            }
+#pragma unroll
+            for (int m = 0; m < NM; ++m) acc[m] = float4_t{0.f, 0.f, 0.f, 0.f};
+            ccg += NW;
         }
+    };
+    // the exit test before every step leaves a group only forwards
+    for (int s0 = 0;; s0 += D) {
+        gs_wait<0>();
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            if (s0 + j >= nsteps) goto done;
+            step(w[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < D; ++j) gs_load<NM>(st, w[j]);
     }
 done:
-    gs_wait<0>();   // the ring's last (unused) loads land before the wave ends
+    gs_wait<0>();   // the last group's unused loads land before the wave ends
     if (__ballot(over) != 0 && lane == 0 && g.range_total) atomicAdd(g.range_total, 1);
 }
 

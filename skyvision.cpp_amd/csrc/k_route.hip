@@ -481,6 +481,60 @@ __global__ void __launch_bounds__(1024) k_front(const float *__restrict__ W, con
     }
 }
 
+// Small batches: with few 16 x 16 (token, expert) tiles k_front leaves most
+// CUs idle while each of its work-groups runs the tile's D / 64 chunk chains
+// (32 at D = 2048, ~4 us of fp64 MFMA on one CU).  Here a tile's chunks are
+// dealt to nsp work-groups of cps waves (work-group 8 q + x: tile q / nsp,
+// split q % nsp; chunk split * cps + wave); each wave computes its chunk's
+// 16 x 16 partial exactly as k_front does and stores it to parts[c][t][e]
+// (fp64); k_topk_parts adds a token's partials in chunk order, so the logits
+// are bit-identical to k_front's.  The Q8_K of x is dealt to the slab's
+// work-groups as in k_front.
+template <bool VEC, int XO>
+__global__ void __launch_bounds__(1024) k_front_parts(const float *__restrict__ W, const float *__restrict__ x,
+                                                      int64_t ldx, int64_t T, int D, int E, int cps,
+                                                      double *__restrict__ parts, Q8Out o) {
+    __shared__ float4 stage[RT_WAVES][256];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nch = (D + 63) / 64, net = (E + 15) / 16, nsp = (nch + cps - 1) / cps;
+    const int lin = blockIdx.x;
+    const int split = lin % nsp, q = lin / nsp, et = q % net;
+    const int64_t t0 = (int64_t)(q / net) * 16;
+    const int e0 = et * 16;
+    float4 *stg = stage[wave];
+    const int c = split * cps + wave;
+    if (c < nch) {
+        RtChunk cur;
+        rt_load<VEC>(cur, x, ldx, t0, T, W, e0, E, D, c, lane);
+        float xv[16], wv[16];
+        rt_transpose(cur.x, stg, lane, xv);
+        rt_transpose(cur.w, stg, lane, wv);
+        double4_t part = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2)
+            part = __builtin_amdgcn_mfma_f64_16x16x4f64((double)xv[s2], (double)wv[s2], part, 0, 0, 0);
+        // slot (lane, r): token row 4 r + lane / 16, expert column lane % 16
+        const int ee = e0 + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t tt = t0 + 4 * r + (lane >> 4);
+            if (tt < T && ee < E) parts[((int64_t)c * T + tt) * E + ee] = part[r];
+        }
+    }
+    if (o.q8 || o.xh) {
+        const int nb = D / QK, ngrp = (nb + 3) >> 2;
+        const int nwg = net * nsp, wg = et * nsp + split, nw = (int)(blockDim.x >> 6);
+        for (int i = wg + nwg * wave; i < 16 * ngrp; i += nwg * nw) {
+            const int64_t row = t0 + i / ngrp;
+            if (row >= T) continue;
+            int8_t *sq = (int8_t *)stg;
+            float *sd = (float *)(stg + 64);
+            if (XO == XO_Q4) q8k_row_group<VEC, XO_Q4>(x, ldx, row, i % ngrp, nb, o, sq, sd, lane);
+            else q8k_row_group<VEC, XO_ANY>(x, ldx, row, i % ngrp, nb, o, sq, sd, lane);
+        }
+    }
+}
+
 // generic form (any D): thread (expert, chunk) computes one partial
 __global__ void __launch_bounds__(256) k_router_split(const float *__restrict__ W, const float *__restrict__ bias,
                                                       const float *__restrict__ x, int64_t ldx, int D, int E,
@@ -535,6 +589,27 @@ int launch_front(const float *W, const float *b, const float *x, int64_t ldx, in
     return hip_check_launch();
 }
 
+int launch_front_parts(const float *W, const float *x, int64_t ldx, int64_t T, int D, int E, int cps,
+                       double *parts, const Q8Out *qx, hipStream_t st) {
+    if (T <= 0) return 0;
+    const int nch = (D + 63) / 64;
+    if (nch > RM_MAX_CHUNKS || cps < 1 || cps > RT_WAVES || T > (int64_t)1 << 24) return -6;
+    if (qx && D % QK) return -6;
+    const bool vec = (D % 64 == 0) && (ldx % 4 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)W % 16 == 0);
+    const int64_t nsp = (nch + cps - 1) / cps, net = (E + 15) / 16, nslab = (T + 15) / 16;
+    const int64_t blocks = nslab * net * nsp;
+    if (blocks > 0x7fffffff) return -6;
+    const Q8Out o = qx ? *qx : Q8Out{};
+    const dim3 grid((unsigned)blocks), block((unsigned)(64 * cps));
+    if (vec && q8_xo(o) == XO_Q4)
+        hipLaunchKernelGGL((k_front_parts<true, XO_Q4>), grid, block, 0, st, W, x, ldx, T, D, E, cps, parts, o);
+    else if (vec)
+        hipLaunchKernelGGL((k_front_parts<true, XO_ANY>), grid, block, 0, st, W, x, ldx, T, D, E, cps, parts, o);
+    else
+        hipLaunchKernelGGL((k_front_parts<false, XO_ANY>), grid, block, 0, st, W, x, ldx, T, D, E, cps, parts, o);
+    return hip_check_launch();
+}
+
 int launch_router(const float *W, const float *b, const float *x, int64_t ldx, int64_t T, int D, int E,
                   float *logits, hipStream_t st) {
     if (T <= 0) return 0;
@@ -575,6 +650,69 @@ int launch_topk_softmax(const float *logits, int64_t ld_logits, int64_t T, int E
     if (gt.kind < 0 || gt.kind > 2) return -6;
     hipLaunchKernelGGL(k_topk_softmax, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, logits, ld_logits, T, E,
                        K, sel, ld_sel, w, gt);
+    return hip_check_launch();
+}
+
+// The same on the chunk partials of k_front_parts, one token per wave and
+// work-group (E <= 64 NPER): lane l first adds its experts' partials in
+// chunk order (fp64, as k_front: every load issued before the first add),
+// rounds to fp32, adds the bias and writes the logits.
+template <int NPER>
+__global__ void __launch_bounds__(64) k_topk_parts(const double *__restrict__ parts, int nch,
+                                                   const float *__restrict__ bias, float *__restrict__ logits,
+                                                   int64_t T, int E, int K, int32_t *__restrict__ sel, int64_t lds,
+                                                   float *__restrict__ w, Gating gt) {
+    static_assert(NPER <= TOPK_MAX_PER_LANE, "experts per lane");
+    const int lane = threadIdx.x;
+    const int64_t t = blockIdx.x;
+    const int64_t cs = T * E;
+    double pv[NPER][RM_MAX_CHUNKS];
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+        const int e = lane + 64 * i;
+        const double *p = parts + t * E + (e < E ? e : 0);
+#pragma unroll
+        for (int c = 0; c < RM_MAX_CHUNKS; ++c) pv[i][c] = c < nch ? p[(int64_t)c * cs] : 0.0;
+    }
+    float raw[TOPK_MAX_PER_LANE];
+#pragma unroll
+    for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) raw[i] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+        const int e = lane + 64 * i;
+        double acc = 0.0;
+#pragma unroll
+        for (int c = 0; c < RM_MAX_CHUNKS; ++c)
+            if (c < nch) acc = acc + pv[i][c];
+        float v = (float)acc;
+        if (e < E) {
+            if (bias) v = v + bias[e];
+            raw[i] = v;
+            logits[t * E + e] = v;
+        }
+    }
+    int mysel;
+    float myw;
+    topk_softmax_regs(raw, E, K, lane, mysel, myw, w != nullptr, gt);
+    if (lane < K) {
+        sel[t * lds + lane] = mysel;
+        if (w) w[t * K + lane] = myw;
+    }
+}
+
+int launch_topk_parts(const double *parts, int D, const float *bias, float *logits, int64_t T, int E, int K,
+                      int32_t *sel, int64_t ld_sel, float *w, hipStream_t st, const Gating &gt) {
+    if (T <= 0) return 0;
+    if (E > 128 || K > 64 || K > E || K <= 0 || T > 0x7fffffff) return -6;
+    if (gt.kind < 0 || gt.kind > 2) return -6;
+    const int nch = (D + 63) / 64;
+    if (nch > RM_MAX_CHUNKS) return -6;
+    if (E <= 64)
+        hipLaunchKernelGGL(k_topk_parts<1>, dim3((unsigned)T), dim3(64), 0, st, parts, nch, bias, logits, T, E, K, sel,
+                           ld_sel, w, gt);
+    else
+        hipLaunchKernelGGL(k_topk_parts<2>, dim3((unsigned)T), dim3(64), 0, st, parts, nch, bias, logits, T, E, K, sel,
+                           ld_sel, w, gt);
     return hip_check_launch();
 }
 

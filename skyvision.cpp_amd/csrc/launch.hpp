@@ -56,6 +56,14 @@ int launch_front(const float *W, const float *b, const float *x, int64_t ldx, in
 struct Gating;
 int launch_topk_softmax(const float *logits, int64_t ld_logits, int64_t T, int E, int K, int32_t *sel,
                         int64_t ld_sel, float *w, hipStream_t st, const Gating &gt);
+// small batches: the router's chunk partials parts[D / 64][T][E] (fp64) by
+// tiles split over the chunks (cps chunks per work-group) plus (qx) the Q8_K
+// of x; then the logits (chunk order, + b) and the top-k / softmax of
+// launch_topk_softmax from them (logits [T][E] written too; E <= 128)
+int launch_front_parts(const float *W, const float *x, int64_t ldx, int64_t T, int D, int E, int cps,
+                       double *parts, const Q8Out *qx, hipStream_t st);
+int launch_topk_parts(const double *parts, int D, const float *bias, float *logits, int64_t T, int E, int K,
+                      int32_t *sel, int64_t ld_sel, float *w, hipStream_t st, const Gating &gt);
 
 struct Dispatch {
     int32_t *counts;     // [E]

@@ -279,15 +279,16 @@ __device__ inline float wave_max_uniform(float m) {
     return lane_f(m, 63);
 }
 
-__device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane, int &mysel, float &myw, bool want_w,
-                                         const Gating &gt = Gating{}) {
+// raw[i]: the logit of expert 64 i + lane (any value past E)
+__device__ inline void topk_softmax_regs(const float (&raw)[TOPK_MAX_PER_LANE], int E, int K, int lane, int &mysel,
+                                         float &myw, bool want_w, const Gating &gt) {
     const int nper = (E + 63) >> 6;
     float v[TOPK_MAX_PER_LANE];
 #pragma unroll
     for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
         const int e = lane + 64 * i;
         if (e < E) {
-            v[i] = l[e];
+            v[i] = raw[i];
             if (gt.kind == 1) v[i] = gating_sigmoid(v[i]) + (gt.sel_bias ? gt.sel_bias[e] : 0.f);
         } else {
             v[i] = -INFINITY;
@@ -344,7 +345,14 @@ __device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane,
         return;
     }
     if (gt.kind == 1) {
-        const float sg = lane < K ? gating_sigmoid(l[mysel]) : 0.f;
+        // the logit of the lane's selected expert, from the lane that holds it
+        float lsel = 0.f;
+#pragma unroll
+        for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
+            const float t = __shfl(raw[i], mysel & 63, 64);
+            if (i == (mysel >> 6)) lsel = t;
+        }
+        const float sg = lane < K ? gating_sigmoid(lsel) : 0.f;
         double sum = 0.0;
         for (int k = 0; k < K; ++k) sum = sum + (double)lane_f(sg, k);
         myw = sg / ((float)sum + gt.eps) * gt.scaling;
@@ -357,6 +365,18 @@ __device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane,
         myw = softmax_selected_wave(lane < K ? mys : 0.f, K, lane);
     }
     if (gt.expert_scale && lane < K) myw = myw * gt.expert_scale[mysel];
+}
+
+// the same, on the E logits at l
+__device__ inline void topk_softmax_wave(const float *l, int E, int K, int lane, int &mysel, float &myw, bool want_w,
+                                         const Gating &gt = Gating{}) {
+    float raw[TOPK_MAX_PER_LANE];
+#pragma unroll
+    for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
+        const int e = lane + 64 * i;
+        raw[i] = e < E ? l[e] : 0.f;
+    }
+    topk_softmax_regs(raw, E, K, lane, mysel, myw, want_w, gt);
 }
 
 }  // namespace mimoe

@@ -524,7 +524,8 @@ int run_experts_b32(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_
 // add: [T][D] added to the routed sum before the residual (or null)
 int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T, const int32_t *ids_gu,
                 const int32_t *ids_dn, const float *w, const float *res, float *out, hipStream_t st,
-                bool x_done = false, bool check_ids = false, const float *add = nullptr) {
+                bool x_done = false, bool check_ids = false, const float *add = nullptr,
+                bool disp_out = true) {
     if (is_b32f(L->gate.type)) return run_experts_b32(c, L, x, T, ids_gu, ids_dn, w, res, out, st, check_ids, add);
     const int D = L->n_embd, E = L->n_expert, K = L->n_expert_used, I = L->n_ff;
     const int64_t rows = T * K;
@@ -539,9 +540,18 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
     const bool gs = g4 && gs_path(c, L, T);
     const int bm = !g4 ? GEMM_BM : gs ? GS_BM : g4_small_tiles(c, L, T) ? G4_BM_SMALL : G4_BM;
     const int max_tiles = (int)((rows + bm - 1) / bm + max_active);
-
-    TRY(launch_dispatch(ids_gu, T, K, E, bm, g4, c->disp[0].view(), st));
-    if (!same_ids) TRY(launch_dispatch(ids_dn, T, K, E, bm, g4, c->disp[1].view(), st));
+    // Small calls on the 32-row tiles, ids from the router: no dispatch
+    // launch, each GEMM work-group finds its tile from the ids itself
+    // (g4_self_tile), unless the caller wants the dispatch's outputs.
+    // Measured (layer us, kernel chain, same box): qwen3omni T = 8 / 16 / 32
+    // / 64: 78.3 / 100.1 / 115.9 / 120.6 -> 74.8 / 96.7 / 113.0 / 118.3;
+    // moondream3 79.3 / 84.3 / 87.9 / 88.5 -> 76.5 / 80.6 / 85.5 / 85.8.
+    const bool self_disp = bm == G4_BM_SMALL && !gs && same_ids && !check_ids && !disp_out && rows <= G4_SD_IDS &&
+                           E <= 256;
+    if (!self_disp) {
+        TRY(launch_dispatch(ids_gu, T, K, E, bm, g4, c->disp[0].view(), st));
+        if (!same_ids) TRY(launch_dispatch(ids_dn, T, K, E, bm, g4, c->disp[1].view(), st));
+    }
     const DispBuf &dg = c->disp[0];
     const DispBuf &dd = same_ids ? c->disp[0] : c->disp[1];
     stage_end(c, "dispatch", st);
@@ -626,6 +636,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         a.tile_r0 = dg.tile_r0; a.tile_start = dg.tile_start; a.tile_rows = dg.tile_rows; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
         a.tile_perm = dg.tile_perm;
         a.bm = bm;
+        if (self_disp) { a.ids = ids_gu; a.nids = (int)rows; a.n_expert = E; }
         a.y = c->f1; a.ldy = I; a.ncols = I; a.xrows = T;
         // gated: the GLU rows as fp16 (half the bytes of their round trip to
         // the Q8_K pass; saturation at the fp16 range is counted)
@@ -645,6 +656,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         d.tile_r0 = dd.tile_r0; d.tile_start = dd.tile_start; d.tile_rows = dd.tile_rows; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles; d.xrows = (int64_t)T * K;
         d.tile_perm = dd.tile_perm;
         d.bm = bm;
+        if (self_disp) { d.ids = ids_dn; d.nids = (int)rows; d.n_expert = E; }
         // the slot rows as fp16 (half the bytes of the round trip to the
         // combine; saturation at the fp16 range is counted)
         d.y = c->z; d.yh = zh = (_Float16 *)c->z; d.range_total = c->range_total; d.ldy = D; d.ncols = D;
@@ -1077,7 +1089,8 @@ int forward_impl(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T
             TRY(launch_topk_softmax(c->logits, E, T, E, K, c->sel, K, c->w, st, gt));
         }
         stage_end(c, "topk_softmax", st);
-        TRY(run_experts(c, L, x, T, c->sel, c->sel, c->w, res, out, st, x_done, false, add));
+        TRY(run_experts(c, L, x, T, c->sel, c->sel, c->w, res, out, st, x_done, false, add,
+                        routing && (routing->counts || routing->offsets || routing->perm)));
     }
     if (routing) {
         const DispBuf &d = c->disp[0];

@@ -39,6 +39,7 @@
 #include "act.hpp"
 #include "common.hpp"
 #include "launch.hpp"
+#include "wave_ops.hpp"
 
 namespace mimoe {
 
@@ -95,6 +96,87 @@ __device__ __forceinline__ G4Tile g4_desc(const G2Args &g, int tile) {
     asm volatile("" : "+s"(t.e), "+s"(t.start), "+s"(t.mrows), "+s"(nt));
     t.nrt = (t.mrows + 31) >> 5;
     t.live = tile < nt;
+    return t;
+}
+
+// Small calls without a dispatch launch (G2Args::ids set, at most
+// G4_SD_IDS ids, bm = G4_BM_SMALL): every work-group derives its own tile
+// from the call's flat ids in LDS (scratch: the first activation buffer,
+// free until the K loop) - the counts per expert, ceil(count / BM) equal
+// tiles per expert in expert order (the dispatch's balanced tiles: the
+// first count % tiles tiles one row longer), the expert holding tile
+// `tile`, and that tile's rows: the expert's flat slot indices in ascending
+// order (ballots per wave, wave totals in LDS), rows r0 .. r0 + rows of
+// them.  Thread m < rows returns row m's slot index in p, else -1.
+static_assert(G4_SD_IDS == 2 * G4_THREADS, "two ids per thread");
+__device__ __forceinline__ G4Tile g4_self_tile(const G2Args &g, int tile, int *s, int &p) {
+    constexpr int BM = G4_BM_SMALL;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = g.n_expert, n = g.nids;
+    int *s_cnt = s;              // [256] rows per expert
+    int *s_wt = s + 256;         // [4] wave totals of the tile scan; [4 .. 8) / [8 .. 12): ballot counts
+    int *s_sel = s + 272;        // [0] expert of the tile (-1: none), [1] its tile index within the expert
+    int *s_rows = s + 288;       // [BM] the tile's slot indices
+    const int id0 = tid < n ? g.ids[tid] : -1;
+    const int id1 = tid + G4_THREADS < n ? g.ids[tid + G4_THREADS] : -1;
+    s_cnt[tid] = 0;
+    if (tid == 0) s_sel[0] = -1;
+    if (tid < BM) s_rows[tid] = 0;   // (every entry a valid row, whatever follows)
+    __syncthreads();
+    if (id0 >= 0 && id0 < E) atomicAdd(&s_cnt[id0], 1);
+    if (id1 >= 0 && id1 < E) atomicAdd(&s_cnt[id1], 1);
+    __syncthreads();
+    // tiles per expert (thread e), inclusive scan over the 256 experts
+    const int cnt_e = tid < E ? s_cnt[tid] : 0;
+    const int nt_e = (cnt_e + BM - 1) / BM;
+    const int inc = wave_incl_scan(nt_e);
+    if (lane == 63) s_wt[wave] = inc;
+    __syncthreads();
+    int before = 0;
+#pragma unroll
+    for (int w = 0; w < G4_WAVES; ++w) before += w < wave ? s_wt[w] : 0;
+    const int ts = before + inc - nt_e;   // the expert's first tile
+    if (nt_e > 0 && tile >= ts && tile < ts + nt_e) {
+        s_sel[0] = tid;
+        s_sel[1] = tile - ts;
+    }
+    __syncthreads();
+    G4Tile t;
+    t.e = s_sel[0];
+    const int sub = s_sel[1];
+    p = -1;
+    t.start = 0;
+    t.live = t.e >= 0;
+    if (!t.live) {
+        t.mrows = 0;
+        t.nrt = 0;
+        return t;
+    }
+    const int cnt = s_cnt[t.e], nt = (cnt + BM - 1) / BM, base = cnt / nt, extra = cnt % nt;
+    const int r0 = sub * base + (sub < extra ? sub : extra);
+    t.mrows = base + (sub < extra ? 1 : 0);
+    t.nrt = (t.mrows + 31) >> 5;
+    // ranks in flat order: the first G4_THREADS ids (id0), then the rest (id1)
+    const uint64_t b0 = __ballot(id0 == t.e), b1 = __ballot(id1 == t.e);
+    const uint64_t below = (1ull << lane) - 1ull;
+    if (lane == 0) {
+        s_wt[4 + wave] = __builtin_popcountll(b0);
+        s_wt[8 + wave] = __builtin_popcountll(b1);
+    }
+    __syncthreads();
+    int pre0 = 0, tot0 = 0, pre1 = 0;
+#pragma unroll
+    for (int w = 0; w < G4_WAVES; ++w) {
+        tot0 += s_wt[4 + w];
+        pre0 += w < wave ? s_wt[4 + w] : 0;
+        pre1 += w < wave ? s_wt[8 + w] : 0;
+    }
+    const int rk0 = pre0 + __builtin_popcountll(b0 & below);
+    const int rk1 = tot0 + pre1 + __builtin_popcountll(b1 & below);
+    if (id0 == t.e && rk0 >= r0 && rk0 < r0 + t.mrows) s_rows[rk0 - r0] = tid;
+    if (id1 == t.e && rk1 >= r0 && rk1 < r0 + t.mrows) s_rows[rk1 - r0] = tid + G4_THREADS;
+    __syncthreads();
+    p = tid < t.mrows ? s_rows[tid] : -1;
     return t;
 }
 
@@ -598,14 +680,16 @@ k_g4_glu(G2Args g) {
     __shared__ __attribute__((aligned(1024))) uint8_t Ws[G4_WAVES][g4_wregion<12>()];
     int tile, ctile;
     g4_coords((int)(g.I / 128), tile, ctile);
-    const G4Tile t = g4_desc(g, tile);
+    const bool self = BM == G4_BM_SMALL && g.ids != nullptr;
+    int my_p = -1;
+    const G4Tile t = self ? g4_self_tile(g, tile, (int *)As0, my_p) : g4_desc(g, tile);
     g4_clock(g, 0, t.live);
     if (!t.live) {
         g4_clock(g, 1, false);
         return;
     }
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int my_p = g4_rows_load(g, t);
+    if (!self) my_p = g4_rows_load(g, t);
     const int nrt = __builtin_amdgcn_readfirstlane(t.nrt);
     const uint32_t Kin = (uint32_t)g.a.K;
     const rsrc_t rx = g4_rsrc(g.xh, g.xrows * (int64_t)Kin * 2);
@@ -648,7 +732,9 @@ k_g4_store(G2Args g) {
     __shared__ __attribute__((aligned(1024))) uint8_t Ws[G4_WAVES][g4_wregion<WT>()];
     int tile, ctile;
     g4_coords((int)((g.ncols + G4_NWG - 1) / G4_NWG), tile, ctile);
-    const G4Tile t = g4_desc(g, tile);
+    const bool self = BM == G4_BM_SMALL && g.ids != nullptr;
+    int my_p = -1;
+    const G4Tile t = self ? g4_self_tile(g, tile, (int *)As0, my_p) : g4_desc(g, tile);
     g4_clock(g, 0, t.live);
     if (!t.live) {
         g4_clock(g, 1, false);
@@ -656,7 +742,7 @@ k_g4_store(G2Args g) {
     }
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int l32 = lane & 31, g2 = lane >> 5;
-    const int my_p = g4_rows_load(g, t);
+    if (!self) my_p = g4_rows_load(g, t);
     const int nrt = __builtin_amdgcn_readfirstlane(t.nrt);
     const uint32_t Kin = (uint32_t)g.a.K;
     const rsrc_t rx = g4_rsrc(g.xh, g.xrows * (int64_t)Kin * 2);
@@ -735,6 +821,9 @@ int gemm4_grid(const G2Args &g) {
 int launch_gemm4(const G2Args &g, hipStream_t st) {
     if (g.max_tiles <= 0) return 0;
     if (g.a.K % QK) return -6;
+    if (g.ids && (g.bm != G4_BM_SMALL || g.nids <= 0 || g.nids > G4_SD_IDS || g.n_expert <= 0 ||
+                  g.n_expert > G4_THREADS))
+        return -6;
     const int64_t lim = 0x7fffffff;
     // byte offsets of the buffer loads are 32-bit
     if (g.xrows <= 0 || g.xrows * g.a.K * 2 > lim || g.a.mat_bytes + 4 > lim) return -6;

@@ -1,5 +1,6 @@
-"""The router of small batches split over its chunks (k_front_parts +
-k_topk_parts), through the C ABI, against the CPU oracle.
+"""Small calls on the kernel chain, through the C ABI, against the CPU
+oracle: the router split over its chunks (k_front_parts + k_topk_parts) and
+the 32-row GEMMs without a dispatch launch (each work-group finds its tile).
 
 Below T x E = 8192 logits, and where the (16-token, 16-expert) tiles alone
 would leave half of the CUs idle, the kernel chain computes each 64-value
@@ -127,4 +128,38 @@ def test_front_split_gating_kinds(gating, T):
     assert np.array_equal(bufs["sel"].download(np.int32, (T, K)), sel), "ids"
     assert np.allclose(bufs["weights"].download(np.float32, (T, K)), w, rtol=1e-6, atol=1e-7), "weights"
     log(f"gating {gating} T={T}: routing bit-exact")
+    ctx.close()
+
+
+SD_CASES = [("qo", 3, T) for T in (8, 16, 32, 64)] + [("md", 0, T) for T in (4, 16, 40, 64)]
+
+
+@pytest.mark.parametrize("name,cfg,T", SD_CASES, ids=[f"{n}-T{t}" for n, _, t in SD_CASES])
+def test_gemm_self_dispatch(name, cfg, T):
+    """Small calls on the 32-row GEMM tiles skip the dispatch launch when the
+    caller asks for no dispatch outputs: each GEMM work-group derives its
+    tile from the ids.  Its output must equal the dispatched call's bit for
+    bit (same tiles, same rows, same K order), and the oracle's to 1e-2."""
+    spec = W.CONFIGS[cfg]["spec"]
+    log(f"case {name} T={T}")
+    ctx = M.Context(0)
+    ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
+    ctx.set_fused_decode(M.DECODE_CHAIN)
+    g = W.GpuLayer(ctx, spec)
+    OL = oracle_layer_dict(g.download_tables(), g.spec, g.download_router(), g.bias_host)
+    x = W.gen_x(ctx, spec, T, copy=2)
+    ref, dbg = O.moe_forward(OL, x.download(np.float32, (T, spec.D)))
+    outs = []
+    for with_routing in (True, False):
+        out = M.DeviceBuffer(4 * T * spec.D)
+        bufs, r = _routing_buffers(T, spec.E, spec.K)
+        M.check("forward", ctx.forward(g.layer, x, T, None, out, r if with_routing else None))
+        outs.append(out.download(np.float32, (T, spec.D)))
+        if with_routing:
+            assert np.array_equal(bufs["perm"].download(np.int32, (T * spec.K,)), dbg["perm"])
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), f"{name} T={T}: self-dispatch differs"
+    e = rel_l2(outs[1], ref)
+    log(f"{name} T={T} self-dispatch: bit-identical to the dispatched call; rel-L2 {e:.3e} "
+        f"max-abs {max_abs(outs[1], ref):.3e}, experts used {int((dbg['counts'] > 0).sum())}/{spec.E}")
+    assert e <= TOL
     ctx.close()

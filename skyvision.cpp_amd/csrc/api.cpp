@@ -419,11 +419,12 @@ bool gs_path(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T) {
 // is expected to make (uniform routing: the experts hit plus one tile per
 // further GS_BM rows), at least one column group per wave (waves per
 // work-group)
-int gs_splits(const mi_moe_ctx *c, int64_t rows, int E, int64_t ncols, int waves) {
+int gs_splits(const mi_moe_ctx *c, int64_t rows, int E, int64_t ncols, int glu) {
     const double hit = E * (1.0 - std::pow(1.0 - 1.0 / E, (double)rows));
     const double tiles = std::max(1.0, hit + std::max(0.0, (double)rows - hit * GS_BM) / GS_BM);
-    const int cap = (int)std::max<int64_t>(1, ncols / 16 / waves);
-    return std::max(1, std::min(cap, (int)std::lround(std::max(1, c->n_cu) / tiles)));
+    const int cap = (int)std::max<int64_t>(1, ncols / 16 / gemm_gs_waves(glu));
+    const int slots = std::max(1, c->n_cu) * gemm_gs_wgs_per_cu(glu);
+    return std::max(1, std::min(cap, (int)std::lround(slots / tiles)));
 }
 
 // Small batches: the router's D / 64 chunks split over work-groups when the
@@ -642,7 +643,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         // the Q8_K pass; saturation at the fp16 range is counted)
         if (gated) { a.yh = (_Float16 *)c->f1; a.range_total = c->range_total; }
         if (!gs) prof_clock(c, a, 0);   // (the skinny kernels record no clocks)
-        TRY(gs ? launch_gemm_gs(a, gs_splits(c, rows, E, gated ? I : a.ncols, gated ? 8 : 16), st) : launch_gemm4(a, st));
+        TRY(gs ? launch_gemm_gs(a, gs_splits(c, rows, E, gated ? I : a.ncols, a.glu), st) : launch_gemm4(a, st));
         stage_end(c, "gate_up", st);
         Q8Out qa;
         qa.xh = c->aact.h; qa.wtype = down.type; qa.order = 1; qa.pre_act = gated ? 0 : MI_ACT_RELU_SQR;
@@ -661,7 +662,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         // combine; saturation at the fp16 range is counted)
         d.y = c->z; d.yh = zh = (_Float16 *)c->z; d.range_total = c->range_total; d.ldy = D; d.ncols = D;
         if (!gs) prof_clock(c, d, 1);
-        TRY(gs ? launch_gemm_gs(d, gs_splits(c, rows, E, D, 16), st) : launch_gemm4(d, st));
+        TRY(gs ? launch_gemm_gs(d, gs_splits(c, rows, E, D, 0), st) : launch_gemm4(d, st));
         stage_end(c, "down", st);
     } else {
         // Q6_K gate/up: fp16 dequant on 16x16x32 MFMA

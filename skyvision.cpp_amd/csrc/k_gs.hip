@@ -39,7 +39,10 @@ namespace mimoe {
 // store, with fewer weight registers per step: 4), so that no work-group of
 // a CU outlasts another (the older work-group's waves win the issue
 // arbitration)
-template <bool GLU> constexpr int gs_waves() { return GLU ? 8 : 16; }
+constexpr int GS_WAVES_GLU = 8, GS_WAVES_ST = 16;   // waves per work-group
+constexpr int GS_WGS_GLU = 1, GS_WGS_ST = 1;         // work-groups per CU
+template <bool GLU> constexpr int gs_waves() { return GLU ? GS_WAVES_GLU : GS_WAVES_ST; }
+template <bool GLU> constexpr int gs_waves_per_simd() { return gs_waves<GLU>() * (GLU ? GS_WGS_GLU : GS_WGS_ST) / 4; }
 constexpr int GS_GROUP_GLU = 3;   // weight steps per load group (GLU: 2 matrices per step)
 constexpr int GS_GROUP_ST = 6;    // (store: 1 matrix per step)
 
@@ -246,7 +249,7 @@ __device__ __forceinline__ void gs_stage_rows(gs_rsrc_t rx, char *As, int arow, 
 // (yh, saturated and counted) or fp32 (y), [p][ldy].  KMAX: the longest
 // activation row the LDS holds.
 template <bool GLU, int ACT, int KMAX>
-__global__ void __launch_bounds__(64 * gs_waves<GLU>()) __attribute__((amdgpu_waves_per_eu(gs_waves<GLU>() / 4, gs_waves<GLU>() / 4)))
+__global__ void __launch_bounds__(64 * gs_waves<GLU>()) __attribute__((amdgpu_waves_per_eu(gs_waves_per_simd<GLU>(), gs_waves_per_simd<GLU>())))
 k_gs(G2Args g, int splits) {
     constexpr int NW = gs_waves<GLU>();
     constexpr int NM = GLU ? 2 : 1, LPS = 3 * NM;
@@ -349,6 +352,9 @@ done:
 }
 
 // ------------------------------------------------------------------ launch
+int gemm_gs_waves(int glu) { return glu ? GS_WAVES_GLU : GS_WAVES_ST; }
+int gemm_gs_wgs_per_cu(int glu) { return glu ? GS_WGS_GLU : GS_WGS_ST; }
+
 int launch_gemm_gs(const G2Args &g, int splits, hipStream_t st) {
     if (g.max_tiles <= 0) return 0;
     if (g.bm != GS_BM || !g.tile_perm || splits < 1 || splits > 64) return -6;

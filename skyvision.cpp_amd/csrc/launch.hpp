@@ -219,6 +219,9 @@ int gemm4_grid(const G2Args &g);   // work-groups launch_gemm4 launches
 // ncols must be a multiple of 16); K <= GS_KMAX.  splits: work-groups per
 // tile, each taking an equal share of the tile's 16-column groups.
 int launch_gemm_gs(const G2Args &g, int splits, hipStream_t st);
+// waves per work-group and work-groups per CU of the skinny products (glu: gate/up)
+int gemm_gs_waves(int glu);
+int gemm_gs_wgs_per_cu(int glu);
 
 // ---- 32-value block formats (Q4_0 = 2, Q5_0 = 6, Q8_0 = 8) and F16 (1)
 // expert tables (k_b32.hip)

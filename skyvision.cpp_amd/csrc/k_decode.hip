@@ -1145,69 +1145,6 @@ __device__ inline float decb_dn_dot(const DecBDn<DT> &r, int sl, const int8_t *a
 }
 
 
-// Top-K of one token's E logits (LDS row l, E <= 256) by one wave, as K rounds
-// of a wave argmax over the values not yet taken: largest first, the lower id
-// first among equal values (ggml_top_k's stable descending order).  Lane k < K
-// gets the k-th id and its weight (the shared softmax over the K selected).
-__device__ inline void decb_topk(const float *l, int E, int K, int lane, int &mysel, float &myw) {
-    float v[TOPK_MAX_PER_LANE];
-    bool avail[TOPK_MAX_PER_LANE];
-#pragma unroll
-    for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
-        const int e = lane + 64 * i;
-        avail[i] = e < E;
-        v[i] = avail[i] ? l[e] : -INFINITY;
-    }
-    // (bv, bi) replaced by (pv, pi) when pv is larger, or equal with a lower id
-    auto take = [](float bv, int bi, float pv, int pi) { return (pv > bv) | ((pv == bv) & (pi < bi)); };
-    mysel = 0;
-    float myval = 0.f;
-    for (int r = 0; r < K; ++r) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int i = 0; i < TOPK_MAX_PER_LANE; ++i) {
-            const int e = lane + 64 * i;
-            if (avail[i] && (take(bv, bi, v[i], e) | (bi == 0x7fffffff))) {
-                bv = v[i];
-                bi = e;
-            }
-        }
-        // every lane of a 16-lane row gets the row's best, then the four rows
-        // are compared in order through scalar reads
-#define DECB_ARGMAX_STEP(CTRL)                                                  \
-        {                                                                       \
-            const float pv = dpp_f<CTRL>(bv);                                   \
-            const int pi = dpp_i<CTRL>(bi);                                     \
-            if (take(bv, bi, pv, pi) | ((bi == 0x7fffffff) & (pi != 0x7fffffff))) { bv = pv; bi = pi; } \
-        }
-        DECB_ARGMAX_STEP(0xB1)
-        DECB_ARGMAX_STEP(0x4E)
-        DECB_ARGMAX_STEP(0x141)
-        DECB_ARGMAX_STEP(0x140)
-#undef DECB_ARGMAX_STEP
-        float wv = lane_f(bv, 0);
-        int wi = __builtin_amdgcn_readlane(bi, 0);
-#pragma unroll
-        for (int row = 1; row < 4; ++row) {
-            const float pv = lane_f(bv, 16 * row);
-            const int pi = __builtin_amdgcn_readlane(bi, 16 * row);
-            if (take(wv, wi, pv, pi) | ((wi == 0x7fffffff) & (pi != 0x7fffffff))) {
-                wv = pv;
-                wi = pi;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < TOPK_MAX_PER_LANE; ++i)
-            if (lane + 64 * i == wi) avail[i] = false;
-        if (lane == r) {
-            mysel = wi;
-            myval = wv;
-        }
-    }
-    myw = softmax_selected_wave(myval, K, lane);
-}
-
 constexpr int DECB_LIST = 1024;   // missing units listed per rescue round
 
 template <int DT, int NB, int NBI>
@@ -1351,7 +1288,7 @@ __global__ void __launch_bounds__(DECB_THREADS) k_decodeb(DecArgs g) {
     for (int t = wave; t < T; t += DECB_WAVES) {
         int mysel;
         float myw;
-        decb_topk(s_logit + t * E, E, K, lane, mysel, myw);
+        topk_softmax_wave(s_logit + t * E, E, K, lane, mysel, myw, true);
         if (lane < K) {
             s_sel[t * K + lane] = mysel;
             s_w[t * K + lane] = myw;

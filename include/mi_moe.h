@@ -125,7 +125,10 @@ typedef struct {
 } mi_moe_layer;
 
 /* Optional routing outputs of mi_moe_forward (device pointers, any may be
- * NULL).  Layouts are row-major with tokens outermost. */
+ * NULL).  Layouts are row-major with tokens outermost.  Asking for counts,
+ * offsets or perm makes small calls (at most 512 ids on the 32-row GEMM
+ * tiles) launch the dispatch kernel that writes them, which the products
+ * otherwise do without; the results are bit-identical either way. */
 typedef struct {
     float   *logits;               /* [T][E]   router logits                      */
     int32_t *sel;                  /* [T][K]   expert ids, descending logit        */

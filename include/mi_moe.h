@@ -181,7 +181,11 @@ int  mi_moe_ctx_reserve(mi_moe_ctx *ctx, int64_t max_tokens, int32_t n_embd, int
  * kept as fp16 for the activations' Q8_K) and down-product outputs (the
  * per-slot rows the weighted sum reads, kept as fp16) beyond it, counted per
  * wave of 64 values that held one.  The products of those rows are inexact (ggml's own
- * fp16 GPU paths overflow there; the integer GEMV path has no such limit).
+ * fp16 GPU paths overflow there; the integer GEMV path has no such limit: a
+ * caller that sees fp16_saturated > 0 can run those calls again on it,
+ * mi_moe_ctx_set_gemm_threshold(ctx, INT64_MAX): exact integer dots at any
+ * token count for layers with n_embd and n_ff <= 2048, slower above the
+ * switch).
  * Any pointer may be NULL.  Synchronizes the context's device. */
 int  mi_moe_ctx_take_errors(mi_moe_ctx *ctx, int64_t *bad_ids, int64_t *wait_failures,
                             int64_t *fp16_saturated);
@@ -361,8 +365,8 @@ int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *ctx, int64_t min_tokens_for_gemm);
  * average (qwen3omni up to 128 tokens, moondream3 up to 64: two work-groups
  * per CU keep twice the weight stream in flight), 192-row tiles above; 1
  * 192-row tiles, 2 32-row tiles at every size; 3 the skinny products (16-row
- * tiles, one work-group per CU, the weight stream held in registers several
- * blocks ahead) on layers whose tables are all Q4_K with n_embd and n_ff <=
+ * tiles, one work-group per CU, the weight stream held in registers a group
+ * of blocks ahead) on layers whose tables are all Q4_K with n_embd and n_ff <=
  * 2048 (others take the shape rule).  Kinds 0-2 give the same bits (the same
  * per-row arithmetic); the skinny products sum each output's products in
  * another order (fp32; the rows agree to ~2e-4 rel-L2 after the activations'

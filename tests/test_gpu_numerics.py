@@ -19,7 +19,9 @@ Cases (moondream3 widths D 2048 / I 1024, Q4_K gate/up, Q6_K down):
   beyond fp16     one token carries 1e6: its Q8_K block exceeds the fp16
                   range; the operands saturate, the call counts the block
                   (mi_moe_ctx_take_errors fp16_saturated), every output
-                  stays finite and the other tokens keep the tolerance
+                  stays finite and the other tokens keep the tolerance; the
+                  integer GEMV path (the fallback the header names for such
+                  calls) counts nothing and meets it on every token
 
 Bars: logits, ids, permutation bit-exact; output rel-L2 <= 1e-2 (the
 north_star tolerance), logged with max-abs for each path; the GEMV path

@@ -2,7 +2,7 @@
 on the kernel chain), through the C ABI, against the CPU oracle, on every
 path a call of that size takes: the fused single-token and batched decode
 kernels, the chain's GEMV, its 32-row GEMMs without a dispatch launch, and
-the 192-row GEMMs.
+the 192-row GEMMs; and rows that start 4 bytes past a 16-byte boundary.
 
 Bars: logits, ids, counts, offsets, permutation bit-exact; weights within
 1e-6; output rel-L2 <= 1e-2 (logged with max-abs).
@@ -75,4 +75,30 @@ def test_e256(K, T, mode, want):
         f"experts used {int((dbg['counts'] > 0).sum())}/256")
     assert np.isfinite(got).all()
     assert e <= TOL
+    ctx.close()
+
+
+@pytest.mark.parametrize("T", [3, 40, 300])
+def test_unaligned_rows(T):
+    """x and res 4 bytes past a 16-byte boundary take the routers' and the
+    Q8_K passes' element-wise load forms: outputs bit-identical to the same
+    rows at an aligned address."""
+    spec = W.qo_spec()
+    ctx = M.Context(0)
+    ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
+    ctx.set_fused_decode(M.DECODE_CHAIN)
+    g = W.GpuLayer(ctx, spec)
+    rng = np.random.default_rng(T)
+    x = rng.standard_normal((T, spec.D)).astype(np.float32)
+    res = rng.standard_normal((T, spec.D)).astype(np.float32)
+    outs = []
+    for shift in (0, 1):
+        xb = M.to_device(np.concatenate([np.zeros(shift, np.float32), x.ravel()]))
+        rb = M.to_device(np.concatenate([np.zeros(shift, np.float32), res.ravel()]))
+        ob = M.DeviceBuffer(4 * (T * spec.D + 1))
+        M.check("forward", ctx.forward(g.layer, C.c_void_p(xb.addr + 4 * shift), T, C.c_void_p(rb.addr + 4 * shift),
+                                       C.c_void_p(ob.addr + 4 * shift)))
+        outs.append(ob.download(np.float32, (T * spec.D + 1,))[shift:shift + T * spec.D])
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), f"T={T}: unaligned rows differ"
+    log(f"T={T}: unaligned x / res / out bit-identical to aligned")
     ctx.close()

@@ -14,6 +14,7 @@
 #include "common.hpp"
 #include "wave_ops.hpp"
 #include "launch.hpp"
+#include "q8h.hpp"
 
 namespace mimoe {
 
@@ -28,7 +29,6 @@ namespace mimoe {
 // a Q4_K / Q6_K consumer (not exact), where a lane's 16 positions are the
 // bytes of four aligned code dwords (at base and base + 32 for each of its two
 // lane groups), XO_ANY whatever o asks for, element by element.
-enum { XO_ANY = 0, XO_Q4 = 1, XO_Q6 = 2 };
 
 // the lane's 16 values of row group (row, grp) (zeros past the row's blocks)
 template <bool VEC, typename ST>
@@ -202,25 +202,8 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const ST *__restrict__ src, in
 }
 
 // fp16 values only (o.xh in a Q4_K / Q6_K 32x32x16 order, no codes, scales or
-// sums): each lane loads its 16 values straight in the output order — four
-// runs of 4 consecutive values at base(g, s) and base(g, s) + 32, g = 0, 1 —
-// so no code bytes are packed, staged in LDS or unpacked again.
-//
-// The value d*q does not depend on which element of largest |x| fixes the
-// scale's sign: with m = max |x| the scale is -127 / (+-m) = -+(127 / m) (a
-// correctly rounded divide is odd), the codes round half to even (odd) and
-// stay inside [-127, 127] (|127 x / m| < 127.5), so d and q change sign
-// together and their product keeps its bits.  Only the sign of a zero
-// product may differ from the element-first form, and a zero adds nothing
-// to an MFMA sum that starts at +0.
-// first of lane s's 4 values A of half g (B: the 4 at + 32); output slot p
-// = 0..7 of the half holds Q4_K A0 A2 B0 B2 A1 A3 B1 B3, Q6_K A0..A3 B0..B3
-template <int XO>
-__device__ __forceinline__ int q8h_base(int s, int g) {
-    return XO == XO_Q4 ? 64 * (2 * (s >> 3) + g) + 4 * (s & 7)
-                       : 128 * (s >> 3) + 16 * g + 4 * ((s & 7) >> 1) + 64 * (s & 1);
-}
-
+// sums): one wave per row group of 4 blocks, 16 lanes per block, each lane
+// loading its 16 values straight in the output order (q8h.hpp).
 template <int XO, typename ST>
 __global__ void __launch_bounds__(256) k_q8k_rows_h(const ST *__restrict__ src, int64_t ld, int64_t nrows, int nb,
                                                     Q8Out o) {
@@ -235,27 +218,7 @@ __global__ void __launch_bounds__(256) k_q8k_rows_h(const ST *__restrict__ src, 
     const bool bok = b < nb;
     float v[16];
     if (bok) {
-        const ST *x = src + row * ld + (int64_t)b * QK;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {   // run r: half g = r >> 1, A (r even) or B
-            const int g = r >> 1, half = r & 1;
-            const int start = q8h_base<XO>(s, g) + 32 * half;
-            float w[4];
-            if constexpr (sizeof(ST) == 2) {
-                const uint2 u = *(const uint2 *)(x + start);
-                const half2_t h0 = __builtin_bit_cast(half2_t, u.x), h1 = __builtin_bit_cast(half2_t, u.y);
-                w[0] = (float)h0[0]; w[1] = (float)h0[1]; w[2] = (float)h1[0]; w[3] = (float)h1[1];
-            } else {
-                const float4 f = *(const float4 *)(x + start);
-                w[0] = f.x; w[1] = f.y; w[2] = f.z; w[3] = f.w;
-            }
-            // the run's 4 values to their output slots
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int p = XO == XO_Q4 ? (i & 1) * 4 + (i >> 1) + 2 * half : i + 4 * half;
-                v[8 * g + p] = w[i];
-            }
-        }
+        q8h_gather<XO>(src + row * ld + (int64_t)b * QK, s, v);
         if (o.pre_act == ACT_RELU_SQR) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) v[i] = relu_sqr(v[i]);
@@ -264,29 +227,7 @@ __global__ void __launch_bounds__(256) k_q8k_rows_h(const ST *__restrict__ src, 
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = 0.f;
     }
-    float m = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
-    m = fmaxf(m, dpp_f<0xB1>(m));
-    m = fmaxf(m, dpp_f<0x4E>(m));
-    m = fmaxf(m, dpp_f<0x141>(m));
-    m = fmaxf(m, dpp_f<0x140>(m));   // largest |x| of the lane's block
-    const bool zero = m == 0.f;
-    const float iscale = zero ? 0.f : 127.f / m;
-    const float d = zero ? 0.f : 1 / iscale;
-    if (!bok) return;
-    uint32_t h[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        half2_t hh;
-        hh[0] = f16_sat(d * __builtin_rintf(iscale * v[2 * k]));
-        hh[1] = f16_sat(d * __builtin_rintf(iscale * v[2 * k + 1]));
-        h[k] = __builtin_bit_cast(uint32_t, hh);
-    }
-    if (s == 0 && o.range_total && f16_over(d)) atomicAdd(o.range_total, 1);
-    uint4 *dst = (uint4 *)(o.xh + row * (int64_t)nb * QK + (int64_t)b * QK + 16 * s);
-    dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
-    dst[1] = make_uint4(h[4], h[5], h[6], h[7]);
+    q8h_quant_store(v, bok, o.xh + row * (int64_t)nb * QK + (int64_t)b * QK, s, o.range_total);
 }
 
 // the compile-time fp16 order for o (XO_ANY when o has no xh)

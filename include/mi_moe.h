@@ -362,8 +362,8 @@ int mi_moe_ctx_stage_clock(mi_moe_ctx *ctx, const char *stage, double *ghz, int 
 int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *ctx, int64_t min_tokens_for_gemm);
 /* Row tiles of the grouped GEMMs of Q4_K gate/up layers: 0 (the default) by
  * shape, 32-row tiles when the call dispatches at most 8 rows per expert on
- * average (qwen3omni up to 128 tokens, moondream3 up to 64: two work-groups
- * per CU keep twice the weight stream in flight), 192-row tiles above; 1
+ * average (qwen3omni up to 128 tokens, moondream3 up to 64: several
+ * work-groups per CU keep more of the weight stream in flight), 192-row tiles above; 1
  * 192-row tiles, 2 32-row tiles at every size; 3 the skinny products (16-row
  * tiles, one work-group per CU, the weight stream held in registers a group
  * of blocks ahead) on layers whose tables are all Q4_K with n_embd and n_ff <=

@@ -385,8 +385,8 @@ bool gemm_path(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T) {
 // else the 16x16x32 GEMM with its fused GLU + Q8_K epilogue (Q6_K gate/up)
 bool g4_path(const mi_moe_layer *L) { return L->gate.type == MI_TYPE_Q4_K || !act_gated(L->act); }
 
-// Row tiles of the 4-wave GEMMs: 32-row tiles (a quarter of the LDS: two
-// work-groups per CU keep twice the weight stream in flight) when the call
+// Row tiles of the 4-wave GEMMs: 32-row tiles (52 KB of LDS with Q4_K
+// weights: three work-groups per CU keep more of the weight stream in flight) when the call
 // dispatches at most G4_SMALL_ROWS rows per expert on average (qwen3omni up
 // to 128 tokens, moondream3 up to 64), where the products are bound by that
 // stream; 192-row balanced tiles above.

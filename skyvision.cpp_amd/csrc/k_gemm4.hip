@@ -25,7 +25,7 @@
 //    the block start and loads the next block over the region, one block
 //    ahead; operands are dequantized to fp16 in-register (Q4_K d*sc*q -
 //    dmin*m, Q6_K d*sc*(q - 32)).
-// LDS: two activation stages of 48 KB and the waves' weight regions (4 x 10
+// LDS: two activation stages of 48 KB and the waves' weight regions (4 x 9
 // KB Q4_K, 4 x 16 KB Q6_K: 160 KB in all); the tile's activation rows sit in
 // the second stage until the K loop has taken its load offsets, the rows'
 // slot indices in the first after the K loop.
@@ -212,7 +212,8 @@ __device__ __forceinline__ const int *g4_publish_rows(_Float16 *As0, int p) {
 // own part of the wave's region, row r of a part at r * SLOTS * 16 bytes.
 //  Q4_K (dword-aligned 144-byte blocks): a row is its whole block, 9 slots
 //   (stride 9 slots spreads 8 rows over all bank groups); 32 rows = 4.5 KB,
-//   loaded by 5 loads of 1 KB (the last one's upper half re-reads row 31).
+//   loaded by 4 loads of 1 KB and one of 512 B (its lanes 32-63 idle), so
+//   that a column tile takes exactly its 4608 bytes of LDS.
 //  Q6_K (210-byte blocks at any even byte): a row is 16 slots: 9 slots of ql
 //   from the dword at or below the block start (sh = bs & 3 bytes before it),
 //   5 slots of qh from the dword at or below bs + 128, 2 slots of scales and
@@ -220,7 +221,7 @@ __device__ __forceinline__ const int *g4_publish_rows(_Float16 *As0, int p) {
 //   k ^ (r & 7).  32 rows = 8 KB = 8 loads.
 template <int WT> struct G4Fmt;
 template <> struct G4Fmt<12> {
-    static constexpr int SLOTS = 9, PART = 5 * 1024, NLD = 5;   // slots per row, bytes per column tile, loads per column tile
+    static constexpr int SLOTS = 9, PART = 32 * 9 * 16, NLD = 5;   // slots per row, bytes per column tile, loads per column tile
 };
 template <> struct G4Fmt<14> {
     static constexpr int SLOTS = 16, PART = 8 * 1024, NLD = 8;
@@ -297,7 +298,10 @@ __device__ __forceinline__ void g4_issue_w(const G4WDma<WT> &dm, uint8_t *W, int
     uint8_t *dst = W + ct * F::PART + 1024 * jj;
     rsrc_t r = dm.r[ct];   // the builtin takes no const-qualified resource
     if constexpr (WT == 12) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)dst, 16, (int)dm.off[ct][jj], b * Q4K_BYTES, 0, 0);
+        // (the last load's lanes past the tile's 288 slots write nothing)
+        if (jj + 1 < F::NLD || (int)(threadIdx.x & 63) < F::PART / 16 - 64 * (F::NLD - 1))
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)dst, 16, (int)dm.off[ct][jj], b * Q4K_BYTES, 0,
+                                                     0);
     } else {
         const uint32_t x = dm.x[ct][jj & 1] + (uint32_t)jj * dm.rstride + (uint32_t)(b * Q6K_BYTES);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)dst, 16, (int)((x & ~3u) + dm.kk[jj & 1]), 0, 0,
@@ -668,11 +672,11 @@ __device__ __forceinline__ void g4_clock(const G2Args &g, int slot, bool live) {
     }
 }
 
-// BM: tile rows (G4_BM; G4_BM_SMALL for few rows per expert: a quarter of
-// the LDS, so that two work-groups share a CU and keep twice the weight
-// stream in flight)
+// BM: tile rows (G4_BM; G4_BM_SMALL for few rows per expert: 52 KB of LDS
+// with Q4_K weights, so that three work-groups share a CU and keep three
+// times the weight stream in flight)
 template <int BM>
-__global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, BM == G4_BM ? 1 : 2)))
+__global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, BM == G4_BM ? 1 : 3)))
 k_g4_glu(G2Args g) {
     constexpr int NA = BM / 32;
     __shared__ __attribute__((aligned(1024))) _Float16 As0[BM * G4_SK];
@@ -724,7 +728,7 @@ k_g4_glu(G2Args g) {
 // rows 256 ctile + 64 w + 32 ct + l32 (rows past ncols read zeros past the
 // matrix's resource or unused bytes, and are not stored).
 template <int WT, int BM>
-__global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, BM == G4_BM ? 1 : 2)))
+__global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, BM == G4_BM ? 1 : 3)))
 k_g4_store(G2Args g) {
     constexpr int NA = BM / 32;
     __shared__ __attribute__((aligned(1024))) _Float16 As0[BM * G4_SK];

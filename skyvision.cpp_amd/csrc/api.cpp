@@ -230,6 +230,19 @@ int check_experts(const mi_tensor &gate, const mi_tensor &up, const mi_tensor &d
     return MI_MOE_OK;
 }
 
+// an optional tiled copy of table t (mi_moe_layer.gate_tiled ..): absent, or
+// Q4_K like t with t's shape and strides, whole 32-row groups, no padding
+int check_tiled(const mi_tensor &tiled, const mi_tensor &t) {
+    if (!tiled.data) return MI_MOE_OK;
+    if (tiled.type != MI_TYPE_Q4_K || t.type != MI_TYPE_Q4_K) return MI_MOE_ERR_TYPE;
+    for (int i = 0; i < 4; ++i)
+        if (tiled.ne[i] != t.ne[i] || tiled.nb[i] != t.nb[i]) return MI_MOE_ERR_SHAPE;
+    if (t.ne[1] % 32 || t.nb[1] != type_row_size(t.type, t.ne[0]) || t.nb[2] != t.nb[1] * (size_t)t.ne[1])
+        return MI_MOE_ERR_SHAPE;
+    if ((uintptr_t)tiled.data % 16) return MI_MOE_ERR_UNSUPPORTED;
+    return MI_MOE_OK;
+}
+
 // shared: validate the shared-expert fields too (the forward; the table form ignores them)
 int validate_layer(const mi_moe_ctx *c, const mi_moe_layer *L, bool need_router, bool shared) {
     if (!L) return MI_MOE_ERR_NULL;
@@ -239,6 +252,12 @@ int validate_layer(const mi_moe_ctx *c, const mi_moe_layer *L, bool need_router,
     if (L->gating < MI_GATING_SOFTMAX_TOPK || L->gating > MI_GATING_SOFTMAX_ALL) return MI_MOE_ERR_ARG;
     if (need_router && !L->router_w) return MI_MOE_ERR_NULL;
     TRY(check_experts(L->gate, L->up, L->down, L->fused_gate_up, L->act, D, I, E));
+    TRY(check_tiled(L->gate_tiled, L->gate));
+    TRY(check_tiled(L->down_tiled, L->down));
+    if (act_gated(L->act) && !L->fused_gate_up) {
+        TRY(check_tiled(L->up_tiled, L->up));
+        if (!L->gate_tiled.data != !L->up_tiled.data) return MI_MOE_ERR_ARG;   // both or neither
+    }
     if (shared && L->sh_n_ff < 0) return MI_MOE_ERR_SHAPE;
     if (shared && L->sh_n_ff > 0) TRY(check_experts(L->sh_gate, L->sh_up, L->sh_down, 0, L->sh_act, D, L->sh_n_ff, 1));
     if (!c->reserved) return MI_MOE_ERR_CAPACITY;
@@ -632,6 +651,12 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         // (ggml: the down mul_mat_id quantizes its F32 input) for the down GEMM
         G2Args a = {};
         a.a = gate; a.b = up; a.glu = gated ? 1 : 0; a.fused = L->fused_gate_up; a.act = L->act; a.I = I;
+        if (!gs && L->gate_tiled.data) {
+            // the tables' tiled copies (the skinny kernels read the rows)
+            a.a.data = (const uint8_t *)L->gate_tiled.data;
+            if (gated && !L->fused_gate_up) a.b.data = (const uint8_t *)L->up_tiled.data;
+            a.tiled = 1;
+        }
         a.xh = c->ax.h; a.ne11 = 1; a.K = K;
         a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.tile_e = dg.tile_e;
         a.tile_r0 = dg.tile_r0; a.tile_start = dg.tile_start; a.tile_rows = dg.tile_rows; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
@@ -653,6 +678,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         stage_end(c, "q8k_act", st);
         G2Args d = {};
         d.a = down; d.glu = 0; d.xh = c->aact.h; d.ne11 = K; d.K = K;
+        if (!gs && L->down_tiled.data) { d.a.data = (const uint8_t *)L->down_tiled.data; d.tiled = 1; }
         d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
         d.tile_r0 = dd.tile_r0; d.tile_start = dd.tile_start; d.tile_rows = dd.tile_rows; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles; d.xrows = (int64_t)T * K;
         d.tile_perm = dd.tile_perm;
@@ -1355,6 +1381,23 @@ int mi_quantize(mi_moe_ctx *c, int32_t type, const float *src, void *dst, int64_
     if ((uintptr_t)src % 4) return MI_MOE_ERR_UNSUPPORTED;
     HIP_TRY(hipSetDevice(c->device));
     return launch_quantize(type, src, dst, nrows * (n_per_row / QK), (hipStream_t)stream);
+}
+
+int mi_moe_tile_q4k(mi_moe_ctx *c, const mi_tensor *src, void *dst, mi_stream_t stream) {
+    if (!c || !src || !src->data || !dst) return MI_MOE_ERR_NULL;
+    if (src->type != MI_TYPE_Q4_K) return MI_MOE_ERR_TYPE;
+    const int64_t K = src->ne[0], N = src->ne[1], n_mat = src->ne[2] * src->ne[3];
+    if (K <= 0 || K % QK || N <= 0 || N % 32 || n_mat <= 0) return MI_MOE_ERR_SHAPE;
+    const size_t rb = type_row_size(MI_TYPE_Q4_K, K);
+    if (src->nb[1] != rb || src->nb[2] != rb * (size_t)N ||
+        (src->ne[3] > 1 && src->nb[3] != src->nb[2] * (size_t)src->ne[2]))
+        return MI_MOE_ERR_SHAPE;
+    if ((uintptr_t)src->data % 16 || (uintptr_t)dst % 16) return MI_MOE_ERR_UNSUPPORTED;
+    const size_t bytes = rb * (size_t)N * (size_t)n_mat;
+    const uintptr_t s0 = (uintptr_t)src->data, d0 = (uintptr_t)dst;
+    if (s0 < d0 + bytes && d0 < s0 + bytes) return MI_MOE_ERR_ARG;   // overlapping
+    HIP_TRY(hipSetDevice(c->device));
+    return launch_tile_q4k(src->data, dst, n_mat, N, (int64_t)rb, (hipStream_t)stream);
 }
 
 int mi_fill_normal(mi_moe_ctx *c, float *dst, int64_t n, uint64_t seed, uint64_t stream_id, float mean,

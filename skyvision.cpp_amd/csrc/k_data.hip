@@ -527,4 +527,30 @@ int launch_quantize(int type, const float *src, void *dst, int64_t nblocks, hipS
     return hip_check_launch();
 }
 
+// Q4_K tables in the grouped GEMMs' tiled order: for every matrix (mat
+// bytes) and every 32-row group of its rows (rb bytes each), block b of the
+// group's rows as 32 x 144 contiguous bytes, then block b + 1.  One thread
+// per 16-byte piece of dst: coalesced stores, 16-byte gathers from the rows.
+__global__ void __launch_bounds__(256) k_tile_q4k(const uint4 *__restrict__ src, uint4 *__restrict__ dst,
+                                                   int64_t pieces, int64_t mat, int64_t rb) {
+    const int64_t group = 32 * rb;
+    for (int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; p < pieces;
+         p += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t o = 16 * p, e = o / mat, in_mat = o - e * mat, t = in_mat / group;
+        const int64_t in_group = in_mat - t * group, b = in_group / (32 * Q4K_BYTES);
+        const int64_t in_block = in_group - b * (32 * Q4K_BYTES), r = in_block / Q4K_BYTES;
+        const int64_t j = in_block - r * Q4K_BYTES;
+        dst[p] = src[(e * mat + (32 * t + r) * rb + Q4K_BYTES * b + j) / 16];
+    }
+}
+
+int launch_tile_q4k(const void *src, void *dst, int64_t n_mat, int64_t rows, int64_t rb, hipStream_t st) {
+    const int64_t pieces = n_mat * rows * rb / 16;
+    if (pieces <= 0) return 0;
+    const int64_t blocks = min((int64_t)65536, (pieces + 255) / 256);
+    hipLaunchKernelGGL(k_tile_q4k, dim3((unsigned)blocks), dim3(256), 0, st, (const uint4 *)src, (uint4 *)dst, pieces,
+                       rows * rb, rb);
+    return hip_check_launch();
+}
+
 }  // namespace mimoe

@@ -246,6 +246,7 @@ template <int WT> struct G4WDma;
 template <> struct G4WDma<12> {
     rsrc_t r[2];
     uint32_t off[2][5];   // [ct][j]: byte offset at block 0 of the lane's 16 bytes
+    uint32_t bstride;     // bytes from one block to the next: 144 (rows), 4608 (tiled)
 };
 template <> struct G4WDma<14> {
     rsrc_t r[2];
@@ -256,10 +257,12 @@ template <> struct G4WDma<14> {
 
 // rowbase[ct]: weight row of row 0 of column tile ct in r[ct]; mis: the
 // matrix's misalignment below a dword (Q6_K; the resource starts at the
-// dword at or below the matrix)
+// dword at or below the matrix); tiled: Q4_K in the tiled order (rowbase a
+// multiple of 32: the tile's block b is the 4608 bytes at rowbase rb + 4608 b,
+// in the order of the LDS image)
 template <int WT>
 __device__ __forceinline__ G4WDma<WT> g4_wdma(rsrc_t r0, rsrc_t r1, const int64_t (&rowbase)[2], uint32_t rb,
-                                              uint32_t mis, int lane) {
+                                              uint32_t mis, int lane, bool tiled = false) {
     G4WDma<WT> dm;
     dm.r[0] = r0;
     dm.r[1] = r1;
@@ -269,8 +272,10 @@ __device__ __forceinline__ G4WDma<WT> g4_wdma(rsrc_t r0, rsrc_t r1, const int64_
 #pragma unroll
             for (int j = 0; j < 5; ++j) {
                 const int q = 64 * j + lane, r = imin(q / 9, 31), k = q - 9 * (q / 9);
-                dm.off[ct][j] = (uint32_t)((rowbase[ct] + r) * rb) + 16u * (uint32_t)k;
+                dm.off[ct][j] = tiled ? (uint32_t)(rowbase[ct] * rb) + 16u * (uint32_t)q
+                                      : (uint32_t)((rowbase[ct] + r) * rb) + 16u * (uint32_t)k;
             }
+        dm.bstride = tiled ? 32u * Q4K_BYTES : (uint32_t)Q4K_BYTES;
     } else {
 #pragma unroll
         for (int par = 0; par < 2; ++par) {
@@ -300,8 +305,8 @@ __device__ __forceinline__ void g4_issue_w(const G4WDma<WT> &dm, uint8_t *W, int
     if constexpr (WT == 12) {
         // (the last load's lanes past the tile's 288 slots write nothing)
         if (jj + 1 < F::NLD || (int)(threadIdx.x & 63) < F::PART / 16 - 64 * (F::NLD - 1))
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)dst, 16, (int)dm.off[ct][jj], b * Q4K_BYTES, 0,
-                                                     0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)dst, 16, (int)dm.off[ct][jj],
+                                                     b * (int)dm.bstride, 0, 0);
     } else {
         const uint32_t x = dm.x[ct][jj & 1] + (uint32_t)jj * dm.rstride + (uint32_t)(b * Q6K_BYTES);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)dst, 16, (int)((x & ~3u) + dm.kk[jj & 1]), 0, 0,
@@ -703,7 +708,7 @@ k_g4_glu(G2Args g) {
     const rsrc_t ra = g4_rsrc(g.a.data + (int64_t)t.e * g.a.mat_bytes, g.a.mat_bytes);
     const rsrc_t rg = g.fused ? ra : g4_rsrc(g.b.data + (int64_t)t.e * g.b.mat_bytes, g.b.mat_bytes);
     const int64_t rowbase[2] = {n0, g.fused ? g.I + n0 : n0};
-    const G4WDma<12> dm = g4_wdma<12>(ra, rg, rowbase, (uint32_t)g.a.row_bytes, 0u, lane);
+    const G4WDma<12> dm = g4_wdma<12>(ra, rg, rowbase, (uint32_t)g.a.row_bytes, 0u, lane, g.tiled != 0);
     g4_issue_w0<12>(dm, Ws[wave]);
     // the activation rows live in the second activation buffer until the K
     // loop has computed its load offsets (its first write comes later)
@@ -756,7 +761,7 @@ k_g4_store(G2Args g) {
     const uint32_t rb = (uint32_t)g.a.row_bytes;
     const int n0 = ctile * G4_NWG + 64 * wave;
     const int64_t rowbase[2] = {n0, n0 + 32};
-    const G4WDma<WT> dm = g4_wdma<WT>(r, r, rowbase, rb, mis, lane);
+    const G4WDma<WT> dm = g4_wdma<WT>(r, r, rowbase, rb, mis, lane, WT == 12 && g.tiled != 0);
     g4_issue_w0<WT>(dm, Ws[wave]);
     int *s_arow = (int *)As1;   // as in k_g4_glu
     g4_rows_publish<BM>(g, my_p, s_arow);
@@ -831,6 +836,11 @@ int launch_gemm4(const G2Args &g, hipStream_t st) {
     const int64_t lim = 0x7fffffff;
     // byte offsets of the buffer loads are 32-bit
     if (g.xrows <= 0 || g.xrows * g.a.K * 2 > lim || g.a.mat_bytes + 4 > lim) return -6;
+    // tiled: whole 32-row groups, matrices without padding between them
+    if (g.tiled && (g.a.type != 12 || g.a.N % 32 || g.a.mat_bytes != g.a.N * g.a.row_bytes ||
+                    (g.glu && !g.fused &&
+                     (g.b.type != 12 || g.b.N % 32 || g.b.mat_bytes != g.b.N * g.b.row_bytes))))
+        return -6;
     const int ntile8 = (g.max_tiles + 7) / 8;
     if (g.glu) {
         // GLU values out (fp32 to y or fp16 to yh, ldy); the work-group covers

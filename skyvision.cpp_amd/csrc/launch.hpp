@@ -23,6 +23,9 @@ int hip_check_launch();
 int launch_fill_normal(float *out, int64_t n, uint64_t seed, uint64_t stream, float mean, float sd,
                        hipStream_t st);
 int launch_quantize(int type, const float *src, void *dst, int64_t nblocks, hipStream_t st);
+// dst = n_mat Q4_K matrices of rows (a multiple of 32) rows of rb bytes in
+// the tiled order of the grouped GEMMs (G2Args::tiled); 16-byte aligned
+int launch_tile_q4k(const void *src, void *dst, int64_t n_mat, int64_t rows, int64_t rb, hipStream_t st);
 // y = x / sqrt(mean(x^2) + eps) per row of D (x may equal y)
 int launch_rmsnorm(const float *x, int64_t T, int D, float eps, float *y, hipStream_t st);
 // y = norm(x) per row of D <= 4096 (norm.hpp; x may equal y)
@@ -191,6 +194,10 @@ struct G2Args {
     // pointers above are then not read
     const int32_t *ids;
     int nids, n_expert;
+    // 1: a (and b) hold Q4_K tables in the tiled order (launch_tile_q4k):
+    // the 32 rows of a column tile give block b as 4608 contiguous bytes,
+    // the LDS image of one column tile's weight loads
+    int tiled;
     int64_t xrows;        // rows of xh (glu = 1: tokens)
     float *y;
     int64_t ldy;

@@ -22,7 +22,7 @@ TYPE_Q4_0, TYPE_Q5_0, TYPE_Q8_0 = 2, 6, 8
 ACT_SILU, ACT_GELU_ERF_GP1, ACT_GELU_TANH, ACT_GELU_ERF, ACT_RELU_SQR = 0, 1, 2, 3, 4
 NORM_NONE, NORM_RMS, NORM_LAYER = 0, 1, 2
 GATING_SOFTMAX_TOPK, GATING_SIGMOID_BIAS, GATING_SOFTMAX_ALL = 0, 1, 2
-ABI_VERSION = 2
+ABI_VERSION = 3
 # mi_moe_status
 OK, ERR_NULL, ERR_SHAPE, ERR_TYPE, ERR_CAPACITY, ERR_HIP = 0, -1, -2, -3, -4, -5
 ERR_UNSUPPORTED, ERR_DEVICE, ERR_ARG, ERR_FORMAT = -6, -7, -8, -9
@@ -58,7 +58,7 @@ class Layer(C.Structure):
                 ("down", Tensor), ("fused_gate_up", i32), ("act", i32), ("gating", i32),
                 ("sel_bias", P), ("expert_scale", P), ("routed_scaling", C.c_float), ("gate_eps", C.c_float),
                 ("sh_n_ff", i32), ("sh_act", i32), ("sh_gate", Tensor), ("sh_up", Tensor), ("sh_down", Tensor),
-                ("sh_gate_inp", P)]
+                ("sh_gate_inp", P), ("gate_tiled", Tensor), ("up_tiled", Tensor), ("down_tiled", Tensor)]
 
 
 class Norm(C.Structure):
@@ -95,6 +95,7 @@ SYMBOLS = {
     "mi_mul_mat_id": ([P, C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor),
                        C.POINTER(Tensor), P], C.c_int),
     "mi_quantize": ([P, i32, P, P, i64, i64, P], C.c_int),
+    "mi_moe_tile_q4k": ([P, C.POINTER(Tensor), P, P], C.c_int),
     "mi_fill_normal": ([P, P, i64, C.c_uint64, C.c_uint64, C.c_float, C.c_float, P], C.c_int),
     "mi_rmsnorm": ([P, P, i64, C.c_int32, C.c_float, P, P], C.c_int),
     "mi_norm": ([P, C.POINTER(Norm), P, i64, C.c_int32, P, P], C.c_int),
@@ -351,6 +352,10 @@ class Context:
     def quantize(self, type_: int, src, dst, nrows: int, n_per_row: int, stream=None) -> int:
         return load().mi_quantize(self.h, type_, _addr(src), _addr(dst), nrows, n_per_row,
                                   _addr(stream))
+
+    def tile_q4k(self, src: Tensor, dst, stream=None) -> int:
+        """dst = src (a Q4_K table) in the grouped GEMMs' tiled order."""
+        return load().mi_moe_tile_q4k(self.h, C.byref(src), _addr(dst), _addr(stream))
 
     def fill_normal(self, dst, n: int, seed: int, stream_id: int, mean: float, std: float,
                     stream=None) -> int:

@@ -2,7 +2,7 @@
 profiler to trace: the layer (16 rotated synthetic copies, seeded like the
 bench) forwarded `--iters` times, captured once into a HIP graph and
 replayed (or issued call by call with --no-graph), on the default product
-paths (the kernel chain with --chain).  Prints the time per call.
+paths (the kernel chain with --chain; the tables' tiled copies with --tiled).  Prints the time per call.
 
     rocprofv3 --kernel-trace --stats -- python3 skyvision.cpp_amd/profile_layer.py --config 3 --tokens 32
 """
@@ -26,6 +26,7 @@ def main():
     ap.add_argument("--copies", type=int, default=16)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--chain", action="store_true", help="the kernel chain also where a fused decode kernel applies")
+    ap.add_argument("--tiled", action="store_true", help="tiled copies of the Q4_K tables for the grouped GEMMs")
     a = ap.parse_args()
     spec = W.CONFIGS[a.config]["spec"]
     T = a.tokens
@@ -34,6 +35,9 @@ def main():
     if a.chain:
         ctx.set_fused_decode(M.DECODE_CHAIN)
     layers = [W.GpuLayer(ctx, spec, copy=c) for c in range(a.copies)]
+    if a.tiled:
+        for g in layers:
+            g.add_tiled(ctx)
     xs = [W.gen_x(ctx, spec, T, copy=c) for c in range(a.copies)]
     out = M.DeviceBuffer(4 * T * spec.D)
     n = len(layers)

@@ -137,6 +137,19 @@ class GpuLayer:
             self.tensor("gate"), self.tensor("up") if "up" in self.tables else None,
             self.tensor("down"), spec.fused, spec.act)
 
+    def add_tiled(self, ctx: M.Context) -> None:
+        """Tiled copies of the Q4_K tables (mi_moe_tile_q4k) attached to the
+        layer descriptor, for the grouped GEMMs to read."""
+        self.tiled = {}
+        for nm, (q, ttype, Kin, N) in self.tables.items():
+            if ttype != M.TYPE_Q4_K:
+                continue
+            dst = M.DeviceBuffer(q.nbytes)
+            M.check("mi_moe_tile_q4k", ctx.tile_q4k(self.tensor(nm), dst))
+            self.tiled[nm] = dst
+            setattr(self.layer, nm + "_tiled", M.tensor(dst, ttype, [Kin, N, self.spec.E]))
+        M.synchronize()
+
     def tensor(self, nm: str) -> M.Tensor:
         q, ttype, Kin, N = self.tables[nm]
         return M.tensor(q, ttype, [Kin, N, self.spec.E])

@@ -5,7 +5,11 @@ prefill (gate/up Q4_K, down Q6_K, E=64, top-8), seeded synthetic data.  One
 step = one full layer forward (router -> top-k -> dispatch -> gate/up GEMM +
 GeGLU -> Q8_K -> down GEMM -> weighted combine) over the 1024 tokens, with
 the inputs resident in HBM.  Steps rotate over --copies distinct layer copies
-so the 256 MB Infinity Cache cannot hold the weights between steps.
+so the 256 MB Infinity Cache cannot hold the weights between steps.  Each
+layer carries tiled copies of its Q4_K tables (mi_moe_tile_q4k, made when
+the layer is built, outside the timed region), which the grouped GEMMs read
+in place of the GGUF rows (same bytes, reordered; bit-identical output);
+--no-tiled runs on the GGUF rows alone.
 
 Printed JSON line (rank 0):
   value          tokens/s of the whole layer (T * steps / time); the K forwards
@@ -261,19 +265,36 @@ def host_cpu() -> str:
     return f"{model} ({', '.join(isa) if isa else 'no AVX2'})"
 
 
-def config3_sweep(copies: int) -> dict:
+def make_layers(ctx, spec, n: int, tiled: bool) -> list:
+    """n seeded layer copies; tiled: with tiled copies of their Q4_K tables
+    (mi_moe_tile_q4k, made at load time, outside every timed region) for the
+    grouped GEMMs to read."""
+    layers = [W.GpuLayer(ctx, spec, copy=c) for c in range(n)]
+    if tiled:
+        for g in layers:
+            g.add_tiled(ctx)
+    return layers
+
+
+TABLES_TILED = "GGUF rows + tiled copies of the Q4_K tables (mi_moe_tile_q4k) for the grouped GEMMs"
+TABLES_ROWS = "GGUF rows only"
+
+
+def config3_sweep(copies: int, tiled: bool = True) -> dict:
     """Config 3: qwen3omni layer (E 128, I 768, SwiGLU, Q4_K), batched decode
     at T = 1, 8, 32, 64 on both product paths of the kernel chain (grouped
     GEMV, grouped MFMA GEMM) and, up to 16 tokens, the fused kernel (the
     single-token kernel at T = 1, the batched one above), rotating layer
     copies.  Bytes per call = the touched experts' tables + the router
     (measured touched count); the crossover is the smallest T at which the
-    chain's GEMM path is faster than its GEMV path."""
+    chain's GEMM path is faster than its GEMV path.  tiled: the GEMM path
+    reads the tables' tiled copies (gemm_rows_ms: the same path on the GGUF
+    rows, beside it)."""
     spec = W.CONFIGS[3]["spec"]
     Ts = W.CONFIGS[3]["tokens"]
     ctx = M.Context(0)
     ctx.reserve(max(Ts), spec.D, spec.I, spec.E, spec.K)
-    layers = [W.GpuLayer(ctx, spec, copy=c) for c in range(copies)]
+    layers = make_layers(ctx, spec, copies, tiled)
     rows = []
     for T in Ts:
         xs = [W.gen_x(ctx, spec, T, copy=c) for c in range(copies)]
@@ -287,11 +308,17 @@ def config3_sweep(copies: int) -> dict:
             ctx.set_gemm_threshold(thr)
             ms, _ = time_layer(ctx, layers, xs, T, out, 100, 10)
             row[f"{name}_ms"] = ms
+        if tiled:
+            for g in layers:
+                g.use_tiled(False)
+            row["gemm_rows_ms"] = time_layer(ctx, layers, xs, T, out, 100, 10)[0]
+            for g in layers:
+                g.use_tiled(True)
         ctx.set_fused_decode(M.DECODE_FUSED)
         ctx.set_gemm_threshold(0)
         if T <= 16:
             row["fused_ms"] = time_layer(ctx, layers, xs, T, out, 100, 10)[0]
-        best = min(v for k, v in row.items() if k.endswith("_ms"))
+        best = min(v for k, v in row.items() if k.endswith("_ms") and k != "gemm_rows_ms")
         row["best_ms"] = best
         row["tokens_per_s"] = T / (best * 1e-3)
         row["GBs"] = nbytes / (best * 1e-3) / 1e9
@@ -305,10 +332,12 @@ def config3_sweep(copies: int) -> dict:
     del layers
     ctx.close()
     return {"workload": "config 3: qwen3omni MoE layer (E 128, top-8, I 768, SwiGLU, Q4_K), batched decode",
-            "layer_copies": copies, "points": rows, "gemm_faster_from_tokens": cross}
+            "layer_copies": copies, "tables": TABLES_TILED if tiled else TABLES_ROWS, "points": rows,
+            "gemm_faster_from_tokens": cross}
 
 
-def config4_stack(n_layers: int = 24, T_prefill: int = 2048, n_decode: int = 256, eps: float = 1e-6) -> dict:
+def config4_stack(n_layers: int = 24, T_prefill: int = 2048, n_decode: int = 256, eps: float = 1e-6,
+                  tiled: bool = True) -> dict:
     """Config 4: 24 moondream-shape layers (Q4_K gate/up and down, per-layer
     seeds), h <- h + MoE_l(RMSNorm(h)) with attention as identity: a
     2048-token prefill through the stack, then 256 single-token steps, each
@@ -320,7 +349,7 @@ def config4_stack(n_layers: int = 24, T_prefill: int = 2048, n_decode: int = 256
     ctx.reserve(T_prefill, spec.D, spec.I, spec.E, spec.K)
     ctx.set_fused_decode(M.DECODE_FUSED)
     t0 = time.perf_counter()
-    layers = [W.GpuLayer(ctx, spec, copy=c) for c in range(n_layers)]
+    layers = make_layers(ctx, spec, n_layers, tiled)
     resident = sum(l.expert_bytes() * spec.E + 4 * spec.E * spec.D for l in layers)
     log(f"config 4: built {n_layers} layers in {time.perf_counter() - t0:.1f}s ({resident / 1e9:.2f} GB)")
     h0 = W.gen_x(ctx, spec, T_prefill)
@@ -460,7 +489,7 @@ def prefill_line(config: int, args, primary: bool) -> dict:
     ctx = M.Context(0)
     ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
     t0 = time.perf_counter()
-    layers = [W.GpuLayer(ctx, spec, copy=c) for c in range(args.copies)]
+    layers = make_layers(ctx, spec, args.copies, not args.no_tiled)
     xs = [W.gen_x(ctx, spec, T, copy=c) for c in range(args.copies)]
     out = M.DeviceBuffer(4 * T * spec.D)
     M.synchronize()
@@ -516,6 +545,7 @@ def prefill_line(config: int, args, primary: bool) -> dict:
         "config": {"workload": f"config {config}: moondream3 MoE layer prefill", "schedule": schedule,
                    "tokens": T, "n_embd": spec.D, "n_expert": spec.E, "n_expert_used": spec.K,
                    "n_ff": spec.I, "gate_up": "Q4_K",
+                   "tables": TABLES_ROWS if args.no_tiled else TABLES_TILED,
                    "down": "Q6_K" if spec.down_type == M.TYPE_Q6_K else "Q4_K",
                    "act": ACT_NAMES[spec.act], "layer_copies": args.copies,
                    "touched_experts": touched, "layer_flops": W.flops(spec, T)},
@@ -576,6 +606,8 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=16)
     ap.add_argument("--config", type=int, default=1, choices=[1, 2])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-tiled", action="store_true",
+                    help="no tiled copies of the Q4_K tables: the grouped GEMMs read the GGUF rows")
     ap.add_argument("--no-graph", action="store_true",
                     help="time the stream-issued forwards only (no HIP graph replay)")
     ap.add_argument("--no-decode", action="store_true")
@@ -685,9 +717,9 @@ def main() -> int:
     del layers0, line
 
     if not args.no_sweeps:
-        result["config3"] = config3_sweep(args.copies)
+        result["config3"] = config3_sweep(args.copies, not args.no_tiled)
         if not args.no_stack:
-            result["config4"] = config4_stack()
+            result["config4"] = config4_stack(tiled=not args.no_tiled)
     result.update({k: v for k, v in extra.items() if k.startswith("stream")})
     print(json.dumps(result), flush=True)
     return 0

@@ -147,8 +147,14 @@ class GpuLayer:
             dst = M.DeviceBuffer(q.nbytes)
             M.check("mi_moe_tile_q4k", ctx.tile_q4k(self.tensor(nm), dst))
             self.tiled[nm] = dst
-            setattr(self.layer, nm + "_tiled", M.tensor(dst, ttype, [Kin, N, self.spec.E]))
         M.synchronize()
+        self.use_tiled(True)
+
+    def use_tiled(self, on: bool) -> None:
+        """Point the descriptor's tiled fields at the copies (on) or at none."""
+        for nm, dst in getattr(self, "tiled", {}).items():
+            q, ttype, Kin, N = self.tables[nm]
+            setattr(self.layer, nm + "_tiled", M.tensor(dst, ttype, [Kin, N, self.spec.E]) if on else M.Tensor())
 
     def tensor(self, nm: str) -> M.Tensor:
         q, ttype, Kin, N = self.tables[nm]

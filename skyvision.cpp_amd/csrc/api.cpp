@@ -258,6 +258,8 @@ int validate_layer(const mi_moe_ctx *c, const mi_moe_layer *L, bool need_router,
         TRY(check_tiled(L->up_tiled, L->up));
         if (!L->gate_tiled.data != !L->up_tiled.data) return MI_MOE_ERR_ARG;   // both or neither
     }
+    if (act_gated(L->act) && L->fused_gate_up && L->gate_tiled.data && I % 32)
+        return MI_MOE_ERR_SHAPE;   // the g half of [h | g] starts on a 32-row group
     if (shared && L->sh_n_ff < 0) return MI_MOE_ERR_SHAPE;
     if (shared && L->sh_n_ff > 0) TRY(check_experts(L->sh_gate, L->sh_up, L->sh_down, 0, L->sh_act, D, L->sh_n_ff, 1));
     if (!c->reserved) return MI_MOE_ERR_CAPACITY;
@@ -651,8 +653,8 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         // (ggml: the down mul_mat_id quantizes its F32 input) for the down GEMM
         G2Args a = {};
         a.a = gate; a.b = up; a.glu = gated ? 1 : 0; a.fused = L->fused_gate_up; a.act = L->act; a.I = I;
-        if (!gs && L->gate_tiled.data) {
-            // the tables' tiled copies (the skinny kernels read the rows)
+        if (L->gate_tiled.data) {
+            // the tables' tiled copies
             a.a.data = (const uint8_t *)L->gate_tiled.data;
             if (gated && !L->fused_gate_up) a.b.data = (const uint8_t *)L->up_tiled.data;
             a.tiled = 1;
@@ -678,7 +680,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         stage_end(c, "q8k_act", st);
         G2Args d = {};
         d.a = down; d.glu = 0; d.xh = c->aact.h; d.ne11 = K; d.K = K;
-        if (!gs && L->down_tiled.data) { d.a.data = (const uint8_t *)L->down_tiled.data; d.tiled = 1; }
+        if (L->down_tiled.data) { d.a.data = (const uint8_t *)L->down_tiled.data; d.tiled = 1; }
         d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
         d.tile_r0 = dd.tile_r0; d.tile_start = dd.tile_start; d.tile_rows = dd.tile_rows; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles; d.xrows = (int64_t)T * K;
         d.tile_perm = dd.tile_perm;

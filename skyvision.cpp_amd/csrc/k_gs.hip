@@ -156,6 +156,7 @@ template <int NM> struct GsStream {
     const uint8_t *ptr[NM];   // lane's row, block 0
     uint32_t qoff;            // 16 + 32 G
     uint32_t cg_stride;       // bytes from a column group of the wave to its next (4 groups of 16 rows)
+    uint32_t bstride;         // bytes from a block of the row to its next: 144 (rows), 4608 (tiled)
     int kb, nb;               // next block, blocks per row
     int left;                 // steps still to load after the next (the last one repeats)
 };
@@ -163,7 +164,7 @@ template <int NM> struct GsStream {
 // issue the next step's 3 NM loads into w and advance (selects, no branch)
 template <int NM>
 __device__ __forceinline__ void gs_load(GsStream<NM> &st, GsW<NM> &w) {
-    const uint32_t boff = (uint32_t)st.kb * Q4K_BYTES;
+    const uint32_t boff = (uint32_t)st.kb * st.bstride;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
         const uint8_t *b = st.ptr[m] + boff;
@@ -269,10 +270,14 @@ k_gs(G2Args g, int splits) {
     const int64_t rb = g.a.row_bytes;
     GsStream<NM> st;
     const int64_t n0 = ncw > 0 ? 16 * (c_lo + wave) + i16 : 0;   // (a wave without steps loads row 0 and never uses it)
-    st.ptr[0] = g.a.data + (int64_t)it.e * g.a.mat_bytes + n0 * rb;
+    // tiled tables: row n's block b at (n / 32) 32 rb + 4608 b + 144 (n % 32);
+    // 16 NW rows on (a whole number of 32-row groups) stays cg_stride
+    const int64_t roff = g.tiled ? (n0 >> 5) * 32 * rb + (n0 & 31) * Q4K_BYTES : n0 * rb;
+    st.ptr[0] = g.a.data + (int64_t)it.e * g.a.mat_bytes + roff;
     if constexpr (GLU) {
-        st.ptr[1] = g.fused ? st.ptr[0] + g.I * rb : g.b.data + (int64_t)it.e * g.b.mat_bytes + n0 * rb;
+        st.ptr[1] = g.fused ? st.ptr[0] + g.I * rb : g.b.data + (int64_t)it.e * g.b.mat_bytes + roff;
     }
+    st.bstride = g.tiled ? 32u * Q4K_BYTES : (uint32_t)Q4K_BYTES;
     st.qoff = 16u + 32u * (uint32_t)G;
     st.cg_stride = (uint32_t)(16 * NW * rb);
     st.kb = 0;
@@ -365,6 +370,12 @@ int launch_gemm_gs(const G2Args &g, int splits, hipStream_t st) {
     const int64_t ncols = g.glu ? g.I : g.ncols;
     if (ncols <= 0 || ncols % 16 || (int64_t)g.max_tiles * splits > lim) return -6;
     if (g.yh ? (g.ldy % 4 || (uintptr_t)g.yh % 8) : (g.ldy % 4 || (uintptr_t)g.y % 16)) return -6;
+    // tiled: whole 32-row groups, no padding between matrices, the fused
+    // matrix's g half starting on a group
+    static_assert(GS_WAVES_GLU % 2 == 0 && GS_WAVES_ST % 2 == 0, "a wave's column groups step whole 32-row groups");
+    if (g.tiled && (g.a.N % 32 || g.a.mat_bytes != g.a.N * g.a.row_bytes || (g.glu && g.fused && g.I % 32) ||
+                    (g.glu && !g.fused && (g.b.N % 32 || g.b.mat_bytes != g.b.N * g.b.row_bytes))))
+        return -6;
     const dim3 grid((unsigned)(g.max_tiles * splits));
     if (g.glu) {
         if (!g.fused && (g.b.type != 12 || g.b.row_bytes != g.a.row_bytes || g.b.mat_bytes + 64 > lim ||

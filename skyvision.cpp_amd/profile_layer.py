@@ -27,6 +27,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--chain", action="store_true", help="the kernel chain also where a fused decode kernel applies")
     ap.add_argument("--tiled", action="store_true", help="tiled copies of the Q4_K tables for the grouped GEMMs")
+    ap.add_argument("--gemm-tiles", type=int, default=0, choices=[0, 1, 2, 3],
+                    help="GEMM row tiles (mi_moe_ctx_set_gemm_tiles): 0 by shape, 3 the skinny products")
     a = ap.parse_args()
     spec = W.CONFIGS[a.config]["spec"]
     T = a.tokens
@@ -34,6 +36,8 @@ def main():
     ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
     if a.chain:
         ctx.set_fused_decode(M.DECODE_CHAIN)
+    if a.gemm_tiles:
+        ctx.set_gemm_tiles(a.gemm_tiles)
     layers = [W.GpuLayer(ctx, spec, copy=c) for c in range(a.copies)]
     if a.tiled:
         for g in layers:

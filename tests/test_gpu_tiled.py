@@ -70,18 +70,24 @@ def test_tile_rejects():
     ctx.close()
 
 
-CASES = ([("qo", 3, T, True) for T in (8,)] + [("qo", 3, T, False) for T in (32, 64, 300)]
-         + [("md_q4", 0, T, False) for T in (16, 64, 1024)] + [("md_q6down", 1, T, False) for T in (64, 1024)])
+# (name, config, T, chain, GEMM tiles: 0 by shape, 3 the skinny 16-row products)
+CASES = ([("qo", 3, 8, True, 0)] + [("qo", 3, T, False, 0) for T in (32, 64, 300)]
+         + [("md_q4", 0, T, False, 0) for T in (16, 64, 1024)]
+         + [("md_q6down", 1, T, False, 0) for T in (64, 1024)]
+         + [("qo_skinny", 3, T, True, 3) for T in (8, 32, 64)] + [("md_q4_skinny", 0, 40, True, 3)])
 
 
-@pytest.mark.parametrize("name,cfg,T,chain", CASES, ids=[f"{c[0]}-T{c[2]}" for c in CASES])
-def test_forward_tiled_bit_identical(name, cfg, T, chain):
+@pytest.mark.parametrize("name,cfg,T,chain,tiles", CASES, ids=[f"{c[0]}-T{c[2]}" for c in CASES])
+def test_forward_tiled_bit_identical(name, cfg, T, chain, tiles):
     spec = W.CONFIGS[cfg]["spec"]
-    log(f"case {name} T={T} chain={chain}")
+    log(f"case {name} T={T} chain={chain} gemm_tiles={tiles}")
     ctx = M.Context(0)
     ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
     if chain:
         ctx.set_fused_decode(M.DECODE_CHAIN)
+    if tiles:
+        ctx.set_gemm_threshold(1)
+        ctx.set_gemm_tiles(tiles)
     g = W.GpuLayer(ctx, spec)
     x = W.gen_x(ctx, spec, T, copy=3)
     outs = []

@@ -122,13 +122,13 @@ typedef struct {
     mi_tensor sh_up;               /* ne=[D, sh_n_ff]; ignored for MI_ACT_RELU_SQR */
     mi_tensor sh_down;             /* ne=[sh_n_ff, D] */
     const float *sh_gate_inp;      /* F32 [D] or NULL (unscaled) */
-    /* Optional copies of Q4_K gate / up / down tables in the tiled order
-     * (mi_moe_tile_q4k), read by the grouped GEMMs instead of the tables
-     * above (the GEMV and fused decode kernels keep reading those); data =
-     * NULL: none.  Same type, ne and nb as the table they copy; with separate
-     * gate and up tables, both or neither; a fused [h | g] table needs n_ff
-     * a multiple of 32.  The output is bit-identical with or without them;
-     * qwen3omni's layer at 32 / 64 tokens: 111 / 118 -> 96 / 103 us. */
+    /* Optional tiled copies of the gate / up (Q4_K) and down (Q4_K, Q6_K)
+     * tables (mi_moe_tile: the descriptor it returns), read by the grouped
+     * GEMMs instead of the tables above (the GEMV and fused decode kernels
+     * keep reading those); data = NULL: none.  With separate gate and up
+     * tables, both or neither; a fused [h | g] table needs n_ff a multiple
+     * of 32.  The output is bit-identical with or without them; qwen3omni's
+     * layer at 32 / 64 tokens: 111 / 118 -> 96 / 103 us. */
     mi_tensor gate_tiled, up_tiled, down_tiled;
 } mi_moe_layer;
 
@@ -305,20 +305,30 @@ int mi_mul_mat_id(mi_moe_ctx *ctx, const mi_tensor *as, const mi_tensor *b, cons
 int mi_quantize(mi_moe_ctx *ctx, int32_t type, const float *src, void *dst, int64_t nrows,
                 int64_t n_per_row, mi_stream_t stream);
 
-/* ---- tiled copies of Q4_K expert tables -----------------------------------
- * dst (the size of src, 16-byte aligned, not overlapping it) = src in the
- * tiled order: for every matrix and every 32-row group of its rows, block b
- * (256 values, 144 bytes) of the group's 32 rows as 4608 contiguous bytes,
- * b = 0, 1, ...  The same bytes as src, only their order differs: a group's
- * 32 rows still occupy their own byte range.  The grouped GEMMs read it as
- * 1 KB runs with consecutive blocks adjacent, which the memory streams
- * ~1.5x as fast as the rows' 144-byte pieces (load-only probe: 6.1 vs 4.1
- * TB/s); mi_moe_forward's small batches gain from it (mi_moe_layer.
- * gate_tiled).  src: Q4_K, ne[1] a multiple of 32, rows
- * contiguous (nb[1] = row size, nb[2] = ne[1] nb[1]), 16-byte aligned.  No
+/* ---- tiled copies of expert tables ------------------------------------------
+ * Load-time copies of Q4_K and Q6_K expert tables in the grouped GEMMs' order,
+ * to attach to a layer (mi_moe_layer.gate_tiled / up_tiled / down_tiled).  No
  * counterpart in the reference (its tables are the GGUF tensors, which this
- * library reads unchanged everywhere else). */
-int mi_moe_tile_q4k(mi_moe_ctx *ctx, const mi_tensor *src, void *dst, mi_stream_t stream);
+ * library reads unchanged everywhere else).  src: ne[1] a multiple of 32,
+ * rows contiguous (nb[1] = row size, nb[2] = ne[1] nb[1]), 16-byte aligned
+ * (Q4_K) / 2-byte aligned (Q6_K).
+ *  Q4_K: the same bytes reordered - for every matrix and every 32-row group,
+ *   block b (256 values, 144 bytes) of the group's 32 rows as 4608 contiguous
+ *   bytes, then block b + 1.  The GEMMs read it as 1 KB runs with consecutive
+ *   blocks adjacent, which the memory streams ~1.5x as fast as the rows'
+ *   144-byte pieces (load-only probe: 6.1 vs 4.1 TB/s): small batches gain.
+ *  Q6_K (down tables): per 32-row group and block b, 9216 bytes: the 6-bit
+ *   codes merged into bytes (8 KB, in the order the GEMM's lanes take them)
+ *   and the 16 sub-block scales as fp16 d * scale (1 KB); 288 bytes per 256
+ *   values instead of 210.  The down GEMM then builds its fp16 operands with
+ *   a third fewer instructions (prefill gains).
+ * The output of a layer is bit-identical with or without the copies.
+ * mi_moe_tiled_bytes: the copy's size in bytes, or a negative mi_moe_status.
+ * mi_moe_tile: dst (16-byte aligned, not overlapping src) = the copy; *desc
+ * (if not NULL) = its descriptor to attach (type and ne of src; nb of the
+ * copy's rows: Q6_K nb[1] = 288 ne[0] / 256). */
+int64_t mi_moe_tiled_bytes(const mi_tensor *src);
+int mi_moe_tile(mi_moe_ctx *ctx, const mi_tensor *src, void *dst, mi_tensor *desc, mi_stream_t stream);
 
 /* Seeded synthetic N(mean, std^2) fill: value i of (seed, stream_id) does not
  * depend on n or the launch shape.  Counterpart of the reference's seeded

@@ -230,15 +230,32 @@ int check_experts(const mi_tensor &gate, const mi_tensor &up, const mi_tensor &d
     return MI_MOE_OK;
 }
 
+// the descriptor of src's tiled copy (type and ne of src, the copy's row
+// strides), for a Q4_K or Q6_K table of whole 32-row groups
+int tiled_desc(const mi_tensor &src, mi_tensor &d) {
+    if (src.type != MI_TYPE_Q4_K && src.type != MI_TYPE_Q6_K) return MI_MOE_ERR_TYPE;
+    const int64_t K = src.ne[0], N = src.ne[1];
+    if (K <= 0 || K % QK || N <= 0 || N % 32 || src.ne[2] <= 0 || src.ne[3] <= 0) return MI_MOE_ERR_SHAPE;
+    d = src;
+    d.data = nullptr;
+    d.nb[0] = src.type == MI_TYPE_Q4_K ? (size_t)Q4K_BYTES : (size_t)Q6X_ROW_BYTES;
+    d.nb[1] = d.nb[0] * (size_t)(K / QK);
+    d.nb[2] = d.nb[1] * (size_t)N;
+    d.nb[3] = d.nb[2] * (size_t)src.ne[2];
+    return MI_MOE_OK;
+}
+
 // an optional tiled copy of table t (mi_moe_layer.gate_tiled ..): absent, or
-// Q4_K like t with t's shape and strides, whole 32-row groups, no padding
-int check_tiled(const mi_tensor &tiled, const mi_tensor &t) {
+// mi_moe_tile's descriptor of t (Q4_K gate / up, Q4_K or Q6_K down)
+int check_tiled(const mi_tensor &tiled, const mi_tensor &t, bool q6k_ok) {
     if (!tiled.data) return MI_MOE_OK;
-    if (tiled.type != MI_TYPE_Q4_K || t.type != MI_TYPE_Q4_K) return MI_MOE_ERR_TYPE;
+    if (tiled.type != t.type || (t.type != MI_TYPE_Q4_K && !(q6k_ok && t.type == MI_TYPE_Q6_K)))
+        return MI_MOE_ERR_TYPE;
+    mi_tensor want;
+    TRY(tiled_desc(t, want));
     for (int i = 0; i < 4; ++i)
-        if (tiled.ne[i] != t.ne[i] || tiled.nb[i] != t.nb[i]) return MI_MOE_ERR_SHAPE;
-    if (t.ne[1] % 32 || t.nb[1] != type_row_size(t.type, t.ne[0]) || t.nb[2] != t.nb[1] * (size_t)t.ne[1])
-        return MI_MOE_ERR_SHAPE;
+        if (tiled.ne[i] != want.ne[i] || (tiled.nb[i] != want.nb[i] && (i < 3 || want.ne[3] > 1)))
+            return MI_MOE_ERR_SHAPE;
     if ((uintptr_t)tiled.data % 16) return MI_MOE_ERR_UNSUPPORTED;
     return MI_MOE_OK;
 }
@@ -252,10 +269,10 @@ int validate_layer(const mi_moe_ctx *c, const mi_moe_layer *L, bool need_router,
     if (L->gating < MI_GATING_SOFTMAX_TOPK || L->gating > MI_GATING_SOFTMAX_ALL) return MI_MOE_ERR_ARG;
     if (need_router && !L->router_w) return MI_MOE_ERR_NULL;
     TRY(check_experts(L->gate, L->up, L->down, L->fused_gate_up, L->act, D, I, E));
-    TRY(check_tiled(L->gate_tiled, L->gate));
-    TRY(check_tiled(L->down_tiled, L->down));
+    TRY(check_tiled(L->gate_tiled, L->gate, false));
+    TRY(check_tiled(L->down_tiled, L->down, true));
     if (act_gated(L->act) && !L->fused_gate_up) {
-        TRY(check_tiled(L->up_tiled, L->up));
+        TRY(check_tiled(L->up_tiled, L->up, false));
         if (!L->gate_tiled.data != !L->up_tiled.data) return MI_MOE_ERR_ARG;   // both or neither
     }
     if (act_gated(L->act) && L->fused_gate_up && L->gate_tiled.data && I % 32)
@@ -680,7 +697,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         stage_end(c, "q8k_act", st);
         G2Args d = {};
         d.a = down; d.glu = 0; d.xh = c->aact.h; d.ne11 = K; d.K = K;
-        if (L->down_tiled.data) { d.a.data = (const uint8_t *)L->down_tiled.data; d.tiled = 1; }
+        if (L->down_tiled.data) { d.a = as_mat(L->down_tiled); d.tiled = 1; }
         d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
         d.tile_r0 = dd.tile_r0; d.tile_start = dd.tile_start; d.tile_rows = dd.tile_rows; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles; d.xrows = (int64_t)T * K;
         d.tile_perm = dd.tile_perm;
@@ -1385,21 +1402,35 @@ int mi_quantize(mi_moe_ctx *c, int32_t type, const float *src, void *dst, int64_
     return launch_quantize(type, src, dst, nrows * (n_per_row / QK), (hipStream_t)stream);
 }
 
-int mi_moe_tile_q4k(mi_moe_ctx *c, const mi_tensor *src, void *dst, mi_stream_t stream) {
+int64_t mi_moe_tiled_bytes(const mi_tensor *src) {
+    if (!src) return MI_MOE_ERR_NULL;
+    mi_tensor d;
+    TRY(tiled_desc(*src, d));
+    return (int64_t)(d.nb[3] * (size_t)src->ne[3]);
+}
+
+int mi_moe_tile(mi_moe_ctx *c, const mi_tensor *src, void *dst, mi_tensor *desc, mi_stream_t stream) {
     if (!c || !src || !src->data || !dst) return MI_MOE_ERR_NULL;
-    if (src->type != MI_TYPE_Q4_K) return MI_MOE_ERR_TYPE;
+    mi_tensor d;
+    TRY(tiled_desc(*src, d));
     const int64_t K = src->ne[0], N = src->ne[1], n_mat = src->ne[2] * src->ne[3];
-    if (K <= 0 || K % QK || N <= 0 || N % 32 || n_mat <= 0) return MI_MOE_ERR_SHAPE;
-    const size_t rb = type_row_size(MI_TYPE_Q4_K, K);
+    const size_t rb = type_row_size(src->type, K);
     if (src->nb[1] != rb || src->nb[2] != rb * (size_t)N ||
         (src->ne[3] > 1 && src->nb[3] != src->nb[2] * (size_t)src->ne[2]))
         return MI_MOE_ERR_SHAPE;
-    if ((uintptr_t)src->data % 16 || (uintptr_t)dst % 16) return MI_MOE_ERR_UNSUPPORTED;
-    const size_t bytes = rb * (size_t)N * (size_t)n_mat;
+    const size_t align = src->type == MI_TYPE_Q4_K ? 16 : 2;
+    if ((uintptr_t)src->data % align || (uintptr_t)dst % 16) return MI_MOE_ERR_UNSUPPORTED;
+    const size_t sbytes = rb * (size_t)N * (size_t)n_mat, dbytes = d.nb[2] * (size_t)n_mat;
     const uintptr_t s0 = (uintptr_t)src->data, d0 = (uintptr_t)dst;
-    if (s0 < d0 + bytes && d0 < s0 + bytes) return MI_MOE_ERR_ARG;   // overlapping
+    if (s0 < d0 + dbytes && d0 < s0 + sbytes) return MI_MOE_ERR_ARG;   // overlapping
     HIP_TRY(hipSetDevice(c->device));
-    return launch_tile_q4k(src->data, dst, n_mat, N, (int64_t)rb, (hipStream_t)stream);
+    TRY(src->type == MI_TYPE_Q4_K ? launch_tile_q4k(src->data, dst, n_mat, N, (int64_t)rb, (hipStream_t)stream)
+                                  : launch_tile_q6k(src->data, dst, n_mat, N, (int64_t)rb, (hipStream_t)stream));
+    if (desc) {
+        d.data = dst;
+        *desc = d;
+    }
+    return MI_MOE_OK;
 }
 
 int mi_fill_normal(mi_moe_ctx *c, float *dst, int64_t n, uint64_t seed, uint64_t stream_id, float mean,

@@ -544,6 +544,72 @@ __global__ void __launch_bounds__(256) k_tile_q4k(const uint4 *__restrict__ src,
     }
 }
 
+// Q6_K tables in the down GEMM's tiled order: per matrix, 32-row group and
+// block b, 9216 bytes = 8 code chunks of 1 KB and one scale chunk of 1 KB,
+// 16 bytes per lane L (row 32 t + L % 32 of the group, half g2 = L / 32).
+// Code chunk 4 h + m holds the lane's merged 6-bit codes (one per byte) of
+// stage h, dword m of its 16-byte ql / qh runs:
+//   a = ql[64 h + 16 g2 + 4 m ..], b = ql[64 h + 32 + 16 g2 + 4 m ..],
+//   c = qh[32 h + 16 g2 + 4 m ..]  (dwords)
+//   {a lo | (c << 4 & 0x30..), a hi | (c & 0x30..), b lo | (c << 2 & 0x30..),
+//    b hi | (c >> 2 & 0x30..)}  (lo = & 0x0F.., hi = >> 4 & 0x0F..)
+// - the codes the GEMM's Q6_K operand builder forms from the rows; the scale
+// chunk holds fp16(d * scales[8 h + 2 j + g2] + 0) at half 4 h + j.  One thread
+// per 16-byte piece; bytes read one at a time (blocks are 2-byte aligned).
+__device__ inline uint32_t rd_u32_bytes(const uint8_t *p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+__global__ void __launch_bounds__(256) k_tile_q6k(const uint8_t *__restrict__ src, uint4 *__restrict__ dst,
+                                                   int64_t pieces, int64_t src_mat, int64_t rb, int64_t ntile,
+                                                   int nb) {
+    for (int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; p < pieces;
+         p += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t tb = p / 576;   // (matrix, group, block), 9 chunks x 64 lanes each
+        const int q = (int)(p - tb * 576), c = q >> 6, L = q & 63, g2 = L >> 5;
+        const int b = (int)(tb % nb);
+        const int64_t mt = tb / nb, t = mt % ntile, e = mt / ntile;
+        const uint8_t *blk = src + e * src_mat + (32 * t + (L & 31)) * rb + (int64_t)Q6K_BYTES * b;
+        uint4 o;
+        if (c < 8) {
+            const int h = c >> 2, m = c & 3;
+            const uint32_t a = rd_u32_bytes(blk + 64 * h + 16 * g2 + 4 * m);
+            const uint32_t bb = rd_u32_bytes(blk + 64 * h + 32 + 16 * g2 + 4 * m);
+            const uint32_t qh = rd_u32_bytes(blk + 128 + 32 * h + 16 * g2 + 4 * m);
+            o.x = (a & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u);
+            o.y = ((a >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u);
+            o.z = (bb & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u);
+            o.w = ((bb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u);
+        } else {
+            const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(blk[208] | (blk[209] << 8)));
+            uint32_t hv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int h = i >> 2, j = i & 3;
+                // (+ 0: a zero scale gives +0 whatever d's sign, as the GEMM's
+                // own conversion of d * scale does)
+                const _Float16 v = (_Float16)(d * (float)(int)(int8_t)blk[192 + 8 * h + 2 * j + g2] + 0.0f);
+                hv[i] = (uint32_t)__builtin_bit_cast(uint16_t, v);
+            }
+            o.x = hv[0] | (hv[1] << 16);
+            o.y = hv[2] | (hv[3] << 16);
+            o.z = hv[4] | (hv[5] << 16);
+            o.w = hv[6] | (hv[7] << 16);
+        }
+        dst[p] = o;
+    }
+}
+
+int launch_tile_q6k(const void *src, void *dst, int64_t n_mat, int64_t rows, int64_t rb, hipStream_t st) {
+    const int nb = (int)(rb / Q6K_BYTES);
+    const int64_t ntile = rows / 32, pieces = n_mat * ntile * nb * 576;
+    if (pieces <= 0) return 0;
+    const int64_t blocks = min((int64_t)65536, (pieces + 255) / 256);
+    hipLaunchKernelGGL(k_tile_q6k, dim3((unsigned)blocks), dim3(256), 0, st, (const uint8_t *)src, (uint4 *)dst,
+                       pieces, rows * rb, rb, ntile, nb);
+    return hip_check_launch();
+}
+
 int launch_tile_q4k(const void *src, void *dst, int64_t n_mat, int64_t rows, int64_t rb, hipStream_t st) {
     const int64_t pieces = n_mat * rows * rb / 16;
     if (pieces <= 0) return 0;

@@ -226,6 +226,12 @@ template <> struct G4Fmt<12> {
 template <> struct G4Fmt<14> {
     static constexpr int SLOTS = 16, PART = 8 * 1024, NLD = 8;
 };
+// Q6_K in the tiled order (launch_tile_q6k): a column tile's block is 8 KB of
+// merged codes, chunk c of 1 KB holding lane i's 16 bytes at 16 i (the LDS
+// image is the copy's bytes), and 1 KB of fp16 scales loaded to registers
+template <> struct G4Fmt<15> {
+    static constexpr int SLOTS = 16, PART = 8 * 1024, NLD = 8;
+};
 template <int WT> constexpr int g4_wregion() { return 2 * G4Fmt<WT>::PART; }
 
 // the whole block's operand bytes of the lane, both stages, per column tile
@@ -233,6 +239,10 @@ template <int WT> struct G4W;
 template <> struct G4W<12> {
     u32x4 hdr[2];       // d, dmin, scales
     u32x4 q[2][2][2];   // [ct][h][half]: qs chunk 2 h + g2 (stage h, steps 0-3 / 4-7)
+};
+template <> struct G4W<15> {
+    u32x4 q[2][2][4];   // [ct][h][m]: codes of stage h, dword m of the runs: a lo, a hi, b lo, b hi
+    u32x4 s[2];         // [ct]: fp16 d * scale of the lane's sub-blocks, half 4 h + j
 };
 template <> struct G4W<14> {
     // [ct][h]: 16 bytes each of ql 64 h + 16 g2 .., ql 64 h + 32 + 16 g2 ..,
@@ -247,6 +257,10 @@ template <> struct G4WDma<12> {
     rsrc_t r[2];
     uint32_t off[2][5];   // [ct][j]: byte offset at block 0 of the lane's 16 bytes
     uint32_t bstride;     // bytes from one block to the next: 144 (rows), 4608 (tiled)
+};
+template <> struct G4WDma<15> {
+    rsrc_t r[2];
+    uint32_t base[2];     // [ct]: byte offset of the column tile's block 0 plus 16 lane
 };
 template <> struct G4WDma<14> {
     rsrc_t r[2];
@@ -276,6 +290,11 @@ __device__ __forceinline__ G4WDma<WT> g4_wdma(rsrc_t r0, rsrc_t r1, const int64_
                                       : (uint32_t)((rowbase[ct] + r) * rb) + 16u * (uint32_t)k;
             }
         dm.bstride = tiled ? 32u * Q4K_BYTES : (uint32_t)Q4K_BYTES;
+    } else if constexpr (WT == 15) {
+        (void)mis;
+        (void)tiled;
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) dm.base[ct] = (uint32_t)(rowbase[ct] * rb) + 16u * (uint32_t)lane;
     } else {
 #pragma unroll
         for (int par = 0; par < 2; ++par) {
@@ -307,6 +326,9 @@ __device__ __forceinline__ void g4_issue_w(const G4WDma<WT> &dm, uint8_t *W, int
         if (jj + 1 < F::NLD || (int)(threadIdx.x & 63) < F::PART / 16 - 64 * (F::NLD - 1))
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)dst, 16, (int)dm.off[ct][jj],
                                                      b * (int)dm.bstride, 0, 0);
+    } else if constexpr (WT == 15) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)dst, 16, (int)(dm.base[ct] + 1024u * (uint32_t)jj),
+                                                 b * (32 * Q6X_ROW_BYTES), 0, 0);
     } else {
         const uint32_t x = dm.x[ct][jj & 1] + (uint32_t)jj * dm.rstride + (uint32_t)(b * Q6K_BYTES);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)dst, 16, (int)((x & ~3u) + dm.kk[jj & 1]), 0, 0,
@@ -320,6 +342,12 @@ __device__ __forceinline__ void g4_issue_w0(const G4WDma<WT> &dm, uint8_t *W) {
     for (int j = 0; j < 2 * G4Fmt<WT>::NLD; ++j) g4_issue_w<WT>(dm, W, j, 0);
 }
 
+// Q6_K tiled: the scales of column tile ct, block b, into registers
+__device__ __forceinline__ u32x4 g4_load_s15(const G4WDma<15> &dm, int ct, int b) {
+    rsrc_t r = dm.r[ct];
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)(dm.base[ct] + 8192u), b * (32 * Q6X_ROW_BYTES), 0);
+}
+
 // the lane's operand bytes of the whole block from the region
 template <int WT>
 __device__ __forceinline__ void g4_copy_w(const uint8_t *W, int l32, int g2, uint32_t sh, G4W<WT> &w) {
@@ -327,7 +355,14 @@ __device__ __forceinline__ void g4_copy_w(const uint8_t *W, int l32, int g2, uin
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
         const uint8_t *row = W + ct * F::PART + l32 * (F::SLOTS * 16);
-        if constexpr (WT == 12) {
+        if constexpr (WT == 15) {
+            (void)row;
+            const uint8_t *img = W + ct * F::PART + 16 * (l32 + 32 * g2);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int m = 0; m < 4; ++m) w.q[ct][h][m] = *(const u32x4 *)(img + 1024 * (4 * h + m));
+        } else if constexpr (WT == 12) {
             w.hdr[ct] = *(const u32x4 *)row;
 #pragma unroll
             for (int h = 0; h < 2; ++h)
@@ -372,6 +407,9 @@ template <> struct G4Sc<12> {
 template <> struct G4Sc<14> {
     half2_t sq[2][4];
 };
+template <> struct G4Sc<15> {
+    half2_t sq[2][4];
+};
 
 template <int WT>
 __device__ __forceinline__ void g4_scales(const G4W<WT> &w, int ct, int g2, int h, uint32_t sh, G4Sc<WT> &s) {
@@ -385,6 +423,16 @@ __device__ __forceinline__ void g4_scales(const G4W<WT> &w, int ct, int g2, int 
         scale_min_k4_reg(4 * h + 2 * g2 + 1, hv.y, hv.z, hv.w, sc, m);
         s.s_hi[ct] = g4_splat(d * (float)sc);
         s.nm_hi[ct] = g4_splat(q4k_center(d, sc, dmin, m));
+    } else if constexpr (WT == 15) {
+        (void)g2;
+        (void)sh;
+        const u32x4 v = w.s[ct];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t dw = v[2 * h + (j >> 1)];
+            const _Float16 x = __builtin_bit_cast(_Float16, (uint16_t)((j & 1) ? dw >> 16 : dw & 0xffffu));
+            s.sq[ct][j] = half2_t{x, x};
+        }
     } else {
         const uint32_t dw = __builtin_amdgcn_alignbyte(w.sc[ct][4], w.sc[ct][4], sh);   // bytes 16 + sh .. : d
         const float d = h2f((uint16_t)(dw & 0xffffu));
@@ -415,6 +463,15 @@ __device__ __forceinline__ uint32_t g4_piece(const G4W<WT> &w, const G4Sc<WT> &s
         else t = g4_u2h2(g4_and_or(x, 0x000F000Fu, 0x64006400u)) - c1032;
         return g4_h22u((p & 1) ? __builtin_elementwise_fma(t, s.s_hi[ct], s.nm_hi[ct])
                                : __builtin_elementwise_fma(t, s.s_lo[ct], s.nm_lo[ct]));
+    } else if constexpr (WT == 15) {
+        // the codes merged at the copy: the Q6_K form below without the merge
+        (void)sh;
+        const half2_t c1056 = {(_Float16)1056.f, (_Float16)1056.f};
+        const int ww = sp & 1;
+        const uint32_t q = w.q[ct][h][sp >> 1][ww + 2 * (p >> 1)];
+        const uint32_t sel = (p & 1) ? 0x04030402u : 0x04010400u;
+        const half2_t sc = s.sq[ct][2 * ww + (p >> 1)];
+        return g4_h22u((g4_u2h2(__builtin_amdgcn_perm(0x64646464u, q, sel)) - c1056) * sc);
     } else {
         const half2_t c1056 = {(_Float16)1056.f, (_Float16)1056.f};
         const int m = sp >> 1, ww = sp & 1;
@@ -530,12 +587,14 @@ __device__ __forceinline__ void g4_stage(const _Float16 *st, uint32_t abase, con
 // data; the epilogue waits for them): measured faster than skipping them
 // behind a uniform test per block, which costs the stage code more than the
 // loads cost.
+// Q6_K tiled (WT 15): sn holds the next block's scales (block 0's loaded
+// with its weights); block b + 1's two scale loads follow its weight loads.
 template <int WT, int NRT, int NA>
 __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_t arowbytes, const G4WDma<WT> &dm,
                                            const uint32_t (&wsh)[2], uint8_t *W, int nb, int wave, int lane,
-                                           _Float16 *As0, _Float16 *As1, f32x16 (&acc)[NA][2]) {
+                                           _Float16 *As0, _Float16 *As1, f32x16 (&acc)[NA][2], u32x4 (&sn)[2]) {
     using F = G4Fmt<WT>;
-    constexpr int NW = 2 * F::NLD;
+    constexpr int NW = 2 * F::NLD, NSL = WT == 15 ? 2 : 0;   // weight loads, scale loads per block
     const int l32 = lane & 31, g2 = lane >> 5;
     const uint32_t abase = 256u * (uint32_t)l32 + 16u * (uint32_t)(g2 ^ (l32 & 15));
     uint32_t aoff[2 * NRT];
@@ -555,7 +614,7 @@ __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_
     // loads at slots 4 i (i < 2 NRT), then, all after the last of them (the
     // sync before stage 1 counts on that order) and after the copy has
     // landed, the NW weight loads and the 2 column tiles' stage-1 scales
-    constexpr int NS = 16 * NRT, S0 = 8 * NRT - 3, NI = NW + 2;
+    constexpr int NS = 16 * NRT, S0 = 8 * NRT - 3, NI = NW + NSL + 2;
     for (int b = 0; b < nb; ++b) {
         // block b + 1's loads go out during block b; the last block reloads
         // itself (valid addresses, data unused) so that no stage branches
@@ -564,6 +623,10 @@ __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_
         const uint32_t sh = WT == 14 ? ((wsh[0] + (uint32_t)(b * Q6K_BYTES)) & 3u) : 0u;
         g4_stage_sync<0>();
         g4_copy_w<WT>(W, l32, g2, sh, w);
+        if constexpr (WT == 15) {
+            w.s[0] = sn[0];
+            w.s[1] = sn[1];
+        }
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) g4_scales<WT>(w, ct, g2, 0, sh, s0);
         g4_stage<WT, NRT>(As0, abase, w, s0, sh, 0, acc, [&](int slot) __attribute__((always_inline)) {
@@ -572,11 +635,16 @@ __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_
 #pragma unroll
             for (int it = 0; it < NI; ++it) {
                 if (S0 + it * (NS - S0) / NI != slot) continue;
-                if (it < NW) g4_issue_w<WT>(dm, W, it, bn);
-                else g4_scales<WT>(w, it - NW, g2, 1, sh, s1);
+                if (it < NW) {
+                    g4_issue_w<WT>(dm, W, it, bn);
+                } else if (it < NW + NSL) {
+                    if constexpr (WT == 15) sn[it - NW] = g4_load_s15(dm, it - NW, bn);
+                } else {
+                    g4_scales<WT>(w, it - NW - NSL, g2, 1, sh, s1);
+                }
             }
         });
-        g4_stage_sync<NW>();
+        g4_stage_sync<NW + NSL>();
         g4_stage<WT, NRT>(As1, abase, w, s1, sh, 1, acc, [&](int slot) __attribute__((always_inline)) {
             if (slot < 2 * NRT) g4_issue_a<NRT>(rx, aoff, wave, slot, As0, bn, 0);
         });
@@ -588,17 +656,17 @@ __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_
 template <int WT, int NA>
 __device__ __forceinline__ void g4_kloop(rsrc_t rx, const int *s_arow, uint32_t arowbytes, const G4WDma<WT> &dm,
                                          const uint32_t (&wsh)[2], uint8_t *W, int nb, int wave, int lane, int nrt,
-                                         _Float16 *As0, _Float16 *As1, f32x16 (&acc)[NA][2]) {
+                                         _Float16 *As0, _Float16 *As1, f32x16 (&acc)[NA][2], u32x4 (&sn)[2]) {
     if constexpr (NA == 1) {
-        g4_kloop_n<WT, 1>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc);
+        g4_kloop_n<WT, 1>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc, sn);
     } else {
         switch (nrt) {
-        case 1: g4_kloop_n<WT, 1>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
-        case 2: g4_kloop_n<WT, 2>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
-        case 3: g4_kloop_n<WT, 3>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
-        case 4: g4_kloop_n<WT, 4>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
-        case 5: g4_kloop_n<WT, 5>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
-        default: g4_kloop_n<WT, 6>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc); break;
+        case 1: g4_kloop_n<WT, 1>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc, sn); break;
+        case 2: g4_kloop_n<WT, 2>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc, sn); break;
+        case 3: g4_kloop_n<WT, 3>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc, sn); break;
+        case 4: g4_kloop_n<WT, 4>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc, sn); break;
+        case 5: g4_kloop_n<WT, 5>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc, sn); break;
+        default: g4_kloop_n<WT, 6>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc, sn); break;
         }
     }
 }
@@ -716,7 +784,8 @@ k_g4_glu(G2Args g) {
     g4_rows_publish<BM>(g, my_p, s_arow);
     const uint32_t wsh[2] = {0u, 0u};
     f32x16 acc[NA][2];
-    g4_kloop<12, NA>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc);
+    u32x4 sn[2];   // (Q6_K tiled only)
+    g4_kloop<12, NA>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc, sn);
     __builtin_amdgcn_s_waitcnt(0);   // no load may land in LDS after the work-group ends
     const int *s_p = g4_publish_rows<BM>((_Float16 *)&Ws[0][0], my_p);   // the row table in the weight region
     switch (g.act) {
@@ -756,19 +825,24 @@ k_g4_store(G2Args g) {
     const uint32_t Kin = (uint32_t)g.a.K;
     const rsrc_t rx = g4_rsrc(g.xh, g.xrows * (int64_t)Kin * 2);
     const uint8_t *mat = g.a.data + (int64_t)t.e * g.a.mat_bytes;
-    const uint32_t mis = WT == 14 ? (uint32_t)((uintptr_t)mat & 3u) : 0u;
+    const uint32_t mis = WT == 14 ? (uint32_t)((uintptr_t)mat & 3u) : 0u;   // (WT 15: the tiled Q6_K copy)
     const rsrc_t r = g4_rsrc(mat - mis, g.a.mat_bytes + mis);
     const uint32_t rb = (uint32_t)g.a.row_bytes;
     const int n0 = ctile * G4_NWG + 64 * wave;
     const int64_t rowbase[2] = {n0, n0 + 32};
     const G4WDma<WT> dm = g4_wdma<WT>(r, r, rowbase, rb, mis, lane, WT == 12 && g.tiled != 0);
     g4_issue_w0<WT>(dm, Ws[wave]);
+    u32x4 sn[2];
+    if constexpr (WT == 15) {
+        sn[0] = g4_load_s15(dm, 0, 0);
+        sn[1] = g4_load_s15(dm, 1, 0);
+    }
     int *s_arow = (int *)As1;   // as in k_g4_glu
     g4_rows_publish<BM>(g, my_p, s_arow);
     // byte offset of the lane's own rows (Q6_K block alignment)
     const uint32_t wsh[2] = {mis + (uint32_t)(n0 + l32) * rb, mis + (uint32_t)(n0 + 32 + l32) * rb};
     f32x16 acc[NA][2];
-    g4_kloop<WT, NA>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc);
+    g4_kloop<WT, NA>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc, sn);
     __builtin_amdgcn_s_waitcnt(0);   // no load may land in LDS after the work-group ends
     // rows 32 rt + 8 (i / 4) + 4 g2 + i % 4, columns n0 + 32 ct + l32
     if (g.yh) {
@@ -837,7 +911,12 @@ int launch_gemm4(const G2Args &g, hipStream_t st) {
     // byte offsets of the buffer loads are 32-bit
     if (g.xrows <= 0 || g.xrows * g.a.K * 2 > lim || g.a.mat_bytes + 4 > lim) return -6;
     // tiled: whole 32-row groups, matrices without padding between them
-    if (g.tiled && (g.a.type != 12 || g.a.N % 32 || g.a.mat_bytes != g.a.N * g.a.row_bytes ||
+    // (Q6_K: the down product only, 288 bytes per 256 values)
+    if (g.tiled && g.a.type == 14 &&
+        (g.glu || g.a.N % 32 || g.a.row_bytes != Q6X_ROW_BYTES * (g.a.K / QK) ||
+         g.a.mat_bytes != g.a.N * g.a.row_bytes))
+        return -6;
+    if (g.tiled && g.a.type != 14 && (g.a.type != 12 || g.a.N % 32 || g.a.mat_bytes != g.a.N * g.a.row_bytes ||
                     (g.glu && !g.fused &&
                      (g.b.type != 12 || g.b.N % 32 || g.b.mat_bytes != g.b.N * g.b.row_bytes))))
         return -6;
@@ -863,6 +942,10 @@ int launch_gemm4(const G2Args &g, hipStream_t st) {
             if ((uintptr_t)g.a.data % 4 || g.a.mat_bytes % 4 || g.a.row_bytes % 4) return -6;
             if (sm) hipLaunchKernelGGL((k_g4_store<12, G4_BM_SMALL>), grid, dim3(G4_THREADS), 0, st, g);
             else hipLaunchKernelGGL((k_g4_store<12, G4_BM>), grid, dim3(G4_THREADS), 0, st, g);
+        } else if (g.a.type == 14 && g.tiled) {
+            if ((uintptr_t)g.a.data % 16) return -6;
+            if (sm) hipLaunchKernelGGL((k_g4_store<15, G4_BM_SMALL>), grid, dim3(G4_THREADS), 0, st, g);
+            else hipLaunchKernelGGL((k_g4_store<15, G4_BM>), grid, dim3(G4_THREADS), 0, st, g);
         } else if (g.a.type == 14) {
             if (sm) hipLaunchKernelGGL((k_g4_store<14, G4_BM_SMALL>), grid, dim3(G4_THREADS), 0, st, g);
             else hipLaunchKernelGGL((k_g4_store<14, G4_BM>), grid, dim3(G4_THREADS), 0, st, g);

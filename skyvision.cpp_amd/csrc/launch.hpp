@@ -26,6 +26,10 @@ int launch_quantize(int type, const float *src, void *dst, int64_t nblocks, hipS
 // dst = n_mat Q4_K matrices of rows (a multiple of 32) rows of rb bytes in
 // the tiled order of the grouped GEMMs (G2Args::tiled); 16-byte aligned
 int launch_tile_q4k(const void *src, void *dst, int64_t n_mat, int64_t rows, int64_t rb, hipStream_t st);
+// dst = n_mat Q6_K matrices of rows (a multiple of 32) rows of rb bytes in
+// the down GEMM's tiled order (9216 bytes per 32-row group and block)
+int launch_tile_q6k(const void *src, void *dst, int64_t n_mat, int64_t rows, int64_t rb, hipStream_t st);
+constexpr int Q6X_ROW_BYTES = 288;   // bytes per 256 values of a row in the Q6_K tiled order
 // y = x / sqrt(mean(x^2) + eps) per row of D (x may equal y)
 int launch_rmsnorm(const float *x, int64_t T, int D, float eps, float *y, hipStream_t st);
 // y = norm(x) per row of D <= 4096 (norm.hpp; x may equal y)
@@ -194,9 +198,10 @@ struct G2Args {
     // pointers above are then not read
     const int32_t *ids;
     int nids, n_expert;
-    // 1: a (and b) hold Q4_K tables in the tiled order (launch_tile_q4k):
-    // the 32 rows of a column tile give block b as 4608 contiguous bytes,
-    // the LDS image of one column tile's weight loads
+    // 1: a (and b) hold tables in the tiled order (launch_tile_q4k: the 32
+    // rows of a column tile give block b as 4608 contiguous bytes, the LDS
+    // image of one column tile's weight loads; launch_tile_q6k: 9216 bytes,
+    // the merged codes' LDS image and the lanes' fp16 scales)
     int tiled;
     int64_t xrows;        // rows of xh (glu = 1: tokens)
     float *y;

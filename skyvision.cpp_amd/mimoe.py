@@ -95,7 +95,8 @@ SYMBOLS = {
     "mi_mul_mat_id": ([P, C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor),
                        C.POINTER(Tensor), P], C.c_int),
     "mi_quantize": ([P, i32, P, P, i64, i64, P], C.c_int),
-    "mi_moe_tile_q4k": ([P, C.POINTER(Tensor), P, P], C.c_int),
+    "mi_moe_tiled_bytes": ([C.POINTER(Tensor)], i64),
+    "mi_moe_tile": ([P, C.POINTER(Tensor), P, C.POINTER(Tensor), P], C.c_int),
     "mi_fill_normal": ([P, P, i64, C.c_uint64, C.c_uint64, C.c_float, C.c_float, P], C.c_int),
     "mi_rmsnorm": ([P, P, i64, C.c_int32, C.c_float, P, P], C.c_int),
     "mi_norm": ([P, C.POINTER(Norm), P, i64, C.c_int32, P, P], C.c_int),
@@ -353,9 +354,11 @@ class Context:
         return load().mi_quantize(self.h, type_, _addr(src), _addr(dst), nrows, n_per_row,
                                   _addr(stream))
 
-    def tile_q4k(self, src: Tensor, dst, stream=None) -> int:
-        """dst = src (a Q4_K table) in the grouped GEMMs' tiled order."""
-        return load().mi_moe_tile_q4k(self.h, C.byref(src), _addr(dst), _addr(stream))
+    def tile(self, src: Tensor, dst, desc: Tensor | None = None, stream=None) -> int:
+        """dst = src (a Q4_K or Q6_K table) in the grouped GEMMs' tiled order;
+        desc (if given) receives the copy's descriptor."""
+        return load().mi_moe_tile(self.h, C.byref(src), _addr(dst), C.byref(desc) if desc is not None else None,
+                                  _addr(stream))
 
     def fill_normal(self, dst, n: int, seed: int, stream_id: int, mean: float, std: float,
                     stream=None) -> int:
@@ -490,6 +493,11 @@ class Event:
         ms = C.c_float()
         call("mi_event_elapsed_ms", C.byref(ms), self.h, end.h)
         return ms.value
+
+
+def tiled_bytes(src: Tensor) -> int:
+    """bytes of src's tiled copy (negative: an mi_moe_status)"""
+    return load().mi_moe_tiled_bytes(C.byref(src))
 
 
 def make_layer(D: int, E: int, K: int, I: int, router_w, router_b, gate: Tensor, up: Tensor | None,

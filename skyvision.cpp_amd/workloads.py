@@ -137,24 +137,27 @@ class GpuLayer:
             self.tensor("gate"), self.tensor("up") if "up" in self.tables else None,
             self.tensor("down"), spec.fused, spec.act)
 
-    def add_tiled(self, ctx: M.Context) -> None:
-        """Tiled copies of the Q4_K tables (mi_moe_tile_q4k) attached to the
-        layer descriptor, for the grouped GEMMs to read."""
+    def add_tiled(self, ctx: M.Context, q6k: bool = True) -> None:
+        """Tiled copies (mi_moe_tile) of the Q4_K tables and, with q6k, of a
+        Q6_K down table, attached to the layer descriptor for the grouped
+        GEMMs to read."""
         self.tiled = {}
         for nm, (q, ttype, Kin, N) in self.tables.items():
-            if ttype != M.TYPE_Q4_K:
+            if ttype != M.TYPE_Q4_K and not (q6k and nm == "down" and ttype == M.TYPE_Q6_K):
                 continue
-            dst = M.DeviceBuffer(q.nbytes)
-            M.check("mi_moe_tile_q4k", ctx.tile_q4k(self.tensor(nm), dst))
-            self.tiled[nm] = dst
+            src = self.tensor(nm)
+            dst = M.DeviceBuffer(M.tiled_bytes(src))
+            desc = M.Tensor()
+            M.check("mi_moe_tile", ctx.tile(src, dst, desc))
+            desc._buf = dst
+            self.tiled[nm] = desc
         M.synchronize()
         self.use_tiled(True)
 
     def use_tiled(self, on: bool) -> None:
         """Point the descriptor's tiled fields at the copies (on) or at none."""
-        for nm, dst in getattr(self, "tiled", {}).items():
-            q, ttype, Kin, N = self.tables[nm]
-            setattr(self.layer, nm + "_tiled", M.tensor(dst, ttype, [Kin, N, self.spec.E]) if on else M.Tensor())
+        for nm, desc in getattr(self, "tiled", {}).items():
+            setattr(self.layer, nm + "_tiled", desc if on else M.Tensor())
 
     def tensor(self, nm: str) -> M.Tensor:
         q, ttype, Kin, N = self.tables[nm]

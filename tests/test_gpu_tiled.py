@@ -1,16 +1,19 @@
-"""Tiled copies of the Q4_K expert tables (mi_moe_tile_q4k) through the C ABI.
+"""Tiled copies of the expert tables (mi_moe_tile) through the C ABI.
 
-The copy holds the table's bytes in the grouped GEMMs' order: for every
-matrix and every 32-row group, block b of the group's 32 rows as 4608
-contiguous bytes, then block b + 1.  A layer that carries the copies
+Q4_K: the table's bytes in the grouped GEMMs' order (for every matrix and
+every 32-row group, block b of the group's 32 rows as 4608 contiguous bytes,
+then block b + 1).  Q6_K (down tables): per 32-row group and block, 8 KB of
+the 6-bit codes merged into bytes in the order the GEMM's lanes take them
+and 1 KB of fp16 d * scale.  A layer that carries the copies
 (mi_moe_layer.gate_tiled / up_tiled / down_tiled) has its grouped GEMMs read
-them, with the same LDS image per column tile as the rows give, so the
-forward must equal the one without copies bit for bit; the oracle bounds
-both (rel-L2 <= 1e-2).
+them, building the same fp16 operands as from the rows, so the forward must
+equal the one without copies bit for bit; the oracle bounds both (rel-L2 <=
+1e-2).
 
-Bars: the layout equals a numpy reorder of the source bytes exactly; the
-forward with copies is bit-identical to the forward without; the argument
-checks return the documented status codes.
+Bars: the layouts equal numpy models of them exactly (the Q6_K model
+decodes the codes from the block fields, the copy must match); the forward
+with copies is bit-identical to the forward without; the argument checks
+return the documented status codes.
 """
 import sys
 
@@ -20,6 +23,7 @@ import pytest
 import mimoe as M
 import pyoracle as O
 import workloads as W
+from _tiled_model import np_tiled, np_tiled_q6k
 from _util import max_abs, oracle_layer_dict, rel_l2
 
 pytestmark = pytest.mark.gpu
@@ -32,26 +36,51 @@ def log(*a):
     sys.stdout.flush()
 
 
-def np_tiled(src: np.ndarray) -> np.ndarray:
-    """src: [E, N, row bytes] of Q4_K rows -> the tiled byte order"""
-    E, N, rb = src.shape
-    nb = rb // 144
-    return src.reshape(E, N // 32, 32, nb, 144).transpose(0, 1, 3, 2, 4).reshape(E, N, rb)
-
-
 @pytest.mark.parametrize("E,N,K", [(1, 32, 256), (3, 64, 512), (5, 96, 2048), (2, 768, 2048)])
 def test_tile_layout(E, N, K):
-    log(f"tile layout E={E} N={N} K={K}")
+    log(f"tile layout Q4_K E={E} N={N} K={K}")
     rb = M.row_size(M.TYPE_Q4_K, K)
     rng = np.random.default_rng(E * 1000 + N + K)
     src = rng.integers(0, 256, size=(E, N, rb), dtype=np.uint8)
     ctx = M.Context(0)
     s = M.to_device(src)
+    t = M.tensor(s, M.TYPE_Q4_K, [K, N, E])
+    assert M.tiled_bytes(t) == src.nbytes
     d = M.DeviceBuffer(src.nbytes).zero()
-    M.check("mi_moe_tile_q4k", ctx.tile_q4k(M.tensor(s, M.TYPE_Q4_K, [K, N, E]), d))
+    desc = M.Tensor()
+    M.check("mi_moe_tile", ctx.tile(t, d, desc))
     M.synchronize()
     got = d.download(np.uint8, (E, N, rb))
     assert np.array_equal(got, np_tiled(src))
+    assert desc.data == d.addr and desc.type == M.TYPE_Q4_K and list(desc.ne) == [K, N, E, 1]
+    assert list(desc.nb)[:3] == [144, rb, rb * N]
+    ctx.close()
+
+
+@pytest.mark.parametrize("E,N,K,off", [(1, 32, 256, 0), (2, 64, 1024, 2), (3, 96, 512, 4)])
+def test_tile_layout_q6k(E, N, K, off):
+    """random blocks with finite d (the scale chunk compares fp16 bits); off:
+    the table starts 2 / 4 bytes into its buffer (Q6_K rows are 2-byte aligned)"""
+    log(f"tile layout Q6_K E={E} N={N} K={K} offset {off}")
+    rb = M.row_size(M.TYPE_Q6_K, K)
+    rng = np.random.default_rng(E * 100 + N + K)
+    src = rng.integers(0, 256, size=(E, N, rb // 210, 210), dtype=np.uint8)
+    src[..., 208:210] = rng.uniform(-0.01, 0.01, size=src.shape[:-1] + (1,)).astype(np.float16).view(np.uint8)
+    src = src.reshape(E, N, rb)
+    ctx = M.Context(0)
+    buf = M.DeviceBuffer(src.nbytes + 16)
+    buf.upload(src, offset=off)
+    t = M.tensor(buf, M.TYPE_Q6_K, [K, N, E], offset=off)
+    nbytes = M.tiled_bytes(t)
+    assert nbytes == E * N * (K // 256) * 288
+    d = M.DeviceBuffer(nbytes).zero()
+    desc = M.Tensor()
+    M.check("mi_moe_tile", ctx.tile(t, d, desc))
+    M.synchronize()
+    got = d.download(np.uint8, (E, N // 32, K // 256, 9216))
+    want = np_tiled_q6k(src)
+    assert np.array_equal(got, want)
+    assert list(desc.nb)[:3] == [288, 288 * (K // 256), 288 * (K // 256) * N]
     ctx.close()
 
 
@@ -60,20 +89,24 @@ def test_tile_rejects():
     K, N, E = 512, 64, 2
     rb = M.row_size(M.TYPE_Q4_K, K)
     s = M.DeviceBuffer(rb * N * E)
-    d = M.DeviceBuffer(rb * N * E)
-    assert ctx.tile_q4k(M.tensor(s, M.TYPE_Q6_K, [K, N, E]), d) == M.ERR_TYPE
-    assert ctx.tile_q4k(M.tensor(s, M.TYPE_Q4_K, [K, 48, E]), d) == M.ERR_SHAPE      # not whole 32-row groups
+    d = M.DeviceBuffer(2 * rb * N * E)
+    assert ctx.tile(M.tensor(s, M.TYPE_Q8_0, [K, N, E]), d) == M.ERR_TYPE
+    assert M.tiled_bytes(M.tensor(s, M.TYPE_F32, [K, N, E])) == M.ERR_TYPE
+    assert ctx.tile(M.tensor(s, M.TYPE_Q4_K, [K, 48, E]), d) == M.ERR_SHAPE      # not whole 32-row groups
     padded = M.tensor(s, M.TYPE_Q4_K, [K, 32, E], nb=[144, rb, rb * 64, rb * 64 * E])
-    assert ctx.tile_q4k(padded, d) == M.ERR_SHAPE                                   # gap between matrices
-    assert ctx.tile_q4k(M.tensor(s, M.TYPE_Q4_K, [K, N, E]), s) == M.ERR_ARG        # in place
-    assert ctx.tile_q4k(M.tensor(s, M.TYPE_Q4_K, [K, N, E]), d.addr + 8) == M.ERR_UNSUPPORTED
+    assert ctx.tile(padded, d) == M.ERR_SHAPE                                   # gap between matrices
+    assert ctx.tile(M.tensor(s, M.TYPE_Q4_K, [K, N, E]), s) == M.ERR_ARG        # in place
+    assert ctx.tile(M.tensor(s, M.TYPE_Q4_K, [K, N, E]), d.addr + 8) == M.ERR_UNSUPPORTED
+    assert ctx.tile(M.tensor(s, M.TYPE_Q4_K, [K, N, E], offset=4), d) == M.ERR_UNSUPPORTED
+    q6 = M.tensor(s, M.TYPE_Q6_K, [K, N // 2, E])
+    assert ctx.tile(q6, s.addr + 16) == M.ERR_ARG                               # the copy overlaps its source
     ctx.close()
 
 
 # (name, config, T, chain, GEMM tiles: 0 by shape, 3 the skinny 16-row products)
 CASES = ([("qo", 3, 8, True, 0)] + [("qo", 3, T, False, 0) for T in (32, 64, 300)]
          + [("md_q4", 0, T, False, 0) for T in (16, 64, 1024)]
-         + [("md_q6down", 1, T, False, 0) for T in (64, 1024)]
+         + [("md_q6down", 1, T, False, 0) for T in (64, 300, 1024)] + [("md_q6down_skew", 2, 1024, False, 0)]
          + [("qo_skinny", 3, T, True, 3) for T in (8, 32, 64)] + [("md_q4_skinny", 0, 40, True, 3)])
 
 
@@ -124,10 +157,13 @@ def test_layer_tiled_checks():
     assert ctx.forward(g.layer, x, T, None, out) == M.ERR_ARG
     g.layer.up_tiled = keep
     q, ttype, Kin, N = g.tables["down"]
-    g.layer.down_tiled = M.tensor(g.tiled["down"], ttype, [Kin, N // 2, spec.E])   # other shape than down
+    dbuf = g.tiled["down"]._buf
+    g.layer.down_tiled = M.tensor(dbuf, ttype, [Kin, N // 2, spec.E])   # other shape than down
     assert ctx.forward(g.layer, x, T, None, out) == M.ERR_SHAPE
-    g.layer.down_tiled = M.tensor(g.tiled["down"], M.TYPE_Q6_K, [Kin, N, spec.E])
+    g.layer.down_tiled = M.tensor(dbuf, M.TYPE_Q6_K, [Kin, N, spec.E])   # other type than down
     assert ctx.forward(g.layer, x, T, None, out) == M.ERR_TYPE
-    g.layer.down_tiled = M.tensor(g.tiled["down"], ttype, [Kin, N, spec.E])
+    g.layer.down_tiled = M.tensor(dbuf, ttype, [Kin, N, spec.E])
     M.check("forward", ctx.forward(g.layer, x, T, None, out))
+    g.layer.gate_tiled = M.tensor(dbuf, M.TYPE_Q6_K, [spec.D, spec.I, spec.E])   # Q6_K copies: down only
+    assert ctx.forward(g.layer, x, T, None, out) == M.ERR_TYPE
     ctx.close()

@@ -6,10 +6,10 @@ step = one full layer forward (router -> top-k -> dispatch -> gate/up GEMM +
 GeGLU -> Q8_K -> down GEMM -> weighted combine) over the 1024 tokens, with
 the inputs resident in HBM.  Steps rotate over --copies distinct layer copies
 so the 256 MB Infinity Cache cannot hold the weights between steps.  Each
-layer carries tiled copies of its Q4_K tables (mi_moe_tile_q4k, made when
-the layer is built, outside the timed region), which the grouped GEMMs read
-in place of the GGUF rows (same bytes, reordered; bit-identical output);
---no-tiled runs on the GGUF rows alone.
+layer carries tiled copies of its tables (mi_moe_tile: Q4_K reordered, Q6_K
+down with merged codes; made when the layer is built, outside the timed
+region), which the grouped GEMMs read in place of the GGUF rows
+(bit-identical output); --no-tiled runs on the GGUF rows alone.
 
 Printed JSON line (rank 0):
   value          tokens/s of the whole layer (T * steps / time); the K forwards
@@ -266,8 +266,8 @@ def host_cpu() -> str:
 
 
 def make_layers(ctx, spec, n: int, tiled: bool) -> list:
-    """n seeded layer copies; tiled: with tiled copies of their Q4_K tables
-    (mi_moe_tile_q4k, made at load time, outside every timed region) for the
+    """n seeded layer copies; tiled: with tiled copies of their tables
+    (mi_moe_tile, made at load time, outside every timed region) for the
     grouped GEMMs to read."""
     layers = [W.GpuLayer(ctx, spec, copy=c) for c in range(n)]
     if tiled:
@@ -276,7 +276,8 @@ def make_layers(ctx, spec, n: int, tiled: bool) -> list:
     return layers
 
 
-TABLES_TILED = "GGUF rows + tiled copies of the Q4_K tables (mi_moe_tile_q4k) for the grouped GEMMs"
+TABLES_TILED = ("GGUF tables + tiled copies (mi_moe_tile: Q4_K gate/up/down, Q6_K down) read by the grouped "
+                "GEMMs, made at load time")
 TABLES_ROWS = "GGUF rows only"
 
 

@@ -242,7 +242,8 @@ Tensor *build_expert_ffn(Session &s, Tensor *x, const std::vector<Tensor *> &gat
 namespace vqa {
 namespace moe {
 
-GraphB::GraphB(int device, const mi_moe_layer &layer, int64_t max_tokens) : layer_(layer), cap_T_(max_tokens) {
+GraphB::GraphB(int device, const mi_moe_layer &layer, int64_t max_tokens, bool tiled)
+    : layer_(layer), cap_T_(max_tokens) {
     const int64_t D = layer.n_embd, K = layer.n_expert_used;
     if (max_tokens <= 0 || D <= 0 || K <= 0) {
         fail(MI_MOE_ERR_SHAPE);
@@ -257,12 +258,40 @@ GraphB::GraphB(int device, const mi_moe_layer &layer, int64_t max_tokens) : laye
         fail(mi_dev_malloc((void **)&d_out_, rows)) || fail(mi_dev_malloc((void **)&d_w_, route)) ||
         fail(mi_dev_malloc((void **)&d_ids_, route)))
         return;
+    if (tiled) attach_tiled();
+}
+
+// Tiled copies of the tables the library takes them for (Q4_K gate / up, a
+// fused [h | g] table with n_ff a multiple of 32, Q4_K or Q6_K down; whole
+// 32-row groups): made on this object's stream, so every later call sees
+// them complete.  A table that does not qualify, or whose copy fails, stays
+// untiled (the status is not touched: the layer runs either way).
+void GraphB::attach_tiled() {
+    auto tile = [&](const mi_tensor &t, mi_tensor &slot) {
+        const int64_t n = mi_moe_tiled_bytes(&t);
+        void *buf = nullptr;
+        if (n <= 0 || mi_dev_malloc(&buf, (size_t)n) != MI_MOE_OK) return false;
+        if (mi_moe_tile(ctx_, &t, buf, &slot, stream_) != MI_MOE_OK) {
+            (void)mi_dev_free(buf);
+            slot = mi_tensor{};
+            return false;
+        }
+        tiled_.push_back(buf);
+        return true;
+    };
+    const bool gated = layer_.act != MI_ACT_RELU_SQR, sep = gated && !layer_.fused_gate_up;
+    const bool gate_ok = layer_.gate.type == MI_TYPE_Q4_K && (!sep || layer_.up.type == MI_TYPE_Q4_K) &&
+                         !(gated && layer_.fused_gate_up && layer_.n_ff % 32);
+    if (gate_ok && tile(layer_.gate, layer_.gate_tiled) && sep && !tile(layer_.up, layer_.up_tiled))
+        layer_.gate_tiled = mi_tensor{};   // both or neither (its buffer is freed with the others)
+    (void)tile(layer_.down, layer_.down_tiled);
 }
 
 GraphB::~GraphB() {
     if (stream_) (void)mi_stream_synchronize(stream_);
     for (void *p : {(void *)d_in_, (void *)d_xmid_, (void *)d_out_, (void *)d_w_, (void *)d_ids_})
         if (p) (void)mi_dev_free(p);
+    for (void *p : tiled_) (void)mi_dev_free(p);
     if (stream_) (void)mi_stream_destroy(stream_);
     mi_moe_ctx_destroy(ctx_);
 }
@@ -530,6 +559,27 @@ int main(int argc, char **argv) {
         CHECK(std::memcmp(got.data(), want_o.data(), sizeof(float) * T * D) == 0, "graphb == mi_moe_forward");
         std::fprintf(stderr, "graphb q4_k layer: %s mi_moe_forward\n",
                      std::memcmp(got.data(), want_o.data(), sizeof(float) * T * D) ? "differs from" : "bit-identical to");
+        // with tiled copies of the tables: 40 rows (past the batched decode
+        // kernel's 16, so the grouped GEMMs run and read the copies)
+        const int T2 = 40;
+        float *xd2 = nullptr, *od2 = nullptr;
+        bool ok2 = mi_dev_malloc((void **)&xd2, sizeof(float) * T2 * D) == 0 &&
+                   mi_dev_malloc((void **)&od2, sizeof(float) * T2 * D) == 0 &&
+                   mi_moe_ctx_reserve(c, T2, D, I, E, K) == 0 &&
+                   mi_fill_normal(c, xd2, (int64_t)T2 * D, 7, 5, 0.f, 1.f, s.stream()) == 0 &&
+                   mi_moe_forward(c, &L, xd2, T2, xd2, od2, nullptr, s.stream()) == 0 && s.compute() == 0;
+        std::vector<float> x2(T2 * D), want2(T2 * D), got2(T2 * D);
+        ok2 = ok2 && mi_memcpy_d2h(x2.data(), xd2, sizeof(float) * T2 * D) == 0 &&
+              mi_memcpy_d2h(want2.data(), od2, sizeof(float) * T2 * D) == 0;
+        CHECK(ok2, "graphb tiled setup");
+        vqa::moe::GraphB gbt(0, L, T2, true);
+        CHECK(gbt.status() == 0 && gbt.feed(x2.data(), x2.data(), T2) == 0 && gbt.compute(got2.data()) == 0,
+              "graphb tiled");
+        CHECK(std::memcmp(got2.data(), want2.data(), sizeof(float) * T2 * D) == 0, "graphb tiled == mi_moe_forward");
+        std::fprintf(stderr, "graphb q4_k layer with tiled copies, %d rows: %s mi_moe_forward\n", T2,
+                     std::memcmp(got2.data(), want2.data(), sizeof(float) * T2 * D) ? "differs from" : "bit-identical to");
+        for (void *p : {(void *)xd2, (void *)od2})
+            if (p) mi_dev_free(p);
         for (void *p : {(void *)tmp, (void *)rw, (void *)xd, (void *)od, gq, dq})
             if (p) mi_dev_free(p);
     }

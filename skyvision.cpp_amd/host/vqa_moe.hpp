@@ -110,8 +110,10 @@ Tensor *build_expert_ffn_table(Session &s, Tensor *x, Tensor *gate_table, Tensor
 class GraphB {
 public:
     // layer: device tables of one MoE layer (mi_gguf_load_moe_layer, or built
-    // by the caller); max_tokens: rows per step
-    GraphB(int device, const mi_moe_layer &layer, int64_t max_tokens);
+    // by the caller); max_tokens: rows per step; tiled: also make and attach
+    // tiled copies of the tables that allow them (mi_moe_tile; owned by this
+    // object, the output stays bit-identical)
+    GraphB(int device, const mi_moe_layer &layer, int64_t max_tokens, bool tiled = false);
     ~GraphB();
     GraphB(const GraphB &) = delete;
     GraphB &operator=(const GraphB &) = delete;
@@ -127,7 +129,9 @@ public:
 
 private:
     int fail(int rc);
+    void attach_tiled();
     mi_moe_layer layer_{};
+    std::vector<void *> tiled_;   // the tiled copies' device buffers
     mi_moe_ctx *ctx_ = nullptr;
     mi_stream_t stream_ = nullptr;
     int64_t cap_T_ = 0, T_ = 0;

@@ -10,7 +10,8 @@ the per-slot and slot-table forms, the residual split, and the nullptr
 returns of the argument checks; and vqa::moe::GraphB, the decode driver's
 graph B (Hooks::build_b / feed_b, moe_decode_driver.hpp:125-144): the same
 known answer with the driver's routing, and a Q4_K layer routing its own
-rows bit-identical to mi_moe_forward."""
+rows bit-identical to mi_moe_forward, also with tiled copies of its tables
+(GraphB's tiled option, 40 rows: the grouped GEMMs read the copies)."""
 import pathlib
 import re
 import subprocess
@@ -61,3 +62,4 @@ def test_selftest_runs_on_gpu():
     assert m, r.stderr
     assert abs(float(m.group(1)) - 3.6423913) < 1e-5 and abs(float(m.group(2)) - 4.1931758) < 1e-5
     assert "graphb q4_k layer: bit-identical to mi_moe_forward" in r.stderr
+    assert "graphb q4_k layer with tiled copies, 40 rows: bit-identical to mi_moe_forward" in r.stderr

@@ -195,17 +195,22 @@ def test_config4_stack_and_fed_back_decode():
     ctx.close()
 
 
-@pytest.mark.parametrize("name,T", [("qo_cfg3", 32), ("qo_cfg3", 64), ("md_cfg1", 300), ("md_cfg1", 40)])
+@pytest.mark.parametrize("name,T", [("qo_cfg3", 32), ("qo_cfg3", 64), ("md_cfg1", 300), ("md_cfg1", 40),
+                                    ("qo_cfg3_tiled", 8), ("qo_cfg3_tiled", 16), ("qo_cfg3_tiled", 64),
+                                    ("md_cfg1_tiled", 24), ("md_cfg1_tiled", 64)])
 def test_gemm_row_tiles(name, T):
     """Both row-tile sizes of the 4-wave GEMMs at one size: 32-row tiles (two
-    work-groups per CU; the default up to 8 dispatched rows per expert) and
-    192-row balanced tiles give the same bits (each output's K order is the
-    same), and match the oracle."""
-    spec = W.CONFIGS[3]["spec"] if name == "qo_cfg3" else W.CONFIGS[1]["spec"]
+    or three work-groups per CU; the default up to 8 dispatched rows per
+    expert) and 192-row balanced tiles give the same bits (each output's K
+    order is the same), and match the oracle.  `_tiled`: the layers carry
+    tiled copies of their tables."""
+    spec = W.CONFIGS[3]["spec"] if name.startswith("qo_cfg3") else W.CONFIGS[1]["spec"]
     log(f"case {name} T={T} row tiles 32 / 192")
     ctx = M.Context(0)
     ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
     g = W.GpuLayer(ctx, spec)
+    if name.endswith("_tiled"):
+        g.add_tiled(ctx)
     x = W.gen_x(ctx, spec, T)
     xh = x.download(np.float32, (T, spec.D))
     ref, dbg = O.moe_forward(_oracle_dict(g), xh)

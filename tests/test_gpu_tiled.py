@@ -24,7 +24,7 @@ import mimoe as M
 import pyoracle as O
 import workloads as W
 from _tiled_model import np_tiled, np_tiled_q6k
-from _util import max_abs, oracle_layer_dict, rel_l2
+from _util import max_abs, oracle_layer_dict, rel_l2, small_spec
 
 pytestmark = pytest.mark.gpu
 
@@ -166,4 +166,34 @@ def test_layer_tiled_checks():
     M.check("forward", ctx.forward(g.layer, x, T, None, out))
     g.layer.gate_tiled = M.tensor(dbuf, M.TYPE_Q6_K, [spec.D, spec.I, spec.E])   # Q6_K copies: down only
     assert ctx.forward(g.layer, x, T, None, out) == M.ERR_TYPE
+    ctx.close()
+
+
+@pytest.mark.parametrize("down_type", [M.TYPE_Q4_K, M.TYPE_Q6_K], ids=["q4k_down", "q6k_down"])
+def test_expert_ffn_tiled_bit_identical(down_type):
+    """The table form (caller's ids, gate/up and down ids different) on the
+    grouped GEMMs reads the copies too: bit-identical to the rows."""
+    spec = small_spec(f"tiled_tbl_{down_type}", D=512, E=8, K=3, I=256, fused=False, down_type=down_type,
+                      act=O.ACT_SILU, seed=0x5EED3200 + down_type)
+    T = 96
+    ctx = M.Context(0)
+    ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
+    ctx.set_gemm_threshold(1)
+    g = W.GpuLayer(ctx, spec)
+    rng = np.random.default_rng(down_type)
+    x = M.to_device(rng.standard_normal((T, spec.D)).astype(np.float32))
+    res = M.to_device(rng.standard_normal((T, spec.D)).astype(np.float32))
+    gu = M.to_device(rng.integers(0, spec.E, size=(T, spec.K)).astype(np.int32))
+    dn = M.to_device(rng.integers(0, spec.E, size=(T, spec.K)).astype(np.int32))
+    w = M.to_device(rng.random((T, spec.K)).astype(np.float32))
+    outs = []
+    for tiled in (False, True):
+        if tiled:
+            g.add_tiled(ctx)
+            assert set(g.tiled) == {"gate", "up", "down"}
+        out = M.DeviceBuffer(4 * T * spec.D)
+        M.check("expert_ffn", ctx.expert_ffn(g.layer, x, T, res, gu, dn, w, out))
+        outs.append(out.download(np.float32, (T, spec.D)))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    log(f"expert_ffn down type {down_type}: tiled bit-identical")
     ctx.close()

@@ -182,8 +182,8 @@ def gpu_reference(ctx, layer, x, T) -> dict:
 
 
 def parity_columns(gpu: dict, ref: np.ndarray, dbg: dict) -> dict:
-    """BASELINE.md's parity columns: routing bit-exactness and the output's
-    rel-L2 / max-abs against the CPU oracle on the same tokens."""
+    """The parity columns of the benchmark: routing bit-exactness and the
+    output's rel-L2 / max-abs against the CPU oracle on the same tokens."""
     exact = {k: bool(np.array_equal(gpu[k], dbg[k])) for k in ("sel", "counts", "offsets", "perm")}
     exact["logits"] = bool(np.array_equal(gpu["logits"].view(np.uint32), dbg["logits"].view(np.uint32)))
     d = (gpu["out"].astype(np.float64) - ref.astype(np.float64)).ravel()

@@ -197,3 +197,42 @@ def test_expert_ffn_tiled_bit_identical(down_type):
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
     log(f"expert_ffn down type {down_type}: tiled bit-identical")
     ctx.close()
+
+
+EDGE = [  # (name, D, E, K, I, fused, down type, T)
+    ("e256_k8", 512, 256, 8, 256, False, M.TYPE_Q4_K, 40),
+    ("e256_k16", 512, 256, 16, 256, False, M.TYPE_Q4_K, 300),
+    ("d256_fused_q6", 256, 16, 4, 256, True, M.TYPE_Q6_K, 96),
+    ("d256_fused_q6_small", 256, 16, 4, 256, True, M.TYPE_Q6_K, 5),
+]
+
+
+@pytest.mark.parametrize("name,D,E,K,I,fused,dt,T", EDGE, ids=[e[0] for e in EDGE])
+def test_tiled_edge_shapes(name, D, E, K, I, fused, dt, T):
+    """Tiled copies at the widest router (E = 256, K up to 16) and at rows
+    of one 256-value block (D = 256: one Q4_K / Q6_K block per row, the
+    tile's block stride is the whole group), on the kernel chain: the output
+    equals the rows' bit for bit and the oracle's to 1e-2."""
+    spec = W.LayerSpec(name, D, E, K, I, fused, M.TYPE_Q4_K, dt, M.ACT_SILU if not fused else M.ACT_GELU_ERF_GP1,
+                       "none", 0x5EED7400 + E + K + D)
+    log(f"case {name} T={T}")
+    ctx = M.Context(0)
+    ctx.reserve(T, spec.D, spec.I, spec.E, spec.K)
+    ctx.set_fused_decode(M.DECODE_CHAIN)
+    ctx.set_gemm_threshold(1)
+    g = W.GpuLayer(ctx, spec)
+    x = W.gen_x(ctx, spec, T, copy=5)
+    outs = []
+    for tiled in (False, True):
+        if tiled:
+            g.add_tiled(ctx)
+        out = M.DeviceBuffer(4 * T * spec.D)
+        M.check("forward", ctx.forward(g.layer, x, T, None, out))
+        outs.append(out.download(np.float32, (T, spec.D)))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), name
+    OL = oracle_layer_dict(g.download_tables(), g.spec, g.download_router(), g.bias_host)
+    ref, _ = O.moe_forward(OL, x.download(np.float32, (T, spec.D)))
+    e = rel_l2(outs[1], ref)
+    log(f"{name} T={T}: tiled bit-identical; rel-L2 {e:.3e} max-abs {max_abs(outs[1], ref):.3e}")
+    assert e <= TOL
+    ctx.close()

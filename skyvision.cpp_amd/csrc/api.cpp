@@ -689,15 +689,23 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         if (!gs) prof_clock(c, a, 0);   // (the skinny kernels record no clocks)
         TRY(gs ? launch_gemm_gs(a, gs_splits(c, rows, E, gated ? I : a.ncols, a.glu), st) : launch_gemm4(a, st));
         stage_end(c, "gate_up", st);
+        // the 32-row down product quantizes its own rows (gated: fp16 GLU rows)
+        const bool own_q8 = bm == G4_BM_SMALL && !gs && gated;
         Q8Out qa;
         qa.xh = c->aact.h; qa.wtype = down.type; qa.order = 1; qa.pre_act = gated ? 0 : MI_ACT_RELU_SQR;
         qa.range_total = c->range_total;
-        if (gated) TRY(launch_q8k_rows((const _Float16 *)c->f1, I, rows, I, qa, st));
-        else TRY(launch_q8k_rows(c->f1, I, rows, I, qa, st));
+        if (own_q8) {
+            // (no pass: the down product's work-groups quantize their rows)
+        } else if (gated) {
+            TRY(launch_q8k_rows((const _Float16 *)c->f1, I, rows, I, qa, st));
+        } else {
+            TRY(launch_q8k_rows(c->f1, I, rows, I, qa, st));
+        }
         stage_end(c, "q8k_act", st);
         G2Args d = {};
         d.a = down; d.glu = 0; d.xh = c->aact.h; d.ne11 = K; d.K = K;
         if (L->down_tiled.data) { d.a = as_mat(L->down_tiled); d.tiled = 1; }
+        if (own_q8) { d.q8src = (const _Float16 *)c->f1; d.q8ld = I; }
         d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
         d.tile_r0 = dd.tile_r0; d.tile_start = dd.tile_start; d.tile_rows = dd.tile_rows; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles; d.xrows = (int64_t)T * K;
         d.tile_perm = dd.tile_perm;

@@ -39,6 +39,7 @@
 #include "act.hpp"
 #include "common.hpp"
 #include "launch.hpp"
+#include "q8h.hpp"
 #include "wave_ops.hpp"
 
 namespace mimoe {
@@ -797,6 +798,35 @@ k_g4_glu(G2Args g) {
     g4_clock(g, 1, true);
 }
 
+// The Q8_K of the tile's activation rows (G2Args::q8src), made by the
+// work-group before its K loop: one wave per (row, 4 blocks), 16 lanes per
+// block (q8h.hpp, the code of the separate pass), written to xh, then every
+// wave's stores out before the first activation loads.  Every column tile of
+// the row tile writes the same bits.
+template <int XO>
+__device__ __forceinline__ void g4_q8_rows(const G2Args &g, int mrows, const int *s_arow, bool count, int wave,
+                                           int lane) {
+    const int nb = (int)(g.a.K / QK), ngrp = (nb + 3) >> 2;
+    const int bl = lane >> 4, s = lane & 15;
+    _Float16 *xh = const_cast<_Float16 *>(g.xh);
+    for (int item = wave; item < mrows * ngrp; item += G4_WAVES) {   // (uniform per wave: DPP inside)
+        const int r = item / ngrp, grp = item - r * ngrp;
+        const int b = 4 * grp + bl;
+        const bool bok = b < nb;
+        const int64_t p = s_arow[r];
+        float v[16];
+        if (bok) {
+            q8h_gather<XO>(g.q8src + p * g.q8ld + (int64_t)b * QK, s, v);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = 0.f;
+        }
+        q8h_quant_store(v, bok, xh + p * (int64_t)nb * QK + (int64_t)b * QK, s, count ? g.range_total : nullptr);
+    }
+    vm_drain();       // this wave's rows are out (block 0's weight loads are in too)
+    __syncthreads();  // every wave's rows before any activation load
+}
+
 // ------------------------------------------------------------------ STORE
 // y[p][n] = sum_k x[p][k] w[n][k] for the tile's rows p; wave w owns weight
 // rows 256 ctile + 64 w + 32 ct + l32 (rows past ncols read zeros past the
@@ -839,6 +869,9 @@ k_g4_store(G2Args g) {
     }
     int *s_arow = (int *)As1;   // as in k_g4_glu
     g4_rows_publish<BM>(g, my_p, s_arow);
+    if constexpr (BM == G4_BM_SMALL) {
+        if (g.q8src) g4_q8_rows<WT == 12 ? XO_Q4 : XO_Q6>(g, t.mrows, s_arow, ctile == 0, wave, lane);
+    }
     // byte offset of the lane's own rows (Q6_K block alignment)
     const uint32_t wsh[2] = {mis + (uint32_t)(n0 + l32) * rb, mis + (uint32_t)(n0 + 32 + l32) * rb};
     f32x16 acc[NA][2];
@@ -919,6 +952,8 @@ int launch_gemm4(const G2Args &g, hipStream_t st) {
     if (g.tiled && g.a.type != 14 && (g.a.type != 12 || g.a.N % 32 || g.a.mat_bytes != g.a.N * g.a.row_bytes ||
                     (g.glu && !g.fused &&
                      (g.b.type != 12 || g.b.N % 32 || g.b.mat_bytes != g.b.N * g.b.row_bytes))))
+        return -6;
+    if (g.q8src && (g.glu || g.bm != G4_BM_SMALL || g.q8ld % 4 || (uintptr_t)g.q8src % 8 || (uintptr_t)g.xh % 16))
         return -6;
     const int ntile8 = (g.max_tiles + 7) / 8;
     if (g.glu) {

@@ -198,6 +198,13 @@ struct G2Args {
     // pointers above are then not read
     const int32_t *ids;
     int nids, n_expert;
+    // or NULL: with bm = G4_BM_SMALL and glu = 0, the activation rows xh of
+    // the tile are first made by its work-groups - the Q8_K of these fp16
+    // rows [.][q8ld] (the down product's GLU rows) in xh's order, the same
+    // bits the separate Q8_K pass writes (work-groups of column tile 0 count
+    // its saturations)
+    const _Float16 *q8src;
+    int64_t q8ld;
     // 1: a (and b) hold tables in the tiled order (launch_tile_q4k: the 32
     // rows of a column tile give block b as 4608 contiguous bytes, the LDS
     // image of one column tile's weight loads; launch_tile_q6k: 9216 bytes,

@@ -396,14 +396,18 @@ int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *ctx, int64_t min_tokens_for_gemm);
 /* Row tiles of the grouped GEMMs of Q4_K gate/up layers: 0 (the default) by
  * shape, 32-row tiles when the call dispatches at most 8 rows per expert on
  * average (qwen3omni up to 128 tokens, moondream3 up to 64: several
- * work-groups per CU keep more of the weight stream in flight), 192-row tiles above; 1
- * 192-row tiles, 2 32-row tiles at every size; 3 the skinny products (16-row
- * tiles, one work-group per CU, the weight stream held in registers a group
- * of blocks ahead) on layers whose tables are all Q4_K with n_embd and n_ff <=
- * 2048 (others take the shape rule).  Kinds 0-2 give the same bits (the same
- * per-row arithmetic); the skinny products sum each output's products in
- * another order (fp32; the rows agree to ~2e-4 rel-L2 after the activations'
- * fp16 and Q8_K roundings). */
+ * work-groups per CU keep more of the weight stream in flight), and within
+ * those 8-row tiles (four work-groups per CU) for the products of Q4_K
+ * tables at most 4 rows per expert on average when the call needs no
+ * dispatch outputs (up to 512 slots); 192-row tiles above; 1 192-row tiles,
+ * 2 32-row tiles at every size; 3 the skinny products (16-row tiles, one
+ * work-group per CU, the weight stream held in registers a group of blocks
+ * ahead) on layers whose tables are all Q4_K with n_embd and n_ff <= 2048
+ * (others take the shape rule); 4 8-row tiles wherever they apply (else
+ * 32-row).  Kinds 0-2 and 4 give the same bits (the same per-row
+ * arithmetic); the skinny products sum each output's products in another
+ * order (fp32; the rows agree to ~2e-4 rel-L2 after the activations' fp16
+ * and Q8_K roundings). */
 int mi_moe_ctx_set_gemm_tiles(mi_moe_ctx *ctx, int kind);
 /* Schedule of decode calls of mi_moe_forward (1 token, and batches of 2..16
  * tokens; for experts of more than 2 MiB, batches that dispatch at most one

@@ -434,8 +434,21 @@ constexpr int64_t G4_SMALL_ROWS = 8;
 // +0.8 us per layer; moondream3 T = 128, half the partials: -3.2 us)
 constexpr int64_t FRONT_SPLIT_TE_MAX = 8192;
 bool g4_small_tiles(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T) {
-    if (c->gemm_tiles == 1 || c->gemm_tiles == 2) return c->gemm_tiles == 2;
+    if (c->gemm_tiles == 1 || c->gemm_tiles == 2 || c->gemm_tiles == 4) return c->gemm_tiles != 1;
     return T * L->n_expert_used <= G4_SMALL_ROWS * L->n_expert;
+}
+// 8-row tiles (G4_BM_TINY) where the 32-row tiles would run without a
+// dispatch launch and a call dispatches at most G4_TINY_ROWS rows per expert
+// on average: 40 KB of LDS with Q4_K weights, four work-groups per CU (a
+// third more of the weight stream in flight than three), at the cost of a
+// second tile (and a second read of the weights) for an expert with more
+// than 8 rows.  Q4_K down tables only for the down product (a Q6_K one
+// keeps 32-row tiles: its LDS allows two work-groups either way).
+constexpr int64_t G4_TINY_ROWS = 4;
+bool g4_tiny_tiles(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T) {
+    if (c->gemm_tiles == 4) return true;
+    if (c->gemm_tiles != 0) return false;
+    return T * L->n_expert_used <= G4_TINY_ROWS * L->n_expert;
 }
 
 // The skinny products (k_gs.hip: 16-row tiles, one work-group per CU, each
@@ -587,6 +600,11 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
     // moondream3 79.3 / 84.3 / 87.9 / 88.5 -> 76.5 / 80.6 / 85.5 / 85.8.
     const bool self_disp = bm == G4_BM_SMALL && !gs && same_ids && !check_ids && !disp_out && rows <= G4_SD_IDS &&
                            E <= 256;
+    // without a dispatch, each product may take 8-row tiles (its own tiles
+    // from the ids; the tile tables are not used)
+    const bool tiny = self_disp && g4_tiny_tiles(c, L, T);
+    const int bm_gu = tiny ? G4_BM_TINY : bm;
+    const int bm_dn = tiny && L->down.type == MI_TYPE_Q4_K ? G4_BM_TINY : bm;
     if (!self_disp) {
         TRY(launch_dispatch(ids_gu, T, K, E, bm, g4, c->disp[0].view(), st));
         if (!same_ids) TRY(launch_dispatch(ids_dn, T, K, E, bm, g4, c->disp[1].view(), st));
@@ -680,8 +698,11 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         a.counts = dg.counts; a.offsets = dg.offsets; a.perm = dg.perm; a.tile_e = dg.tile_e;
         a.tile_r0 = dg.tile_r0; a.tile_start = dg.tile_start; a.tile_rows = dg.tile_rows; a.n_tiles = dg.n_tiles; a.max_tiles = max_tiles;
         a.tile_perm = dg.tile_perm;
-        a.bm = bm;
-        if (self_disp) { a.ids = ids_gu; a.nids = (int)rows; a.n_expert = E; }
+        a.bm = bm_gu;
+        if (self_disp) {
+            a.ids = ids_gu; a.nids = (int)rows; a.n_expert = E;
+            a.max_tiles = (int)((rows + bm_gu - 1) / bm_gu + max_active);
+        }
         a.y = c->f1; a.ldy = I; a.ncols = I; a.xrows = T;
         // gated: the GLU rows as fp16 (half the bytes of their round trip to
         // the Q8_K pass; saturation at the fp16 range is counted)
@@ -690,7 +711,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         TRY(gs ? launch_gemm_gs(a, gs_splits(c, rows, E, gated ? I : a.ncols, a.glu), st) : launch_gemm4(a, st));
         stage_end(c, "gate_up", st);
         // the 32-row down product quantizes its own rows (gated: fp16 GLU rows)
-        const bool own_q8 = bm == G4_BM_SMALL && !gs && gated;
+        const bool own_q8 = bm_dn <= G4_BM_SMALL && !gs && gated;
         Q8Out qa;
         qa.xh = c->aact.h; qa.wtype = down.type; qa.order = 1; qa.pre_act = gated ? 0 : MI_ACT_RELU_SQR;
         qa.range_total = c->range_total;
@@ -709,8 +730,11 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
         d.counts = dd.counts; d.offsets = dd.offsets; d.perm = dd.perm; d.tile_e = dd.tile_e;
         d.tile_r0 = dd.tile_r0; d.tile_start = dd.tile_start; d.tile_rows = dd.tile_rows; d.n_tiles = dd.n_tiles; d.max_tiles = max_tiles; d.xrows = (int64_t)T * K;
         d.tile_perm = dd.tile_perm;
-        d.bm = bm;
-        if (self_disp) { d.ids = ids_dn; d.nids = (int)rows; d.n_expert = E; }
+        d.bm = bm_dn;
+        if (self_disp) {
+            d.ids = ids_dn; d.nids = (int)rows; d.n_expert = E;
+            d.max_tiles = (int)((rows + bm_dn - 1) / bm_dn + max_active);
+        }
         // the slot rows as fp16 (half the bytes of the round trip to the
         // combine; saturation at the fp16 range is counted)
         d.y = c->z; d.yh = zh = (_Float16 *)c->z; d.range_total = c->range_total; d.ldy = D; d.ncols = D;
@@ -985,7 +1009,7 @@ int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *c, int64_t t) {
 
 int mi_moe_ctx_set_gemm_tiles(mi_moe_ctx *c, int kind) {
     if (!c) return MI_MOE_ERR_NULL;
-    if (kind < 0 || kind > 3) return MI_MOE_ERR_ARG;
+    if (kind < 0 || kind > 4) return MI_MOE_ERR_ARG;
     c->gemm_tiles = kind;
     return MI_MOE_OK;
 }

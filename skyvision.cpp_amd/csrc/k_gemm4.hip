@@ -110,8 +110,8 @@ __device__ __forceinline__ G4Tile g4_desc(const G2Args &g, int tile) {
 // order (ballots per wave, wave totals in LDS), rows r0 .. r0 + rows of
 // them.  Thread m < rows returns row m's slot index in p, else -1.
 static_assert(G4_SD_IDS == 2 * G4_THREADS, "two ids per thread");
+template <int BM>
 __device__ __forceinline__ G4Tile g4_self_tile(const G2Args &g, int tile, int *s, int &p) {
-    constexpr int BM = G4_BM_SMALL;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = g.n_expert, n = g.nids;
     int *s_cnt = s;              // [256] rows per expert
@@ -517,6 +517,21 @@ __device__ __forceinline__ void g4_issue_a(rsrc_t rx, const uint32_t (&aoff)[2 *
                                              512 * b + 256 * h, 0, 0);
 }
 
+// tiles of TR < 32 rows (G4_BM_TINY): rows 4 w .. 4 w + 3 by wave w < TR / 4,
+// one load per stage; the operands of rows TR .. 31 read rows r % TR (their
+// products are not stored)
+template <int TR>
+__device__ __forceinline__ uint32_t g4_aoff_tiny(const int *s_arow, int wave, int lane, uint32_t rowbytes) {
+    const int r = imin(4 * wave + (lane >> 4), TR - 1);
+    return (uint32_t)s_arow[r] * rowbytes + 16u * (uint32_t)((lane & 15) ^ (r & 15));
+}
+template <int TR>
+__device__ __forceinline__ void g4_issue_a_tiny(rsrc_t rx, uint32_t off, int wave, _Float16 *st, int b, int h) {
+    if (wave < TR / 4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t *)(st + 4 * wave * G4_SK), 16, (int)off,
+                                                 512 * b + 256 * h, 0, 0);
+}
+
 // activation operand of step sp, row tile rt: lane (l32, g2) reads row
 // 32 rt + l32, K chunk 2 sp + g2, at slot chunk ^ (l32 % 16); abase =
 // 256 l32 + 16 (g2 ^ (l32 % 16)) bytes, so the step's offset is abase ^ 32 sp
@@ -590,16 +605,27 @@ __device__ __forceinline__ void g4_stage(const _Float16 *st, uint32_t abase, con
 // loads cost.
 // Q6_K tiled (WT 15): sn holds the next block's scales (block 0's loaded
 // with its weights); block b + 1's two scale loads follow its weight loads.
-template <int WT, int NRT, int NA>
+template <int WT, int NRT, int NA, int TR = 0>
 __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_t arowbytes, const G4WDma<WT> &dm,
                                            const uint32_t (&wsh)[2], uint8_t *W, int nb, int wave, int lane,
                                            _Float16 *As0, _Float16 *As1, f32x16 (&acc)[NA][2], u32x4 (&sn)[2]) {
     using F = G4Fmt<WT>;
+    static_assert(TR == 0 || NRT == 1, "tiny tiles: one row tile");
     constexpr int NW = 2 * F::NLD, NSL = WT == 15 ? 2 : 0;   // weight loads, scale loads per block
     const int l32 = lane & 31, g2 = lane >> 5;
-    const uint32_t abase = 256u * (uint32_t)l32 + 16u * (uint32_t)(g2 ^ (l32 & 15));
+    const int ar = TR ? (l32 & (TR - 1)) : l32;   // the activation row the lane's operand reads
+    const uint32_t abase = 256u * (uint32_t)ar + 16u * (uint32_t)(g2 ^ (ar & 15));
     uint32_t aoff[2 * NRT];
-    g4_aoffsets<NRT>(s_arow, wave, lane, arowbytes, aoff);
+    if constexpr (TR > 0) {
+        aoff[0] = aoff[1] = g4_aoff_tiny<TR>(s_arow, wave, lane, arowbytes);
+    } else {
+        g4_aoffsets<NRT>(s_arow, wave, lane, arowbytes, aoff);
+    }
+    auto issue_a = [&](int j, _Float16 *st, int bb, int h) __attribute__((always_inline)) {
+        if constexpr (TR > 0) g4_issue_a_tiny<TR>(rx, aoff[0], wave, st, bb, h);
+        else g4_issue_a<NRT>(rx, aoff, wave, j, st, bb, h);
+    };
+    constexpr int NAL = TR > 0 ? 1 : 2 * NRT;   // activation loads per stage (per wave)
 #pragma unroll
     for (int rt = 0; rt < NA; ++rt)
 #pragma unroll
@@ -610,7 +636,7 @@ __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_
     G4Sc<WT> s0, s1;
     // (block 0's weight loads are out already: g4_issue_w0)
 #pragma unroll
-    for (int j = 0; j < 2 * NRT; ++j) g4_issue_a<NRT>(rx, aoff, wave, j, As0, 0, 0);
+    for (int j = 0; j < NAL; ++j) issue_a(j, As0, 0, 0);
     // extra work of stage 0 spread over its 16 NRT slots: the activation
     // loads at slots 4 i (i < 2 NRT), then, all after the last of them (the
     // sync before stage 1 counts on that order) and after the copy has
@@ -631,7 +657,7 @@ __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) g4_scales<WT>(w, ct, g2, 0, sh, s0);
         g4_stage<WT, NRT>(As0, abase, w, s0, sh, 0, acc, [&](int slot) __attribute__((always_inline)) {
-            if ((slot & 3) == 0 && (slot >> 2) < 2 * NRT) g4_issue_a<NRT>(rx, aoff, wave, slot >> 2, As1, b, 1);
+            if ((slot & 3) == 0 && (slot >> 2) < NAL) issue_a(slot >> 2, As1, b, 1);
             if (slot == S0) __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the copy is in registers
 #pragma unroll
             for (int it = 0; it < NI; ++it) {
@@ -647,19 +673,19 @@ __device__ __forceinline__ void g4_kloop_n(rsrc_t rx, const int *s_arow, uint32_
         });
         g4_stage_sync<NW + NSL>();
         g4_stage<WT, NRT>(As1, abase, w, s1, sh, 1, acc, [&](int slot) __attribute__((always_inline)) {
-            if (slot < 2 * NRT) g4_issue_a<NRT>(rx, aoff, wave, slot, As0, bn, 0);
+            if (slot < NAL) issue_a(slot, As0, bn, 0);
         });
     }
 }
 
 // one specialization per row-tile count (branch once per work-group); NA
 // row tiles of accumulators (the tile size's)
-template <int WT, int NA>
+template <int WT, int NA, int TR = 0>
 __device__ __forceinline__ void g4_kloop(rsrc_t rx, const int *s_arow, uint32_t arowbytes, const G4WDma<WT> &dm,
                                          const uint32_t (&wsh)[2], uint8_t *W, int nb, int wave, int lane, int nrt,
                                          _Float16 *As0, _Float16 *As1, f32x16 (&acc)[NA][2], u32x4 (&sn)[2]) {
     if constexpr (NA == 1) {
-        g4_kloop_n<WT, 1>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc, sn);
+        g4_kloop_n<WT, 1, 1, TR>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc, sn);
     } else {
         switch (nrt) {
         case 1: g4_kloop_n<WT, 1>(rx, s_arow, arowbytes, dm, wsh, W, nb, wave, lane, As0, As1, acc, sn); break;
@@ -685,7 +711,7 @@ __device__ __forceinline__ void g4_coords(int nct, int &tile, int &ctile) {
 // tile 0 holds their h (gate) rows, column tile 1 their g (up) rows; the GLU
 // values go out as rows (fp32 to y, or fp16 to yh), whose Q8_K for the down
 // product needs whole 256-column blocks, which span two work-groups.
-template <int ACT, int NA>
+template <int ACT, int NA, int BM>
 __device__ __forceinline__ void g4_glu_store(const G2Args &g, const f32x16 (&acc)[NA][2], const G4Tile &t,
                                              int ctile, int wave, int lane, const int *s_p, _Float16 *As0,
                                              _Float16 *As1) {
@@ -700,8 +726,9 @@ __device__ __forceinline__ void g4_glu_store(const G2Args &g, const f32x16 (&acc
             if (rt >= t.nrt) break;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
+                if (BM < 32 && 8 * (i >> 2) >= BM) continue;   // (rows past a tiny tile's)
                 const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
-                _Float16 *row = m < (16 * NA) ? As0 + m * 256 : As1 + (m - (16 * NA)) * 256;
+                _Float16 *row = m < (BM / 2) ? As0 + m * 256 : As1 + (m - (BM / 2)) * 256;
                 const float v = act_pair_fast<ACT>(acc[rt][0][i], acc[rt][1][i]);
                 over = over || !(fabsf(v) <= kF16Max);
                 row[32 * wave + l32] = f16_sat(v);
@@ -711,7 +738,7 @@ __device__ __forceinline__ void g4_glu_store(const G2Args &g, const f32x16 (&acc
         __syncthreads();
         for (int idx = threadIdx.x; idx < t.mrows * 16; idx += G4_THREADS) {
             const int r = idx >> 4, c = idx & 15;
-            const _Float16 *row = r < (16 * NA) ? As0 + r * 256 : As1 + (r - (16 * NA)) * 256;
+            const _Float16 *row = r < (BM / 2) ? As0 + r * 256 : As1 + (r - (BM / 2)) * 256;
             *(uint4 *)(g.yh + (int64_t)s_p[r] * g.ldy + (int64_t)ctile * 128 + 8 * c) = *(const uint4 *)(row + 8 * c);
         }
         return;
@@ -721,15 +748,16 @@ __device__ __forceinline__ void g4_glu_store(const G2Args &g, const f32x16 (&acc
         if (rt >= t.nrt) break;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
+            if (BM < 32 && 8 * (i >> 2) >= BM) continue;
             const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
-            float *row = (float *)(m < (16 * NA) ? As0 + m * 256 : As1 + (m - (16 * NA)) * 256);
+            float *row = (float *)(m < (BM / 2) ? As0 + m * 256 : As1 + (m - (BM / 2)) * 256);
             row[32 * wave + l32] = act_pair_fast<ACT>(acc[rt][0][i], acc[rt][1][i]);
         }
     }
     __syncthreads();
     for (int idx = threadIdx.x; idx < t.mrows * 32; idx += G4_THREADS) {
         const int r = idx >> 5, c = idx & 31;
-        const float *row = (const float *)(r < (16 * NA) ? As0 + r * 256 : As1 + (r - (16 * NA)) * 256);
+        const float *row = (const float *)(r < (BM / 2) ? As0 + r * 256 : As1 + (r - (BM / 2)) * 256);
         *(float4 *)(g.y + (int64_t)s_p[r] * g.ldy + (int64_t)ctile * 128 + 4 * c) = *(const float4 *)(row + 4 * c);
     }
 }
@@ -750,17 +778,18 @@ __device__ __forceinline__ void g4_clock(const G2Args &g, int slot, bool live) {
 // with Q4_K weights, so that three work-groups share a CU and keep three
 // times the weight stream in flight)
 template <int BM>
-__global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, BM == G4_BM ? 1 : 3)))
-k_g4_glu(G2Args g) {
-    constexpr int NA = BM / 32;
+__global__ void __launch_bounds__(G4_THREADS)
+    __attribute__((amdgpu_waves_per_eu(BM == G4_BM_TINY ? 4 : 1, BM == G4_BM ? 1 : BM == G4_BM_TINY ? 4 : 3)))
+    k_g4_glu(G2Args g) {
+    constexpr int NA = BM >= 32 ? BM / 32 : 1, TR = BM < 32 ? BM : 0;
     __shared__ __attribute__((aligned(1024))) _Float16 As0[BM * G4_SK];
     __shared__ __attribute__((aligned(1024))) _Float16 As1[BM * G4_SK];
     __shared__ __attribute__((aligned(1024))) uint8_t Ws[G4_WAVES][g4_wregion<12>()];
     int tile, ctile;
     g4_coords((int)(g.I / 128), tile, ctile);
-    const bool self = BM == G4_BM_SMALL && g.ids != nullptr;
+    const bool self = BM <= G4_BM_SMALL && g.ids != nullptr;
     int my_p = -1;
-    const G4Tile t = self ? g4_self_tile(g, tile, (int *)As0, my_p) : g4_desc(g, tile);
+    const G4Tile t = self ? g4_self_tile<BM>(g, tile, (int *)As0, my_p) : g4_desc(g, tile);
     g4_clock(g, 0, t.live);
     if (!t.live) {
         g4_clock(g, 1, false);
@@ -786,14 +815,14 @@ k_g4_glu(G2Args g) {
     const uint32_t wsh[2] = {0u, 0u};
     f32x16 acc[NA][2];
     u32x4 sn[2];   // (Q6_K tiled only)
-    g4_kloop<12, NA>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc, sn);
+    g4_kloop<12, NA, TR>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc, sn);
     __builtin_amdgcn_s_waitcnt(0);   // no load may land in LDS after the work-group ends
     const int *s_p = g4_publish_rows<BM>((_Float16 *)&Ws[0][0], my_p);   // the row table in the weight region
     switch (g.act) {
-    case 0: g4_glu_store<0, NA>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
-    case 1: g4_glu_store<1, NA>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
-    case 2: g4_glu_store<2, NA>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
-    default: g4_glu_store<3, NA>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
+    case 0: g4_glu_store<0, NA, BM>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
+    case 1: g4_glu_store<1, NA, BM>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
+    case 2: g4_glu_store<2, NA, BM>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
+    default: g4_glu_store<3, NA, BM>(g, acc, t, ctile, wave, lane, s_p, As0, As1); break;
     }
     g4_clock(g, 1, true);
 }
@@ -832,17 +861,18 @@ __device__ __forceinline__ void g4_q8_rows(const G2Args &g, int mrows, const int
 // rows 256 ctile + 64 w + 32 ct + l32 (rows past ncols read zeros past the
 // matrix's resource or unused bytes, and are not stored).
 template <int WT, int BM>
-__global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, BM == G4_BM ? 1 : 3)))
-k_g4_store(G2Args g) {
-    constexpr int NA = BM / 32;
+__global__ void __launch_bounds__(G4_THREADS)
+    __attribute__((amdgpu_waves_per_eu(BM == G4_BM_TINY ? 4 : 1, BM == G4_BM ? 1 : BM == G4_BM_TINY ? 4 : 3)))
+    k_g4_store(G2Args g) {
+    constexpr int NA = BM >= 32 ? BM / 32 : 1, TR = BM < 32 ? BM : 0;
     __shared__ __attribute__((aligned(1024))) _Float16 As0[BM * G4_SK];
     __shared__ __attribute__((aligned(1024))) _Float16 As1[BM * G4_SK];
     __shared__ __attribute__((aligned(1024))) uint8_t Ws[G4_WAVES][g4_wregion<WT>()];
     int tile, ctile;
     g4_coords((int)((g.ncols + G4_NWG - 1) / G4_NWG), tile, ctile);
-    const bool self = BM == G4_BM_SMALL && g.ids != nullptr;
+    const bool self = BM <= G4_BM_SMALL && g.ids != nullptr;
     int my_p = -1;
-    const G4Tile t = self ? g4_self_tile(g, tile, (int *)As0, my_p) : g4_desc(g, tile);
+    const G4Tile t = self ? g4_self_tile<BM>(g, tile, (int *)As0, my_p) : g4_desc(g, tile);
     g4_clock(g, 0, t.live);
     if (!t.live) {
         g4_clock(g, 1, false);
@@ -869,13 +899,13 @@ k_g4_store(G2Args g) {
     }
     int *s_arow = (int *)As1;   // as in k_g4_glu
     g4_rows_publish<BM>(g, my_p, s_arow);
-    if constexpr (BM == G4_BM_SMALL) {
+    if constexpr (BM <= G4_BM_SMALL) {
         if (g.q8src) g4_q8_rows<WT == 12 ? XO_Q4 : XO_Q6>(g, t.mrows, s_arow, ctile == 0, wave, lane);
     }
     // byte offset of the lane's own rows (Q6_K block alignment)
     const uint32_t wsh[2] = {mis + (uint32_t)(n0 + l32) * rb, mis + (uint32_t)(n0 + 32 + l32) * rb};
     f32x16 acc[NA][2];
-    g4_kloop<WT, NA>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc, sn);
+    g4_kloop<WT, NA, TR>(rx, s_arow, 2u * Kin, dm, wsh, Ws[wave], (int)(Kin / QK), wave, lane, nrt, As0, As1, acc, sn);
     __builtin_amdgcn_s_waitcnt(0);   // no load may land in LDS after the work-group ends
     // rows 32 rt + 8 (i / 4) + 4 g2 + i % 4, columns n0 + 32 ct + l32
     if (g.yh) {
@@ -890,6 +920,7 @@ k_g4_store(G2Args g) {
             if (rt >= nrt) break;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
+                if (BM < 32 && 8 * (i >> 2) >= BM) continue;   // (rows past a tiny tile's)
                 const int m = 32 * rt + 8 * (i >> 2) + 4 * g2 + (i & 3);
                 _Float16 *row = m < (BM / 2) ? As0 + m * G4_NWG : As1 + (m - (BM / 2)) * G4_NWG;
 #pragma unroll
@@ -937,9 +968,10 @@ int gemm4_grid(const G2Args &g) {
 int launch_gemm4(const G2Args &g, hipStream_t st) {
     if (g.max_tiles <= 0) return 0;
     if (g.a.K % QK) return -6;
-    if (g.ids && (g.bm != G4_BM_SMALL || g.nids <= 0 || g.nids > G4_SD_IDS || g.n_expert <= 0 ||
-                  g.n_expert > G4_THREADS))
+    if (g.ids && ((g.bm != G4_BM_SMALL && g.bm != G4_BM_TINY) || g.nids <= 0 || g.nids > G4_SD_IDS ||
+                  g.n_expert <= 0 || g.n_expert > G4_THREADS))
         return -6;
+    if (g.bm == G4_BM_TINY && !g.ids) return -6;   // tiny tiles only without a dispatch
     const int64_t lim = 0x7fffffff;
     // byte offsets of the buffer loads are 32-bit
     if (g.xrows <= 0 || g.xrows * g.a.K * 2 > lim || g.a.mat_bytes + 4 > lim) return -6;
@@ -953,7 +985,7 @@ int launch_gemm4(const G2Args &g, hipStream_t st) {
                     (g.glu && !g.fused &&
                      (g.b.type != 12 || g.b.N % 32 || g.b.mat_bytes != g.b.N * g.b.row_bytes))))
         return -6;
-    if (g.q8src && (g.glu || g.bm != G4_BM_SMALL || g.q8ld % 4 || (uintptr_t)g.q8src % 8 || (uintptr_t)g.xh % 16))
+    if (g.q8src && (g.glu || g.bm > G4_BM_SMALL || g.q8ld % 4 || (uintptr_t)g.q8src % 8 || (uintptr_t)g.xh % 16))
         return -6;
     const int ntile8 = (g.max_tiles + 7) / 8;
     if (g.glu) {
@@ -966,7 +998,8 @@ int launch_gemm4(const G2Args &g, hipStream_t st) {
         if (!g.fused && ((uintptr_t)g.b.data % 4 || g.b.mat_bytes % 4)) return -6;
         const int nct = (int)(g.I / 128);
         const dim3 grid((unsigned)(8 * nct * ntile8));
-        if (g.bm == G4_BM_SMALL) hipLaunchKernelGGL(k_g4_glu<G4_BM_SMALL>, grid, dim3(G4_THREADS), 0, st, g);
+        if (g.bm == G4_BM_TINY) hipLaunchKernelGGL(k_g4_glu<G4_BM_TINY>, grid, dim3(G4_THREADS), 0, st, g);
+        else if (g.bm == G4_BM_SMALL) hipLaunchKernelGGL(k_g4_glu<G4_BM_SMALL>, grid, dim3(G4_THREADS), 0, st, g);
         else hipLaunchKernelGGL(k_g4_glu<G4_BM>, grid, dim3(G4_THREADS), 0, st, g);
     } else {
         const int nct = (int)((g.ncols + G4_NWG - 1) / G4_NWG);
@@ -975,8 +1008,11 @@ int launch_gemm4(const G2Args &g, hipStream_t st) {
         const bool sm = g.bm == G4_BM_SMALL;
         if (g.a.type == 12) {
             if ((uintptr_t)g.a.data % 4 || g.a.mat_bytes % 4 || g.a.row_bytes % 4) return -6;
-            if (sm) hipLaunchKernelGGL((k_g4_store<12, G4_BM_SMALL>), grid, dim3(G4_THREADS), 0, st, g);
+            if (g.bm == G4_BM_TINY) hipLaunchKernelGGL((k_g4_store<12, G4_BM_TINY>), grid, dim3(G4_THREADS), 0, st, g);
+            else if (sm) hipLaunchKernelGGL((k_g4_store<12, G4_BM_SMALL>), grid, dim3(G4_THREADS), 0, st, g);
             else hipLaunchKernelGGL((k_g4_store<12, G4_BM>), grid, dim3(G4_THREADS), 0, st, g);
+        } else if (g.bm == G4_BM_TINY) {
+            return -6;   // (tiny tiles: Q4_K down tables only)
         } else if (g.a.type == 14 && g.tiled) {
             if ((uintptr_t)g.a.data % 16) return -6;
             if (sm) hipLaunchKernelGGL((k_g4_store<15, G4_BM_SMALL>), grid, dim3(G4_THREADS), 0, st, g);

@@ -191,14 +191,15 @@ struct G2Args {
     const int32_t *tile_start, *tile_rows;   // the tiles' perm starts and row counts
     const int32_t *tile_perm;                // skinny products: [max_tiles][GS_BM] the tiles' perm entries
     int max_tiles;
-    int bm;               // tile rows of the dispatch: G4_BM, or G4_BM_SMALL (few rows per expert)
-    // or NULL: with bm = G4_BM_SMALL, no dispatch launch - every work-group
+    int bm;               // tile rows of the dispatch: G4_BM, or G4_BM_SMALL (few rows per expert),
+                          // or G4_BM_TINY (with ids)
+    // or NULL: with bm = G4_BM_SMALL or G4_BM_TINY, no dispatch launch - every work-group
     // derives its tile (the balanced dispatch's) from the call's nids <= 512
     // flat expert ids in [0, n_expert), n_expert <= 256; the dispatch
     // pointers above are then not read
     const int32_t *ids;
     int nids, n_expert;
-    // or NULL: with bm = G4_BM_SMALL and glu = 0, the activation rows xh of
+    // or NULL: with bm <= G4_BM_SMALL and glu = 0, the activation rows xh of
     // the tile are first made by its work-groups - the Q8_K of these fp16
     // rows [.][q8ld] (the down product's GLU rows) in xh's order, the same
     // bits the separate Q8_K pass writes (work-groups of column tile 0 count
@@ -228,6 +229,7 @@ struct G2Args {
 };
 constexpr int G4_BM = 192;
 constexpr int G4_BM_SMALL = 32;   // tiles of few rows per expert (G2Args::bm)
+constexpr int G4_BM_TINY = 8;     // tiles of at most 8 rows (G2Args::bm; only with ids: no dispatch launch)
 constexpr int G4_SD_IDS = 512;    // most ids of a call whose GEMM work-groups find their tiles themselves (G2Args::ids)
 int launch_gemm4(const G2Args &g, hipStream_t st);
 int gemm4_grid(const G2Args &g);   // work-groups launch_gemm4 launches

@@ -217,17 +217,21 @@ def test_gemm_row_tiles(name, T):
     ctx.set_fused_decode(M.DECODE_CHAIN)
     ctx.set_gemm_threshold(1)
     outs = []
-    for kind in (1, 2):
+    for kind in (1, 2, 4):   # 192-row, 32-row, 8-row (without a dispatch launch) tiles
         ctx.set_gemm_tiles(kind)
         out = M.DeviceBuffer(4 * T * spec.D)
         bufs, r = _routing_buffers(T, spec.E, spec.K)
-        M.check("forward", ctx.forward(g.layer, x, T, None, out, r))
+        # (8-row tiles need a call without dispatch outputs)
+        M.check("forward", ctx.forward(g.layer, x, T, None, out, r if kind != 4 else None))
         got = out.download(np.float32, (T, spec.D))
-        _check_routing(bufs, dbg, T, spec.E, spec.K, f"{name} T={T} tiles {kind}")
+        if kind != 4:
+            _check_routing(bufs, dbg, T, spec.E, spec.K, f"{name} T={T} tiles {kind}")
         e = rel_l2(got, ref)
-        log(f"{name} T={T} row tiles {'192' if kind == 1 else '32'}: rel-L2 {e:.3e} max-abs {max_abs(got, ref):.3e}")
+        log(f"{name} T={T} row tiles {({1: '192', 2: '32', 4: '8'})[kind]}: rel-L2 {e:.3e} "
+            f"max-abs {max_abs(got, ref):.3e}")
         assert e <= TOL
         outs.append(got)
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
     assert ctx.take_all_errors() == (0, 0, 0)
     ctx.close()

@@ -101,7 +101,7 @@ __device__ __forceinline__ G4Tile g4_desc(const G2Args &g, int tile) {
 }
 
 // Small calls without a dispatch launch (G2Args::ids set, at most
-// G4_SD_IDS ids, bm = G4_BM_SMALL): every work-group derives its own tile
+// G4_SD_IDS ids, bm = G4_BM_SMALL or G4_BM_TINY): every work-group derives its own tile
 // from the call's flat ids in LDS (scratch: the first activation buffer,
 // free until the K loop) - the counts per expert, ceil(count / BM) equal
 // tiles per expert in expert order (the dispatch's balanced tiles: the
@@ -776,7 +776,8 @@ __device__ __forceinline__ void g4_clock(const G2Args &g, int slot, bool live) {
 
 // BM: tile rows (G4_BM; G4_BM_SMALL for few rows per expert: 52 KB of LDS
 // with Q4_K weights, so that three work-groups share a CU and keep three
-// times the weight stream in flight)
+// times the weight stream in flight; G4_BM_TINY, calls without a dispatch
+// launch and at most 4 rows per expert: 40 KB, four work-groups per CU)
 template <int BM>
 __global__ void __launch_bounds__(G4_THREADS)
     __attribute__((amdgpu_waves_per_eu(BM == G4_BM_TINY ? 4 : 1, BM == G4_BM ? 1 : BM == G4_BM_TINY ? 4 : 3)))

@@ -354,6 +354,10 @@ bool plan_decodeb(const mi_moe_ctx *c, const mi_moe_layer *L, const float *x, in
     // 105.7 vs 91.8 us; qwen3omni T = 16, one row per expert: 92.2 vs 101.1).
     const int64_t ebytes = L->gate.nb[2] + (L->fused_gate_up ? 0 : L->up.nb[2]) + L->down.nb[2];
     if (ebytes > (2LL << 20) && T * L->n_expert_used > L->n_expert) return false;
+    // With tiled table copies the chain's GEMMs stream faster: past 8 tokens
+    // they win (qwen3omni, same box: T = 9 / 10 / 12 / 16 chain 66.2 / 66.9 /
+    // 71.2 / 79.6 against 71.1 / 72.8 / 78.6 / 87.3 us; T = 8: 64.8 vs 55.9).
+    if (ebytes > (2LL << 20) && L->gate_tiled.data && T > 8) return false;
     if (decodeb_tw_words(T, D, E, K, I) > c->decb_words) return false;
     if (L->gating != MI_GATING_SOFTMAX_TOPK || L->expert_scale) return false;
     if (!act_gated(L->act) || L->sh_n_ff > 0) return false;

@@ -612,8 +612,10 @@ __global__ void __launch_bounds__(64) k_topk_parts(const double *__restrict__ pa
     for (int i = 0; i < NPER; ++i) {
         const int e = lane + 64 * i;
         const double *p = parts + t * E + (e < E ? e : 0);
+        // branch-free: chunks past nch re-load the last one (never added), so
+        // no load waits for an earlier one (nch >= 1)
 #pragma unroll
-        for (int c = 0; c < RM_MAX_CHUNKS; ++c) pv[i][c] = c < nch ? p[(int64_t)c * cs] : 0.0;
+        for (int c = 0; c < RM_MAX_CHUNKS; ++c) pv[i][c] = p[(int64_t)(c < nch ? c : nch - 1) * cs];
     }
     float raw[TOPK_MAX_PER_LANE];
 #pragma unroll

@@ -399,12 +399,15 @@ int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *ctx, int64_t min_tokens_for_gemm);
  * work-groups per CU keep more of the weight stream in flight), and within
  * those 8-row tiles (four work-groups per CU) for the products of Q4_K
  * tables at most 4 rows per expert on average when the call needs no
- * dispatch outputs (up to 512 slots); 192-row tiles above; 1 192-row tiles,
+ * dispatch outputs (up to 512 slots); 64-row tiles above 8 and up to 48 rows
+ * per expert (two work-groups per CU with Q4_K weights, nearly every expert
+ * still one tile); 192-row tiles above; 1 192-row tiles,
  * 2 32-row tiles at every size; 3 the skinny products (16-row tiles, one
  * work-group per CU, the weight stream held in registers a group of blocks
  * ahead) on layers whose tables are all Q4_K with n_embd and n_ff <= 2048
  * (others take the shape rule); 4 8-row tiles wherever they apply (else
- * 32-row).  Kinds 0-2 and 4 give the same bits (the same per-row
+ * 32-row); 5 64-row tiles at every size.  Kinds 0-2, 4 and 5 give the same
+ * bits (the same per-row
  * arithmetic); the skinny products sum each output's products in another
  * order (fp32; the rows agree to ~2e-4 rel-L2 after the activations' fp16
  * and Q8_K roundings). */

@@ -111,7 +111,7 @@ struct mi_moe_ctx {
     int32_t *bad_total = nullptr;   // caller ids outside [0, E) since the last take
     int32_t *range_total = nullptr; // GEMM-path Q8_K blocks saturated at the fp16 range
     int64_t gemm_threshold = 0;   // 0: the shape rule of use_gemm
-    int gemm_tiles = 0;           // Q4_K GEMM row tiles: 0 by shape, 1 G4_BM, 2 G4_BM_SMALL, 3 GS_BM (k_gs)
+    int gemm_tiles = 0;           // Q4_K GEMM row tiles: 0 by shape, 1 G4_BM, 2 G4_BM_SMALL, 3 GS_BM (k_gs), 4 G4_BM_TINY, 5 G4_BM_MID
     int n_cu = 0;                 // compute units of the device
     // single-token fused kernel (k_decode.hip)
     int fused_decode = MI_DECODE_FUSED;
@@ -438,7 +438,8 @@ constexpr int64_t G4_SMALL_ROWS = 8;
 // +0.8 us per layer; moondream3 T = 128, half the partials: -3.2 us)
 constexpr int64_t FRONT_SPLIT_TE_MAX = 8192;
 bool g4_small_tiles(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T) {
-    if (c->gemm_tiles == 1 || c->gemm_tiles == 2 || c->gemm_tiles == 4) return c->gemm_tiles != 1;
+    if (c->gemm_tiles == 1 || c->gemm_tiles == 2 || c->gemm_tiles == 4 || c->gemm_tiles == 5)
+        return c->gemm_tiles == 2 || c->gemm_tiles == 4;
     return T * L->n_expert_used <= G4_SMALL_ROWS * L->n_expert;
 }
 // 8-row tiles (G4_BM_TINY) where the 32-row tiles would run without a
@@ -453,6 +454,21 @@ bool g4_tiny_tiles(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T) {
     if (c->gemm_tiles == 4) return true;
     if (c->gemm_tiles != 0) return false;
     return T * L->n_expert_used <= G4_TINY_ROWS * L->n_expert;
+}
+
+// 64-row tiles (G4_BM_MID: 68 KB of LDS with Q4_K weights, two work-groups
+// per CU, one's dequant beside the other's MFMA) past G4_SMALL_ROWS and up to
+// G4_MID_ROWS dispatched rows per expert on average: nearly every expert is
+// still one tile, so the weights stream once as with 192-row tiles.
+// Measured (qwen3omni, tiled copies, same box, layer us): T = 256 / 512
+// 136.9 / 155.7 -> 116.0 / 133.6 (gate/up 66.5 / 74.0 -> 55.3 / 63.3, down
+// 45.8 / 50.2 -> 35.3 / 40.6); at 64 rows per expert (T = 1024) 192.3 ->
+// 198.6 and moondream3 at 128, 184.7 -> 231: experts split into several
+// tiles stream their weights again.
+constexpr int64_t G4_MID_ROWS = 48;
+bool g4_mid_tiles(const mi_moe_ctx *c, const mi_moe_layer *L, int64_t T) {
+    if (c->gemm_tiles != 0) return c->gemm_tiles == 5;
+    return T * L->n_expert_used <= G4_MID_ROWS * L->n_expert;
 }
 
 // The skinny products (k_gs.hip: 16-row tiles, one work-group per CU, each
@@ -594,7 +610,7 @@ int run_experts(mi_moe_ctx *c, const mi_moe_layer *L, const float *x, int64_t T,
     // GEMM_BM-row tiles otherwise
     const bool g4 = gemm && g4_path(L);
     const bool gs = g4 && gs_path(c, L, T);
-    const int bm = !g4 ? GEMM_BM : gs ? GS_BM : g4_small_tiles(c, L, T) ? G4_BM_SMALL : G4_BM;
+    const int bm = !g4 ? GEMM_BM : gs ? GS_BM : g4_small_tiles(c, L, T) ? G4_BM_SMALL : g4_mid_tiles(c, L, T) ? G4_BM_MID : G4_BM;
     const int max_tiles = (int)((rows + bm - 1) / bm + max_active);
     // Small calls on the 32-row tiles, ids from the router: no dispatch
     // launch, each GEMM work-group finds its tile from the ids itself
@@ -1013,7 +1029,7 @@ int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *c, int64_t t) {
 
 int mi_moe_ctx_set_gemm_tiles(mi_moe_ctx *c, int kind) {
     if (!c) return MI_MOE_ERR_NULL;
-    if (kind < 0 || kind > 4) return MI_MOE_ERR_ARG;
+    if (kind < 0 || kind > 5) return MI_MOE_ERR_ARG;
     c->gemm_tiles = kind;
     return MI_MOE_OK;
 }
@@ -1414,6 +1430,7 @@ int mi_mul_mat_id(mi_moe_ctx *c, const mi_tensor *as, const mi_tensor *b, const 
     qx.xh = c->ax.h; qx.wtype = as->type; qx.order = 1; qx.range_total = c->range_total;
     TRY(launch_q8k_rows(bp, Kin, T * ne11, Kin, qx, st));
     G2Args a = {};
+    a.bm = G4_BM;   // the dispatch's balanced 192-row tiles
     a.a = M; a.glu = 0; a.xh = c->ax.h; a.ne11 = (int)ne11; a.K = (int)n_used;
     a.counts = dsp.counts; a.offsets = dsp.offsets; a.perm = dsp.perm; a.tile_e = dsp.tile_e;
     a.tile_r0 = dsp.tile_r0; a.tile_start = dsp.tile_start; a.tile_rows = dsp.tile_rows; a.n_tiles = dsp.n_tiles; a.max_tiles = max_tiles; a.xrows = T * ne11;

@@ -780,7 +780,7 @@ __device__ __forceinline__ void g4_clock(const G2Args &g, int slot, bool live) {
 // launch and at most 4 rows per expert: 40 KB, four work-groups per CU)
 template <int BM>
 __global__ void __launch_bounds__(G4_THREADS)
-    __attribute__((amdgpu_waves_per_eu(BM == G4_BM_TINY ? 4 : 1, BM == G4_BM ? 1 : BM == G4_BM_TINY ? 4 : 3)))
+    __attribute__((amdgpu_waves_per_eu(BM == G4_BM_TINY ? 4 : BM == G4_BM_MID ? 2 : 1, BM == G4_BM ? 1 : BM == G4_BM_TINY ? 4 : BM == G4_BM_MID ? 2 : 3)))
     k_g4_glu(G2Args g) {
     constexpr int NA = BM >= 32 ? BM / 32 : 1, TR = BM < 32 ? BM : 0;
     __shared__ __attribute__((aligned(1024))) _Float16 As0[BM * G4_SK];
@@ -863,7 +863,7 @@ __device__ __forceinline__ void g4_q8_rows(const G2Args &g, int mrows, const int
 // matrix's resource or unused bytes, and are not stored).
 template <int WT, int BM>
 __global__ void __launch_bounds__(G4_THREADS)
-    __attribute__((amdgpu_waves_per_eu(BM == G4_BM_TINY ? 4 : 1, BM == G4_BM ? 1 : BM == G4_BM_TINY ? 4 : 3)))
+    __attribute__((amdgpu_waves_per_eu(BM == G4_BM_TINY ? 4 : BM == G4_BM_MID ? 2 : 1, BM == G4_BM ? 1 : BM == G4_BM_TINY ? 4 : BM == G4_BM_MID ? 2 : 3)))
     k_g4_store(G2Args g) {
     constexpr int NA = BM >= 32 ? BM / 32 : 1, TR = BM < 32 ? BM : 0;
     __shared__ __attribute__((aligned(1024))) _Float16 As0[BM * G4_SK];
@@ -973,6 +973,7 @@ int launch_gemm4(const G2Args &g, hipStream_t st) {
                   g.n_expert <= 0 || g.n_expert > G4_THREADS))
         return -6;
     if (g.bm == G4_BM_TINY && !g.ids) return -6;   // tiny tiles only without a dispatch
+    if (g.bm != G4_BM && g.bm != G4_BM_MID && g.bm != G4_BM_SMALL && g.bm != G4_BM_TINY) return -6;
     const int64_t lim = 0x7fffffff;
     // byte offsets of the buffer loads are 32-bit
     if (g.xrows <= 0 || g.xrows * g.a.K * 2 > lim || g.a.mat_bytes + 4 > lim) return -6;
@@ -1001,25 +1002,29 @@ int launch_gemm4(const G2Args &g, hipStream_t st) {
         const dim3 grid((unsigned)(8 * nct * ntile8));
         if (g.bm == G4_BM_TINY) hipLaunchKernelGGL(k_g4_glu<G4_BM_TINY>, grid, dim3(G4_THREADS), 0, st, g);
         else if (g.bm == G4_BM_SMALL) hipLaunchKernelGGL(k_g4_glu<G4_BM_SMALL>, grid, dim3(G4_THREADS), 0, st, g);
+        else if (g.bm == G4_BM_MID) hipLaunchKernelGGL(k_g4_glu<G4_BM_MID>, grid, dim3(G4_THREADS), 0, st, g);
         else hipLaunchKernelGGL(k_g4_glu<G4_BM>, grid, dim3(G4_THREADS), 0, st, g);
     } else {
         const int nct = (int)((g.ncols + G4_NWG - 1) / G4_NWG);
         const dim3 grid((unsigned)(8 * nct * ntile8));
         if (g.yh && (g.ncols % G4_NWG || g.ldy % 8 || (uintptr_t)g.yh % 16)) return -6;
-        const bool sm = g.bm == G4_BM_SMALL;
+        const bool sm = g.bm == G4_BM_SMALL, mid = g.bm == G4_BM_MID;
         if (g.a.type == 12) {
             if ((uintptr_t)g.a.data % 4 || g.a.mat_bytes % 4 || g.a.row_bytes % 4) return -6;
             if (g.bm == G4_BM_TINY) hipLaunchKernelGGL((k_g4_store<12, G4_BM_TINY>), grid, dim3(G4_THREADS), 0, st, g);
             else if (sm) hipLaunchKernelGGL((k_g4_store<12, G4_BM_SMALL>), grid, dim3(G4_THREADS), 0, st, g);
+            else if (mid) hipLaunchKernelGGL((k_g4_store<12, G4_BM_MID>), grid, dim3(G4_THREADS), 0, st, g);
             else hipLaunchKernelGGL((k_g4_store<12, G4_BM>), grid, dim3(G4_THREADS), 0, st, g);
         } else if (g.bm == G4_BM_TINY) {
             return -6;   // (tiny tiles: Q4_K down tables only)
         } else if (g.a.type == 14 && g.tiled) {
             if ((uintptr_t)g.a.data % 16) return -6;
             if (sm) hipLaunchKernelGGL((k_g4_store<15, G4_BM_SMALL>), grid, dim3(G4_THREADS), 0, st, g);
+            else if (mid) hipLaunchKernelGGL((k_g4_store<15, G4_BM_MID>), grid, dim3(G4_THREADS), 0, st, g);
             else hipLaunchKernelGGL((k_g4_store<15, G4_BM>), grid, dim3(G4_THREADS), 0, st, g);
         } else if (g.a.type == 14) {
             if (sm) hipLaunchKernelGGL((k_g4_store<14, G4_BM_SMALL>), grid, dim3(G4_THREADS), 0, st, g);
+            else if (mid) hipLaunchKernelGGL((k_g4_store<14, G4_BM_MID>), grid, dim3(G4_THREADS), 0, st, g);
             else hipLaunchKernelGGL((k_g4_store<14, G4_BM>), grid, dim3(G4_THREADS), 0, st, g);
         } else {
             return -3;

@@ -279,7 +279,8 @@ class Context:
 
     def set_gemm_tiles(self, kind: int) -> None:
         """Q4_K-gate GEMM row tiles: 0 by shape, 1 192-row, 2 32-row, 3 the
-        skinny 16-row products (all-Q4_K layers), 4 8-row where they apply"""
+        skinny 16-row products (all-Q4_K layers), 4 8-row where they apply,
+        5 64-row"""
         call("mi_moe_ctx_set_gemm_tiles", self.h, int(kind))
 
     def set_fused_decode(self, mode) -> None:

@@ -27,8 +27,10 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--chain", action="store_true", help="the kernel chain also where a fused decode kernel applies")
     ap.add_argument("--tiled", action="store_true", help="tiled copies of the Q4_K tables for the grouped GEMMs")
-    ap.add_argument("--gemm-tiles", type=int, default=0, choices=[0, 1, 2, 3],
-                    help="GEMM row tiles (mi_moe_ctx_set_gemm_tiles): 0 by shape, 3 the skinny products")
+    ap.add_argument("--gemm-tiles", type=int, default=0, choices=[0, 1, 2, 3, 4, 5],
+                    help="GEMM row tiles (mi_moe_ctx_set_gemm_tiles): 0 by shape, 1 192 rows, 2 32 rows, "
+                         "3 the skinny products, 4 8 rows, 5 64 rows")
+    ap.add_argument("--stages", action="store_true", help="also the per-stage averages of 32 profiled calls")
     a = ap.parse_args()
     spec = W.CONFIGS[a.config]["spec"]
     T = a.tokens
@@ -72,6 +74,16 @@ def main():
               flush=True)
         g.destroy()
         s.destroy()
+    if a.stages:
+        ctx.set_profiling(True)
+        acc = {}
+        for i in range(32):
+            M.check("forward", ctx.forward(layers[i % n].layer, xs[i % n], T, None, out))
+            for k, v in ctx.stage_times():
+                acc[k] = acc.get(k, 0.0) + v / 32
+        ctx.set_profiling(False)
+        print(f"config {a.config} T={T} stages (us): " + ", ".join(f"{k} {1e3 * v:.1f}" for k, v in acc.items()),
+              flush=True)
     ctx.close()
 
 

@@ -199,9 +199,9 @@ def test_config4_stack_and_fed_back_decode():
                                     ("qo_cfg3_tiled", 8), ("qo_cfg3_tiled", 16), ("qo_cfg3_tiled", 64),
                                     ("md_cfg1_tiled", 24), ("md_cfg1_tiled", 64)])
 def test_gemm_row_tiles(name, T):
-    """Both row-tile sizes of the 4-wave GEMMs at one size: 32-row tiles (two
-    or three work-groups per CU; the default up to 8 dispatched rows per
-    expert) and 192-row balanced tiles give the same bits (each output's K
+    """Every row-tile size of the 4-wave GEMMs at one size: 8-, 32- and 64-row
+    tiles (two to four work-groups per CU; 32 rows the default up to 8
+    dispatched rows per expert) and 192-row balanced tiles give the same bits (each output's K
     order is the same), and match the oracle.  `_tiled`: the layers carry
     tiled copies of their tables."""
     spec = W.CONFIGS[3]["spec"] if name.startswith("qo_cfg3") else W.CONFIGS[1]["spec"]
@@ -217,7 +217,7 @@ def test_gemm_row_tiles(name, T):
     ctx.set_fused_decode(M.DECODE_CHAIN)
     ctx.set_gemm_threshold(1)
     outs = []
-    for kind in (1, 2, 4):   # 192-row, 32-row, 8-row (without a dispatch launch) tiles
+    for kind in (1, 2, 4, 5):   # 192-row, 32-row, 8-row (without a dispatch launch), 64-row tiles
         ctx.set_gemm_tiles(kind)
         out = M.DeviceBuffer(4 * T * spec.D)
         bufs, r = _routing_buffers(T, spec.E, spec.K)
@@ -227,11 +227,12 @@ def test_gemm_row_tiles(name, T):
         if kind != 4:
             _check_routing(bufs, dbg, T, spec.E, spec.K, f"{name} T={T} tiles {kind}")
         e = rel_l2(got, ref)
-        log(f"{name} T={T} row tiles {({1: '192', 2: '32', 4: '8'})[kind]}: rel-L2 {e:.3e} "
+        log(f"{name} T={T} row tiles {({1: '192', 2: '32', 4: '8', 5: '64'})[kind]}: rel-L2 {e:.3e} "
             f"max-abs {max_abs(got, ref):.3e}")
         assert e <= TOL
         outs.append(got)
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
     assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
+    assert np.array_equal(outs[0].view(np.uint32), outs[3].view(np.uint32))
     assert ctx.take_all_errors() == (0, 0, 0)
     ctx.close()

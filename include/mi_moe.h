@@ -134,7 +134,7 @@ typedef struct {
 
 /* Optional routing outputs of mi_moe_forward (device pointers, any may be
  * NULL).  Layouts are row-major with tokens outermost.  Asking for counts,
- * offsets or perm makes small calls (at most 512 ids on the 32-row GEMM
+ * offsets or perm makes small calls (at most 1024 ids on the 32-row GEMM
  * tiles) launch the dispatch kernel that writes them, which the products
  * otherwise do without; the results are bit-identical either way. */
 typedef struct {
@@ -399,7 +399,7 @@ int mi_moe_ctx_set_gemm_threshold(mi_moe_ctx *ctx, int64_t min_tokens_for_gemm);
  * work-groups per CU keep more of the weight stream in flight), and within
  * those 8-row tiles (four work-groups per CU) for the products of Q4_K
  * tables at most 4 rows per expert on average when the call needs no
- * dispatch outputs (up to 512 slots); 64-row tiles above 8 and up to 48 rows
+ * dispatch outputs (up to 1024 slots); 64-row tiles above 8 and up to 48 rows
  * per expert (two work-groups per CU with Q4_K weights, nearly every expert
  * still one tile); 192-row tiles above; 1 192-row tiles,
  * 2 32-row tiles at every size; 3 the skinny products (16-row tiles, one

@@ -109,23 +109,26 @@ __device__ __forceinline__ G4Tile g4_desc(const G2Args &g, int tile) {
 // `tile`, and that tile's rows: the expert's flat slot indices in ascending
 // order (ballots per wave, wave totals in LDS), rows r0 .. r0 + rows of
 // them.  Thread m < rows returns row m's slot index in p, else -1.
-static_assert(G4_SD_IDS == 2 * G4_THREADS, "two ids per thread");
+constexpr int G4_SD_NPT = G4_SD_IDS / G4_THREADS;   // ids per thread
+static_assert(G4_SD_IDS == G4_SD_NPT * G4_THREADS && G4_SD_NPT <= 4, "whole ids per thread");
 template <int BM>
 __device__ __forceinline__ G4Tile g4_self_tile(const G2Args &g, int tile, int *s, int &p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = g.n_expert, n = g.nids;
     int *s_cnt = s;              // [256] rows per expert
-    int *s_wt = s + 256;         // [4] wave totals of the tile scan; [4 .. 8) / [8 .. 12): ballot counts
-    int *s_sel = s + 272;        // [0] expert of the tile (-1: none), [1] its tile index within the expert
+    int *s_wt = s + 256;         // [4] wave totals of the tile scan; [4 + 4 j, 8 + 4 j): ballot counts of id j
+    int *s_sel = s + 280;        // [0] expert of the tile (-1: none), [1] its tile index within the expert
     int *s_rows = s + 288;       // [BM] the tile's slot indices
-    const int id0 = tid < n ? g.ids[tid] : -1;
-    const int id1 = tid + G4_THREADS < n ? g.ids[tid + G4_THREADS] : -1;
+    int id[G4_SD_NPT];           // thread i holds ids i + j * G4_THREADS
+#pragma unroll
+    for (int j = 0; j < G4_SD_NPT; ++j) id[j] = tid + j * G4_THREADS < n ? g.ids[tid + j * G4_THREADS] : -1;
     s_cnt[tid] = 0;
     if (tid == 0) s_sel[0] = -1;
     if (tid < BM) s_rows[tid] = 0;   // (every entry a valid row, whatever follows)
     __syncthreads();
-    if (id0 >= 0 && id0 < E) atomicAdd(&s_cnt[id0], 1);
-    if (id1 >= 0 && id1 < E) atomicAdd(&s_cnt[id1], 1);
+#pragma unroll
+    for (int j = 0; j < G4_SD_NPT; ++j)
+        if (id[j] >= 0 && id[j] < E) atomicAdd(&s_cnt[id[j]], 1);
     __syncthreads();
     // tiles per expert (thread e), inclusive scan over the 256 experts
     const int cnt_e = tid < E ? s_cnt[tid] : 0;
@@ -157,25 +160,29 @@ __device__ __forceinline__ G4Tile g4_self_tile(const G2Args &g, int tile, int *s
     const int r0 = sub * base + (sub < extra ? sub : extra);
     t.mrows = base + (sub < extra ? 1 : 0);
     t.nrt = (t.mrows + 31) >> 5;
-    // ranks in flat order: the first G4_THREADS ids (id0), then the rest (id1)
-    const uint64_t b0 = __ballot(id0 == t.e), b1 = __ballot(id1 == t.e);
+    // ranks in flat order: ids 0 .. G4_THREADS - 1 (id[0]), then the next
+    // G4_THREADS (id[1]), ...
     const uint64_t below = (1ull << lane) - 1ull;
-    if (lane == 0) {
-        s_wt[4 + wave] = __builtin_popcountll(b0);
-        s_wt[8 + wave] = __builtin_popcountll(b1);
+    uint64_t bal[G4_SD_NPT];
+#pragma unroll
+    for (int j = 0; j < G4_SD_NPT; ++j) {
+        bal[j] = __ballot(id[j] == t.e);
+        if (lane == 0) s_wt[4 + 4 * j + wave] = __builtin_popcountll(bal[j]);
     }
     __syncthreads();
-    int pre0 = 0, tot0 = 0, pre1 = 0;
+    int done = 0;   // the expert's ids among the earlier groups
 #pragma unroll
-    for (int w = 0; w < G4_WAVES; ++w) {
-        tot0 += s_wt[4 + w];
-        pre0 += w < wave ? s_wt[4 + w] : 0;
-        pre1 += w < wave ? s_wt[8 + w] : 0;
+    for (int j = 0; j < G4_SD_NPT; ++j) {
+        int pre = 0, tot = 0;
+#pragma unroll
+        for (int w = 0; w < G4_WAVES; ++w) {
+            tot += s_wt[4 + 4 * j + w];
+            pre += w < wave ? s_wt[4 + 4 * j + w] : 0;
+        }
+        const int rk = done + pre + __builtin_popcountll(bal[j] & below);
+        if (id[j] == t.e && rk >= r0 && rk < r0 + t.mrows) s_rows[rk - r0] = tid + j * G4_THREADS;
+        done += tot;
     }
-    const int rk0 = pre0 + __builtin_popcountll(b0 & below);
-    const int rk1 = tot0 + pre1 + __builtin_popcountll(b1 & below);
-    if (id0 == t.e && rk0 >= r0 && rk0 < r0 + t.mrows) s_rows[rk0 - r0] = tid;
-    if (id1 == t.e && rk1 >= r0 && rk1 < r0 + t.mrows) s_rows[rk1 - r0] = tid + G4_THREADS;
     __syncthreads();
     p = tid < t.mrows ? s_rows[tid] : -1;
     return t;

@@ -194,7 +194,7 @@ struct G2Args {
     int bm;               // tile rows of the dispatch: G4_BM, G4_BM_MID, or G4_BM_SMALL (few rows
                           // per expert), or G4_BM_TINY (with ids)
     // or NULL: with bm = G4_BM_SMALL or G4_BM_TINY, no dispatch launch - every work-group
-    // derives its tile (the balanced dispatch's) from the call's nids <= 512
+    // derives its tile (the balanced dispatch's) from the call's nids <= 1024
     // flat expert ids in [0, n_expert), n_expert <= 256; the dispatch
     // pointers above are then not read
     const int32_t *ids;
@@ -231,7 +231,7 @@ constexpr int G4_BM = 192;
 constexpr int G4_BM_SMALL = 32;   // tiles of few rows per expert (G2Args::bm)
 constexpr int G4_BM_MID = 64;     // two work-groups per CU (G2Args::bm; Q4_K weights)
 constexpr int G4_BM_TINY = 8;     // tiles of at most 8 rows (G2Args::bm; only with ids: no dispatch launch)
-constexpr int G4_SD_IDS = 512;    // most ids of a call whose GEMM work-groups find their tiles themselves (G2Args::ids)
+constexpr int G4_SD_IDS = 1024;    // most ids of a call whose GEMM work-groups find their tiles themselves (G2Args::ids)
 int launch_gemm4(const G2Args &g, hipStream_t st);
 int gemm4_grid(const G2Args &g);   // work-groups launch_gemm4 launches
 
